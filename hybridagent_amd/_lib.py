@@ -1,0 +1,291 @@
+"""ctypes binding of libw4a16moe.so (the C ABI declared in include/w4a16moe.h).
+
+Tensors stay owned by PyTorch: this module checks device / dtype / shape /
+contiguity, allocates outputs and workspaces through torch's caching
+allocator, passes raw device pointers plus ``torch.cuda.current_stream()``,
+and maps non-zero status codes to ``ValueError`` (bad arguments) or
+``RuntimeError`` (launch failures).  There is no CPU fallback: every entry
+point requires CUDA (HIP) tensors and the built library, and raises if
+either is missing.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libw4a16moe.so"
+
+W4A16_OK = 0
+_STATUS_EXC = {1: ValueError, 2: ValueError, 3: ValueError, 4: ValueError, 5: ValueError,
+               6: RuntimeError}
+
+# name -> (restype, argtypes); the exact set declared in include/w4a16moe.h
+_VP, _I64, _SZ, _F32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_size_t, ctypes.c_float
+SIGNATURES = {
+    "w4a16moe_version": (ctypes.c_int, []),
+    "w4a16moe_status_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "w4a16_dequantize": (ctypes.c_int, [_VP, _VP, _VP, _I64, _I64, _I64, _VP]),
+    "w4a16_linear_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
+    "w4a16_linear": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
+    "moe_router_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
+    "moe_router_topk": (ctypes.c_int, [_VP, _VP, _F32, _VP, _VP, _F32, _I64, _I64, _I64, _I64,
+                                       _VP, _VP, _VP, _VP, _SZ, _VP]),
+    "moe_topk_from_logits": (ctypes.c_int, [_VP, _VP, _I64, _I64, _I64, _VP, _VP, _VP]),
+    "moe_sort_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
+    "moe_sort_permute": (ctypes.c_int, [_VP, _I64, _I64, _I64, _VP, _VP, _VP, _SZ, _VP]),
+    "moe_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
+    "moe_forward": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64,
+                                   _I64, _I64, _VP, _SZ, _VP]),
+}
+
+_lib = None
+
+
+def load(path: os.PathLike | str | None = None) -> ctypes.CDLL:
+    """Load (once) and return the library; raise if it has not been built."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path is not None else LIB_PATH
+    if not p.exists():
+        raise RuntimeError(
+            f"{p} not found: the W4A16 MoE HIP library is not built "
+            "(run `python -m hybridagent_amd.build`); there is no fallback path")
+    lib = ctypes.CDLL(str(p))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def available() -> bool:
+    """True when the library file exists and loads."""
+    try:
+        load()
+        return True
+    except (RuntimeError, OSError):
+        return False
+
+
+def status_string(status: int) -> str:
+    return load().w4a16moe_status_string(status).decode()
+
+
+def _check(status: int, what: str) -> None:
+    if status != W4A16_OK:
+        exc = _STATUS_EXC.get(status, RuntimeError)
+        raise exc(f"{what}: {status_string(status)} (status {status})")
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_gpu(*tensors: torch.Tensor) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError(
+                "hybridagent_amd W4A16 kernels run on the GPU only (got a CPU tensor); "
+                "there is no CPU fallback")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} vs {t.device}")
+    return dev
+
+
+def _bf16(t: torch.Tensor, name: str) -> torch.Tensor:
+    if t.dtype != torch.bfloat16:
+        raise ValueError(f"{name} must be bfloat16, got {t.dtype}")
+    return t.contiguous()
+
+
+def _i32(t: torch.Tensor, name: str) -> torch.Tensor:
+    if t.dtype != torch.int32:
+        raise ValueError(f"{name} must be int32, got {t.dtype}")
+    return t.contiguous()
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor | None:
+    if nbytes == 0:
+        return None
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+def infer_group_size(K: int, n_groups: int) -> int:
+    """Group size G (power of two >= 32) with ceil(K / G) == n_groups."""
+    if n_groups <= 0:
+        raise ValueError("scale has no groups")
+    if n_groups == 1:
+        g = 32
+        while g < K:
+            g *= 2
+        return g
+    g = 32
+    while g <= K:
+        if -(-K // g) == n_groups:
+            return g
+        g *= 2
+    raise ValueError(f"no power-of-two group size gives ceil({K}/G) == {n_groups}")
+
+
+# --------------------------------------------------------------------------- ops
+
+def dequantize(packed: torch.Tensor, scale: torch.Tensor, group_size: int | None = None) -> torch.Tensor:
+    """bf16 [..., N, K] = bf16_RNE(q * s)   (quantization.py:132-137)."""
+    dev = _require_gpu(packed, scale)
+    packed = _i32(packed, "packed")
+    scale = _bf16(scale, "scale")
+    K = packed.shape[-1] * 8
+    if scale.shape[:-1] != packed.shape[:-1]:
+        raise ValueError(f"scale leading shape {tuple(scale.shape)} does not match packed {tuple(packed.shape)}")
+    G = group_size or infer_group_size(K, scale.shape[-1])
+    if scale.shape[-1] != -(-K // G):
+        raise ValueError(f"scale has {scale.shape[-1]} groups, expected ceil({K}/{G})")
+    out = torch.empty((*packed.shape[:-1], K), dtype=torch.bfloat16, device=dev)
+    rows = packed.numel() // max(1, packed.shape[-1])
+    with torch.cuda.device(dev):
+        _check(load().w4a16_dequantize(_ptr(packed), _ptr(scale), _ptr(out), rows, K, G, _stream(dev)),
+               "w4a16_dequantize")
+    return out
+
+
+def linear(x: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tensor,
+           bias: torch.Tensor | None = None, group_size: int | None = None) -> torch.Tensor:
+    """y = x @ dequant(W)^T (+ bias)   (quantization.py:171-175); x [..., K] bf16."""
+    dev = _require_gpu(x, w_packed, w_scale, bias)
+    x = _bf16(x, "x")
+    w_packed = _i32(w_packed, "weight_packed")
+    w_scale = _bf16(w_scale, "weight_scale")
+    if bias is not None:
+        bias = _bf16(bias, "bias")
+    N, K8 = w_packed.shape
+    K = K8 * 8
+    if x.shape[-1] != K:
+        raise ValueError(f"x has {x.shape[-1]} features, weight expects {K}")
+    if w_scale.shape[0] != N:
+        raise ValueError("weight_scale rows do not match weight_packed")
+    G = group_size or infer_group_size(K, w_scale.shape[-1])
+    if w_scale.shape[-1] != -(-K // G):
+        raise ValueError(f"weight_scale has {w_scale.shape[-1]} groups, expected ceil({K}/{G})")
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, K)
+    M = x2.shape[0]
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    lib = load()
+    ws = _workspace(lib.w4a16_linear_workspace_bytes(M, K, G), dev)
+    with torch.cuda.device(dev):
+        _check(lib.w4a16_linear(_ptr(x2), _ptr(w_packed), _ptr(w_scale), _ptr(bias), _ptr(y), M, N, K, G,
+                                _ptr(ws), 0 if ws is None else ws.numel(), _stream(dev)),
+               "w4a16_linear")
+    return y.reshape(*lead, N)
+
+
+def router_topk(hidden: torch.Tensor, router_scale: torch.Tensor, scalar_root: float,
+                proj_w: torch.Tensor, per_expert_scale: torch.Tensor, eps: float, top_k: int,
+                return_logits: bool = False):
+    """Router of backends.py:111-117 -> (top_k_weights fp32, top_k_index int64[, logits bf16])."""
+    dev = _require_gpu(hidden, router_scale, proj_w, per_expert_scale)
+    H = hidden.shape[-1]
+    h2 = _bf16(hidden, "hidden").reshape(-1, H)
+    router_scale = _bf16(router_scale, "router scale")
+    proj_w = _bf16(proj_w, "router proj weight")
+    per_expert_scale = _bf16(per_expert_scale, "per_expert_scale")
+    E = proj_w.shape[0]
+    if proj_w.shape[1] != H or router_scale.numel() != H or per_expert_scale.numel() != E:
+        raise ValueError("router parameter shapes do not match hidden size / expert count")
+    M = h2.shape[0]
+    idx = torch.empty((M, top_k), dtype=torch.int64, device=dev)
+    w = torch.empty((M, top_k), dtype=torch.float32, device=dev)
+    logits = torch.empty((M, E), dtype=torch.bfloat16, device=dev) if return_logits else None
+    lib = load()
+    ws = _workspace(lib.moe_router_workspace_bytes(M, H, E), dev)
+    with torch.cuda.device(dev):
+        _check(lib.moe_router_topk(_ptr(h2), _ptr(router_scale), float(scalar_root), _ptr(proj_w),
+                                   _ptr(per_expert_scale), float(eps), M, H, E, top_k, _ptr(logits),
+                                   _ptr(idx), _ptr(w), _ptr(ws), 0 if ws is None else ws.numel(),
+                                   _stream(dev)),
+               "moe_router_topk")
+    if return_logits:
+        return w, idx, logits
+    return w, idx
+
+
+def topk_from_logits(logits: torch.Tensor, per_expert_scale: torch.Tensor, top_k: int):
+    """softmax/top-k/renormalise/per-expert scale on given bf16 logits [M, E]."""
+    dev = _require_gpu(logits, per_expert_scale)
+    logits = _bf16(logits, "logits")
+    per_expert_scale = _bf16(per_expert_scale, "per_expert_scale")
+    M, E = logits.shape
+    idx = torch.empty((M, top_k), dtype=torch.int64, device=dev)
+    w = torch.empty((M, top_k), dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        _check(load().moe_topk_from_logits(_ptr(logits), _ptr(per_expert_scale), M, E, top_k, _ptr(idx),
+                                           _ptr(w), _stream(dev)),
+               "moe_topk_from_logits")
+    return w, idx
+
+
+def sort_permute(top_k_index: torch.Tensor, num_experts: int):
+    """(sorted_pos int32 [M*k], expert_offsets int32 [E+1])   (quantization.py:266-276)."""
+    dev = _require_gpu(top_k_index)
+    idx = top_k_index.to(torch.int64).contiguous()
+    M, k = idx.shape
+    sorted_pos = torch.empty(M * k, dtype=torch.int32, device=dev)
+    offsets = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
+    lib = load()
+    ws = _workspace(lib.moe_sort_workspace_bytes(max(M, 1), k, num_experts), dev)
+    with torch.cuda.device(dev):
+        _check(lib.moe_sort_permute(_ptr(idx), M, k, num_experts, _ptr(sorted_pos), _ptr(offsets), _ptr(ws),
+                                    0 if ws is None else ws.numel(), _stream(dev)),
+               "moe_sort_permute")
+    return sorted_pos, offsets
+
+
+def moe_forward(hidden_states: torch.Tensor, top_k_index: torch.Tensor, top_k_weights: torch.Tensor,
+                gu_packed: torch.Tensor, gu_scale: torch.Tensor, dn_packed: torch.Tensor,
+                dn_scale: torch.Tensor, group_size: int | None = None) -> torch.Tensor:
+    """W4A16 MoE layer output [T, H] bf16  (quantization.py:88-129)."""
+    dev = _require_gpu(hidden_states, top_k_index, top_k_weights, gu_packed, gu_scale, dn_packed, dn_scale)
+    H = hidden_states.shape[-1]
+    x = _bf16(hidden_states, "hidden_states").reshape(-1, H)
+    idx = top_k_index.reshape(x.shape[0], -1).to(torch.int64).contiguous()
+    w = top_k_weights.reshape(x.shape[0], -1).to(torch.float32).contiguous()
+    gu_packed = _i32(gu_packed, "gate_up_packed")
+    dn_packed = _i32(dn_packed, "down_packed")
+    gu_scale = _bf16(gu_scale, "gate_up_scale")
+    dn_scale = _bf16(dn_scale, "down_scale")
+    E, two_i, h8 = gu_packed.shape
+    I = two_i // 2
+    if h8 * 8 != H or dn_packed.shape != (E, H, I // 8) or two_i % 2:
+        raise ValueError(f"expert weight shapes {tuple(gu_packed.shape)} / {tuple(dn_packed.shape)} "
+                         f"do not match hidden size {H}")
+    G = group_size or infer_group_size(H, gu_scale.shape[-1])
+    if gu_scale.shape != (E, two_i, -(-H // G)) or dn_scale.shape != (E, H, -(-I // G)):
+        raise ValueError(f"scale shapes {tuple(gu_scale.shape)} / {tuple(dn_scale.shape)} "
+                         f"do not match group size {G}")
+    if w.shape != idx.shape:
+        raise ValueError("top_k_weights and top_k_index shapes differ")
+    M, k = idx.shape
+    out = torch.empty((M, H), dtype=torch.bfloat16, device=dev)
+    lib = load()
+    ws = _workspace(lib.moe_workspace_bytes(max(M, 1), k, E, H, I), dev)
+    with torch.cuda.device(dev):
+        _check(lib.moe_forward(_ptr(x), _ptr(idx), _ptr(w), _ptr(gu_packed), _ptr(gu_scale), _ptr(dn_packed),
+                               _ptr(dn_scale), _ptr(out), M, k, E, H, I, G, _ptr(ws),
+                               0 if ws is None else ws.numel(), _stream(dev)),
+               "moe_forward")
+    return out.reshape(*hidden_states.shape[:-1], H)

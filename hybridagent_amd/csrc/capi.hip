@@ -1,0 +1,279 @@
+// C ABI of libw4a16moe.so: host-side validation, workspace carving and
+// kernel launches.  See include/w4a16moe.h for the contract of each entry
+// point and the reference function it replaces.
+#include "w4a16moe.h"
+
+#include "launch.hpp"
+
+using namespace w4a16;
+
+namespace {
+
+constexpr int kVersion = (0 << 16) | (2 << 8) | 0;
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline bool valid_group(int64_t G) { return G >= 32 && G <= (1 << 20) && (G & (G - 1)) == 0; }
+
+inline size_t round256(size_t b) { return (b + 255) & ~size_t(255); }
+
+// Bump allocator over a caller-provided workspace.
+struct Carve {
+  char* base;
+  size_t used = 0;
+  explicit Carve(void* p) : base(static_cast<char*>(p)) {}
+  template <typename T>
+  T* take(size_t count) {
+    T* p = reinterpret_cast<T*>(base ? base + used : nullptr);
+    used += round256(count * sizeof(T));
+    return p;
+  }
+};
+
+inline int launch_status(hipError_t e) { return e == hipSuccess ? W4A16_OK : W4A16_ERR_LAUNCH; }
+
+inline int router_ksplit(int64_t M) { return M <= 64 ? 8 : 1; }
+
+// One shared description of the MoE workspace so sizing and carving agree.
+struct MoeLayout {
+  int32_t* offsets;
+  int32_t* active;
+  int32_t* counters;
+  int32_t* sorted_pos;
+  int32_t* tiles;
+  uint16_t* xp;
+  uint16_t* inter;
+  uint16_t* dn;
+  size_t bytes;
+};
+
+MoeLayout moe_layout(void* ws, int64_t M, int64_t k, int64_t E, int64_t H, int64_t I) {
+  Carve c(ws);
+  MoeLayout L;
+  L.offsets = c.take<int32_t>(E + 1);
+  L.active = c.take<int32_t>(E);
+  L.counters = c.take<int32_t>(2);
+  L.sorted_pos = c.take<int32_t>(M * k);
+  L.tiles = c.take<int32_t>(M * k / kPrefillBM + E + 1);
+  L.xp = c.take<uint16_t>(M * H);
+  L.inter = c.take<uint16_t>(M * k * I);
+  L.dn = c.take<uint16_t>(M * k * H);
+  L.bytes = c.used;
+  return L;
+}
+
+}  // namespace
+
+extern "C" {
+
+int w4a16moe_version(void) { return kVersion; }
+
+const char* w4a16moe_status_string(int status) {
+  switch (status) {
+    case W4A16_OK: return "ok";
+    case W4A16_ERR_NULL: return "a required pointer is NULL";
+    case W4A16_ERR_SHAPE: return "a size is out of range or inconsistent";
+    case W4A16_ERR_GROUP: return "unsupported group size (power of two >= 32 required)";
+    case W4A16_ERR_ALIGN: return "a pointer is not 16-byte aligned";
+    case W4A16_ERR_WORKSPACE: return "workspace missing or too small";
+    case W4A16_ERR_LAUNCH: return "HIP kernel launch failed";
+    default: return "unknown status";
+  }
+}
+
+int w4a16_dequantize(const int32_t* packed, const uint16_t* scale, uint16_t* out, int64_t rows,
+                     int64_t K, int64_t group_size, void* stream) {
+  if (rows < 0 || K <= 0 || K % 8 != 0 || K > (1 << 24)) return W4A16_ERR_SHAPE;
+  if (!valid_group(group_size)) return W4A16_ERR_GROUP;
+  if (rows == 0) return W4A16_OK;
+  if (!packed || !scale || !out) return W4A16_ERR_NULL;
+  if (!aligned16(out)) return W4A16_ERR_ALIGN;
+  return launch_status(launch_dequant(packed, scale, out, rows, (int)K, (int)group_size,
+                                      static_cast<hipStream_t>(stream)));
+}
+
+size_t w4a16_linear_workspace_bytes(int64_t M, int64_t K, int64_t group_size) {
+  if (M <= 0 || K <= 0) return 0;
+  return group_size % 128 == 0 ? round256(size_t(M) * K * 2) : 0;
+}
+
+int w4a16_linear(const uint16_t* x, const int32_t* w_packed, const uint16_t* w_scale,
+                 const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int64_t K,
+                 int64_t group_size, void* workspace, size_t workspace_bytes, void* stream) {
+  if (M < 0 || N <= 0 || K <= 0 || K % 32 != 0 || K > (1 << 24) || N > (1 << 24) ||
+      M > (1 << 24))
+    return W4A16_ERR_SHAPE;
+  if (!valid_group(group_size)) return W4A16_ERR_GROUP;
+  if (M == 0) return W4A16_OK;
+  if (!x || !w_packed || !w_scale || !y) return W4A16_ERR_NULL;
+  if (!aligned16(x) || !aligned16(w_packed)) return W4A16_ERR_ALIGN;
+  const size_t need = w4a16_linear_workspace_bytes(M, K, group_size);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return W4A16_ERR_WORKSPACE;
+  if (need > 0 && !aligned16(workspace)) return W4A16_ERR_ALIGN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool bias_form = group_size % 128 == 0;
+  const uint16_t* act = x;
+  if (bias_form) {
+    uint16_t* xp = static_cast<uint16_t*>(workspace);
+    hipError_t e = launch_bias_order(x, xp, M, (int)K, s);
+    if (e != hipSuccess) return W4A16_ERR_LAUNCH;
+    act = xp;
+  }
+  DecodeArgs a{};
+  a.act = act;
+  a.wp = w_packed;
+  a.ws = w_scale;
+  a.bias = bias;
+  a.out = y;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.G = (int)group_size;
+  a.ng = (int)((K + group_size - 1) / group_size);
+  a.topk = 1;
+  a.I = 0;
+  return launch_status(launch_decode(kModeDense, bias_form, a, (int)((N + 15) / 16), 1, s));
+}
+
+size_t moe_router_workspace_bytes(int64_t M, int64_t H, int64_t E) {
+  if (M <= 0 || H <= 0 || E <= 0) return 0;
+  return round256(size_t(M) * H * 2) + round256(size_t(router_ksplit(M)) * M * E * 4);
+}
+
+int moe_router_topk(const uint16_t* hidden, const uint16_t* router_scale, float scalar_root,
+                    const uint16_t* proj_w, const uint16_t* per_expert_scale, float eps,
+                    int64_t M, int64_t H, int64_t E, int64_t top_k, uint16_t* logits_out,
+                    int64_t* topk_idx, float* topk_w, void* workspace, size_t workspace_bytes,
+                    void* stream) {
+  if (M < 0 || M > (1 << 24) || H <= 0 || H % 32 != 0 || H > (1 << 20) || E <= 0 ||
+      E > kMaxExperts || top_k <= 0 || top_k > kMaxTopK || top_k > E)
+    return W4A16_ERR_SHAPE;
+  if (M == 0) return W4A16_OK;
+  if (!hidden || !router_scale || !proj_w || !per_expert_scale || !topk_idx || !topk_w)
+    return W4A16_ERR_NULL;
+  if (!aligned16(hidden) || !aligned16(proj_w)) return W4A16_ERR_ALIGN;
+  const size_t need = moe_router_workspace_bytes(M, H, E);
+  if (workspace == nullptr || workspace_bytes < need) return W4A16_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return W4A16_ERR_ALIGN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Carve c(workspace);
+  uint16_t* r = c.take<uint16_t>(M * H);
+  const int ks = router_ksplit(M);
+  float* partial = c.take<float>(size_t(ks) * M * E);
+  hipError_t e = launch_router_norm(hidden, router_scale, scalar_root, eps, r, (int)M, (int)H, s);
+  if (e == hipSuccess) e = launch_router_logits(r, proj_w, partial, (int)M, (int)H, (int)E, ks, s);
+  if (e == hipSuccess)
+    e = launch_router_topk(partial, ks, nullptr, per_expert_scale, logits_out, topk_idx, topk_w,
+                           (int)M, (int)E, (int)top_k, s);
+  return launch_status(e);
+}
+
+int moe_topk_from_logits(const uint16_t* logits, const uint16_t* per_expert_scale, int64_t M,
+                         int64_t E, int64_t top_k, int64_t* topk_idx, float* topk_w,
+                         void* stream) {
+  if (M < 0 || M > (1 << 24) || E <= 0 || E > kMaxExperts || top_k <= 0 || top_k > kMaxTopK ||
+      top_k > E)
+    return W4A16_ERR_SHAPE;
+  if (M == 0) return W4A16_OK;
+  if (!logits || !per_expert_scale || !topk_idx || !topk_w) return W4A16_ERR_NULL;
+  return launch_status(launch_router_topk(nullptr, 0, logits, per_expert_scale, nullptr, topk_idx,
+                                          topk_w, (int)M, (int)E, (int)top_k,
+                                          static_cast<hipStream_t>(stream)));
+}
+
+size_t moe_sort_workspace_bytes(int64_t M, int64_t top_k, int64_t E) {
+  if (M <= 0 || top_k <= 0 || E <= 0) return 0;
+  return round256(size_t(E) * 4) + round256(8) + round256(size_t(M * top_k / kPrefillBM + E + 1) * 4);
+}
+
+int moe_sort_permute(const int64_t* topk_idx, int64_t M, int64_t top_k, int64_t E,
+                     int32_t* sorted_pos, int32_t* expert_offsets, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  if (M < 0 || top_k <= 0 || top_k > kMaxTopK || E <= 0 || E > kMaxExperts ||
+      M * top_k > (int64_t(1) << 30))
+    return W4A16_ERR_SHAPE;
+  if (!expert_offsets) return W4A16_ERR_NULL;
+  if (M > 0 && (!topk_idx || !sorted_pos)) return W4A16_ERR_NULL;
+  const size_t need = moe_sort_workspace_bytes(M > 0 ? M : 1, top_k, E);
+  if (workspace == nullptr || workspace_bytes < need) return W4A16_ERR_WORKSPACE;
+  Carve c(workspace);
+  int32_t* active = c.take<int32_t>(E);
+  int32_t* counters = c.take<int32_t>(2);
+  int32_t* tiles = c.take<int32_t>(M * top_k / kPrefillBM + E + 1);
+  return launch_status(launch_sort(topk_idx, (int)M, (int)top_k, (int)E, sorted_pos,
+                                   expert_offsets, active, counters, tiles, kPrefillBM,
+                                   static_cast<hipStream_t>(stream)));
+}
+
+size_t moe_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I) {
+  if (M <= 0 || top_k <= 0 || E <= 0 || H <= 0 || I <= 0) return 0;
+  return moe_layout(nullptr, M, top_k, E, H, I).bytes;
+}
+
+int moe_forward(const uint16_t* hidden, const int64_t* topk_idx, const float* topk_w,
+                const int32_t* gu_packed, const uint16_t* gu_scale, const int32_t* dn_packed,
+                const uint16_t* dn_scale, uint16_t* out, int64_t M, int64_t top_k, int64_t E,
+                int64_t H, int64_t I, int64_t group_size, void* workspace,
+                size_t workspace_bytes, void* stream) {
+  if (M < 0 || top_k <= 0 || top_k > kMaxTopK || E <= 0 || E > kMaxExperts || H <= 0 ||
+      H % 32 != 0 || I <= 0 || I % 32 != 0 || H > (1 << 20) || I > (1 << 20) ||
+      M * top_k > (int64_t(1) << 30) / (H > I ? H : I))
+    return W4A16_ERR_SHAPE;
+  if (!valid_group(group_size)) return W4A16_ERR_GROUP;
+  if (M == 0) return W4A16_OK;
+  if (!hidden || !topk_idx || !topk_w || !gu_packed || !gu_scale || !dn_packed || !dn_scale ||
+      !out)
+    return W4A16_ERR_NULL;
+  if (!aligned16(hidden) || !aligned16(gu_packed) || !aligned16(dn_packed) || !aligned16(out))
+    return W4A16_ERR_ALIGN;
+  const MoeLayout need = moe_layout(nullptr, M, top_k, E, H, I);
+  if (workspace == nullptr || workspace_bytes < need.bytes) return W4A16_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return W4A16_ERR_ALIGN;
+  const MoeLayout L = moe_layout(workspace, M, top_k, E, H, I);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool bias_form = group_size % 128 == 0;
+  const int max_slots = (int)(M * top_k < E ? M * top_k : E);
+
+  hipError_t e = launch_sort(topk_idx, (int)M, (int)top_k, (int)E, L.sorted_pos, L.offsets,
+                             L.active, L.counters, L.tiles, kPrefillBM, s);
+  if (e != hipSuccess) return W4A16_ERR_LAUNCH;
+  const uint16_t* act = hidden;
+  if (bias_form) {
+    e = launch_bias_order(hidden, L.xp, M, (int)H, s);
+    if (e != hipSuccess) return W4A16_ERR_LAUNCH;
+    act = L.xp;
+  }
+  DecodeArgs a{};
+  a.sorted_pos = L.sorted_pos;
+  a.offsets = L.offsets;
+  a.active = L.active;
+  a.n_active = L.counters;
+  a.topk = (int)top_k;
+  a.G = (int)group_size;
+  a.I = (int)I;
+  // gate_up + gated GELU
+  a.act = act;
+  a.wp = gu_packed;
+  a.ws = gu_scale;
+  a.out = L.inter;
+  a.M = (int)M;
+  a.N = (int)(2 * I);
+  a.K = (int)H;
+  a.ng = (int)((H + group_size - 1) / group_size);
+  e = launch_decode(kModeGateUp, bias_form, a, (int)(I / 8), max_slots, s);
+  if (e != hipSuccess) return W4A16_ERR_LAUNCH;
+  // down
+  a.act = L.inter;
+  a.wp = dn_packed;
+  a.ws = dn_scale;
+  a.out = L.dn;
+  a.N = (int)H;
+  a.K = (int)I;
+  a.ng = (int)((I + group_size - 1) / group_size);
+  e = launch_decode(kModeDown, bias_form, a, (int)((H + 15) / 16), max_slots, s);
+  if (e != hipSuccess) return W4A16_ERR_LAUNCH;
+  return launch_status(launch_combine(L.dn, topk_idx, topk_w, out, (int)M, (int)top_k, (int)E,
+                                      (int)H, s));
+}
+
+}  // extern "C"

@@ -1,0 +1,141 @@
+// Shared device helpers for the gfx950 W4A16 MoE kernels.
+//
+// Packed int4 layout (compressed-tensors "pack-quantized", the reference's
+// hybrid_agent/quantization.py:132-137): int32 word p[n, j] holds
+// w[n, 8j+i] for i = 0..7 in bits 4i..4i+3 as offset binary u = q + 8.
+//
+// Two ways of turning a word into a bf16x8 MFMA operand are used:
+//
+//  * "bias" form (decode path, group size a multiple of 128): the bf16 bit
+//    pattern 0x4300 | u is exactly 128 + u, so one v_and_or_b32 per pair
+//    gives two operands.  Pairs come out as (nibble i, nibble i+4), i = 0..3,
+//    so the activation operand must hold its 8-blocks in the order
+//    [0,4,1,5,2,6,3,7] ("bias order").  The MFMA then computes
+//    sum x*(128+u) = sum x*q + 136*sum x; the 136*sum x term is produced by a
+//    second MFMA against a constant-136 operand and removed per group, where
+//    the group scale is applied to the fp32 accumulator.
+//
+//  * "exact" form (prefill path and group sizes below 128): each weight is
+//    dequantised to bf16_RNE(q * s), bit-identical to the reference's
+//    dequantize_int4_packed, in natural K order.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace w4a16 {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(16))) float f32x16_t;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
+
+// The bias form's per-element offset: 128 + 8 (q = u - 8).
+constexpr uint32_t kBiasPair = 0x43004300u;     // bf16x2 (128, 128)
+constexpr uint32_t kBias136Pair = 0x43084308u;  // bf16x2 (136, 136)
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
+  return __uint_as_float(b << 16);
+}
+
+// f32 -> bf16 bits, round to nearest even (lowers to v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  __bf16 h = (__bf16)f;
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  bf16x2_t v;
+  v.x = (__bf16)lo;
+  v.y = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ float round_bf16(float f) {
+  return bf16_bits_to_f32(f32_to_bf16_bits(f));
+}
+
+// Bias-form unpack of one packed word: 4 dwords of bf16 pairs
+// (128+u_i, 128+u_{i+4}) for i = 0..3.
+__device__ __forceinline__ u32x4_t unpack_bias(uint32_t w) {
+  u32x4_t r;
+  r.x = (w & 0x000F000Fu) | kBiasPair;
+  r.y = ((w >> 4) & 0x000F000Fu) | kBiasPair;
+  r.z = ((w >> 8) & 0x000F000Fu) | kBiasPair;
+  r.w = ((w >> 12) & 0x000F000Fu) | kBiasPair;
+  return r;
+}
+
+// Exact unpack of one packed word with scale s: 8 values bf16_RNE(q*s).
+// BIAS_ORDER selects the element order: natural (k = 0..7) or bias order
+// (0,4,1,5,2,6,3,7) to pair with bias-ordered activations.
+template <bool BIAS_ORDER>
+__device__ __forceinline__ u32x4_t unpack_exact(uint32_t w, float s) {
+  const uint32_t lo = w & 0x0F0F0F0Fu;          // nibbles 0,2,4,6 in bytes 0..3
+  const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;   // nibbles 1,3,5,7 in bytes 0..3
+  const float m8 = -8.0f * s;
+  // (u - 8) * s computed as fma(u, s, -8s): both products are exact in fp32
+  // (|u| <= 15, s has 8 significant bits), so the fma returns q*s exactly.
+  const float v0 = __builtin_fmaf((float)(lo & 0xFFu), s, m8);
+  const float v2 = __builtin_fmaf((float)((lo >> 8) & 0xFFu), s, m8);
+  const float v4 = __builtin_fmaf((float)((lo >> 16) & 0xFFu), s, m8);
+  const float v6 = __builtin_fmaf((float)(lo >> 24), s, m8);
+  const float v1 = __builtin_fmaf((float)(hi & 0xFFu), s, m8);
+  const float v3 = __builtin_fmaf((float)((hi >> 8) & 0xFFu), s, m8);
+  const float v5 = __builtin_fmaf((float)((hi >> 16) & 0xFFu), s, m8);
+  const float v7 = __builtin_fmaf((float)(hi >> 24), s, m8);
+  u32x4_t r;
+  if (BIAS_ORDER) {
+    r.x = pack_bf16x2(v0, v4);
+    r.y = pack_bf16x2(v1, v5);
+    r.z = pack_bf16x2(v2, v6);
+    r.w = pack_bf16x2(v3, v7);
+  } else {
+    r.x = pack_bf16x2(v0, v1);
+    r.y = pack_bf16x2(v2, v3);
+    r.z = pack_bf16x2(v4, v5);
+    r.w = pack_bf16x2(v6, v7);
+  }
+  return r;
+}
+
+// Natural-order 8-block of bf16 (4 dwords) -> bias order [0,4,1,5,2,6,3,7].
+__device__ __forceinline__ u32x4_t to_bias_order(u32x4_t d) {
+  // d.x=(x0,x1) d.y=(x2,x3) d.z=(x4,x5) d.w=(x6,x7)
+  u32x4_t r;
+  r.x = __builtin_amdgcn_perm(d.z, d.x, 0x05040100u);  // (x0, x4)
+  r.y = __builtin_amdgcn_perm(d.z, d.x, 0x07060302u);  // (x1, x5)
+  r.z = __builtin_amdgcn_perm(d.w, d.y, 0x05040100u);  // (x2, x6)
+  r.w = __builtin_amdgcn_perm(d.w, d.y, 0x07060302u);  // (x3, x7)
+  return r;
+}
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t v) {
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+__device__ __forceinline__ f32x4_t mfma16(u32x4_t a, u32x4_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+// 16-byte global load / store helpers.
+__device__ __forceinline__ u32x4_t ld16(const void* p) {
+  return *reinterpret_cast<const u32x4_t*>(p);
+}
+__device__ __forceinline__ void st16(void* p, u32x4_t v) {
+  *reinterpret_cast<u32x4_t*>(p) = v;
+}
+
+// gelu_pytorch_tanh: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), fp32.
+__device__ __forceinline__ float gelu_tanh_f32(float x) {
+  const float k0 = 0.7978845608028654f;
+  const float k1 = 0.044715f;
+  const float inner = k0 * (x + k1 * x * x * x);
+  return 0.5f * x * (1.0f + tanhf(inner));
+}
+
+}  // namespace w4a16

@@ -1,0 +1,66 @@
+// Internal launch interface between the C-ABI layer (capi.hip) and the
+// kernel translation units.  Every launcher is asynchronous on `stream` and
+// returns hipSuccess or the launch error.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace w4a16 {
+
+constexpr int kMaxExperts = 512;
+constexpr int kMaxTopK = 32;
+// m-tile (token rows) of the prefill grouped GEMM
+constexpr int kPrefillBM = 128;
+
+// Arguments of the decode-shaped (few rows per weight matrix) MFMA kernel.
+struct DecodeArgs {
+  const uint16_t* act;        // activation rows (bf16), row length K
+  const int32_t* wp;          // packed weights [E?, N, K/8]
+  const uint16_t* ws;         // bf16 scales [E?, N, ng]
+  const uint16_t* bias;       // dense only, nullable, [N]
+  uint16_t* out;              // output rows
+  const int32_t* sorted_pos;  // MoE: [M*k] rows t*k+j in expert-segment order
+  const int32_t* offsets;     // MoE: [E+1]
+  const int32_t* active;      // MoE: active expert ids, ascending
+  const int32_t* n_active;    // MoE: [1]
+  int M;     // dense: activation rows
+  int N;     // weight rows per expert
+  int K;     // reduction length
+  int G;     // group size
+  int ng;    // ceil(K / G)
+  int topk;  // MoE k
+  int I;     // gate_up: intermediate size (N / 2)
+};
+
+enum DecodeMode { kModeDense = 0, kModeGateUp = 1, kModeDown = 2 };
+
+hipError_t launch_dequant(const int32_t* packed, const uint16_t* scale, uint16_t* out,
+                          int64_t rows, int K, int G, hipStream_t s);
+hipError_t launch_bias_order(const uint16_t* x, uint16_t* xp, int64_t rows, int K, hipStream_t s);
+hipError_t launch_decode(int mode, bool bias_form, const DecodeArgs& a, int grid_x, int grid_y,
+                         hipStream_t s);
+hipError_t launch_combine(const uint16_t* dn, const int64_t* idx, const float* w, uint16_t* out,
+                          int M, int topk, int E, int H, hipStream_t s);
+hipError_t launch_sort(const int64_t* idx, int M, int topk, int E, int32_t* sorted_pos,
+                       int32_t* offsets, int32_t* active, int32_t* counters, int32_t* tiles,
+                       int BM, hipStream_t s);
+hipError_t launch_router_norm(const uint16_t* h, const uint16_t* scale, float scalar_root,
+                              float eps, uint16_t* r, int M, int H, hipStream_t s);
+hipError_t launch_router_logits(const uint16_t* r, const uint16_t* proj, float* partial, int M,
+                                int H, int E, int ksplit, hipStream_t s);
+hipError_t launch_router_topk(const float* partial, int ksplit, const uint16_t* logits_in,
+                              const uint16_t* per_expert_scale, uint16_t* logits_out,
+                              int64_t* idx, float* w, int M, int E, int topk, hipStream_t s);
+hipError_t launch_prefill_gateup(const uint16_t* x, const int32_t* sorted_pos,
+                                 const int32_t* offsets, const int32_t* tiles,
+                                 const int32_t* counters, const int32_t* gu_packed,
+                                 const uint16_t* gu_scale, uint16_t* inter, int max_tiles,
+                                 int topk, int H, int I, int G, hipStream_t s);
+hipError_t launch_prefill_down(const uint16_t* inter, const int32_t* sorted_pos,
+                               const int32_t* offsets, const int32_t* tiles,
+                               const int32_t* counters, const int32_t* dn_packed,
+                               const uint16_t* dn_scale, uint16_t* dn, int max_tiles, int topk,
+                               int H, int I, int G, hipStream_t s);
+
+}  // namespace w4a16

@@ -1,0 +1,126 @@
+/*
+ * w4a16moe.h -- C ABI of the MI355X (gfx950) W4A16 mixture-of-experts library
+ * (libw4a16moe.so, built from hybridagent_amd/csrc).
+ *
+ * Replaces the W4A16 MoE hot path of HybridAgent, hybrid_agent/quantization.py
+ * and the router block of hybrid_agent/backends.py.  Every entry point:
+ *   - takes raw device pointers, sizes and a hipStream_t passed as void*
+ *     (NULL = the default stream);
+ *   - validates its arguments on the host before touching the GPU and returns
+ *     a W4A16_* status (0 = success);
+ *   - never allocates: scratch memory is a caller-provided workspace whose
+ *     size the matching *_workspace_bytes() function returns;
+ *   - is asynchronous on the given stream, performs no host synchronisation
+ *     and keeps no global mutable state (re-entrant across streams/threads).
+ *
+ * Data layout (compressed-tensors pack-quantized, quantization.py:1-5,132-137,
+ * 153-159, 191-218):
+ *   packed weights  int32 [.., N, K/8]; word j of row n holds w[n, 8j+i] for
+ *                   i = 0..7 in bits 4i..4i+3 as q + 8 (q in [-8, 7]);
+ *   scales          bf16  [.., N, ceil(K/G)]; group g covers columns
+ *                   g*G .. min(K, (g+1)*G) - 1 (the last group may be partial);
+ *   activations     bf16, row-major, rows of length K;
+ *   bf16 values are passed as uint16_t bit patterns.
+ * Constraints: K % 32 == 0 for every reduction length, G a power of two
+ * >= 32, pointers 16-byte aligned, E <= 512, top_k <= 32.
+ */
+#ifndef W4A16MOE_H
+#define W4A16MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__) || defined(__clang__)
+#define W4A16_API __attribute__((visibility("default")))
+#else
+#define W4A16_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum w4a16_status {
+  W4A16_OK = 0,
+  W4A16_ERR_NULL = 1,      /* a required pointer is NULL */
+  W4A16_ERR_SHAPE = 2,     /* a size is out of range or inconsistent */
+  W4A16_ERR_GROUP = 3,     /* unsupported group size */
+  W4A16_ERR_ALIGN = 4,     /* a pointer is not 16-byte aligned */
+  W4A16_ERR_WORKSPACE = 5, /* workspace missing or too small */
+  W4A16_ERR_LAUNCH = 6     /* a HIP launch failed */
+};
+
+/* (major << 16) | (minor << 8) | patch */
+W4A16_API int w4a16moe_version(void);
+
+/* Static description of a status code. */
+W4A16_API const char* w4a16moe_status_string(int status);
+
+/* dequantize_int4_packed(packed, scale, shifts)  -- quantization.py:132-137
+ * out[r, k] = bf16_RNE(q[r, k] * scale[r, k / G]), bit-identical to the
+ * reference's bf16 dequant.  rows = product of the leading dims.          */
+W4A16_API int w4a16_dequantize(const int32_t* packed, const uint16_t* scale, uint16_t* out, int64_t rows,
+                     int64_t K, int64_t group_size, void* stream);
+
+/* Linear4Bit.forward  -- quantization.py:171-175
+ * y[M, N] = x[M, K] @ dequant(W)^T (+ bias[N]), fp32 accumulation, bf16 out.
+ * bias may be NULL.                                                        */
+W4A16_API size_t w4a16_linear_workspace_bytes(int64_t M, int64_t K, int64_t group_size);
+W4A16_API int w4a16_linear(const uint16_t* x, const int32_t* w_packed, const uint16_t* w_scale,
+                 const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int64_t K,
+                 int64_t group_size, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Router  -- backends.py:111-117 (HF Gemma4TextRouter.forward,
+ * transformers/models/gemma4/modeling_gemma4.py:1335-1356):
+ *   r       = bf16(bf16(rms_norm(hidden) * router_scale) * scalar_root)
+ *   logits  = bf16(r @ proj_w^T)                     (fp32 accumulation)
+ *   p       = softmax(logits) in fp32
+ *   topk_idx, topk_w = top_k of p (value desc, then lower index), renormalised
+ *   topk_w *= per_expert_scale[topk_idx]
+ * hidden [M, H], router_scale [H], proj_w [E, H], per_expert_scale [E] bf16;
+ * logits_out [M, E] bf16 may be NULL; topk_idx int64 [M, top_k];
+ * topk_w float32 [M, top_k].                                               */
+W4A16_API size_t moe_router_workspace_bytes(int64_t M, int64_t H, int64_t E);
+W4A16_API int moe_router_topk(const uint16_t* hidden, const uint16_t* router_scale, float scalar_root,
+                    const uint16_t* proj_w, const uint16_t* per_expert_scale, float eps,
+                    int64_t M, int64_t H, int64_t E, int64_t top_k, uint16_t* logits_out,
+                    int64_t* topk_idx, float* topk_w, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
+/* Softmax / top-k / renormalise / per-expert scale from given bf16 logits
+ * [M, E]  -- backends.py:114-117.                                          */
+W4A16_API int moe_topk_from_logits(const uint16_t* logits, const uint16_t* per_expert_scale, int64_t M,
+                         int64_t E, int64_t top_k, int64_t* topk_idx, float* topk_w,
+                         void* stream);
+
+/* Token -> expert grouping  -- quantization.py:266-276 (implicit order of
+ * torch.where over one_hot(top_k_index).permute(2,1,0)[e]).
+ * sorted_pos int32 [M*top_k]: rows t*top_k + j of the token-major
+ * flattening, grouped by ascending expert, k-slot-major / token-minor inside
+ * each expert; expert_offsets int32 [E+1]: segment bounds.  Indices outside
+ * [0, E) are skipped (the reference's "expert_idx == num_experts" rows).   */
+W4A16_API size_t moe_sort_workspace_bytes(int64_t M, int64_t top_k, int64_t E);
+W4A16_API int moe_sort_permute(const int64_t* topk_idx, int64_t M, int64_t top_k, int64_t E,
+                     int32_t* sorted_pos, int32_t* expert_offsets, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
+/* Gemma4TextExperts4Bit.forward / fused_triton_4bit_moe_forward
+ *   -- quantization.py:88-129, 225-240
+ * out[M, H] = sum_j bf16(topk_w[t,j]) * down_e(gelu_tanh(gate_e(x)) * up_e(x))
+ * with e = topk_idx[t, j], bf16 rounding at the reference's points.
+ * hidden [M, H] bf16; topk_idx int64 [M, top_k]; topk_w float32 [M, top_k];
+ * gu_packed int32 [E, 2I, H/8] (gate rows 0..I-1, up rows I..2I-1);
+ * gu_scale bf16 [E, 2I, ceil(H/G)]; dn_packed int32 [E, H, I/8];
+ * dn_scale bf16 [E, H, ceil(I/G)].                                         */
+W4A16_API size_t moe_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I);
+W4A16_API int moe_forward(const uint16_t* hidden, const int64_t* topk_idx, const float* topk_w,
+                const int32_t* gu_packed, const uint16_t* gu_scale, const int32_t* dn_packed,
+                const uint16_t* dn_scale, uint16_t* out, int64_t M, int64_t top_k, int64_t E,
+                int64_t H, int64_t I, int64_t group_size, void* workspace,
+                size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* W4A16MOE_H */

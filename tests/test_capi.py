@@ -1,0 +1,122 @@
+"""C-ABI library checks that need no GPU: it loads, exports exactly what
+include/w4a16moe.h declares, and rejects bad arguments on the host before any
+HIP call (status codes -> Python exceptions)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from hybridagent_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "w4a16moe.h"
+
+
+def header_functions():
+    txt = HEADER.read_text()
+    return set(re.findall(r"W4A16_API\s+[\w\s\*]+?\b(\w+)\s*\(", txt))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libw4a16moe.so not built")
+    return _lib.load()
+
+
+def test_header_matches_binding_table():
+    assert header_functions() == set(_lib.SIGNATURES)
+
+
+def test_library_exports_every_header_symbol(lib):
+    for name in header_functions():
+        assert hasattr(lib, name), name
+
+
+def test_version_and_status_strings(lib):
+    assert lib.w4a16moe_version() >> 16 == 0
+    for code in range(7):
+        assert lib.w4a16moe_status_string(code)
+    assert lib.w4a16moe_status_string(0).decode() == "ok"
+
+
+NULL = None
+
+
+def test_linear_host_validation(lib):
+    fake = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    # K not a multiple of 32
+    assert lib.w4a16_linear(fake, fake, fake, NULL, fake, 4, 16, 40, 32, NULL, 0, NULL) == 2
+    # group size not a power of two / too small
+    assert lib.w4a16_linear(fake, fake, fake, NULL, fake, 4, 16, 64, 48, NULL, 0, NULL) == 3
+    assert lib.w4a16_linear(fake, fake, fake, NULL, fake, 4, 16, 64, 16, NULL, 0, NULL) == 3
+    # null pointer
+    assert lib.w4a16_linear(NULL, fake, fake, NULL, fake, 4, 16, 64, 32, NULL, 0, NULL) == 1
+    # misaligned activation pointer
+    assert lib.w4a16_linear(ctypes.c_void_p(4098), fake, fake, NULL, fake, 4, 16, 64, 32, NULL, 0, NULL) == 4
+    # bias-form (G % 128 == 0) needs a workspace
+    assert lib.w4a16_linear_workspace_bytes(4, 256, 128) >= 4 * 256 * 2
+    assert lib.w4a16_linear(fake, fake, fake, NULL, fake, 4, 16, 256, 128, NULL, 0, NULL) == 5
+    # M == 0 is a no-op
+    assert lib.w4a16_linear(NULL, NULL, NULL, NULL, NULL, 0, 16, 64, 32, NULL, 0, NULL) == 0
+
+
+def test_moe_host_validation(lib):
+    fake = ctypes.c_void_p(4096)
+    args = [fake] * 8
+    ws_need = lib.moe_workspace_bytes(8, 8, 128, 2816, 704)
+    assert ws_need > 8 * 8 * (2816 + 704) * 2
+    # E too large
+    assert lib.moe_forward(*args, 8, 8, 1024, 2816, 704, 128, fake, ws_need, NULL) == 2
+    # top_k > 32
+    assert lib.moe_forward(*args, 8, 33, 128, 2816, 704, 128, fake, ws_need, NULL) == 2
+    # I not a multiple of 32
+    assert lib.moe_forward(*args, 8, 8, 128, 2816, 700, 128, fake, ws_need, NULL) == 2
+    # bad group
+    assert lib.moe_forward(*args, 8, 8, 128, 2816, 704, 96, fake, ws_need, NULL) == 3
+    # workspace too small
+    assert lib.moe_forward(*args, 8, 8, 128, 2816, 704, 128, fake, ws_need - 1, NULL) == 5
+    # null weight pointer
+    bad = list(args)
+    bad[3] = NULL
+    assert lib.moe_forward(*bad, 8, 8, 128, 2816, 704, 128, fake, ws_need, NULL) == 1
+    # router: top_k > E
+    assert lib.moe_router_topk(fake, fake, 0.1, fake, fake, 1e-6, 4, 2816, 4, 8, NULL, fake, fake,
+                               fake, 1 << 20, NULL) == 2
+    assert lib.moe_topk_from_logits(fake, fake, 4, 128, 0, fake, fake, NULL) == 2
+    assert lib.moe_sort_permute(fake, 4, 8, 128, fake, fake, NULL, 0, NULL) == 5
+
+
+def test_dequant_host_validation(lib):
+    fake = ctypes.c_void_p(4096)
+    assert lib.w4a16_dequantize(fake, fake, fake, 4, 12, 32, NULL) == 2
+    assert lib.w4a16_dequantize(fake, fake, fake, 4, 64, 24, NULL) == 3
+    assert lib.w4a16_dequantize(fake, fake, ctypes.c_void_p(4097), 4, 64, 32, NULL) == 4
+
+
+def test_infer_group_size():
+    assert _lib.infer_group_size(2816, 22) == 128
+    assert _lib.infer_group_size(2816, 88) == 32
+    assert _lib.infer_group_size(704, 6) == 128   # partial last group
+    assert _lib.infer_group_size(704, 22) == 32
+    assert _lib.infer_group_size(704, 11) == 64
+    assert _lib.infer_group_size(64, 1) == 64
+    with pytest.raises(ValueError):
+        _lib.infer_group_size(2816, 7)
+
+
+def test_python_ops_refuse_cpu_tensors():
+    x = torch.zeros(2, 64, dtype=torch.bfloat16)
+    wp = torch.zeros(16, 8, dtype=torch.int32)
+    ws = torch.zeros(16, 2, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        _lib.linear(x, wp, ws)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        _lib.dequantize(wp, ws)
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(RuntimeError, match="not built"):
+        _lib.load(tmp_path / "libw4a16moe.so")

@@ -1,0 +1,257 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the numpy oracle.
+
+Bars: bit-exact for dequantised weights, routing indices (given identical
+logits) and the token permutation; max_abs_rel <= 1e-2 for layer outputs
+(``max|y - y_ref| / max|y_ref|``, the tolerance the north star states).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from hybridagent_amd import _lib, synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+E, H, I, K_TOP = 128, 2816, 704, 8
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _bits(t):
+    return t.detach().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.fixture(scope="module")
+def dev():
+    assert _lib.available(), "libw4a16moe.so must be built"
+    return torch.device("cuda:0")
+
+
+# ------------------------------------------------------------------ dequant
+
+@pytest.mark.parametrize("N,K,G", [(64, 2816, 128), (48, 704, 128), (32, 704, 32), (16, 256, 64)])
+def test_dequant_bit_exact(dev, N, K, G):
+    p = synth.packed_int4((N, K), seed=1)
+    s = synth.group_scales((N, K), G, seed=2)
+    got = _lib.dequantize(p.to(dev), s.to(dev))
+    torch.cuda.synchronize()
+    ref = oracle.dequantize(p.numpy(), _bits(s), G)
+    assert np.array_equal(_bits(got), oracle.to_bf16_bits(ref))
+
+
+# ------------------------------------------------------------------ dense linear (config 1)
+
+@pytest.mark.parametrize("M", [1, 4, 16, 64])
+@pytest.mark.parametrize("K,N", [(2816, 2816), (2816, 1408), (704, 2816)])
+def test_dense_linear_config1(dev, M, K, N):
+    G = 128
+    x = synth.activations(M, K, seed=10 + M)
+    p = synth.packed_int4((N, K), seed=11)
+    s = synth.group_scales((N, K), G, seed=12)
+    y = _lib.linear(x.to(dev), p.to(dev), s.to(dev))
+    ref = oracle.linear(_np(x), p.numpy(), _bits(s), G)
+    err = oracle.max_abs_rel(_np(y), ref)
+    print(f"dense M={M} K={K} N={N} max_abs_rel={err:.2e}")
+    assert err <= TOL
+
+
+@pytest.mark.parametrize("G", [32, 64, 256])
+def test_dense_linear_other_groups_and_bias(dev, G):
+    M, K, N = 5, 1024, 96
+    x = synth.activations(M, K, seed=20)
+    p = synth.packed_int4((N, K), seed=21)
+    s = synth.group_scales((N, K), G, seed=22)
+    b = synth.activations(1, N, seed=23)[0]
+    y = _lib.linear(x.to(dev), p.to(dev), s.to(dev), b.to(dev), group_size=G)
+    ref = oracle.linear(_np(x), p.numpy(), _bits(s), G, bias=_np(b))
+    assert oracle.max_abs_rel(_np(y), ref) <= TOL
+
+
+def test_dense_linear_many_rows(dev):
+    # M > 64 exercises the row-chunk loop
+    M, K, N, G = 150, 512, 80, 128
+    x = synth.activations(M, K, seed=30)
+    p = synth.packed_int4((N, K), seed=31)
+    s = synth.group_scales((N, K), G, seed=32)
+    y = _lib.linear(x.to(dev), p.to(dev), s.to(dev))
+    assert oracle.max_abs_rel(_np(y), oracle.linear(_np(x), p.numpy(), _bits(s), G)) <= TOL
+
+
+# ------------------------------------------------------------------ router
+
+def _router_inputs(M, seed):
+    rw = synth.router_weights(E, H, seed=seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    rw.scale = (1 + 0.05 * torch.randn(H, generator=g)).to(torch.bfloat16)
+    rw.per_expert_scale = (1 + 0.05 * torch.randn(E, generator=g)).to(torch.bfloat16)
+    h = synth.activations(M, H, seed=seed + 2)
+    return h, rw
+
+
+@pytest.mark.parametrize("M", [1, 8, 64, 300])
+def test_topk_from_identical_logits_bit_exact(dev, M):
+    h, rw = _router_inputs(M, seed=40)
+    logits = oracle.router_logits(_np(h), _np(rw.scale), rw.scalar_root, _np(rw.proj), rw.eps)
+    lt = torch.from_numpy(logits).to(torch.bfloat16)
+    w, idx = _lib.topk_from_logits(lt.to(dev), rw.per_expert_scale.to(dev), K_TOP)
+    ridx, rw_ = oracle.topk_from_logits(logits, _np(rw.per_expert_scale), K_TOP)
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    np.testing.assert_allclose(w.cpu().numpy(), rw_, rtol=2e-6, atol=1e-7)
+
+
+def test_topk_tie_rule(dev):
+    lg = torch.tensor([[1.0, 3.0, 3.0, 2.0, 3.0, -1.0, 0.5, 3.0]], dtype=torch.bfloat16)
+    w, idx = _lib.topk_from_logits(lg.to(dev), torch.ones(8, dtype=torch.bfloat16, device=dev), 5)
+    assert idx.cpu().tolist() == [[1, 2, 4, 7, 3]]
+
+
+@pytest.mark.parametrize("M", [1, 32, 257])
+def test_router_end_to_end(dev, M):
+    h, rw = _router_inputs(M, seed=50)
+    w, idx, lg = _lib.router_topk(h.to(dev), rw.scale.to(dev), rw.scalar_root, rw.proj.to(dev),
+                                  rw.per_expert_scale.to(dev), rw.eps, K_TOP, return_logits=True)
+    ref_lg, ref_idx, ref_w = oracle.router(_np(h), _np(rw.scale), rw.scalar_root, _np(rw.proj),
+                                           _np(rw.per_expert_scale), rw.eps, K_TOP)
+    got_lg = _np(lg)
+    ulp = np.abs(oracle.to_bf16_bits(got_lg).astype(np.int32) - oracle.to_bf16_bits(ref_lg).astype(np.int32))
+    assert ulp.max() <= 1 and (ulp > 0).mean() < 0.02
+    # indices: equal wherever the oracle's k-th / (k+1)-th logits are not within
+    # the logits' own 1-ulp disagreement
+    srt = -np.sort(-ref_lg, axis=1)
+    gap = srt[:, K_TOP - 1] - srt[:, K_TOP]
+    safe = gap > 2 * np.abs(srt[:, K_TOP - 1]) * 2.0 ** -7
+    got_idx = idx.cpu().numpy()
+    if M >= 32:
+        assert safe.mean() > 0.5
+    assert np.array_equal(np.sort(got_idx[safe], 1), np.sort(ref_idx[safe], 1))
+    # the kernel is bit-exact against its own logits
+    idx2, w2 = oracle.topk_from_logits(got_lg, _np(rw.per_expert_scale), K_TOP)
+    assert np.array_equal(got_idx, idx2)
+    np.testing.assert_allclose(w.cpu().numpy(), w2, rtol=2e-6, atol=1e-7)
+
+
+# ------------------------------------------------------------------ sort / permute
+
+@pytest.mark.parametrize("M", [1, 8, 64, 777, 4096])
+def test_sort_permute_bit_exact(dev, M):
+    g = torch.Generator().manual_seed(60 + M)
+    idx = torch.stack([torch.randperm(E, generator=g)[:K_TOP] for _ in range(M)])
+    sp, off = _lib.sort_permute(idx.to(dev), E)
+    ref_sp, ref_off = oracle.sort_permute(idx.numpy(), E)
+    assert np.array_equal(off.cpu().numpy(), ref_off)
+    assert np.array_equal(sp.cpu().numpy(), ref_sp)
+
+
+def test_sort_permute_skewed_and_invalid(dev):
+    # Zipf-skewed routing with empty experts, plus "no expert" slots (index E)
+    rw = synth.zipf_router_weights(E, H, seed=70)
+    x = synth.zipf_activations(2048, H, seed=71)
+    lg = oracle.router_logits(_np(x), _np(rw.scale), rw.scalar_root, _np(rw.proj), rw.eps)
+    idx, _ = oracle.topk_from_logits(lg, _np(rw.per_expert_scale), K_TOP)
+    idx[::7, 3] = E
+    sp, off = _lib.sort_permute(torch.from_numpy(idx).to(dev), E)
+    flat = idx.T.reshape(-1)
+    keep = flat < E
+    order = np.argsort(np.where(keep, flat, E), kind="stable")[: keep.sum()]
+    M = idx.shape[0]
+    ref_sp = ((order % M) * K_TOP + order // M).astype(np.int32)
+    n = int(keep.sum())
+    assert off.cpu().numpy()[-1] == n
+    assert np.array_equal(sp.cpu().numpy()[:n], ref_sp)
+    assert (np.diff(off.cpu().numpy()) == 0).sum() >= 8
+
+
+# ------------------------------------------------------------------ MoE layer
+
+@pytest.fixture(scope="module")
+def moe128(dev):
+    wts = synth.moe_weights(E, H, I, 128, seed=100)
+    gpu = {k: getattr(wts, k).to(dev) for k in ("gate_up_packed", "gate_up_scale", "down_packed", "down_scale")}
+    cpu = {k: getattr(wts, k) for k in gpu}
+    return cpu, gpu
+
+
+def _route(M, seed):
+    g = torch.Generator().manual_seed(seed)
+    idx = torch.stack([torch.randperm(E, generator=g)[:K_TOP] for _ in range(M)])
+    w = torch.rand(M, K_TOP, generator=g) + 0.05
+    return idx, (w / w.sum(1, keepdim=True)).float()
+
+
+def _moe_ref(x, idx, w, cpu, G, rows=None, path="fused"):
+    rows = np.arange(x.shape[0]) if rows is None else rows
+    return oracle.moe_forward(_np(x)[rows], idx.numpy()[rows], w.numpy()[rows],
+                              cpu["gate_up_packed"].numpy(), _bits(cpu["gate_up_scale"]),
+                              cpu["down_packed"].numpy(), _bits(cpu["down_scale"]), G, path=path)
+
+
+def _moe_gpu(x, idx, w, gpu, dev):
+    return _lib.moe_forward(x.to(dev), idx.to(dev), w.to(dev), gpu["gate_up_packed"], gpu["gate_up_scale"],
+                            gpu["down_packed"], gpu["down_scale"])
+
+
+@pytest.mark.parametrize("M", [1, 8, 32, 64])
+def test_moe_decode_config2(dev, moe128, M):
+    cpu, gpu = moe128
+    x = synth.activations(M, H, seed=200 + M)
+    idx, w = _route(M, seed=300 + M)
+    y = _moe_gpu(x, idx, w, gpu, dev)
+    ref = _moe_ref(x, idx, w, cpu, 128)
+    err = oracle.max_abs_rel(_np(y), ref)
+    print(f"moe decode M={M} max_abs_rel={err:.2e}")
+    assert err <= TOL
+
+
+def test_moe_matches_loop_path(dev, moe128):
+    cpu, gpu = moe128
+    M = 16
+    x = synth.activations(M, H, seed=210)
+    idx, w = _route(M, seed=310)
+    y = _moe_gpu(x, idx, w, gpu, dev)
+    assert oracle.max_abs_rel(_np(y), _moe_ref(x, idx, w, cpu, 128, path="loop")) <= TOL
+
+
+def test_moe_prefill_sample_rows(dev, moe128):
+    cpu, gpu = moe128
+    M = 512
+    x = synth.activations(M, H, seed=220)
+    idx, w = _route(M, seed=320)
+    y = _moe_gpu(x, idx, w, gpu, dev)
+    rows = np.arange(0, M, 37)
+    err = oracle.max_abs_rel(_np(y)[rows], _moe_ref(x, idx, w, cpu, 128, rows=rows))
+    print(f"moe prefill M={M} sampled max_abs_rel={err:.2e}")
+    assert err <= TOL
+
+
+def test_moe_invalid_slots_contribute_nothing(dev, moe128):
+    cpu, gpu = moe128
+    M = 6
+    x = synth.activations(M, H, seed=230)
+    idx, w = _route(M, seed=330)
+    idx_bad = idx.clone()
+    idx_bad[:, 5:] = E        # the reference's "no expert" index
+    w_cut = w.clone()
+    w_cut[:, 5:] = 0.0
+    y_bad = _moe_gpu(x, idx_bad, w, gpu, dev)
+    y_cut = _moe_gpu(x, idx, w_cut, gpu, dev)
+    assert torch.equal(y_bad.cpu(), y_cut.cpu())
+
+
+@pytest.mark.parametrize("G", [32, 64])
+def test_moe_small_groups(dev, G):
+    e, h, i = 16, 512, 192
+    wts = synth.moe_weights(e, h, i, G, seed=400 + G)
+    M = 24
+    x = synth.activations(M, h, seed=401)
+    g = torch.Generator().manual_seed(402)
+    idx = torch.stack([torch.randperm(e, generator=g)[:4] for _ in range(M)])
+    w = torch.rand(M, 4, generator=g).float()
+    y = _lib.moe_forward(x.to(dev), idx.to(dev), w.to(dev), wts.gate_up_packed.to(dev), wts.gate_up_scale.to(dev),
+                         wts.down_packed.to(dev), wts.down_scale.to(dev))
+    ref = oracle.moe_forward(_np(x), idx.numpy(), w.numpy(), wts.gate_up_packed.numpy(), _bits(wts.gate_up_scale),
+                             wts.down_packed.numpy(), _bits(wts.down_scale), G)
+    assert oracle.max_abs_rel(_np(y), ref) <= TOL

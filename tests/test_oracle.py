@@ -1,0 +1,357 @@
+"""Pins for the numpy oracle (CPU only).
+
+Each test checks an oracle function against something other than its own
+formula: known-answer words, exhaustive enumeration, brute force, torch CPU
+library routines on identical operands, or invariants that a plausible
+mistake (dropped term, wrong shift, transposed operand, wrong order) breaks.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+from oracle import bf16_round, from_bf16_bits, to_bf16_bits
+
+
+def _bf16_np(t: torch.Tensor) -> np.ndarray:
+    return t.float().numpy()
+
+
+def _ulp_diff_bf16(a, b) -> np.ndarray:
+    ia = to_bf16_bits(a).astype(np.int32)
+    ib = to_bf16_bits(b).astype(np.int32)
+    return np.abs(ia - ib)
+
+
+# --------------------------------------------------------------------- bf16
+
+def test_bf16_round_matches_torch():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * 10,
+        rng.standard_normal(20000).astype(np.float32) * 1e-3,
+        # exact ties between two bf16 neighbours (round-half-even cases)
+        (from_bf16_bits(np.arange(0x3F80, 0x4080, dtype=np.uint16)).view(np.uint32) + 0x8000).view(np.float32),
+        np.array([0.0, -0.0, 1.0, -1.0, 3.0e38, -3.0e38], np.float32),
+    ])
+    ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(bf16_round(x).view(np.uint32), ref.view(np.uint32))
+
+
+# --------------------------------------------------------------------- int4 layout
+
+def test_unpack_known_words():
+    words = np.array([0x76543210, 0xFEDCBA98, 0x88888888, 0x00000000], np.uint32).view(np.int32)
+    q = oracle.unpack_int4(words[:, None])
+    assert q[0].tolist() == [-8, -7, -6, -5, -4, -3, -2, -1]
+    assert q[1].tolist() == [0, 1, 2, 3, 4, 5, 6, 7]
+    assert q[2].tolist() == [0] * 8
+    assert q[3].tolist() == [-8] * 8
+
+
+def test_unpack_exhaustive_nibbles():
+    # every nibble value at every position
+    for pos in range(8):
+        for u in range(16):
+            w = np.array([[(0x88888888 & ~(0xF << (4 * pos)) | (u << (4 * pos))) & 0xFFFFFFFF]],
+                         np.uint32).view(np.int32)
+            q = oracle.unpack_int4(w)[0]
+            expect = [0] * 8
+            expect[pos] = u - 8
+            assert q.tolist() == expect
+
+
+def test_pack_unpack_roundtrip():
+    rng = np.random.default_rng(1)
+    q = rng.integers(-8, 8, size=(7, 96))
+    p = oracle.pack_int4(q)
+    assert p.dtype == np.int32 and p.shape == (7, 12)
+    assert np.array_equal(oracle.unpack_int4(p), q)
+    # word-level: first word of row 0 equals sum of (q+8) << 4i
+    w0 = sum(int(q[0, i] + 8) << (4 * i) for i in range(8))
+    assert int(p[0, 0].view(np.uint32)) == w0
+
+
+def test_dequant_exhaustive_vs_torch():
+    # all 16 nibbles x a sweep of bf16 scales; torch bf16 multiply is the library pin
+    scales = torch.tensor(np.geomspace(1e-4, 4.0, 61), dtype=torch.float32).to(torch.bfloat16)
+    q = torch.arange(-8, 8, dtype=torch.int32)
+    ref = (q.to(torch.bfloat16)[None, :] * scales[:, None]).float().numpy()
+    # build packed rows: K = 16 -> 2 words per row, G = 16 (one group per row)
+    qrow = np.tile(np.arange(-8, 8), (len(scales), 1))
+    packed = oracle.pack_int4(qrow)
+    sb = to_bf16_bits(scales.float().numpy())[:, None]
+    got = oracle.dequantize(packed, sb, 16)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_dequant_partial_last_group_equals_zero_pad():
+    rng = np.random.default_rng(2)
+    N, K, G = 5, 704, 128
+    q = rng.integers(-8, 8, size=(N, K))
+    s = bf16_round(rng.uniform(0.005, 0.02, size=(N, 6)).astype(np.float32))
+    d = oracle.dequantize(oracle.pack_int4(q), to_bf16_bits(s), G)
+    qpad = np.concatenate([q, np.zeros((N, 64), q.dtype)], axis=1)
+    dpad = oracle.dequantize(oracle.pack_int4(qpad), to_bf16_bits(s), G)
+    assert np.array_equal(d, dpad[:, :K])
+    # group boundaries: column 639 uses scale 4, column 640 uses scale 5
+    assert d[0, 639] == bf16_round(np.float32(q[0, 639]) * s[0, 4])
+    assert d[0, 640] == bf16_round(np.float32(q[0, 640]) * s[0, 5])
+    with pytest.raises(ValueError):
+        oracle.dequantize(oracle.pack_int4(q), to_bf16_bits(s[:, :5]), G)
+
+
+def test_dequant_reference_group32_layout():
+    # the reference's own view(*scale.shape, 32) form (quantization.py:137) on torch
+    rng = np.random.default_rng(3)
+    N, K = 6, 128
+    q = rng.integers(-8, 8, size=(N, K))
+    packed = oracle.pack_int4(q)
+    s = torch.tensor(rng.uniform(0.005, 0.02, (N, K // 32)), dtype=torch.float32).to(torch.bfloat16)
+    pt = torch.from_numpy(packed)
+    shifts = torch.arange(0, 32, 4, dtype=torch.int32)
+    qt = ((pt.unsqueeze(-1) >> shifts) & 0xF) - 8
+    ref = (qt.to(torch.bfloat16).view(N, K // 32, 32) * s.unsqueeze(-1)).flatten(-2).float().numpy()
+    got = oracle.dequantize(packed, to_bf16_bits(s.float().numpy()), 32)
+    assert np.array_equal(got, ref)
+
+
+# --------------------------------------------------------------------- dense linear
+
+def _tiny_linear_case(rng, M, K, N, G):
+    q = rng.integers(-8, 8, size=(N, K))
+    s = bf16_round(rng.uniform(0.005, 0.02, size=(N, oracle.num_groups(K, G))).astype(np.float32))
+    x = bf16_round(rng.standard_normal((M, K)).astype(np.float32))
+    return x, q, s
+
+
+def test_linear_bruteforce_tiny():
+    rng = np.random.default_rng(4)
+    for (M, K, N, G) in [(3, 64, 5, 32), (2, 96, 3, 64), (1, 40, 4, 16)]:
+        x, q, s = _tiny_linear_case(rng, M, K, N, G)
+        got = oracle.linear(x, oracle.pack_int4(q), to_bf16_bits(s), G)
+        ref = np.zeros((M, N))
+        for m in range(M):
+            for n in range(N):
+                acc = 0.0
+                for kk in range(K):
+                    w = float(bf16_round(np.float32(q[n, kk]) * s[n, kk // G]).reshape(()))
+                    acc += float(x[m, kk]) * w
+                ref[m, n] = acc
+        # fp32 vs fp64 accumulation: at most one bf16 ulp apart
+        assert _ulp_diff_bf16(got, ref.astype(np.float32)).max() <= 1
+
+
+def test_linear_vs_torch_flinear():
+    rng = np.random.default_rng(5)
+    M, K, N, G = 16, 2816, 64, 128
+    x, q, s = _tiny_linear_case(rng, M, K, N, G)
+    got = oracle.linear(x, oracle.pack_int4(q), to_bf16_bits(s), G)
+    w = oracle.dequantize(oracle.pack_int4(q), to_bf16_bits(s), G)
+    ref = F.linear(torch.from_numpy(x).to(torch.bfloat16), torch.from_numpy(w).to(torch.bfloat16)).float().numpy()
+    assert oracle.max_abs_rel(got, ref) < 4e-3
+    assert _ulp_diff_bf16(got, ref).max() <= 2
+
+
+def test_linear_transpose_sensitivity():
+    # a transposed/flipped weight or dropped scale must fail the comparison
+    rng = np.random.default_rng(6)
+    x, q, s = _tiny_linear_case(rng, 4, 128, 128, 32)
+    y = oracle.linear(x, oracle.pack_int4(q), to_bf16_bits(s), 32)
+    y_t = oracle.linear(x, oracle.pack_int4(q.T.copy()), to_bf16_bits(s), 32)
+    assert oracle.max_abs_rel(y_t, y) > 0.1
+
+
+# --------------------------------------------------------------------- activations / norms
+
+def test_gelu_tanh_vs_torch():
+    x = torch.linspace(-8, 8, 40001).to(torch.bfloat16)
+    ref = F.gelu(x, approximate="tanh").float().numpy()
+    got = oracle.gelu_tanh(x.float().numpy())
+    # torch's vectorised tanh and numpy's differ by an fp32 ulp: allow one bf16
+    # ulp, or 1e-6 absolute in the far negative tail where 1 + tanh cancels
+    d = _ulp_diff_bf16(got, ref)
+    tail = np.abs(got - ref) <= 1e-6
+    assert np.all((d <= 1) | tail) and (d > 0).mean() < 0.05
+
+
+def test_rms_norm_vs_torch():
+    x = torch.randn(64, 2816, generator=torch.Generator().manual_seed(7)).to(torch.bfloat16)
+    wt = (1 + 0.1 * torch.randn(2816, generator=torch.Generator().manual_seed(8))).to(torch.bfloat16)
+    for weight in (None, wt):
+        ref = F.rms_norm(x, (2816,), weight, 1e-6).float().numpy()
+        got = oracle.rms_norm(x.float().numpy(), None if weight is None else weight.float().numpy(), 1e-6)
+        assert _ulp_diff_bf16(got, ref).max() <= 1
+
+
+# --------------------------------------------------------------------- router
+
+def _router_case(M=32, E=128, H=2816, seed=9):
+    g = torch.Generator().manual_seed(seed)
+    h = torch.randn(M, H, generator=g).to(torch.bfloat16)
+    proj = (0.02 * torch.randn(E, H, generator=g)).to(torch.bfloat16)
+    scale = (1 + 0.05 * torch.randn(H, generator=g)).to(torch.bfloat16)
+    pes = (1 + 0.05 * torch.randn(E, generator=g)).to(torch.bfloat16)
+    return h, proj, scale, pes
+
+
+def test_router_logits_vs_torch():
+    h, proj, scale, pes = _router_case()
+    H = h.shape[1]
+    r = F.rms_norm(h, (H,), None, 1e-6) * scale * (H ** -0.5)      # backends.py:112
+    ref = F.linear(r, proj).float().numpy()                          # backends.py:113
+    got = oracle.router_logits(h.float().numpy(), scale.float().numpy(), H ** -0.5,
+                               proj.float().numpy(), 1e-6)
+    assert _ulp_diff_bf16(got, ref).max() <= 1
+    assert (_ulp_diff_bf16(got, ref) > 0).mean() < 0.02
+
+
+def test_topk_vs_torch_on_identical_logits():
+    h, proj, scale, pes = _router_case(M=256)
+    H = h.shape[1]
+    logits = oracle.router_logits(h.float().numpy(), scale.float().numpy(), H ** -0.5,
+                                  proj.float().numpy(), 1e-6)
+    lt = torch.from_numpy(logits).to(torch.bfloat16)
+    probs = F.softmax(lt, dim=-1, dtype=torch.float32)               # backends.py:114
+    tw, ti = torch.topk(probs, k=8, dim=-1)                          # :115
+    tw = tw / tw.sum(dim=-1, keepdim=True)                           # :116
+    tw = tw * pes[ti]                                                # :117
+    idx, w = oracle.topk_from_logits(logits, pes.float().numpy(), 8)
+    # rows without a tie among the top-9 logits must match torch exactly
+    srt = -np.sort(-logits, axis=1)
+    tie_free = np.all(np.diff(srt[:, :9], axis=1) < 0, axis=1)
+    assert tie_free.sum() > 100
+    assert np.array_equal(idx[tie_free], ti.numpy()[tie_free])
+    np.testing.assert_allclose(w[tie_free], tw.numpy()[tie_free], rtol=2e-6, atol=1e-7)
+
+
+def test_topk_invariants_and_tie_rule():
+    lg = np.array([[1.0, 3.0, 3.0, 2.0, 3.0, -1.0]], np.float32)
+    idx, w = oracle.topk_from_logits(lg, np.ones(6, np.float32), 4)
+    assert idx.tolist() == [[1, 2, 4, 3]]           # value desc, then index asc
+    assert abs(float(w.sum()) - 1.0) < 1e-6
+    rng = np.random.default_rng(10)
+    lg = bf16_round(rng.standard_normal((500, 128)).astype(np.float32))
+    idx, w = oracle.topk_from_logits(lg, np.ones(128, np.float32), 8)
+    for r in range(500):
+        assert len(set(idx[r].tolist())) == 8
+        v = lg[r, idx[r]]
+        assert np.all(np.diff(v) <= 0)
+        assert v[-1] >= np.sort(lg[r])[-9]  # nothing outside the top-8 is larger
+    np.testing.assert_allclose(w.sum(1), 1.0, rtol=1e-6)
+    pes = rng.uniform(0.5, 1.5, 128).astype(np.float32)
+    _, w2 = oracle.topk_from_logits(lg, pes, 8)
+    np.testing.assert_allclose(w2, w * pes[idx], rtol=1e-6)
+
+
+# --------------------------------------------------------------------- permutation
+
+def test_sort_permute_vs_torch_where_bruteforce():
+    # the reference's own procedure (quantization.py:268-276) executed with torch
+    g = torch.Generator().manual_seed(11)
+    for (M, k, E) in [(1, 8, 128), (5, 3, 6), (37, 8, 16), (64, 8, 128)]:
+        idx = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(M)])
+        mask = F.one_hot(idx, num_classes=E + 1).permute(2, 1, 0)
+        expect = []
+        for e in range(E):
+            kpos, tok = torch.where(mask[e])
+            expect += (tok * k + kpos).tolist()
+        sp, off = oracle.sort_permute(idx.numpy(), E)
+        assert sp.tolist() == expect
+        counts = torch.bincount(idx.flatten(), minlength=E)
+        assert off[0] == 0 and np.array_equal(np.diff(off), counts.numpy())
+
+
+def test_sort_permute_bijection_and_stable_argsort():
+    rng = np.random.default_rng(12)
+    M, k, E = 4096, 8, 128
+    idx = np.stack([rng.permutation(E)[:k] for _ in range(M)])
+    sp, off = oracle.sort_permute(idx, E)
+    assert np.array_equal(np.sort(sp), np.arange(M * k))
+    order = torch.argsort(torch.from_numpy(idx.T.reshape(-1).copy()), stable=True).numpy()
+    assert np.array_equal(sp, (order % M) * k + order // M)
+    flat = idx.reshape(-1)
+    for e in (0, 17, 127):
+        seg = sp[off[e]:off[e + 1]]
+        assert np.all(flat[seg] == e)
+
+
+# --------------------------------------------------------------------- MoE
+
+def _moe_case(M, E=16, H=256, I=192, k=4, G=64, seed=13):
+    rng = np.random.default_rng(seed)
+    gu = oracle.pack_int4(rng.integers(-8, 8, size=(E, 2 * I, H)))
+    gus = to_bf16_bits(rng.uniform(0.005, 0.02, size=(E, 2 * I, oracle.num_groups(H, G))).astype(np.float32))
+    dn = oracle.pack_int4(rng.integers(-8, 8, size=(E, H, I)))
+    dns = to_bf16_bits(rng.uniform(0.005, 0.02, size=(E, H, oracle.num_groups(I, G))).astype(np.float32))
+    x = bf16_round(rng.standard_normal((M, H)).astype(np.float32))
+    idx = np.stack([rng.permutation(E)[:k] for _ in range(M)])
+    w = rng.uniform(0.05, 1.0, size=(M, k)).astype(np.float32)
+    w = w / w.sum(1, keepdims=True)
+    return x, idx, w, gu, gus, dn, dns
+
+
+def test_moe_fused_vs_loop_paths():
+    x, idx, w, gu, gus, dn, dns = _moe_case(24)
+    y_fused = oracle.moe_forward(x, idx, w, gu, gus, dn, dns, 64, path="fused")
+    y_loop = oracle.moe_forward(x, idx, w, gu, gus, dn, dns, 64, path="loop")
+    assert oracle.max_abs_rel(y_fused, y_loop) < 1e-2
+    assert oracle.max_abs_rel(y_fused, y_loop) > 0  # different rounding points
+
+
+def test_moe_top1_reduces_to_dense_linear():
+    x, idx, w, gu, gus, dn, dns = _moe_case(6, k=1)
+    w = np.ones_like(w)
+    y = oracle.moe_forward(x, idx, w, gu, gus, dn, dns, 64)
+    I = gu.shape[1] // 2
+    for t in range(6):
+        e = idx[t, 0]
+        g = oracle.linear(x[t:t + 1], gu[e], gus[e], 64)
+        a = bf16_round(oracle.gelu_tanh(g[:, :I]) * g[:, I:])
+        d = oracle.linear(a, dn[e], dns[e], 64)
+        assert np.array_equal(y[t:t + 1], d)
+
+
+def test_moe_gate_rows_first():
+    # swapping the gate and up halves of gate_up must change the output
+    x, idx, w, gu, gus, dn, dns = _moe_case(4)
+    I = gu.shape[1] // 2
+    y = oracle.moe_forward(x, idx, w, gu, gus, dn, dns, 64)
+    gu_sw = np.concatenate([gu[:, I:], gu[:, :I]], axis=1)
+    gus_sw = np.concatenate([gus[:, I:], gus[:, :I]], axis=1)
+    y_sw = oracle.moe_forward(x, idx, w, gu_sw, gus_sw, dn, dns, 64)
+    assert oracle.max_abs_rel(y_sw, y) > 0.1
+
+
+def test_moe_combine_linear_in_weights():
+    x, idx, w, gu, gus, dn, dns = _moe_case(8)
+    _, inter = oracle.moe_forward(x, idx, w, gu, gus, dn, dns, 64, return_intermediates=True)
+    dnv = inter["dn"]
+    y = oracle.moe_forward(x, idx, w, gu, gus, dn, dns, 64)
+    expect = (bf16_round(dnv * bf16_round(w)[:, :, None])).sum(1)
+    assert np.array_equal(y, bf16_round(expect))
+    # doubling the weights doubles the output (power-of-two scaling is exact in bf16)
+    y2 = oracle.moe_forward(x, idx, 2 * w, gu, gus, dn, dns, 64)
+    assert np.array_equal(y2, 2 * y)
+
+
+# --------------------------------------------------------------------- HybridLink (config-4 harness)
+
+def test_hybridlink_vs_torch_modules():
+    torch.manual_seed(14)
+    H = 64
+    lin1, lin2 = torch.nn.Linear(H, H), torch.nn.Linear(H, H)
+    ln1, ln2 = torch.nn.LayerNorm(H), torch.nn.LayerNorm(H)
+    with torch.no_grad():
+        for ln in (ln1, ln2):
+            ln.weight.uniform_(0.5, 1.5)
+            ln.bias.uniform_(-0.1, 0.1)
+    h = torch.randn(5, H)
+    ref = ln2(h + lin2(torch.nn.GELU()(lin1(ln1(h))))).detach().numpy()
+    p = lambda t: t.detach().numpy()
+    got = oracle.hybridlink(p(h), p(lin1.weight), p(lin1.bias), p(lin2.weight), p(lin2.bias),
+                            p(ln1.weight), p(ln1.bias), p(ln2.weight), p(ln2.bias))
+    np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-5)
