@@ -39,6 +39,10 @@ SIGNATURES = {
     "moe_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
     "moe_forward": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64,
                                    _I64, _I64, _VP, _SZ, _VP]),
+    "moe_plan": (ctypes.c_int, [_VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
+    "moe_gate_up": (ctypes.c_int, [_VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
+    "moe_down": (ctypes.c_int, [_VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
+    "moe_combine": (ctypes.c_int, [_VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
 }
 
 _lib = None
@@ -289,3 +293,54 @@ def moe_forward(hidden_states: torch.Tensor, top_k_index: torch.Tensor, top_k_we
                                0 if ws is None else ws.numel(), _stream(dev)),
                "moe_forward")
     return out.reshape(*hidden_states.shape[:-1], H)
+
+
+class MoEStages:
+    """The four stages of ``moe_forward`` on one preallocated workspace.
+
+    For callers that schedule or time the stages separately (the benchmark
+    times ``gate_up`` alone); ``forward`` runs all four.  Sizes are fixed at
+    construction; the workspace carries the routing plan and intermediates
+    between stages, so calls must be made in order on one stream.
+    """
+
+    def __init__(self, M: int, top_k: int, E: int, H: int, I: int, group_size: int, device):
+        self.M, self.k, self.E, self.H, self.I, self.G = M, top_k, E, H, I, group_size
+        self.device = torch.device(device)
+        self.lib = load()
+        nbytes = self.lib.moe_workspace_bytes(max(M, 1), top_k, E, H, I)
+        self.ws = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        self.out = torch.empty((M, H), dtype=torch.bfloat16, device=self.device)
+
+    def _dims(self):
+        return self.M, self.k, self.E, self.H, self.I
+
+    def plan(self, hidden: torch.Tensor, top_k_index: torch.Tensor) -> None:
+        s = _stream(self.device)
+        _check(self.lib.moe_plan(_ptr(hidden), _ptr(top_k_index), *self._dims(), self.G, _ptr(self.ws),
+                                 self.ws.numel(), s), "moe_plan")
+
+    def gate_up(self, hidden: torch.Tensor, gu_packed: torch.Tensor, gu_scale: torch.Tensor) -> None:
+        s = _stream(self.device)
+        _check(self.lib.moe_gate_up(_ptr(hidden), _ptr(gu_packed), _ptr(gu_scale), *self._dims(), self.G,
+                                    _ptr(self.ws), self.ws.numel(), s), "moe_gate_up")
+
+    def down(self, dn_packed: torch.Tensor, dn_scale: torch.Tensor) -> None:
+        s = _stream(self.device)
+        _check(self.lib.moe_down(_ptr(dn_packed), _ptr(dn_scale), *self._dims(), self.G, _ptr(self.ws),
+                                 self.ws.numel(), s), "moe_down")
+
+    def combine(self, top_k_index: torch.Tensor, top_k_weights: torch.Tensor) -> torch.Tensor:
+        s = _stream(self.device)
+        _check(self.lib.moe_combine(_ptr(top_k_index), _ptr(top_k_weights), _ptr(self.out), *self._dims(),
+                                    _ptr(self.ws), self.ws.numel(), s), "moe_combine")
+        return self.out
+
+    def forward(self, hidden, top_k_index, top_k_weights, gu_packed, gu_scale, dn_packed, dn_scale):
+        for t in (hidden, top_k_index, top_k_weights, gu_packed, gu_scale, dn_packed, dn_scale):
+            if not t.is_contiguous() or t.device != self.device:
+                raise ValueError("MoEStages.forward expects contiguous tensors on its device")
+        self.plan(hidden, top_k_index)
+        self.gate_up(hidden, gu_packed, gu_scale)
+        self.down(dn_packed, dn_scale)
+        return self.combine(top_k_index, top_k_weights)

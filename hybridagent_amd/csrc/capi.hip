@@ -34,6 +34,10 @@ inline int launch_status(hipError_t e) { return e == hipSuccess ? W4A16_OK : W4A
 
 inline int router_ksplit(int64_t M) { return M <= 64 ? 8 : 1; }
 
+// Token counts up to this use the decode kernels; larger batches the
+// prefill grouped-GEMM kernels.
+constexpr int64_t kDecodeMaxM = 1 << 30;
+
 // One shared description of the MoE workspace so sizing and carving agree.
 struct MoeLayout {
   int32_t* offsets;
@@ -210,59 +214,99 @@ size_t moe_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t H, int64
   return moe_layout(nullptr, M, top_k, E, H, I).bytes;
 }
 
-int moe_forward(const uint16_t* hidden, const int64_t* topk_idx, const float* topk_w,
-                const int32_t* gu_packed, const uint16_t* gu_scale, const int32_t* dn_packed,
-                const uint16_t* dn_scale, uint16_t* out, int64_t M, int64_t top_k, int64_t E,
-                int64_t H, int64_t I, int64_t group_size, void* workspace,
-                size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Shared validation of the MoE entry points; fills *L on success.
+int moe_check(int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t G,
+              void* workspace, size_t workspace_bytes, MoeLayout* L) {
   if (M < 0 || top_k <= 0 || top_k > kMaxTopK || E <= 0 || E > kMaxExperts || H <= 0 ||
       H % 32 != 0 || I <= 0 || I % 32 != 0 || H > (1 << 20) || I > (1 << 20) ||
       M * top_k > (int64_t(1) << 30) / (H > I ? H : I))
     return W4A16_ERR_SHAPE;
-  if (!valid_group(group_size)) return W4A16_ERR_GROUP;
+  if (!valid_group(G)) return W4A16_ERR_GROUP;
   if (M == 0) return W4A16_OK;
-  if (!hidden || !topk_idx || !topk_w || !gu_packed || !gu_scale || !dn_packed || !dn_scale ||
-      !out)
-    return W4A16_ERR_NULL;
-  if (!aligned16(hidden) || !aligned16(gu_packed) || !aligned16(dn_packed) || !aligned16(out))
-    return W4A16_ERR_ALIGN;
   const MoeLayout need = moe_layout(nullptr, M, top_k, E, H, I);
   if (workspace == nullptr || workspace_bytes < need.bytes) return W4A16_ERR_WORKSPACE;
   if (!aligned16(workspace)) return W4A16_ERR_ALIGN;
-  const MoeLayout L = moe_layout(workspace, M, top_k, E, H, I);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool bias_form = group_size % 128 == 0;
-  const int max_slots = (int)(M * top_k < E ? M * top_k : E);
+  *L = moe_layout(workspace, M, top_k, E, H, I);
+  return W4A16_OK;
+}
 
-  hipError_t e = launch_sort(topk_idx, (int)M, (int)top_k, (int)E, L.sorted_pos, L.offsets,
-                             L.active, L.counters, L.tiles, kPrefillBM, s);
-  if (e != hipSuccess) return W4A16_ERR_LAUNCH;
-  const uint16_t* act = hidden;
-  if (bias_form) {
-    e = launch_bias_order(hidden, L.xp, M, (int)H, s);
-    if (e != hipSuccess) return W4A16_ERR_LAUNCH;
-    act = L.xp;
-  }
+inline bool use_prefill(int64_t M) { return M > kDecodeMaxM; }
+
+// decode GEMMs read bias-ordered activations staged by moe_plan
+// (G % 128 == 0); the prefill GEMMs and the exact decode path read them as
+// given
+inline bool staged_activations(int64_t M, int64_t G) { return G % 128 == 0 && !use_prefill(M); }
+
+DecodeArgs expert_args(const MoeLayout& L, int64_t M, int64_t top_k, int64_t I, int64_t G) {
   DecodeArgs a{};
   a.sorted_pos = L.sorted_pos;
   a.offsets = L.offsets;
   a.active = L.active;
   a.n_active = L.counters;
   a.topk = (int)top_k;
-  a.G = (int)group_size;
+  a.G = (int)G;
   a.I = (int)I;
-  // gate_up + gated GELU
-  a.act = act;
+  a.M = (int)M;
+  return a;
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe_plan(const uint16_t* hidden, const int64_t* topk_idx, int64_t M, int64_t top_k,
+             int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
+             size_t workspace_bytes, void* stream) {
+  MoeLayout L{};
+  int st = moe_check(M, top_k, E, H, I, group_size, workspace, workspace_bytes, &L);
+  if (st != W4A16_OK || M == 0) return st;
+  if (!hidden || !topk_idx) return W4A16_ERR_NULL;
+  if (!aligned16(hidden)) return W4A16_ERR_ALIGN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = launch_sort(topk_idx, (int)M, (int)top_k, (int)E, L.sorted_pos, L.offsets,
+                             L.active, L.counters, L.tiles, kPrefillBM, s);
+  if (e != hipSuccess) return W4A16_ERR_LAUNCH;
+  if (staged_activations(M, group_size)) e = launch_bias_order(hidden, L.xp, M, (int)H, s);
+  return launch_status(e);
+}
+
+int moe_gate_up(const uint16_t* hidden, const int32_t* gu_packed, const uint16_t* gu_scale,
+                int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t group_size,
+                void* workspace, size_t workspace_bytes, void* stream) {
+  MoeLayout L{};
+  int st = moe_check(M, top_k, E, H, I, group_size, workspace, workspace_bytes, &L);
+  if (st != W4A16_OK || M == 0) return st;
+  if (!hidden || !gu_packed || !gu_scale) return W4A16_ERR_NULL;
+  if (!aligned16(hidden) || !aligned16(gu_packed)) return W4A16_ERR_ALIGN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int max_slots = (int)(M * top_k < E ? M * top_k : E);
+  DecodeArgs a = expert_args(L, M, top_k, I, group_size);
+  a.act = staged_activations(M, group_size) ? L.xp : hidden;
   a.wp = gu_packed;
   a.ws = gu_scale;
   a.out = L.inter;
-  a.M = (int)M;
   a.N = (int)(2 * I);
   a.K = (int)H;
   a.ng = (int)((H + group_size - 1) / group_size);
-  e = launch_decode(kModeGateUp, bias_form, a, (int)(I / 8), max_slots, s);
-  if (e != hipSuccess) return W4A16_ERR_LAUNCH;
-  // down
+  return launch_status(
+      launch_decode(kModeGateUp, group_size % 128 == 0, a, (int)(I / 8), max_slots, s));
+}
+
+int moe_down(const int32_t* dn_packed, const uint16_t* dn_scale, int64_t M, int64_t top_k,
+             int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
+             size_t workspace_bytes, void* stream) {
+  MoeLayout L{};
+  int st = moe_check(M, top_k, E, H, I, group_size, workspace, workspace_bytes, &L);
+  if (st != W4A16_OK || M == 0) return st;
+  if (!dn_packed || !dn_scale) return W4A16_ERR_NULL;
+  if (!aligned16(dn_packed)) return W4A16_ERR_ALIGN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int max_slots = (int)(M * top_k < E ? M * top_k : E);
+  DecodeArgs a = expert_args(L, M, top_k, I, group_size);
   a.act = L.inter;
   a.wp = dn_packed;
   a.ws = dn_scale;
@@ -270,10 +314,45 @@ int moe_forward(const uint16_t* hidden, const int64_t* topk_idx, const float* to
   a.N = (int)H;
   a.K = (int)I;
   a.ng = (int)((I + group_size - 1) / group_size);
-  e = launch_decode(kModeDown, bias_form, a, (int)((H + 15) / 16), max_slots, s);
-  if (e != hipSuccess) return W4A16_ERR_LAUNCH;
+  return launch_status(
+      launch_decode(kModeDown, group_size % 128 == 0, a, (int)((H + 15) / 16), max_slots, s));
+}
+
+int moe_combine(const int64_t* topk_idx, const float* topk_w, uint16_t* out, int64_t M,
+                int64_t top_k, int64_t E, int64_t H, int64_t I, void* workspace,
+                size_t workspace_bytes, void* stream) {
+  MoeLayout L{};
+  int st = moe_check(M, top_k, E, H, I, 128, workspace, workspace_bytes, &L);
+  if (st != W4A16_OK || M == 0) return st;
+  if (!topk_idx || !topk_w || !out) return W4A16_ERR_NULL;
+  if (!aligned16(out)) return W4A16_ERR_ALIGN;
   return launch_status(launch_combine(L.dn, topk_idx, topk_w, out, (int)M, (int)top_k, (int)E,
-                                      (int)H, s));
+                                      (int)H, static_cast<hipStream_t>(stream)));
+}
+
+int moe_forward(const uint16_t* hidden, const int64_t* topk_idx, const float* topk_w,
+                const int32_t* gu_packed, const uint16_t* gu_scale, const int32_t* dn_packed,
+                const uint16_t* dn_scale, uint16_t* out, int64_t M, int64_t top_k, int64_t E,
+                int64_t H, int64_t I, int64_t group_size, void* workspace,
+                size_t workspace_bytes, void* stream) {
+  MoeLayout L{};
+  int st = moe_check(M, top_k, E, H, I, group_size, workspace, workspace_bytes, &L);
+  if (st != W4A16_OK || M == 0) return st;
+  if (!hidden || !topk_idx || !topk_w || !gu_packed || !gu_scale || !dn_packed || !dn_scale ||
+      !out)
+    return W4A16_ERR_NULL;
+  st = moe_plan(hidden, topk_idx, M, top_k, E, H, I, group_size, workspace, workspace_bytes,
+                stream);
+  if (st == W4A16_OK)
+    st = moe_gate_up(hidden, gu_packed, gu_scale, M, top_k, E, H, I, group_size, workspace,
+                     workspace_bytes, stream);
+  if (st == W4A16_OK)
+    st = moe_down(dn_packed, dn_scale, M, top_k, E, H, I, group_size, workspace,
+                  workspace_bytes, stream);
+  if (st == W4A16_OK)
+    st = moe_combine(topk_idx, topk_w, out, M, top_k, E, H, I, workspace, workspace_bytes,
+                     stream);
+  return st;
 }
 
 }  // extern "C"

@@ -111,12 +111,38 @@ W4A16_API int moe_sort_permute(const int64_t* topk_idx, int64_t M, int64_t top_k
  * hidden [M, H] bf16; topk_idx int64 [M, top_k]; topk_w float32 [M, top_k];
  * gu_packed int32 [E, 2I, H/8] (gate rows 0..I-1, up rows I..2I-1);
  * gu_scale bf16 [E, 2I, ceil(H/G)]; dn_packed int32 [E, H, I/8];
- * dn_scale bf16 [E, H, ceil(I/G)].                                         */
+ * dn_scale bf16 [E, H, ceil(I/G)].  Slots whose index is outside [0, E)
+ * contribute nothing.  moe_forward = moe_plan + moe_gate_up + moe_down +
+ * moe_combine on one workspace.                                            */
 W4A16_API size_t moe_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I);
 W4A16_API int moe_forward(const uint16_t* hidden, const int64_t* topk_idx, const float* topk_w,
                 const int32_t* gu_packed, const uint16_t* gu_scale, const int32_t* dn_packed,
                 const uint16_t* dn_scale, uint16_t* out, int64_t M, int64_t top_k, int64_t E,
                 int64_t H, int64_t I, int64_t group_size, void* workspace,
+                size_t workspace_bytes, void* stream);
+
+/* The four stages of moe_forward, for callers that schedule or time them
+ * separately.  They share one workspace of moe_workspace_bytes(M, top_k, E,
+ * H, I) bytes that carries the routing plan and the intermediate
+ * activations from stage to stage; call them in this order, on one stream,
+ * with identical sizes.
+ *   moe_plan      expert sort of topk_idx (quantization.py:266-276) and the
+ *                 activation staging for the expert GEMMs;
+ *   moe_gate_up   grouped gate_up GEMM with the gated GELU fused
+ *                 (first Triton launch + glue, quantization.py:112-120);
+ *   moe_down      grouped down GEMM (second launch, quantization.py:122-127);
+ *   moe_combine   weighted top-k sum into out (quantization.py:128-129).    */
+W4A16_API int moe_plan(const uint16_t* hidden, const int64_t* topk_idx, int64_t M, int64_t top_k,
+             int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
+             size_t workspace_bytes, void* stream);
+W4A16_API int moe_gate_up(const uint16_t* hidden, const int32_t* gu_packed, const uint16_t* gu_scale, int64_t M, int64_t top_k,
+                int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
+                size_t workspace_bytes, void* stream);
+W4A16_API int moe_down(const int32_t* dn_packed, const uint16_t* dn_scale, int64_t M, int64_t top_k,
+             int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
+             size_t workspace_bytes, void* stream);
+W4A16_API int moe_combine(const int64_t* topk_idx, const float* topk_w, uint16_t* out, int64_t M,
+                int64_t top_k, int64_t E, int64_t H, int64_t I, void* workspace,
                 size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
