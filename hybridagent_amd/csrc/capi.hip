@@ -37,15 +37,16 @@ inline int router_ksplit(int64_t M) { return M <= 64 ? 8 : 1; }
 // Token counts up to this use the decode kernels; larger batches the
 // prefill grouped-GEMM kernels.
 constexpr int64_t kDecodeMaxM = 1 << 30;
+// longest reduction the streaming kernels stage in LDS (one row per pass)
+constexpr int64_t kMaxStreamK = 49152 / 2;
 
 // One shared description of the MoE workspace so sizing and carving agree.
 struct MoeLayout {
   int32_t* offsets;
-  int32_t* active;
+  int32_t* desc;
   int32_t* counters;
   int32_t* sorted_pos;
   int32_t* tiles;
-  uint16_t* xp;
   uint16_t* inter;
   uint16_t* dn;
   size_t bytes;
@@ -55,11 +56,10 @@ MoeLayout moe_layout(void* ws, int64_t M, int64_t k, int64_t E, int64_t H, int64
   Carve c(ws);
   MoeLayout L;
   L.offsets = c.take<int32_t>(E + 1);
-  L.active = c.take<int32_t>(E);
+  L.desc = c.take<int32_t>(4 * E);
   L.counters = c.take<int32_t>(2);
   L.sorted_pos = c.take<int32_t>(M * k);
   L.tiles = c.take<int32_t>(M * k / kPrefillBM + E + 1);
-  L.xp = c.take<uint16_t>(M * H);
   L.inter = c.take<uint16_t>(M * k * I);
   L.dn = c.take<uint16_t>(M * k * H);
   L.bytes = c.used;
@@ -97,8 +97,10 @@ int w4a16_dequantize(const int32_t* packed, const uint16_t* scale, uint16_t* out
 }
 
 size_t w4a16_linear_workspace_bytes(int64_t M, int64_t K, int64_t group_size) {
-  if (M <= 0 || K <= 0) return 0;
-  return group_size % 128 == 0 ? round256(size_t(M) * K * 2) : 0;
+  (void)M;
+  (void)K;
+  (void)group_size;
+  return 0;  // the dense path needs no scratch memory
 }
 
 int w4a16_linear(const uint16_t* x, const int32_t* w_packed, const uint16_t* w_scale,
@@ -111,20 +113,13 @@ int w4a16_linear(const uint16_t* x, const int32_t* w_packed, const uint16_t* w_s
   if (M == 0) return W4A16_OK;
   if (!x || !w_packed || !w_scale || !y) return W4A16_ERR_NULL;
   if (!aligned16(x) || !aligned16(w_packed)) return W4A16_ERR_ALIGN;
-  const size_t need = w4a16_linear_workspace_bytes(M, K, group_size);
-  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return W4A16_ERR_WORKSPACE;
-  if (need > 0 && !aligned16(workspace)) return W4A16_ERR_ALIGN;
+  (void)workspace;
+  (void)workspace_bytes;
+  if (K > kMaxStreamK) return W4A16_ERR_SHAPE;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool bias_form = group_size % 128 == 0;
-  const uint16_t* act = x;
-  if (bias_form) {
-    uint16_t* xp = static_cast<uint16_t*>(workspace);
-    hipError_t e = launch_bias_order(x, xp, M, (int)K, s);
-    if (e != hipSuccess) return W4A16_ERR_LAUNCH;
-    act = xp;
-  }
   DecodeArgs a{};
-  a.act = act;
+  a.act = x;
   a.wp = w_packed;
   a.ws = w_scale;
   a.bias = bias;
@@ -136,7 +131,8 @@ int w4a16_linear(const uint16_t* x, const int32_t* w_packed, const uint16_t* w_s
   a.ng = (int)((K + group_size - 1) / group_size);
   a.topk = 1;
   a.I = 0;
-  return launch_status(launch_decode(kModeDense, bias_form, a, (int)((N + 15) / 16), 1, s));
+  a.rows_hint = (int)(M < 16 ? M : 16);
+  return launch_status(launch_decode(kModeDense, bias_form, a, 1, s));
 }
 
 size_t moe_router_workspace_bytes(int64_t M, int64_t H, int64_t E) {
@@ -187,7 +183,7 @@ int moe_topk_from_logits(const uint16_t* logits, const uint16_t* per_expert_scal
 
 size_t moe_sort_workspace_bytes(int64_t M, int64_t top_k, int64_t E) {
   if (M <= 0 || top_k <= 0 || E <= 0) return 0;
-  return round256(size_t(E) * 4) + round256(8) + round256(size_t(M * top_k / kPrefillBM + E + 1) * 4);
+  return round256(size_t(E) * 16) + round256(8) + round256(size_t(M * top_k / kPrefillBM + E + 1) * 4);
 }
 
 int moe_sort_permute(const int64_t* topk_idx, int64_t M, int64_t top_k, int64_t E,
@@ -201,11 +197,11 @@ int moe_sort_permute(const int64_t* topk_idx, int64_t M, int64_t top_k, int64_t 
   const size_t need = moe_sort_workspace_bytes(M > 0 ? M : 1, top_k, E);
   if (workspace == nullptr || workspace_bytes < need) return W4A16_ERR_WORKSPACE;
   Carve c(workspace);
-  int32_t* active = c.take<int32_t>(E);
+  int32_t* desc = c.take<int32_t>(4 * E);
   int32_t* counters = c.take<int32_t>(2);
   int32_t* tiles = c.take<int32_t>(M * top_k / kPrefillBM + E + 1);
   return launch_status(launch_sort(topk_idx, (int)M, (int)top_k, (int)E, sorted_pos,
-                                   expert_offsets, active, counters, tiles, kPrefillBM,
+                                   expert_offsets, desc, counters, tiles, kPrefillBM,
                                    static_cast<hipStream_t>(stream)));
 }
 
@@ -222,7 +218,7 @@ namespace {
 int moe_check(int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t G,
               void* workspace, size_t workspace_bytes, MoeLayout* L) {
   if (M < 0 || top_k <= 0 || top_k > kMaxTopK || E <= 0 || E > kMaxExperts || H <= 0 ||
-      H % 32 != 0 || I <= 0 || I % 32 != 0 || H > (1 << 20) || I > (1 << 20) ||
+      H % 32 != 0 || I <= 0 || I % 32 != 0 || H > kMaxStreamK || I > kMaxStreamK ||
       M * top_k > (int64_t(1) << 30) / (H > I ? H : I))
     return W4A16_ERR_SHAPE;
   if (!valid_group(G)) return W4A16_ERR_GROUP;
@@ -236,21 +232,17 @@ int moe_check(int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t
 
 inline bool use_prefill(int64_t M) { return M > kDecodeMaxM; }
 
-// decode GEMMs read bias-ordered activations staged by moe_plan
-// (G % 128 == 0); the prefill GEMMs and the exact decode path read them as
-// given
-inline bool staged_activations(int64_t M, int64_t G) { return G % 128 == 0 && !use_prefill(M); }
-
 DecodeArgs expert_args(const MoeLayout& L, int64_t M, int64_t top_k, int64_t I, int64_t G) {
   DecodeArgs a{};
   a.sorted_pos = L.sorted_pos;
-  a.offsets = L.offsets;
-  a.active = L.active;
+  a.desc = L.desc;
   a.n_active = L.counters;
   a.topk = (int)top_k;
   a.G = (int)G;
   a.I = (int)I;
   a.M = (int)M;
+  // an expert gets each token at most once: at most M rows
+  a.rows_hint = (int)(M < 16 ? M : 16);
   return a;
 }
 
@@ -268,9 +260,7 @@ int moe_plan(const uint16_t* hidden, const int64_t* topk_idx, int64_t M, int64_t
   if (!aligned16(hidden)) return W4A16_ERR_ALIGN;
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = launch_sort(topk_idx, (int)M, (int)top_k, (int)E, L.sorted_pos, L.offsets,
-                             L.active, L.counters, L.tiles, kPrefillBM, s);
-  if (e != hipSuccess) return W4A16_ERR_LAUNCH;
-  if (staged_activations(M, group_size)) e = launch_bias_order(hidden, L.xp, M, (int)H, s);
+                             L.desc, L.counters, L.tiles, kPrefillBM, s);
   return launch_status(e);
 }
 
@@ -285,15 +275,14 @@ int moe_gate_up(const uint16_t* hidden, const int32_t* gu_packed, const uint16_t
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int max_slots = (int)(M * top_k < E ? M * top_k : E);
   DecodeArgs a = expert_args(L, M, top_k, I, group_size);
-  a.act = staged_activations(M, group_size) ? L.xp : hidden;
+  a.act = hidden;
   a.wp = gu_packed;
   a.ws = gu_scale;
   a.out = L.inter;
   a.N = (int)(2 * I);
   a.K = (int)H;
   a.ng = (int)((H + group_size - 1) / group_size);
-  return launch_status(
-      launch_decode(kModeGateUp, group_size % 128 == 0, a, (int)(I / 8), max_slots, s));
+  return launch_status(launch_decode(kModeGateUp, group_size % 128 == 0, a, max_slots, s));
 }
 
 int moe_down(const int32_t* dn_packed, const uint16_t* dn_scale, int64_t M, int64_t top_k,
@@ -314,8 +303,7 @@ int moe_down(const int32_t* dn_packed, const uint16_t* dn_scale, int64_t M, int6
   a.N = (int)H;
   a.K = (int)I;
   a.ng = (int)((I + group_size - 1) / group_size);
-  return launch_status(
-      launch_decode(kModeDown, group_size % 128 == 0, a, (int)((H + 15) / 16), max_slots, s));
+  return launch_status(launch_decode(kModeDown, group_size % 128 == 0, a, max_slots, s));
 }
 
 int moe_combine(const int64_t* topk_idx, const float* topk_w, uint16_t* out, int64_t M,

@@ -56,14 +56,23 @@ __device__ __forceinline__ float round_bf16(float f) {
 }
 
 // Bias-form unpack of one packed word: 4 dwords of bf16 pairs
-// (128+u_i, 128+u_{i+4}) for i = 0..3.
-__device__ __forceinline__ u32x4_t unpack_bias(uint32_t w) {
+// (128+u_i, 128+u_{i+4}) for i = 0..3.  `mask` = 0x000F000F and `bias` =
+// 0x43004300 are passed in (already in registers): gfx9 VOP3 instructions take
+// no literal operands, so with register constants each pair is one
+// v_and_or_b32 (7 instructions per word instead of 11).
+__device__ __forceinline__ u32x4_t unpack_bias(uint32_t w, uint32_t mask, uint32_t bias) {
   u32x4_t r;
-  r.x = (w & 0x000F000Fu) | kBiasPair;
-  r.y = ((w >> 4) & 0x000F000Fu) | kBiasPair;
-  r.z = ((w >> 8) & 0x000F000Fu) | kBiasPair;
-  r.w = ((w >> 12) & 0x000F000Fu) | kBiasPair;
+  r.x = (w & mask) | bias;
+  r.y = ((w >> 4) & mask) | bias;
+  r.z = ((w >> 8) & mask) | bias;
+  r.w = ((w >> 12) & mask) | bias;
   return r;
+}
+
+// Hides a value from constant folding so it stays in a register.
+__device__ __forceinline__ uint32_t opaque(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
 }
 
 // Exact unpack of one packed word with scale s: 8 values bf16_RNE(q*s).
@@ -120,6 +129,24 @@ __device__ __forceinline__ f32x4_t mfma16(u32x4_t a, u32x4_t b, f32x4_t c) {
 
 __device__ __forceinline__ f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+// Raw buffer access (gfx9 descriptor: 32-bit data format, no stride).  The
+// base and size live in SGPRs when wave-uniform; each lane supplies a 32-bit
+// byte offset; reads past num_bytes return zero.
+constexpr int kBufferRsrcWord3 = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t num_bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)num_bytes,
+                                           kBufferRsrcWord3);
+}
+
+__device__ __forceinline__ u32x4_t buf_ld16(__amdgpu_buffer_rsrc_t r, int voff, int imm) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff + imm, 0, 0));
+}
+
+__device__ __forceinline__ uint16_t buf_ld_u16(__amdgpu_buffer_rsrc_t r, int voff) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, voff, 0, 0);
 }
 
 // 16-byte global load / store helpers.

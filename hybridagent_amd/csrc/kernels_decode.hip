@@ -2,12 +2,11 @@
 // matrix, so the packed weights stream from HBM once and the arithmetic runs
 // on 16x16x32 bf16 MFMA tiles.
 //
-//   k_decode<MODE, BIAS>   one workgroup = 16 weight rows (MFMA columns) of
-//                          one expert; its 4 wavefronts split K into 128-wide
-//                          tiles (wave w takes tiles w, w+4, ...) and reduce
-//                          through LDS.  Each lane streams its weight rows
-//                          with 16-byte loads: lanes kb = 0..3 of a column
-//                          read 64 contiguous bytes of the row per tile.
+//   k_decode<MODE, BIAS, TPW, KSPLIT>  persistent workgroups stream the
+//                          packed weight rows of the active experts with
+//                          16-byte loads (lanes kb = 0..3 of a column read 64
+//                          contiguous bytes of the row per 128-wide k tile);
+//                          activations are staged once per expert in LDS.
 //   MODE = dense  : y = x W^T (+bias)                (quantization.py:171-175)
 //   MODE = gateup : inter = gelu(x Wg^T) * (x Wu^T)  (quantization.py:112-120)
 //                   columns 0..7 of the tile are gate rows n0..n0+7 and
@@ -16,6 +15,8 @@
 //   MODE = down   : dn[t*k+j] = inter W_d^T          (quantization.py:122-127)
 //
 // k_bias_order, k_combine and k_dequant are the small helpers around it.
+#include <type_traits>
+
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -74,187 +75,438 @@ hipError_t launch_bias_order(const uint16_t* x, uint16_t* xp, int64_t rows, int 
 }
 
 // ---------------------------------------------------------------------------
-// the decode MFMA kernel
+// the decode MFMA kernel (persistent weight streamer)
 // ---------------------------------------------------------------------------
 // Operand layout of v_mfma_f32_16x16x32_bf16 as used here: lane l supplies
 // A[row l%16][8*(l/16) .. +7] and B[8*(l/16) .. +7][col l%16]; the result lane
 // l holds D[4*(l/16) + r][l%16], r = 0..3.  A and B only need to agree on the
-// k index carried by (l/16, element), so each lane simply feeds 8 consecutive
+// k index carried by (l/16, element), so each lane feeds 8 consecutive
 // (bias- or natural-ordered) k values of its own 32-element chunk per step.
-template <int MODE, bool BIAS>
-__global__ __launch_bounds__(256) void k_decode(DecodeArgs a) {
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
-  const int j = lane & 15;   // MFMA column (weight row within the tile) / A row
-  const int kb = lane >> 4;  // which 32-element chunk of the 128-wide k tile
+//
+// Work split: every workgroup serves exactly one active expert.  The grid is
+// max_slots x wg_per_slot workgroups; workgroup w takes expert slot
+// w / wg_per_slot (exiting if that slot is not active) and a contiguous run of
+// that expert's column tiles ("items": 4/KSPLIT groups of 16 weight rows).
+// It stages the expert's activation rows into LDS once per pass of rb rows
+// (an expert with more than rb rows makes several passes over its weights),
+// then streams its items.  Inside an item, each 16-row column group's K range
+// is split over KSPLIT wavefronts (wavefront ks takes the contiguous 128-wide
+// k tiles ks*TPW .. ks*TPW + TPW - 1, so its back-to-back loads cover whole
+// 128-byte lines of each weight row), each holding TPW tiles' weight loads
+// (one 16-byte load per lane per tile) in registers.  Each weight register
+// is reloaded with the next item's tile as soon as it has been unpacked, so
+// weight traffic stays in flight across the MFMAs, the split-K reduction
+// (through LDS) and the epilogue.
+//
+// LDS activation layout ("fragment order"): the 16-byte piece holding
+// elements 8b..8b+7 of staged row j lives at slot
+//   (16*(b/16) + 4*(b%4) + (b/4)%4) * rb + j
+// i.e. grouped by (k tile, lane chunk, MFMA step), so a wavefront's
+// ds_read_b128 of one MFMA step is contiguous and bank-conflict free.
+constexpr int kStreamThreads = 256;
 
+__device__ __forceinline__ int frag_slot(int b, int rb, int j) {
+  return (16 * (b >> 4) + 4 * (b & 3) + ((b >> 2) & 3)) * rb + j;
+}
+
+template <int MODE, bool BIAS, int TPW, int KSPLIT, bool LONGK>
+__global__ __launch_bounds__(kStreamThreads) __attribute__((amdgpu_waves_per_eu(TPW >= 6 ? 3 : 4, 8)))
+void k_decode(DecodeArgs a) {
+  constexpr int CG = 4 / KSPLIT;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  u32x4_t* __restrict__ lds_a = reinterpret_cast<u32x4_t*>(smem_raw);
+  // per (k tile, staged row) bias correction, after the activation fragments
+  const int ntiles = ((a.K >> 5) + 3) >> 2;
+  float* __restrict__ csum = reinterpret_cast<float*>(smem_raw + (size_t)ntiles * 16 * a.rb * 16);
+  __shared__ f32x4_t red[4][64];
+  __shared__ int tok[16];
+
+  const int tid = threadIdx.x;
+  // wave-uniform values are pinned to SGPRs: branches on them must be
+  // scalar, or the compiler merges in-flight load registers under exec
+  // masks with copies that wait for the loads
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int cg = wave / KSPLIT;
+  const int ks = wave - cg * KSPLIT;
+  const int j = lane & 15;   // MFMA column (weight row in the group) / A row
+  const int kb = lane >> 4;  // 32-element chunk of the 128-wide k tile
+
+  // this workgroup's expert and item range
+  const int slot = (int)blockIdx.x / a.wg_per_slot;
+  const int part = (int)blockIdx.x - slot * a.wg_per_slot;
   int e = 0, seg0 = 0, rows = a.M;
   if (MODE != kModeDense) {
-    const int slot = blockIdx.y;
-    if (slot >= *a.n_active) return;  // uniform across the workgroup
-    e = a.active[slot];
-    seg0 = a.offsets[e];
-    rows = a.offsets[e + 1] - seg0;
+    const int U = __builtin_amdgcn_readfirstlane(*a.n_active);
+    if (slot >= U) return;  // uniform across the workgroup
+    const int4 d = *reinterpret_cast<const int4*>(a.desc + 4 * slot);
+    e = __builtin_amdgcn_readfirstlane(d.x);
+    seg0 = __builtin_amdgcn_readfirstlane(d.y);
+    rows = __builtin_amdgcn_readfirstlane(d.z);
   }
+  const int per = (a.n_ct + a.wg_per_slot - 1) / a.wg_per_slot;
+  const int begin = part * per;
+  const int end = min(a.n_ct, begin + per);
+  if (begin >= end || rows <= 0) return;
 
-  int wrow;
-  if (MODE == kModeGateUp) {
-    const int n0 = blockIdx.x * 8;
-    wrow = (j < 8) ? (n0 + j) : (a.I + n0 + (j - 8));
-  } else {
-    wrow = blockIdx.x * 16 + j;
-  }
-  const bool col_ok = wrow < a.N;
-  const int64_t grow = (int64_t)e * a.N + (col_ok ? wrow : 0);
-  const uint32_t* __restrict__ wr = reinterpret_cast<const uint32_t*>(a.wp) + grow * (a.K >> 3);
-  const uint16_t* __restrict__ sr = a.ws + grow * a.ng;
+  const int K8 = a.K >> 3;
   const int nchunks = a.K >> 5;
-  const int ntiles = (nchunks + 3) >> 2;
+  const int rb = a.rb;                 // staged rows per pass, a power of two <= 16
+  const int jr_read = j & (rb - 1);    // A row this lane reads (rows >= rb only
+                                       // feed output rows that are discarded)
+  const int tile0 = ks * TPW;          // this wavefront's first k tile
 
-  __shared__ f32x4_t red[4][4][64];
+  // Chunks past K in the last tile read zeros from LDS (their weight operand
+  // is the next row's bytes); that padding is written once here and never
+  // touched by staging.  Rows past the staged ones hold stale values, which
+  // only reach output rows that are not stored.
+  for (int b = K8 + tid / rb; b < 16 * ntiles; b += kStreamThreads / rb)
+    lds_a[frag_slot(b, rb, tid & (rb - 1))] = u32x4_t{0u, 0u, 0u, 0u};
 
-  const u32x4_t c136 = {kBias136Pair, kBias136Pair, kBias136Pair, kBias136Pair};
-  const u32x4_t zero4 = {0u, 0u, 0u, 0u};
+  const uint32_t kMask = opaque(0x000F000Fu), kBias = opaque(kBiasPair);
 
-  for (int mc = 0; mc < rows; mc += 64) {
-    const int nmt = min(4, (rows - mc + 15) >> 4);
-    const uint16_t* arow[4];
-    bool aok[4];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const int i = mc + 16 * mt + j;
-      aok[mt] = (mt < nmt) && (i < rows);
-      int64_t r = 0;
-      if (aok[mt]) {
-        if (MODE == kModeDense) r = i;
-        else if (MODE == kModeGateUp) r = a.sorted_pos[seg0 + i] / a.topk;
-        else r = seg0 + i;
-      }
-      arow[mt] = a.act + r * a.K;
+  // weight row of this lane's MFMA column for column tile ct
+  auto weight_row = [&](int ct, bool* ok) -> int {
+    const int colblk = ct * CG + cg;
+    if (MODE == kModeGateUp) {
+      const int n0 = colblk * 8;
+      *ok = colblk * 8 + 8 <= a.I;
+      return *ok ? ((j < 8) ? (n0 + j) : (a.I + n0 + (j - 8))) : 0;
     }
+    const int wrow = colblk * 16 + j;
+    *ok = wrow < a.N;
+    return *ok ? wrow : 0;
+  };
 
-    f32x4_t acc[4];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // The expert's weight / scale matrices as buffer descriptors (SGPRs): each
+  // lane carries one byte offset per item.  Rows past the matrix read as
+  // zero; chunks past the row end read the next row, harmless because their
+  // activation operand is zero.
+  const __amdgpu_buffer_rsrc_t wsrc =
+      make_rsrc(reinterpret_cast<const uint32_t*>(a.wp) + (int64_t)e * a.N * K8, (uint32_t)a.N * K8 * 4u);
+  const __amdgpu_buffer_rsrc_t ssrc = make_rsrc(a.ws + (int64_t)e * a.N * a.ng, (uint32_t)a.N * a.ng * 2u);
+  struct Off {
+    int woff, srow;
+  };
+  auto off_of = [&](int ct) -> Off {
+    bool ok;
+    const int wrow = weight_row(ct, &ok);
+    return Off{wrow * K8 * 4 + 16 * kb, wrow * a.ng};
+  };
+  auto scale_off = [&](const Off& o, int t) -> int {
+    const int g = BIAS ? (t * 128) / a.G : ((4 * t + kb) * 32) / a.G;
+    return (o.srow + g) * 2;
+  };
 
-    for (int t = wave; t < ntiles; t += 4) {
-      const int c = 4 * t + kb;
-      const bool cok = c < nchunks;
-      const u32x4_t bw = (cok && col_ok) ? ld16(wr + 4 * c) : zero4;
-      u32x4_t av[4][4];
+  u32x4_t bw[TPW];
+  // raw bf16 bits, kept 16-bit until use: widening them where the loop
+  // carries them would wait for the loads (see load_batch)
+  uint16_t sc[TPW];
+
+  // All loads of one batch are issued back to back; converting a scale right
+  // away would make the wavefront wait for it and -- loads retiring in order --
+  // for every weight load before it.
+  auto load_batch = [&](const Off& o, int tb) {
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
+    for (int i = 0; i < TPW; ++i) bw[i] = buf_ld16(wsrc, o.woff + 64 * tb, 64 * i);
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-          av[mt][s] = (aok[mt] && cok) ? ld16(arow[mt] + 32 * c + 8 * s) : zero4;
+    for (int i = 0; i < TPW; ++i) sc[i] = buf_ld_u16(ssrc, scale_off(o, tb + i));
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Stage activation rows [mc, mc + nr) into LDS.  One task = one (row, k
+  // tile): 16 pieces of 16 bytes, reordered for the bias form, stored in
+  // fragment order, and -- for the bias form -- summed into
+  // csum[t][row] = 136 * (sum of the row's tile elements), the correction the
+  // bias form subtracts per group.
+  auto stage = [&](int mc, int nr) {
+    __syncthreads();  // previous readers of lds_a / csum / tok are done
+    if (MODE == kModeGateUp && tid < nr) tok[tid] = a.sorted_pos[seg0 + mc + tid] / a.topk;
+    __syncthreads();
+    for (int q = tid; q < nr * ntiles; q += kStreamThreads) {
+      const int jr = q / ntiles;
+      const int t = q - jr * ntiles;
+      int64_t row;
+      if (MODE == kModeDense) row = mc + jr;
+      else if (MODE == kModeGateUp) row = tok[jr];
+      else row = seg0 + mc + jr;
+      const uint16_t* src = a.act + row * a.K + 128 * t;
+      const int nb = min(16, K8 - 16 * t);
+      float sum = 0.f;
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        u32x4_t v[8];
+#pragma unroll
+        for (int b8 = 0; b8 < 8; ++b8) {
+          const int bb = 8 * half + b8;
+          v[b8] = bb < nb ? ld16(src + 8 * bb) : u32x4_t{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int b8 = 0; b8 < 8; ++b8) {
+          const int bb = 8 * half + b8;
+          if (bb < nb) {
+            u32x4_t x = v[b8];
+            // gate_up / dense read caller activations in natural order; down
+            // reads intermediate rows the gate_up epilogue wrote in bias order
+            if (BIAS && MODE != kModeDown) x = to_bias_order(x);
+            if (BIAS) {
+              sum += bf16_bits_to_f32(x.x & 0xFFFFu) + bf16_bits_to_f32(x.x >> 16) +
+                     bf16_bits_to_f32(x.y & 0xFFFFu) + bf16_bits_to_f32(x.y >> 16) +
+                     bf16_bits_to_f32(x.z & 0xFFFFu) + bf16_bits_to_f32(x.z >> 16) +
+                     bf16_bits_to_f32(x.w & 0xFFFFu) + bf16_bits_to_f32(x.w >> 16);
+            }
+            lds_a[frag_slot(16 * t + bb, rb, jr)] = x;
+          }
+        }
+      }
+      if (BIAS) csum[t * 16 + jr] = 136.0f * sum;
+    }
+    __syncthreads();
+  };
+
+  // One tile batch into acc.  With REFILL, each weight register is reloaded
+  // from `nx` as soon as it has been unpacked, so the next loads overlap the
+  // rest of this item's work without a second register set.  The reload is
+  // unconditional (the caller picks the source): a conditional reload makes
+  // the compiler merge old and new values with register copies, and copying
+  // a register that a load is filling waits for every load in flight.
+  auto mma_batch = [&](int tb, f32x4_t& acc, auto refill_tag, const Off& nx) {
+    constexpr bool REFILL = decltype(refill_tag)::value;
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      // Tiles past K (the last wavefront's spare slots) run on the last real
+      // tile's activations with a zero scale, adding exactly 0: branch-free,
+      // so every weight register has one unconditional definition.
+      const int t = tb + i;
+      const bool t_ok = t < ntiles;
+      const int tc = t_ok ? t : ntiles - 1;
+      u32x4_t A[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) A[s] = lds_a[frag_slot(16 * tc + 4 * kb + s, rb, jr_read)];
+      // the bias form scales a whole tile, the exact form one lane chunk
+      const bool s_ok = t_ok && (BIAS || 4 * t + kb < nchunks);
+      const float sci = s_ok ? bf16_bits_to_f32(sc[i]) : 0.f;
+      u32x4_t bv[4];
+      if (BIAS) {
+        bv[0] = unpack_bias(bw[i].x, kMask, kBias);
+        bv[1] = unpack_bias(bw[i].y, kMask, kBias);
+        bv[2] = unpack_bias(bw[i].z, kMask, kBias);
+        bv[3] = unpack_bias(bw[i].w, kMask, kBias);
+      } else {
+        bv[0] = unpack_exact<false>(bw[i].x, sci);
+        bv[1] = unpack_exact<false>(bw[i].y, sci);
+        bv[2] = unpack_exact<false>(bw[i].z, sci);
+        bv[3] = unpack_exact<false>(bw[i].w, sci);
+      }
+      if (REFILL) {
+        bw[i] = buf_ld16(wsrc, nx.woff + 64 * tb, 64 * i);
+        sc[i] = buf_ld_u16(ssrc, scale_off(nx, tc));
       }
       if (BIAS) {
-        // one scale per lane column for the whole 128-wide tile (G % 128 == 0)
-        const float sc = col_ok ? bf16_bits_to_f32(sr[(t * 128) / a.G]) : 0.f;
-        u32x4_t bv[4];
-        bv[0] = unpack_bias(bw.x);
-        bv[1] = unpack_bias(bw.y);
-        bv[2] = unpack_bias(bw.z);
-        bv[3] = unpack_bias(bw.w);
+        f32x4_t g = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          if (mt < nmt) {
-            f32x4_t g = {0.f, 0.f, 0.f, 0.f};
-            f32x4_t cr = {0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < 4; ++s) g = mfma16(A[s], bv[s], g);
+        // output rows 4*kb .. 4*kb+3 of this lane: their 136 * sum(x)
+        const f32x4_t cr = *reinterpret_cast<const f32x4_t*>(csum + tc * 16 + 4 * kb);
 #pragma unroll
-            for (int s = 0; s < 4; ++s) g = mfma16(av[mt][s], bv[s], g);
-#pragma unroll
-            for (int s = 0; s < 4; ++s) cr = mfma16(av[mt][s], c136, cr);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[mt][r] = __builtin_fmaf(sc, g[r] - cr[r], acc[mt][r]);
-          }
-        }
+        for (int q = 0; q < 4; ++q) acc[q] = __builtin_fmaf(sci, g[q] - cr[q], acc[q]);
       } else {
-        // each lane's 32-element chunk lies inside one group (G >= 32)
-        const float sc = (col_ok && cok) ? bf16_bits_to_f32(sr[(32 * c) / a.G]) : 0.f;
-        u32x4_t bv[4];
-        bv[0] = unpack_exact<false>(bw.x, sc);
-        bv[1] = unpack_exact<false>(bw.y, sc);
-        bv[2] = unpack_exact<false>(bw.z, sc);
-        bv[3] = unpack_exact<false>(bw.w, sc);
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          if (mt < nmt) {
-#pragma unroll
-            for (int s = 0; s < 4; ++s) acc[mt] = mfma16(av[mt][s], bv[s], acc[mt]);
-          }
-        }
+        for (int s = 0; s < 4; ++s) acc = mfma16(A[s], bv[s], acc);
       }
+      // keep the next tile's LDS reads and unpacking from being hoisted
+      // above this one (bounds the live registers to one tile's operands)
+      __builtin_amdgcn_sched_barrier(0);
     }
+  };
 
-    // split-K reduction over the 4 wavefronts
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-      if (mt < nmt) red[wave][mt][lane] = acc[mt];
-    __syncthreads();
-    const int mt = wave;  // wavefront w finishes m-tile w
-    if (mt < nmt) {
-      f32x4_t v = red[0][mt][lane];
-#pragma unroll
-      for (int w = 1; w < 4; ++w) {
-        const f32x4_t o = red[w][mt][lane];
-        v[0] += o[0]; v[1] += o[1]; v[2] += o[2]; v[3] += o[3];
-      }
-      const int ibase = mc + 16 * mt + 4 * (lane >> 4);
-      if (MODE == kModeDense) {
-        const int n = blockIdx.x * 16 + j;
-        const float b = (a.bias != nullptr && col_ok) ? bf16_bits_to_f32(a.bias[n]) : 0.f;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int i = ibase + r;
-          if (col_ok && i < rows) a.out[(int64_t)i * a.N + n] = f32_to_bf16_bits(v[r] + b);
-        }
-      } else if (MODE == kModeGateUp) {
-        // lane j (< 8) holds gate column n0+j, lane j+8 the matching up column
-        const int n0 = blockIdx.x * 8;
-        const int pos = BIAS ? ((j & 3) * 2 + ((j >> 2) & 1)) : j;  // bias-order slot
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float up = __shfl_xor(v[r], 8);
-          const int i = ibase + r;
-          if (j < 8 && i < rows) {
-            const float gate = round_bf16(v[r]);
-            const float act = round_bf16(gelu_tanh_f32(gate));
-            const float h = act * round_bf16(up);
-            a.out[(int64_t)(seg0 + i) * a.I + n0 + pos] = f32_to_bf16_bits(h);
-          }
-        }
+  const Off first = off_of(begin);
+  if (!LONGK) load_batch(first, tile0);
+  for (int mc = 0; mc < rows; mc += rb) {
+    const int nr = min(rb, rows - mc);
+    const bool last_pass = __builtin_amdgcn_readfirstlane(mc + rb >= rows) != 0;
+    stage(mc, nr);
+    for (int ct = begin; ct < end; ++ct) {
+      bool col_ok;
+      weight_row(ct, &col_ok);
+      const int colblk = ct * CG + cg;
+      // the weights that follow this item's: the next item's, or -- after
+      // the last item of a pass that is not the last -- the first item's
+      const Off nx = ct + 1 < end ? off_of(ct + 1) : first;
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+      if (!LONGK) {
+        mma_batch(tile0, acc, std::true_type{}, nx);
       } else {
-        const int n = blockIdx.x * 16 + j;
+        const Off cur = off_of(ct);
+        for (int tb = tile0; tb < ntiles; tb += KSPLIT * TPW) {
+          load_batch(cur, tb);
+          mma_batch(tb, acc, std::false_type{}, nx);
+        }
+      }
+      (void)last_pass;
+      // split-K reduction over the KSPLIT wavefronts of this column group
+      f32x4_t v = acc;
+      bool owner = true;
+      if (KSPLIT > 1) {
+        red[wave][lane] = acc;
+        __syncthreads();
+        owner = ks == 0;
+        if (owner) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int i = ibase + r;
-          if (col_ok && i < rows) {
-            const int64_t orow = a.sorted_pos[seg0 + i];
-            a.out[orow * a.N + n] = f32_to_bf16_bits(v[r]);
+          for (int w = 1; w < KSPLIT; ++w) {
+            const f32x4_t o = red[wave + w][lane];
+            v[0] += o[0]; v[1] += o[1]; v[2] += o[2]; v[3] += o[3];
           }
         }
       }
+      if (owner) {
+        // output row 4*kb + q of the MFMA tile is staged row 4*kb + q of this
+        // pass; only the pass's nr rows exist
+        const int ibase = mc + 4 * kb;
+        const int iend = mc + nr;
+        if (MODE == kModeDense) {
+          const int n = colblk * 16 + j;
+          const float bb = (a.bias != nullptr && col_ok) ? bf16_bits_to_f32(a.bias[n]) : 0.f;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int i = ibase + q;
+            if (col_ok && i < iend) a.out[(int64_t)i * a.N + n] = f32_to_bf16_bits(v[q] + bb);
+          }
+        } else if (MODE == kModeGateUp) {
+          // lane j (< 8) holds gate column n0+j, lane j+8 the matching up column
+          const int n0 = colblk * 8;
+          const int pos = BIAS ? ((j & 3) * 2 + ((j >> 2) & 1)) : j;  // bias-order slot
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float up = __shfl_xor(v[q], 8);
+            const int i = ibase + q;
+            if (j < 8 && i < iend && col_ok) {
+              const float gate = round_bf16(v[q]);
+              const float act = round_bf16(gelu_tanh_f32(gate));
+              const float h = act * round_bf16(up);
+              a.out[(int64_t)(seg0 + i) * a.I + n0 + pos] = f32_to_bf16_bits(h);
+            }
+          }
+        } else {
+          const int n = colblk * 16 + j;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int i = ibase + q;
+            if (col_ok && i < iend) {
+              const int64_t orow = a.sorted_pos[seg0 + i];
+              a.out[orow * a.N + n] = f32_to_bf16_bits(v[q]);
+            }
+          }
+        }
+      }
+      if (KSPLIT > 1) __syncthreads();  // red is reused by the next item
     }
-    __syncthreads();
   }
 }
 
-hipError_t launch_decode(int mode, bool bias_form, const DecodeArgs& a, int grid_x, int grid_y,
-                         hipStream_t s) {
-  if (grid_x <= 0 || grid_y <= 0) return hipSuccess;
-  dim3 grid(grid_x, grid_y), block(256);
-#define W4A16_LAUNCH(M_, B_) hipLaunchKernelGGL((k_decode<M_, B_>), grid, block, 0, s, a)
-  if (mode == kModeDense) {
-    if (bias_form) W4A16_LAUNCH(kModeDense, true); else W4A16_LAUNCH(kModeDense, false);
-  } else if (mode == kModeGateUp) {
-    if (bias_form) W4A16_LAUNCH(kModeGateUp, true); else W4A16_LAUNCH(kModeGateUp, false);
-  } else {
-    if (bias_form) W4A16_LAUNCH(kModeDown, true); else W4A16_LAUNCH(kModeDown, false);
+// Decode launch shapes: (k tiles per wavefront, wavefronts per K range).
+struct DecodeShape {
+  int tpw;
+  int ksplit;
+};
+
+static DecodeShape decode_shape(int K) {
+  const int ntiles = ((K >> 5) + 3) >> 2;
+  if (ntiles <= 2) return {2, 1};
+  if (ntiles <= 4) return {4, 1};
+  if (ntiles <= 6) return {6, 1};   // down, K = 704: 6 tiles, 4 column groups
+  if (ntiles <= 8) return {2, 4};
+  if (ntiles <= 16) return {4, 4};
+  return {6, 4};                    // gate_up, K = 2816: 22 tiles over 4 wavefronts
+}
+
+// activation rows staged per LDS pass: the largest power of two <= 16 whose
+// fragment-layout footprint fits 48 KB of LDS
+static int stage_rows(int K) {
+  const int ntiles = ((K >> 5) + 3) >> 2;
+  const int bytes_per_row = ntiles * 16 * 16;  // fragment layout pads the last tile
+  int rb = 16;
+  while (rb > 1 && rb * bytes_per_row > 49152) rb >>= 1;
+  return rb;
+}
+
+static int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
   }
-#undef W4A16_LAUNCH
+  return cached[dev];
+}
+
+// LDS bytes of one workgroup: activation fragments + per (tile, row)
+// corrections (16 rows: rows past the staged ones are read for discarded
+// outputs).
+static size_t stream_lds(const DecodeArgs& a) {
+  const int ntiles = ((a.K >> 5) + 3) >> 2;
+  return (size_t)ntiles * 16 * a.rb * 16 + (size_t)ntiles * 16 * 4;
+}
+
+template <int MODE, bool BIAS, int TPW, int KSPLIT, bool LONGK>
+static hipError_t launch_stream(DecodeArgs a, int max_slots, hipStream_t s) {
+  auto kern = k_decode<MODE, BIAS, TPW, KSPLIT, LONGK>;
+  // workgroups per expert: fill the chip with the workgroups that fit at
+  // once, spread over the experts that can be active, at most one per item
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kStreamThreads, stream_lds(a)) !=
+          hipSuccess || per_cu <= 0)
+    per_cu = 1;
+  const int64_t resident = (int64_t)device_cus() * per_cu;
+  int64_t wps = (resident + max_slots - 1) / max_slots;
+  if (wps > a.n_ct) wps = a.n_ct;
+  if (wps < 1) wps = 1;
+  a.wg_per_slot = (int)wps;
+  const int64_t grid = (int64_t)max_slots * wps;
+  if (grid <= 0) return hipSuccess;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kStreamThreads), stream_lds(a), s, a);
   return hipGetLastError();
+}
+
+template <int MODE, bool BIAS>
+static hipError_t launch_decode_mode(DecodeArgs a, int max_slots, hipStream_t s) {
+  const DecodeShape sh = decode_shape(a.K);
+  const int cg = 4 / sh.ksplit;
+  const int ncolblk = MODE == kModeGateUp ? a.I / 8 : (a.N + 15) / 16;
+  a.n_ct = (ncolblk + cg - 1) / cg;
+  // rows staged per pass: enough for the rows an expert can have (at most
+  // the row count of the batch), capped by the LDS budget
+  a.rb = stage_rows(a.K);
+  int rows_cap = 1;
+  while (rows_cap < a.rows_hint && rows_cap < 16) rows_cap <<= 1;
+  if (a.rb > rows_cap) a.rb = rows_cap;
+  const int ntiles = ((a.K >> 5) + 3) >> 2;
+#define W4A16_DEC(T_, K_) return launch_stream<MODE, BIAS, T_, K_, false>(a, max_slots, s)
+  if (ntiles > 24) return launch_stream<MODE, BIAS, 6, 4, true>(a, max_slots, s);
+  if (sh.ksplit == 1) {
+    if (sh.tpw == 2) W4A16_DEC(2, 1);
+    if (sh.tpw == 4) W4A16_DEC(4, 1);
+    W4A16_DEC(6, 1);
+  }
+  if (sh.tpw == 2) W4A16_DEC(2, 4);
+  if (sh.tpw == 4) W4A16_DEC(4, 4);
+  W4A16_DEC(6, 4);
+#undef W4A16_DEC
+}
+
+hipError_t launch_decode(int mode, bool bias_form, DecodeArgs a, int max_slots, hipStream_t s) {
+  if (max_slots <= 0) return hipSuccess;
+  if (mode == kModeDense)
+    return bias_form ? launch_decode_mode<kModeDense, true>(a, max_slots, s)
+                     : launch_decode_mode<kModeDense, false>(a, max_slots, s);
+  if (mode == kModeGateUp)
+    return bias_form ? launch_decode_mode<kModeGateUp, true>(a, max_slots, s)
+                     : launch_decode_mode<kModeGateUp, false>(a, max_slots, s);
+  return bias_form ? launch_decode_mode<kModeDown, true>(a, max_slots, s)
+                   : launch_decode_mode<kModeDown, false>(a, max_slots, s);
 }
 
 // ---------------------------------------------------------------------------

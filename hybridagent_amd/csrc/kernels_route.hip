@@ -9,7 +9,8 @@
 //   k_moe_sort       stable counting sort of the k-major flattening of
 //                    top_k_index by expert -> per-expert segments in the
 //                    reference's visiting order (quantization.py:266-276),
-//                    plus the active-expert list and the prefill tile list.
+//                    plus one work descriptor per active expert and the
+//                    prefill tile list.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -121,6 +122,7 @@ hipError_t launch_router_logits(const uint16_t* r, const uint16_t* proj, float* 
 // softmax / top-k / renormalise: one wavefront per token, E <= 512
 // ---------------------------------------------------------------------------
 constexpr int kTopkPerLane = kMaxExperts / 64;
+constexpr int kRouterMaxSplit = 8;
 
 __global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ partial, int ksplit,
                                                      const uint16_t* __restrict__ logits_in,
@@ -140,8 +142,14 @@ __global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ p
     float v = -INFINITY;
     if (q < per && e < E) {
       if (partial != nullptr) {
+        // all K-split partials in flight at once, summed in split order
+        float pv[kRouterMaxSplit];
+#pragma unroll
+        for (int ks = 0; ks < kRouterMaxSplit; ++ks)
+          pv[ks] = ks < ksplit ? partial[((int64_t)ks * M + m) * E + e] : 0.f;
         float s = 0.f;
-        for (int ks = 0; ks < ksplit; ++ks) s += partial[((int64_t)ks * M + m) * E + e];
+#pragma unroll
+        for (int ks = 0; ks < kRouterMaxSplit; ++ks) s += pv[ks];
         const uint16_t b = f32_to_bf16_bits(s);
         if (logits_out != nullptr) logits_out[m * E + e] = b;
         v = bf16_bits_to_f32(b);
@@ -214,6 +222,7 @@ hipError_t launch_router_topk(const float* partial, int ksplit, const uint16_t* 
                               const uint16_t* per_expert_scale, uint16_t* logits_out,
                               int64_t* idx, float* w, int M, int E, int topk, hipStream_t s) {
   if (M == 0) return hipSuccess;
+  if (ksplit > kRouterMaxSplit) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_router_topk, dim3((M + 3) / 4), dim3(256), 0, s, partial, ksplit,
                      logits_in, per_expert_scale, logits_out, idx, w, M, E, topk);
   return hipGetLastError();
@@ -221,6 +230,8 @@ hipError_t launch_router_topk(const float* partial, int ksplit, const uint16_t* 
 
 // ---------------------------------------------------------------------------
 // expert sort: one workgroup of 1024 threads
+//   desc[4*u .. 4*u+3] = (expert, segment start, segment rows, 0) for the u-th
+//     active expert in ascending expert order
 //   counters[0] = number of active experts, counters[1] = number of prefill tiles
 //   tiles[i] = (expert << 16) | m_tile for the i-th (expert, m-tile) pair
 // ---------------------------------------------------------------------------
@@ -250,7 +261,7 @@ __global__ __launch_bounds__(kSortThreads) void k_moe_sort(const int64_t* __rest
                                                           int topk, int E,
                                                           int32_t* __restrict__ sorted_pos,
                                                           int32_t* __restrict__ offsets,
-                                                          int32_t* __restrict__ active,
+                                                          int32_t* __restrict__ desc,
                                                           int32_t* __restrict__ counters,
                                                           int32_t* __restrict__ tiles, int BM) {
   __shared__ int cnt[kMaxExperts];
@@ -282,7 +293,10 @@ __global__ __launch_bounds__(kSortThreads) void k_moe_sort(const int64_t* __rest
   if (tid == 0) offsets[E] = tot;
   int nact;
   const int apos = block_excl_scan(c > 0 ? 1 : 0, wsum, &nact);
-  if (tid < E && c > 0) active[apos] = tid;
+  if (tid < E && c > 0) {
+    const int4 d = make_int4(tid, off, c, 0);
+    *reinterpret_cast<int4*>(desc + 4 * apos) = d;
+  }
   const int nt = (c + BM - 1) / BM;
   int ntiles;
   const int tpos = block_excl_scan(nt, wsum, &ntiles);
@@ -336,10 +350,10 @@ __global__ __launch_bounds__(kSortThreads) void k_moe_sort(const int64_t* __rest
 }
 
 hipError_t launch_sort(const int64_t* idx, int M, int topk, int E, int32_t* sorted_pos,
-                       int32_t* offsets, int32_t* active, int32_t* counters, int32_t* tiles,
+                       int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
                        int BM, hipStream_t s) {
   hipLaunchKernelGGL(k_moe_sort, dim3(1), dim3(kSortThreads), 0, s, idx, M, topk, E, sorted_pos,
-                     offsets, active, counters, tiles, BM);
+                     offsets, desc, counters, tiles, BM);
   return hipGetLastError();
 }
 

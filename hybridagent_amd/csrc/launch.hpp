@@ -21,8 +21,7 @@ struct DecodeArgs {
   const uint16_t* bias;       // dense only, nullable, [N]
   uint16_t* out;              // output rows
   const int32_t* sorted_pos;  // MoE: [M*k] rows t*k+j in expert-segment order
-  const int32_t* offsets;     // MoE: [E+1]
-  const int32_t* active;      // MoE: active expert ids, ascending
+  const int32_t* desc;        // MoE: [E][4] (expert, segment start, rows, 0) per active slot
   const int32_t* n_active;    // MoE: [1]
   int M;     // dense: activation rows
   int N;     // weight rows per expert
@@ -31,6 +30,10 @@ struct DecodeArgs {
   int ng;    // ceil(K / G)
   int topk;  // MoE k
   int I;     // gate_up: intermediate size (N / 2)
+  int rb;    // activation rows staged in LDS per pass (<= 16)
+  int n_ct;  // work items (column tiles) per expert
+  int rows_hint;    // most activation rows one expert can have (set by the caller)
+  int wg_per_slot;  // workgroups sharing one expert's items (set by the launcher)
 };
 
 enum DecodeMode { kModeDense = 0, kModeGateUp = 1, kModeDown = 2 };
@@ -38,12 +41,12 @@ enum DecodeMode { kModeDense = 0, kModeGateUp = 1, kModeDown = 2 };
 hipError_t launch_dequant(const int32_t* packed, const uint16_t* scale, uint16_t* out,
                           int64_t rows, int K, int G, hipStream_t s);
 hipError_t launch_bias_order(const uint16_t* x, uint16_t* xp, int64_t rows, int K, hipStream_t s);
-hipError_t launch_decode(int mode, bool bias_form, const DecodeArgs& a, int grid_x, int grid_y,
-                         hipStream_t s);
+// max_slots: upper bound of active experts (1 for dense)
+hipError_t launch_decode(int mode, bool bias_form, DecodeArgs a, int max_slots, hipStream_t s);
 hipError_t launch_combine(const uint16_t* dn, const int64_t* idx, const float* w, uint16_t* out,
                           int M, int topk, int E, int H, hipStream_t s);
 hipError_t launch_sort(const int64_t* idx, int M, int topk, int E, int32_t* sorted_pos,
-                       int32_t* offsets, int32_t* active, int32_t* counters, int32_t* tiles,
+                       int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
                        int BM, hipStream_t s);
 hipError_t launch_router_norm(const uint16_t* h, const uint16_t* scale, float scalar_root,
                               float eps, uint16_t* r, int M, int H, hipStream_t s);
