@@ -70,10 +70,12 @@ class Layer:
         return _lib.router_topk(x, rw.scale, rw.scalar_root, rw.proj, rw.per_expert_scale, rw.eps, TOPK)
 
     def forward(self, x):
-        w, idx = self.route(x)
-        ew = self.ew
-        return _lib.moe_forward(x, idx, w, ew.gate_up_packed, ew.gate_up_scale, ew.down_packed,
-                                ew.down_scale, group_size=G)
+        """Router + experts (the MoE half of backends.py:111-122) through one C-ABI call."""
+        rw, ew = self.rw, self.ew
+        out, _, _ = _lib.moe_layer_forward(x, rw.scale, rw.scalar_root, rw.proj, rw.per_expert_scale,
+                                           rw.eps, TOPK, x, ew.gate_up_packed, ew.gate_up_scale,
+                                           ew.down_packed, ew.down_scale, group_size=G)
+        return out
 
 
 def time_graph(fn, calls_per_replay: int, steps: int, warmup: int) -> float:

@@ -43,6 +43,9 @@ SIGNATURES = {
     "moe_gate_up": (ctypes.c_int, [_VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "moe_down": (ctypes.c_int, [_VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "moe_combine": (ctypes.c_int, [_VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
+    "moe_layer_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
+    "moe_layer_forward": (ctypes.c_int, [_VP, _VP, _F32, _VP, _VP, _F32, _VP, _VP, _VP, _VP, _VP, _VP,
+                                         _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
 }
 
 _lib = None
@@ -293,6 +296,47 @@ def moe_forward(hidden_states: torch.Tensor, top_k_index: torch.Tensor, top_k_we
                                0 if ws is None else ws.numel(), _stream(dev)),
                "moe_forward")
     return out.reshape(*hidden_states.shape[:-1], H)
+
+
+def moe_layer_forward(router_in: torch.Tensor, router_scale: torch.Tensor, scalar_root: float,
+                      proj_w: torch.Tensor, per_expert_scale: torch.Tensor, eps: float, top_k: int,
+                      hidden_states: torch.Tensor, gu_packed: torch.Tensor, gu_scale: torch.Tensor,
+                      dn_packed: torch.Tensor, dn_scale: torch.Tensor, group_size: int | None = None):
+    """Router (backends.py:111-117) on ``router_in`` + experts (quantization.py:88-129) on
+    ``hidden_states`` in one call -> (out [T, H] bf16, top_k_weights fp32, top_k_index int64)."""
+    dev = _require_gpu(router_in, router_scale, proj_w, per_expert_scale, hidden_states, gu_packed,
+                       gu_scale, dn_packed, dn_scale)
+    H = hidden_states.shape[-1]
+    r2 = _bf16(router_in, "router_in").reshape(-1, H)
+    x = _bf16(hidden_states, "hidden_states").reshape(-1, H)
+    if r2.shape != x.shape:
+        raise ValueError("router input and expert input must have the same shape")
+    router_scale = _bf16(router_scale, "router scale")
+    proj_w = _bf16(proj_w, "router proj weight")
+    per_expert_scale = _bf16(per_expert_scale, "per_expert_scale")
+    gu_packed, dn_packed = _i32(gu_packed, "gate_up_packed"), _i32(dn_packed, "down_packed")
+    gu_scale, dn_scale = _bf16(gu_scale, "gate_up_scale"), _bf16(dn_scale, "down_scale")
+    E, two_i, h8 = gu_packed.shape
+    I = two_i // 2
+    if h8 * 8 != H or dn_packed.shape != (E, H, I // 8) or proj_w.shape != (E, H):
+        raise ValueError("router / expert weight shapes do not match the hidden size")
+    G = group_size or infer_group_size(H, gu_scale.shape[-1])
+    if gu_scale.shape != (E, two_i, -(-H // G)) or dn_scale.shape != (E, H, -(-I // G)):
+        raise ValueError(f"scale shapes do not match group size {G}")
+    M = x.shape[0]
+    out = torch.empty((M, H), dtype=torch.bfloat16, device=dev)
+    idx = torch.empty((M, top_k), dtype=torch.int64, device=dev)
+    w = torch.empty((M, top_k), dtype=torch.float32, device=dev)
+    lib = load()
+    ws = _workspace(lib.moe_layer_workspace_bytes(max(M, 1), top_k, E, H, I), dev)
+    with torch.cuda.device(dev):
+        _check(lib.moe_layer_forward(_ptr(r2), _ptr(router_scale), float(scalar_root), _ptr(proj_w),
+                                     _ptr(per_expert_scale), float(eps), _ptr(x), _ptr(gu_packed),
+                                     _ptr(gu_scale), _ptr(dn_packed), _ptr(dn_scale), _ptr(out), _ptr(idx),
+                                     _ptr(w), M, top_k, E, H, I, G, _ptr(ws),
+                                     0 if ws is None else ws.numel(), _stream(dev)),
+               "moe_layer_forward")
+    return out.reshape(*hidden_states.shape[:-1], H), w, idx
 
 
 class MoEStages:

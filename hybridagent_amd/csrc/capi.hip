@@ -40,6 +40,18 @@ constexpr int64_t kDecodeMaxM = 1 << 30;
 // longest reduction the streaming kernels stage in LDS (one row per pass)
 constexpr int64_t kMaxStreamK = 49152 / 2;
 
+// Router partial logits: a normalisation pass into r, then the K-split
+// MFMA logits.  (Normalising inside the logits kernel was measured slower:
+// every wavefront then re-reads whole rows.)
+hipError_t launch_router_partials(const uint16_t* hidden, const uint16_t* scale, float root,
+                                  float eps, const uint16_t* proj, uint16_t* r, float* partial,
+                                  int64_t M, int64_t H, int64_t E, hipStream_t s) {
+  const int ks = router_ksplit(M);
+  hipError_t e = launch_router_norm(hidden, scale, root, eps, r, (int)M, (int)H, s);
+  if (e == hipSuccess) e = launch_router_logits(r, proj, partial, (int)M, (int)H, (int)E, ks, s);
+  return e;
+}
+
 // One shared description of the MoE workspace so sizing and carving agree.
 struct MoeLayout {
   int32_t* offsets;
@@ -151,7 +163,7 @@ int moe_router_topk(const uint16_t* hidden, const uint16_t* router_scale, float 
   if (M == 0) return W4A16_OK;
   if (!hidden || !router_scale || !proj_w || !per_expert_scale || !topk_idx || !topk_w)
     return W4A16_ERR_NULL;
-  if (!aligned16(hidden) || !aligned16(proj_w)) return W4A16_ERR_ALIGN;
+  if (!aligned16(hidden) || !aligned16(proj_w) || !aligned16(router_scale)) return W4A16_ERR_ALIGN;
   const size_t need = moe_router_workspace_bytes(M, H, E);
   if (workspace == nullptr || workspace_bytes < need) return W4A16_ERR_WORKSPACE;
   if (!aligned16(workspace)) return W4A16_ERR_ALIGN;
@@ -160,8 +172,8 @@ int moe_router_topk(const uint16_t* hidden, const uint16_t* router_scale, float 
   uint16_t* r = c.take<uint16_t>(M * H);
   const int ks = router_ksplit(M);
   float* partial = c.take<float>(size_t(ks) * M * E);
-  hipError_t e = launch_router_norm(hidden, router_scale, scalar_root, eps, r, (int)M, (int)H, s);
-  if (e == hipSuccess) e = launch_router_logits(r, proj_w, partial, (int)M, (int)H, (int)E, ks, s);
+  hipError_t e = launch_router_partials(hidden, router_scale, scalar_root, eps, proj_w, r, partial,
+                                        M, H, E, s);
   if (e == hipSuccess)
     e = launch_router_topk(partial, ks, nullptr, per_expert_scale, logits_out, topk_idx, topk_w,
                            (int)M, (int)E, (int)top_k, s);
@@ -340,6 +352,57 @@ int moe_forward(const uint16_t* hidden, const int64_t* topk_idx, const float* to
   if (st == W4A16_OK)
     st = moe_combine(topk_idx, topk_w, out, M, top_k, E, H, I, workspace, workspace_bytes,
                      stream);
+  return st;
+}
+
+size_t moe_layer_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I) {
+  if (M <= 0 || top_k <= 0 || E <= 0 || H <= 0 || I <= 0) return 0;
+  return moe_layout(nullptr, M, top_k, E, H, I).bytes + moe_router_workspace_bytes(M, H, E);
+}
+
+int moe_layer_forward(const uint16_t* router_in, const uint16_t* router_scale, float scalar_root,
+                      const uint16_t* proj_w, const uint16_t* per_expert_scale, float eps,
+                      const uint16_t* hidden, const int32_t* gu_packed, const uint16_t* gu_scale,
+                      const int32_t* dn_packed, const uint16_t* dn_scale, uint16_t* out,
+                      int64_t* topk_idx, float* topk_w, int64_t M, int64_t top_k, int64_t E,
+                      int64_t H, int64_t I, int64_t group_size, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+  if (M < 0 || M > (1 << 24) || top_k > E) return W4A16_ERR_SHAPE;
+  if (M == 0) {
+    MoeLayout dummy{};
+    return moe_check(0, top_k, E, H, I, group_size, nullptr, 0, &dummy);
+  }
+  if (workspace == nullptr || workspace_bytes < moe_layer_workspace_bytes(M, top_k, E, H, I))
+    return W4A16_ERR_WORKSPACE;
+  const size_t moe_bytes = moe_layout(nullptr, M, top_k, E, H, I).bytes;
+  MoeLayout L{};
+  int st = moe_check(M, top_k, E, H, I, group_size, workspace, moe_bytes, &L);
+  if (st != W4A16_OK) return st;
+  if (!router_in || !router_scale || !proj_w || !per_expert_scale || !hidden || !gu_packed ||
+      !gu_scale || !dn_packed || !dn_scale || !out || !topk_idx || !topk_w)
+    return W4A16_ERR_NULL;
+  if (!aligned16(router_in) || !aligned16(proj_w) || !aligned16(router_scale) || !aligned16(hidden) ||
+      !aligned16(gu_packed) || !aligned16(dn_packed) || !aligned16(out))
+    return W4A16_ERR_ALIGN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Carve c(static_cast<char*>(workspace) + moe_bytes);
+  uint16_t* r = c.take<uint16_t>(M * H);
+  float* partial = c.take<float>(size_t(router_ksplit(M)) * M * E);
+  hipError_t e = launch_router_partials(router_in, router_scale, scalar_root, eps, proj_w, r,
+                                        partial, M, H, E, s);
+  if (e != hipSuccess) return W4A16_ERR_LAUNCH;
+  e = launch_router_topk(partial, router_ksplit(M), nullptr, per_expert_scale, nullptr, topk_idx,
+                         topk_w, (int)M, (int)E, (int)top_k, s);
+  if (e != hipSuccess) return W4A16_ERR_LAUNCH;
+  st = moe_plan(hidden, topk_idx, M, top_k, E, H, I, group_size, workspace, moe_bytes, stream);
+  if (st != W4A16_OK) return st;
+  st = moe_gate_up(hidden, gu_packed, gu_scale, M, top_k, E, H, I, group_size, workspace,
+                   moe_bytes, stream);
+  if (st == W4A16_OK)
+    st = moe_down(dn_packed, dn_scale, M, top_k, E, H, I, group_size, workspace, moe_bytes,
+                  stream);
+  if (st == W4A16_OK)
+    st = moe_combine(topk_idx, topk_w, out, M, top_k, E, H, I, workspace, moe_bytes, stream);
   return st;
 }
 

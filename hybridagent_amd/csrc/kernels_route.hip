@@ -124,16 +124,14 @@ hipError_t launch_router_logits(const uint16_t* r, const uint16_t* proj, float* 
 constexpr int kTopkPerLane = kMaxExperts / 64;
 constexpr int kRouterMaxSplit = 8;
 
-__global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ partial, int ksplit,
-                                                     const uint16_t* __restrict__ logits_in,
-                                                     const uint16_t* __restrict__ pes,
-                                                     uint16_t* __restrict__ logits_out,
-                                                     int64_t* __restrict__ idx_out,
-                                                     float* __restrict__ w_out, int M, int E,
-                                                     int topk) {
-  const int lane = threadIdx.x & 63;
-  const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (m >= M) return;  // uniform per wavefront
+// Routing of one token by one wavefront: bf16 logits (from K-split partials
+// or given), softmax denominator, top-k by (logit desc, index asc), weights.
+// Lane i < topk returns selection i in *sel_e / *sel_w.
+__device__ void route_token(const float* __restrict__ partial, int ksplit,
+                            const uint16_t* __restrict__ logits_in,
+                            const uint16_t* __restrict__ pes, uint16_t* __restrict__ logits_out,
+                            int64_t m, int M, int E, int topk, int lane, int* sel_e,
+                            float* sel_w) {
   float lg[kTopkPerLane];
   const int per = (E + 63) >> 6;
 #pragma unroll
@@ -212,9 +210,26 @@ __global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ p
     }
     psum += p;
   }
+  *sel_e = my_i;
+  *sel_w = (lane < topk) ? (my_p / psum) * bf16_bits_to_f32(pes[my_i]) : 0.f;
+}
+
+__global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ partial, int ksplit,
+                                                     const uint16_t* __restrict__ logits_in,
+                                                     const uint16_t* __restrict__ pes,
+                                                     uint16_t* __restrict__ logits_out,
+                                                     int64_t* __restrict__ idx_out,
+                                                     float* __restrict__ w_out, int M, int E,
+                                                     int topk) {
+  const int lane = threadIdx.x & 63;
+  const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= M) return;  // uniform per wavefront
+  int se;
+  float sw;
+  route_token(partial, ksplit, logits_in, pes, logits_out, m, M, E, topk, lane, &se, &sw);
   if (lane < topk) {
-    idx_out[m * topk + lane] = my_i;
-    w_out[m * topk + lane] = (my_p / psum) * bf16_bits_to_f32(pes[my_i]);
+    idx_out[m * topk + lane] = se;
+    w_out[m * topk + lane] = sw;
   }
 }
 
@@ -257,13 +272,10 @@ __device__ int block_excl_scan(int v, int* wsum, int* total) {
   return res;
 }
 
-__global__ __launch_bounds__(kSortThreads) void k_moe_sort(const int64_t* __restrict__ idx, int M,
-                                                          int topk, int E,
-                                                          int32_t* __restrict__ sorted_pos,
-                                                          int32_t* __restrict__ offsets,
-                                                          int32_t* __restrict__ desc,
-                                                          int32_t* __restrict__ counters,
-                                                          int32_t* __restrict__ tiles, int BM) {
+__global__ __launch_bounds__(kSortThreads) void k_moe_sort(
+    const int64_t* __restrict__ idx_in, int M, int topk, int E, int32_t* __restrict__ sorted_pos,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ desc, int32_t* __restrict__ counters,
+    int32_t* __restrict__ tiles, int BM) {
   __shared__ int cnt[kMaxExperts];
   __shared__ int run[kMaxExperts];
   __shared__ int wcnt[kSortWaves][kMaxExperts];
@@ -271,18 +283,20 @@ __global__ __launch_bounds__(kSortThreads) void k_moe_sort(const int64_t* __rest
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int total = M * topk;
 
+  auto expert_of = [&](int row) -> int64_t { return idx_in[row]; };
+
   for (int e = tid; e < E; e += kSortThreads) {
     cnt[e] = 0;
     for (int w = 0; w < kSortWaves; ++w) wcnt[w][e] = 0;
   }
   __syncthreads();
   for (int p = tid; p < total; p += kSortThreads) {
-    const int64_t e = idx[p];
+    const int64_t e = expert_of(p);
     if (e >= 0 && e < E) atomicAdd(&cnt[(int)e], 1);
   }
   __syncthreads();
 
-  // offsets, active list and tile list (E <= 512 < 1024 threads)
+  // offsets, work descriptors and tile list (E <= 512 < 1024 threads)
   const int c = tid < E ? cnt[tid] : 0;
   int tot;
   const int off = block_excl_scan(c, wsum, &tot);
@@ -318,7 +332,7 @@ __global__ __launch_bounds__(kSortThreads) void k_moe_sort(const int64_t* __rest
     if (p < total) {
       const int jj = p / M, t = p - jj * M;
       row = t * topk + jj;
-      const int64_t ev = idx[row];
+      const int64_t ev = expert_of(row);
       if (ev >= 0 && ev < E) e = (int)ev;
     }
     const bool ok = e >= 0;
@@ -338,12 +352,12 @@ __global__ __launch_bounds__(kSortThreads) void k_moe_sort(const int64_t* __rest
     }
     __syncthreads();
     for (int ee = tid; ee < E; ee += kSortThreads) {
-      int s = 0;
+      int s2 = 0;
       for (int w = 0; w < kSortWaves; ++w) {
-        s += wcnt[w][ee];
+        s2 += wcnt[w][ee];
         wcnt[w][ee] = 0;
       }
-      run[ee] += s;
+      run[ee] += s2;
     }
     __syncthreads();
   }

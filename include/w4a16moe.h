@@ -145,6 +145,20 @@ W4A16_API int moe_combine(const int64_t* topk_idx, const float* topk_w, uint16_t
                 int64_t top_k, int64_t E, int64_t H, int64_t I, void* workspace,
                 size_t workspace_bytes, void* stream);
 
+/* Router + experts in one call: the MoE half of _ffn_moe_4bit_step
+ *   -- backends.py:111-122
+ * router_in [M, H] feeds the router (moe_router_topk semantics), hidden
+ * [M, H] feeds the experts (moe_forward semantics); they may alias.  Writes
+ * out [M, H] and the routing topk_idx [M, top_k] / topk_w [M, top_k].     */
+W4A16_API size_t moe_layer_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I);
+W4A16_API int moe_layer_forward(const uint16_t* router_in, const uint16_t* router_scale, float scalar_root,
+                      const uint16_t* proj_w, const uint16_t* per_expert_scale, float eps,
+                      const uint16_t* hidden, const int32_t* gu_packed, const uint16_t* gu_scale,
+                      const int32_t* dn_packed, const uint16_t* dn_scale, uint16_t* out,
+                      int64_t* topk_idx, float* topk_w, int64_t M, int64_t top_k, int64_t E,
+                      int64_t H, int64_t I, int64_t group_size, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

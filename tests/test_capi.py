@@ -56,9 +56,10 @@ def test_linear_host_validation(lib):
     assert lib.w4a16_linear(NULL, fake, fake, NULL, fake, 4, 16, 64, 32, NULL, 0, NULL) == 1
     # misaligned activation pointer
     assert lib.w4a16_linear(ctypes.c_void_p(4098), fake, fake, NULL, fake, 4, 16, 64, 32, NULL, 0, NULL) == 4
-    # bias-form (G % 128 == 0) needs a workspace
-    assert lib.w4a16_linear_workspace_bytes(4, 256, 128) >= 4 * 256 * 2
-    assert lib.w4a16_linear(fake, fake, fake, NULL, fake, 4, 16, 256, 128, NULL, 0, NULL) == 5
+    # the dense path needs no scratch memory
+    assert lib.w4a16_linear_workspace_bytes(4, 256, 128) == 0
+    # K beyond what one LDS pass stages
+    assert lib.w4a16_linear(fake, fake, fake, NULL, fake, 4, 16, 32768, 128, NULL, 0, NULL) == 2
     # M == 0 is a no-op
     assert lib.w4a16_linear(NULL, NULL, NULL, NULL, NULL, 0, 16, 64, 32, NULL, 0, NULL) == 0
 
@@ -87,6 +88,13 @@ def test_moe_host_validation(lib):
                                fake, 1 << 20, NULL) == 2
     assert lib.moe_topk_from_logits(fake, fake, 4, 128, 0, fake, fake, NULL) == 2
     assert lib.moe_sort_permute(fake, 4, 8, 128, fake, fake, NULL, 0, NULL) == 5
+    # fused layer: workspace too small, then a misaligned router scale
+    lw = lib.moe_layer_workspace_bytes(8, 8, 128, 2816, 704)
+    assert lw > ws_need
+    largs = [fake, fake, 0.1, fake, fake, 1e-6, fake, fake, fake, fake, fake, fake, fake, fake]
+    assert lib.moe_layer_forward(*largs, 8, 8, 128, 2816, 704, 128, fake, lw - 1, NULL) == 5
+    largs[1] = ctypes.c_void_p(4098)
+    assert lib.moe_layer_forward(*largs, 8, 8, 128, 2816, 704, 128, fake, lw, NULL) == 4
 
 
 def test_dequant_host_validation(lib):
