@@ -36,7 +36,7 @@ inline int router_ksplit(int64_t M) { return M <= 64 ? 8 : 1; }
 
 // Token counts up to this use the decode kernels; larger batches the
 // prefill grouped-GEMM kernels.
-constexpr int64_t kDecodeMaxM = 1 << 30;
+constexpr int64_t kDecodeMaxM = 256;
 // longest reduction the streaming kernels stage in LDS (one row per pass)
 constexpr int64_t kMaxStreamK = 49152 / 2;
 
@@ -242,7 +242,31 @@ int moe_check(int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t
   return W4A16_OK;
 }
 
-inline bool use_prefill(int64_t M) { return M > kDecodeMaxM; }
+// The prefill kernels stage K in 64-wide steps and tile N by 128 weight rows
+// (gate_up: 64 gate + 64 up rows); other shapes stay on the decode kernels.
+inline bool use_prefill(int64_t M, int64_t H, int64_t I) {
+  return M > kDecodeMaxM && H % 128 == 0 && I % 64 == 0;
+}
+
+PrefillArgs prefill_args(const MoeLayout& L, int64_t M, int64_t top_k, int64_t I, int64_t G) {
+  PrefillArgs a{};
+  a.sorted_pos = L.sorted_pos;
+  a.offsets = L.offsets;
+  a.tiles = L.tiles;
+  a.counters = L.counters;
+  a.topk = (int)top_k;
+  a.G = (int)G;
+  a.I = (int)I;
+  (void)M;
+  return a;
+}
+
+// most m-tiles the sort can emit: one partial tile per active expert plus
+// the full ones
+inline int max_mtiles(int64_t M, int64_t top_k, int64_t E) {
+  const int64_t rows = M * top_k;
+  return (int)(rows / kPrefillBM + (rows < E ? rows : E));
+}
 
 DecodeArgs expert_args(const MoeLayout& L, int64_t M, int64_t top_k, int64_t I, int64_t G) {
   DecodeArgs a{};
@@ -285,6 +309,18 @@ int moe_gate_up(const uint16_t* hidden, const int32_t* gu_packed, const uint16_t
   if (!hidden || !gu_packed || !gu_scale) return W4A16_ERR_NULL;
   if (!aligned16(hidden) || !aligned16(gu_packed)) return W4A16_ERR_ALIGN;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (use_prefill(M, H, I)) {
+    PrefillArgs p = prefill_args(L, M, top_k, I, group_size);
+    p.act = hidden;
+    p.wp = gu_packed;
+    p.ws = gu_scale;
+    p.out = L.inter;
+    p.N = (int)(2 * I);
+    p.K = (int)H;
+    p.ng = (int)((H + group_size - 1) / group_size);
+    p.n_nt = (int)(I / 64);
+    return launch_status(launch_prefill(kModeGateUp, p, max_mtiles(M, top_k, E), s));
+  }
   const int max_slots = (int)(M * top_k < E ? M * top_k : E);
   DecodeArgs a = expert_args(L, M, top_k, I, group_size);
   a.act = hidden;
@@ -306,6 +342,18 @@ int moe_down(const int32_t* dn_packed, const uint16_t* dn_scale, int64_t M, int6
   if (!dn_packed || !dn_scale) return W4A16_ERR_NULL;
   if (!aligned16(dn_packed)) return W4A16_ERR_ALIGN;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (use_prefill(M, H, I)) {
+    PrefillArgs p = prefill_args(L, M, top_k, I, group_size);
+    p.act = L.inter;
+    p.wp = dn_packed;
+    p.ws = dn_scale;
+    p.out = L.dn;
+    p.N = (int)H;
+    p.K = (int)I;
+    p.ng = (int)((I + group_size - 1) / group_size);
+    p.n_nt = (int)(H / kPfBN);
+    return launch_status(launch_prefill(kModeDown, p, max_mtiles(M, top_k, E), s));
+  }
   const int max_slots = (int)(M * top_k < E ? M * top_k : E);
   DecodeArgs a = expert_args(L, M, top_k, I, group_size);
   a.act = L.inter;

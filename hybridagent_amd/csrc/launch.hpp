@@ -10,8 +10,9 @@ namespace w4a16 {
 
 constexpr int kMaxExperts = 512;
 constexpr int kMaxTopK = 32;
-// m-tile (token rows) of the prefill grouped GEMM
+// m-tile (token rows) and n-tile (weight rows) of the prefill grouped GEMM
 constexpr int kPrefillBM = 128;
+constexpr int kPfBN = 128;
 
 // Arguments of the decode-shaped (few rows per weight matrix) MFMA kernel.
 struct DecodeArgs {
@@ -36,6 +37,20 @@ struct DecodeArgs {
   int wg_per_slot;  // workgroups sharing one expert's items (set by the launcher)
 };
 
+// Arguments of the prefill-shaped grouped GEMM (kernels_prefill.hip).
+struct PrefillArgs {
+  const uint16_t* act;        // gate_up: hidden [M, K]; down: inter [M*k, K] in segment order
+  const int32_t* wp;          // packed weights [E, N, K/8]
+  const uint16_t* ws;         // bf16 scales [E, N, ng]
+  uint16_t* out;              // gate_up: inter [M*k, I]; down: dn rows t*k+j [M*k, N]
+  const int32_t* sorted_pos;  // [M*k] rows t*k+j in expert-segment order
+  const int32_t* offsets;     // [E+1] segment starts
+  const int32_t* tiles;       // m-tiles (expert << 16 | tile index in the segment)
+  const int32_t* counters;    // [1] = number of m-tiles
+  int N, K, G, ng, topk, I;
+  int n_nt;                   // n-tiles per m-tile
+};
+
 enum DecodeMode { kModeDense = 0, kModeGateUp = 1, kModeDown = 2 };
 
 hipError_t launch_dequant(const int32_t* packed, const uint16_t* scale, uint16_t* out,
@@ -55,15 +70,7 @@ hipError_t launch_router_logits(const uint16_t* r, const uint16_t* proj, float* 
 hipError_t launch_router_topk(const float* partial, int ksplit, const uint16_t* logits_in,
                               const uint16_t* per_expert_scale, uint16_t* logits_out,
                               int64_t* idx, float* w, int M, int E, int topk, hipStream_t s);
-hipError_t launch_prefill_gateup(const uint16_t* x, const int32_t* sorted_pos,
-                                 const int32_t* offsets, const int32_t* tiles,
-                                 const int32_t* counters, const int32_t* gu_packed,
-                                 const uint16_t* gu_scale, uint16_t* inter, int max_tiles,
-                                 int topk, int H, int I, int G, hipStream_t s);
-hipError_t launch_prefill_down(const uint16_t* inter, const int32_t* sorted_pos,
-                               const int32_t* offsets, const int32_t* tiles,
-                               const int32_t* counters, const int32_t* dn_packed,
-                               const uint16_t* dn_scale, uint16_t* dn, int max_tiles, int topk,
-                               int H, int I, int G, hipStream_t s);
+// prefill grouped GEMM: one launch per stage, items = (m-tile, n-tile)
+hipError_t launch_prefill(int mode, PrefillArgs a, int max_mtiles, hipStream_t s);
 
 }  // namespace w4a16

@@ -280,3 +280,105 @@ def test_layer_forward_router_plus_experts(dev, moe128, M):
     rows = np.arange(0, M, max(1, M // 16))
     ref = _moe_ref(x, idx.cpu(), w.cpu(), cpu, 128, rows=rows)
     assert oracle.max_abs_rel(_np(y)[rows], ref) <= TOL
+
+
+# ------------------------------------------------------ prefill grouped GEMM
+# Batches above the decode threshold run the LDS-tiled grouped GEMM.
+
+def _skewed_route(M, seed, hot=8):
+    # every token routed to the same `hot` experts (in a per-token order):
+    # segments of M rows, i.e. several m-tiles per expert plus a partial one
+    g = torch.Generator().manual_seed(seed)
+    hot_ids = torch.randperm(E, generator=g)[:hot]
+    idx = torch.stack([hot_ids[torch.randperm(hot, generator=g)][:K_TOP] for _ in range(M)])
+    w = torch.rand(M, K_TOP, generator=g) + 0.05
+    return idx, (w / w.sum(1, keepdim=True)).float()
+
+
+@pytest.mark.parametrize("M", [257, 300])
+def test_moe_prefill_skewed_segments(dev, moe128, M):
+    cpu, gpu = moe128
+    x = synth.activations(M, H, seed=700 + M)
+    idx, w = _skewed_route(M, seed=710 + M)
+    y = _moe_gpu(x, idx, w, gpu, dev)
+    rows = np.r_[0:4, M // 2, M - 3:M]
+    err = oracle.max_abs_rel(_np(y)[rows], _moe_ref(x, idx, w, cpu, 128, rows=rows))
+    print(f"moe prefill skewed M={M} max_abs_rel={err:.2e}")
+    assert err <= TOL
+
+
+def test_moe_prefill_invalid_slots(dev, moe128):
+    cpu, gpu = moe128
+    M = 400
+    x = synth.activations(M, H, seed=720)
+    idx, w = _route(M, seed=721)
+    idx_bad = idx.clone()
+    idx_bad[::3, 6:] = E
+    idx_bad[1::7, 0] = -1
+    w_cut = w.clone()
+    w_cut[::3, 6:] = 0.0
+    w_cut[1::7, 0] = 0.0
+    assert torch.equal(_moe_gpu(x, idx_bad, w, gpu, dev).cpu(), _moe_gpu(x, idx, w_cut, gpu, dev).cpu())
+
+
+@pytest.mark.parametrize("G", [32, 64, 128])
+def test_moe_prefill_groups(dev, G):
+    e, h, i, k = 16, 512, 192, 4
+    wts = synth.moe_weights(e, h, i, G, seed=730 + G)
+    M = 320
+    x = synth.activations(M, h, seed=731)
+    g = torch.Generator().manual_seed(732)
+    idx = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(M)])
+    w = torch.rand(M, k, generator=g).float()
+    y = _lib.moe_forward(x.to(dev), idx.to(dev), w.to(dev), wts.gate_up_packed.to(dev), wts.gate_up_scale.to(dev),
+                         wts.down_packed.to(dev), wts.down_scale.to(dev))
+    rows = np.arange(0, M, 11)
+    ref = oracle.moe_forward(_np(x)[rows], idx.numpy()[rows], w.numpy()[rows], wts.gate_up_packed.numpy(),
+                             _bits(wts.gate_up_scale), wts.down_packed.numpy(), _bits(wts.down_scale), G)
+    err = oracle.max_abs_rel(_np(y)[rows], ref)
+    print(f"moe prefill G={G} max_abs_rel={err:.2e}")
+    assert err <= TOL
+
+
+def test_moe_large_batch_untiled_shape(dev):
+    # H not a multiple of 128 / I not a multiple of 64: large batches stay on
+    # the streaming kernels and must still match
+    e, h, i, k, G = 8, 544, 160, 2, 32
+    wts = synth.moe_weights(e, h, i, G, seed=740)
+    M = 300
+    x = synth.activations(M, h, seed=741)
+    g = torch.Generator().manual_seed(742)
+    idx = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(M)])
+    w = torch.rand(M, k, generator=g).float()
+    y = _lib.moe_forward(x.to(dev), idx.to(dev), w.to(dev), wts.gate_up_packed.to(dev), wts.gate_up_scale.to(dev),
+                         wts.down_packed.to(dev), wts.down_scale.to(dev))
+    rows = np.arange(0, M, 13)
+    ref = oracle.moe_forward(_np(x)[rows], idx.numpy()[rows], w.numpy()[rows], wts.gate_up_packed.numpy(),
+                             _bits(wts.gate_up_scale), wts.down_packed.numpy(), _bits(wts.down_scale), G)
+    assert oracle.max_abs_rel(_np(y)[rows], ref) <= TOL
+
+
+def test_moe_prefill_config3_zipf(dev, moe128):
+    # M=4096 with Zipf routing, sampled rows against the
+    # oracle, plus two size-independent properties of the tiled GEMM:
+    #  * batch invariance: a token's output does not depend on which other
+    #    tokens share its tiles (same row in a different batch -> same bits);
+    #  * permutation equivariance: permuting tokens permutes the output.
+    cpu, gpu = moe128
+    M = 4096
+    x = synth.zipf_activations(M, H, seed=750)
+    rw = synth.zipf_router_weights(E, H, seed=751)
+    w_full, idx_full = _lib.router_topk(x.to(dev), rw.scale.to(dev), rw.scalar_root, rw.proj.to(dev),
+                                        rw.per_expert_scale.to(dev), rw.eps, K_TOP)
+    idx, w = idx_full.cpu(), w_full.cpu()
+    y = _moe_gpu(x, idx, w, gpu, dev).cpu()
+    rows = np.r_[0:3, 1000, 2047, 3333, M - 2:M]
+    err = oracle.max_abs_rel(_np(y)[rows], _moe_ref(x, idx, w, cpu, 128, rows=rows))
+    print(f"moe prefill config3 M={M} sampled max_abs_rel={err:.2e}")
+    assert err <= TOL
+    sub = torch.arange(0, M, 13)        # 316 tokens: still above the decode threshold
+    y_sub = _moe_gpu(x[sub], idx[sub], w[sub], gpu, dev).cpu()
+    assert torch.equal(y_sub, y[sub])
+    perm = torch.randperm(M, generator=torch.Generator().manual_seed(752))
+    y_perm = _moe_gpu(x[perm], idx[perm], w[perm], gpu, dev).cpu()
+    assert torch.equal(y_perm, y[perm])
