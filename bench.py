@@ -161,6 +161,53 @@ def prefill(dev, steps, warmup, n_layers):
     return res
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gateup_decode_M64_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the roofline kernel from the committed counter
+    summary (rocprofv3 FETCH_SIZE / WRITE_SIZE runs scaled by the plain-copy
+    calibration); None when no summary is present."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for ln in f:
+                if ln.startswith("traffic_bytes_per_launch:"):
+                    return int(ln.split(":", 1)[1].strip())
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def roofline(kern):
+    return {
+        "bound": "hbm",
+        "kernel": kern["kernel"],
+        "M": kern["M"],
+        "achieved": round(kern["gbps"], 2),
+        "peak": PEAK_HBM_GBS,
+        "unit": "GB/s",
+        "frac": round(kern["gbps"] / PEAK_HBM_GBS, 4),
+        "traffic": measured_traffic(),
+        "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT),
+        "us_per_launch": round(kern["us"], 3),
+        "algorithmic_bytes_per_launch": int(kern["bytes"]),
+    }
+
+
+def calibrate_copy(dev) -> int:
+    """A plain device-to-device copy of a known size: what FETCH_SIZE and
+    WRITE_SIZE read for it gives the counters' scale on this GPU."""
+    n = 256 << 20
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(8):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "device copy", "bytes_read": n, "bytes_written": n, "calls": 8}))
+    return 0
+
+
 def cpu_baseline(budget_s: float):
     """numpy oracle on this host's cores, bounded decode sample (M=32, one layer)."""
     import numpy as np
@@ -232,6 +279,12 @@ def main(argv=None):
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--only-roofline", action="store_true",
+                    help="time only the roofline kernel (for rocprofv3 counter runs)")
+    ap.add_argument("--only-prefill", action="store_true",
+                    help="time only the prefill layer (for rocprofv3 counter runs)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run a plain 256 MiB device copy 8 times (counter calibration) and exit")
     args = ap.parse_args(argv)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -243,12 +296,22 @@ def main(argv=None):
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
     dev = torch.device("cuda:0")
+    if args.calibrate_copy:
+        return calibrate_copy(dev)
     _lib.load()
     torch.manual_seed(0)
+    if args.only_prefill:
+        pre = prefill(dev, max(8, args.steps // 4), max(2, args.warmup // 4), min(args.layers, 4))
+        print(json.dumps({"prefill": pre}), flush=True)
+        return 0
 
     log(f"building {args.layers} decode layers ({args.layers * (E * EXPERT_BYTES + ROUTER_BYTES) / 1e9:.2f} GB)")
     layers = [Layer(seed=100 + 17 * i, dev=dev) for i in range(args.layers)]
     torch.cuda.synchronize()
+    if args.only_roofline:
+        kern = gateup_kernel(layers, dev, max(DECODE_MS), args.steps, args.warmup)
+        print(json.dumps({"roofline": roofline(kern)}), flush=True)
+        return 0
     dec = decode_sweep(layers, dev, args.steps, args.warmup)
     kern = gateup_kernel(layers, dev, max(DECODE_MS), args.steps, args.warmup)
     log(f"gate_up kernel M={kern['M']}: {kern['us']:.1f} us, {kern['gbps']:.0f} GB/s")
@@ -283,18 +346,7 @@ def main(argv=None):
             "hidden": H, "experts": E, "top_k": TOPK, "intermediate": I, "group_size": G,
             "layers_rotated": args.layers, "timing": "HIP graph replay, HIP events",
         },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": kern["kernel"],
-            "M": kern["M"],
-            "achieved": round(kern["gbps"], 2),
-            "peak": PEAK_HBM_GBS,
-            "unit": "GB/s",
-            "frac": round(kern["gbps"] / PEAK_HBM_GBS, 4),
-            "traffic": None,
-            "us_per_launch": round(kern["us"], 3),
-            "algorithmic_bytes_per_launch": int(kern["bytes"]),
-        },
+        "roofline": roofline(kern),
         "decode": {str(M): {k: (round(v, 4) if isinstance(v, float) else v) for k, v in d.items()}
                    for M, d in dec.items()},
         "prefill": None if pre is None else {k: (round(v, 4) if isinstance(v, float) else v)
