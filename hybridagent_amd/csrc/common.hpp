@@ -157,6 +157,45 @@ __device__ __forceinline__ void st16(void* p, u32x4_t v) {
   *reinterpret_cast<u32x4_t*>(p) = v;
 }
 
+// All-lane wavefront reductions through DPP, no LDS round trips: a
+// butterfly inside each 16-lane row (quad swaps, then row rotations by 4 and
+// 8), then the four row results combined from v_readlane.  Every lane gets
+// the result.
+template <typename Op>
+__device__ __forceinline__ uint32_t dpp_row_reduce(uint32_t v, Op op) {
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));   // quad [1,0,3,2]
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));   // quad [2,3,0,1]
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xF, 0xF, false));  // row_ror:4
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false));  // row_ror:8
+  return v;
+}
+
+template <typename Op>
+__device__ __forceinline__ uint32_t dpp_wave_reduce(uint32_t v, Op op) {
+  v = dpp_row_reduce(v, op);
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
+  const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)v, 32);
+  const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  return op(op(r0, r1), op(r2, r3));
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  return dpp_wave_reduce(v, [](uint32_t x, uint32_t y) { return x > y ? x : y; });
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+  return __uint_as_float(dpp_wave_reduce(__float_as_uint(v), [](uint32_t x, uint32_t y) {
+    return __float_as_uint(fmaxf(__uint_as_float(x), __uint_as_float(y)));
+  }));
+}
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+  return __uint_as_float(dpp_wave_reduce(__float_as_uint(v), [](uint32_t x, uint32_t y) {
+    return __float_as_uint(__uint_as_float(x) + __uint_as_float(y));
+  }));
+}
+
 // gelu_pytorch_tanh: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), fp32.
 __device__ __forceinline__ float gelu_tanh_f32(float x) {
   const float k0 = 0.7978845608028654f;

@@ -19,17 +19,7 @@ namespace w4a16 {
 // ---------------------------------------------------------------------------
 // wave / block reductions
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return wave_sum_f32(v); }
 
 __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
 #pragma unroll
@@ -127,82 +117,90 @@ constexpr int kRouterMaxSplit = 8;
 // Routing of one token by one wavefront: bf16 logits (from K-split partials
 // or given), softmax denominator, top-k by (logit desc, index asc), weights.
 // Lane i < topk returns selection i in *sel_e / *sel_w.
-__device__ void route_token(const float* __restrict__ partial, int ksplit,
+// KS = number of K-split partial sums to add (1 or kRouterMaxSplit), or 0 to
+// read finished bf16 logits; each lane holds experts lane + 64 q, q < PER
+// (PER = ceil(E / 64) rounded up to a power of two).  Every load of the token
+// is issued before any is used (addresses clamped into range, out-of-range
+// values masked after).
+template <int KS, int PER>
+__device__ void route_token(const float* __restrict__ partial,
                             const uint16_t* __restrict__ logits_in,
                             const uint16_t* __restrict__ pes, uint16_t* __restrict__ logits_out,
                             int64_t m, int M, int E, int topk, int lane, int* sel_e,
                             float* sel_w) {
-  float lg[kTopkPerLane];
+  float lg[PER];
   const int per = (E + 63) >> 6;
+  if (KS > 0) {
+    float pv[PER][KS > 0 ? KS : 1];
 #pragma unroll
-  for (int q = 0; q < kTopkPerLane; ++q) {
-    const int e = lane + 64 * q;
-    float v = -INFINITY;
-    if (q < per && e < E) {
-      if (partial != nullptr) {
-        // all K-split partials in flight at once, summed in split order
-        float pv[kRouterMaxSplit];
+    for (int q = 0; q < PER; ++q) {
+      const int e = min(lane + 64 * q, E - 1);
 #pragma unroll
-        for (int ks = 0; ks < kRouterMaxSplit; ++ks)
-          pv[ks] = ks < ksplit ? partial[((int64_t)ks * M + m) * E + e] : 0.f;
-        float s = 0.f;
-#pragma unroll
-        for (int ks = 0; ks < kRouterMaxSplit; ++ks) s += pv[ks];
-        const uint16_t b = f32_to_bf16_bits(s);
-        if (logits_out != nullptr) logits_out[m * E + e] = b;
-        v = bf16_bits_to_f32(b);
-      } else {
-        v = bf16_bits_to_f32(logits_in[m * E + e]);
-      }
-      if (v != v) v = -INFINITY;  // NaN never wins a slot; selection stays in range
+      for (int ks = 0; ks < KS; ++ks) pv[q][ks] = partial[((int64_t)ks * M + m) * E + e];
     }
-    lg[q] = v;
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      // summed in split order
+      float sum = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) sum += pv[q][ks];
+      const uint16_t b = f32_to_bf16_bits(sum);
+      const int e = lane + 64 * q;
+      const bool ok = q < per && e < E;
+      if (ok && logits_out != nullptr) logits_out[m * E + e] = b;
+      const float v = bf16_bits_to_f32(b);
+      lg[q] = (ok && v == v) ? v : -INFINITY;  // NaN never wins a slot
+    }
+  } else {
+    uint16_t lb[PER];
+#pragma unroll
+    for (int q = 0; q < PER; ++q) lb[q] = logits_in[m * E + min(lane + 64 * q, E - 1)];
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const bool ok = q < per && lane + 64 * q < E;
+      const float v = bf16_bits_to_f32(lb[q]);
+      lg[q] = (ok && v == v) ? v : -INFINITY;
+    }
   }
   // softmax denominator over all experts (fp32)
   float mx = -INFINITY;
 #pragma unroll
-  for (int q = 0; q < kTopkPerLane; ++q) mx = fmaxf(mx, lg[q]);
-  mx = wave_max(mx);
+  for (int q = 0; q < PER; ++q) mx = fmaxf(mx, lg[q]);
+  mx = wave_max_f32(mx);
   float den = 0.f;
 #pragma unroll
-  for (int q = 0; q < kTopkPerLane; ++q)
+  for (int q = 0; q < PER; ++q)
     if (q < per && lane + 64 * q < E) den += expf(lg[q] - mx);
-  den = wave_sum(den);
+  den = wave_sum_f32(den);
 
-  // top-k by (logit desc, index asc): logits are exact bf16 values, so the
-  // selection does not depend on exp/division rounding.  Selection `it` is
-  // kept by lane `it` (topk <= 32 < 64).
+  // top-k by (logit desc, index asc).  Logits are exact bf16 values, so each
+  // expert gets a unique 32-bit key: the bf16 bits mapped to an unsigned
+  // order (-0 taken as +0, as the float comparison does) above the inverted
+  // index.  Each step takes the wavefront's largest key (a DPP reduction) and
+  // clears it; selection `it` is kept by lane `it` (topk <= 32 < 64).
+  uint32_t key[PER];
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int e = lane + 64 * q;
+    uint32_t b = __float_as_uint(lg[q]) >> 16;
+    if (b == 0x8000u) b = 0u;
+    const uint32_t mono = (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
+    key[q] = (q < per && e < E) ? ((mono << 16) | (0xFFFFu - (uint32_t)e)) : 0u;
+  }
   float my_p = 0.f;
   int my_i = 0;
   float psum = 0.f;
-  bool taken[kTopkPerLane];
-#pragma unroll
-  for (int q = 0; q < kTopkPerLane; ++q) taken[q] = false;
   for (int it = 0; it < topk; ++it) {
-    float bv = -INFINITY;
-    int bi = 0x7FFFFFFF;
+    uint32_t best = 0u;
 #pragma unroll
-    for (int q = 0; q < kTopkPerLane; ++q) {
-      const int e = lane + 64 * q;
-      if (q < per && e < E && !taken[q] && (lg[q] > bv || (lg[q] == bv && e < bi))) {
-        bv = lg[q];
-        bi = e;
-      }
-    }
+    for (int q = 0; q < PER; ++q) best = key[q] > best ? key[q] : best;
+    const uint32_t kmax = wave_max_u32(best);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o);
-      const int oi = __shfl_xor(bi, o);
-      if (ov > bv || (ov == bv && oi < bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    if ((bi & 63) == lane) {
-#pragma unroll
-      for (int q = 0; q < kTopkPerLane; ++q)
-        if (q == (bi >> 6)) taken[q] = true;
-    }
+    for (int q = 0; q < PER; ++q) key[q] = key[q] == kmax ? 0u : key[q];
+    const int bi = (int)(0xFFFFu - (kmax & 0xFFFFu));
+    const uint32_t mono = kmax >> 16;
+    const uint32_t bb = (mono & 0x8000u) ? (mono & 0x7FFFu) : (~mono & 0xFFFFu);
+    const float bv = bf16_bits_to_f32(bb);
     const float p = expf(bv - mx) / den;
     if (lane == it) {
       my_p = p;
@@ -214,7 +212,8 @@ __device__ void route_token(const float* __restrict__ partial, int ksplit,
   *sel_w = (lane < topk) ? (my_p / psum) * bf16_bits_to_f32(pes[my_i]) : 0.f;
 }
 
-__global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ partial, int ksplit,
+template <int KS, int PER>
+__global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ partial,
                                                      const uint16_t* __restrict__ logits_in,
                                                      const uint16_t* __restrict__ pes,
                                                      uint16_t* __restrict__ logits_out,
@@ -226,20 +225,45 @@ __global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ p
   if (m >= M) return;  // uniform per wavefront
   int se;
   float sw;
-  route_token(partial, ksplit, logits_in, pes, logits_out, m, M, E, topk, lane, &se, &sw);
+  route_token<KS, PER>(partial, logits_in, pes, logits_out, m, M, E, topk, lane, &se, &sw);
   if (lane < topk) {
     idx_out[m * topk + lane] = se;
     w_out[m * topk + lane] = sw;
   }
 }
 
+template <int KS>
+void launch_topk_ks(const float* partial, const uint16_t* logits_in, const uint16_t* pes,
+                    uint16_t* logits_out, int64_t* idx, float* w, int M, int E, int topk,
+                    hipStream_t s) {
+  const dim3 grid((M + 3) / 4), block(256);
+  if (E <= 64)
+    hipLaunchKernelGGL((k_router_topk<KS, 1>), grid, block, 0, s, partial, logits_in, pes,
+                       logits_out, idx, w, M, E, topk);
+  else if (E <= 128)
+    hipLaunchKernelGGL((k_router_topk<KS, 2>), grid, block, 0, s, partial, logits_in, pes,
+                       logits_out, idx, w, M, E, topk);
+  else if (E <= 256)
+    hipLaunchKernelGGL((k_router_topk<KS, 4>), grid, block, 0, s, partial, logits_in, pes,
+                       logits_out, idx, w, M, E, topk);
+  else
+    hipLaunchKernelGGL((k_router_topk<KS, kTopkPerLane>), grid, block, 0, s, partial, logits_in,
+                       pes, logits_out, idx, w, M, E, topk);
+}
+
 hipError_t launch_router_topk(const float* partial, int ksplit, const uint16_t* logits_in,
                               const uint16_t* per_expert_scale, uint16_t* logits_out,
                               int64_t* idx, float* w, int M, int E, int topk, hipStream_t s) {
   if (M == 0) return hipSuccess;
-  if (ksplit > kRouterMaxSplit) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_router_topk, dim3((M + 3) / 4), dim3(256), 0, s, partial, ksplit,
-                     logits_in, per_expert_scale, logits_out, idx, w, M, E, topk);
+  if (partial == nullptr)
+    launch_topk_ks<0>(partial, logits_in, per_expert_scale, logits_out, idx, w, M, E, topk, s);
+  else if (ksplit == kRouterMaxSplit)
+    launch_topk_ks<kRouterMaxSplit>(partial, logits_in, per_expert_scale, logits_out, idx, w, M,
+                                    E, topk, s);
+  else if (ksplit == 1)
+    launch_topk_ks<1>(partial, logits_in, per_expert_scale, logits_out, idx, w, M, E, topk, s);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
