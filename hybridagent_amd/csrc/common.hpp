@@ -196,12 +196,18 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
   }));
 }
 
-// gelu_pytorch_tanh: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), fp32.
+// gelu_pytorch_tanh, 0.5 x (1 + tanh(u)) with u = sqrt(2/pi) (x + 0.044715 x^3),
+// evaluated through the identity 0.5 (1 + tanh(u)) = 1 / (1 + exp(-2u)) in
+// fp32 (one exponential, one reciprocal; exact limits -0 and x for large |x|).
 __device__ __forceinline__ float gelu_tanh_f32(float x) {
-  const float k0 = 0.7978845608028654f;
-  const float k1 = 0.044715f;
-  const float inner = k0 * (x + k1 * x * x * x);
-  return 0.5f * x * (1.0f + tanhf(inner));
+  const float u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+  return __fdividef(x, 1.0f + __expf(-2.0f * u));
+}
+
+// Value of the lane 8 positions away inside the 16-lane row (j <-> j ^ 8),
+// through DPP row rotation.
+__device__ __forceinline__ float lane_xor8(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
 }
 
 }  // namespace w4a16

@@ -104,13 +104,19 @@ hipError_t launch_bias_order(const uint16_t* x, uint16_t* xp, int64_t rows, int 
 // i.e. grouped by (k tile, lane chunk, MFMA step), so a wavefront's
 // ds_read_b128 of one MFMA step is contiguous and bank-conflict free.
 constexpr int kStreamThreads = 256;
+// items whose weight loads are in flight per wavefront (register sets).
+// One set, refilled tile by tile while the item is multiplied, measured
+// fastest: deeper rings slowed the streamer down.
+constexpr int kRing = 1;
 
 __device__ __forceinline__ int frag_slot(int b, int rb, int j) {
   return (16 * (b >> 4) + 4 * (b & 3) + ((b >> 2) & 3)) * rb + j;
 }
 
-template <int MODE, bool BIAS, int TPW, int KSPLIT, bool LONGK>
-__global__ __launch_bounds__(kStreamThreads) __attribute__((amdgpu_waves_per_eu(TPW >= 6 ? 3 : 4, 8)))
+// WIDE (group size 128, an even number of groups per row): the scales of one
+// item's TPW tiles are consecutive bf16 values, fetched with one load.
+template <int MODE, bool BIAS, int TPW, int KSPLIT, bool LONGK, bool WIDE>
+__global__ __launch_bounds__(kStreamThreads) __attribute__((amdgpu_waves_per_eu(TPW >= 4 ? 2 : 4, 8)))
 void k_decode(DecodeArgs a) {
   constexpr int CG = 4 / KSPLIT;
   extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -118,7 +124,10 @@ void k_decode(DecodeArgs a) {
   // per (k tile, staged row) bias correction, after the activation fragments
   const int ntiles = ((a.K >> 5) + 3) >> 2;
   float* __restrict__ csum = reinterpret_cast<float*>(smem_raw + (size_t)ntiles * 16 * a.rb * 16);
-  __shared__ f32x4_t red[4][64];
+  static_assert(KSPLIT == 1 || KSPLIT == 4, "the split-K epilogue gives wavefront ks output row ks");
+  static_assert(!WIDE || (BIAS && !LONGK), "wide scale loads serve the bias form");
+  // split-K partials, double-buffered so one barrier per item suffices
+  __shared__ f32x4_t red[2][4][64];
   __shared__ int tok[16];
 
   const int tid = threadIdx.x;
@@ -144,10 +153,16 @@ void k_decode(DecodeArgs a) {
     seg0 = __builtin_amdgcn_readfirstlane(d.y);
     rows = __builtin_amdgcn_readfirstlane(d.z);
   }
-  const int per = (a.n_ct + a.wg_per_slot - 1) / a.wg_per_slot;
+  // items per workgroup, a multiple of the register ring depth so every
+  // workgroup walks whole rounds; items past n_ct (the last workgroup's
+  // padding) compute on row 0 and store nothing
+  constexpr int RING = LONGK ? 1 : kRing;
+  int per = (a.n_ct + a.wg_per_slot - 1) / a.wg_per_slot;
+  per = (per + RING - 1) / RING * RING;
   const int begin = part * per;
   const int end = min(a.n_ct, begin + per);
   if (begin >= end || rows <= 0) return;
+  const int end_pad = begin + per;
 
   const int K8 = a.K >> 3;
   const int nchunks = a.K >> 5;
@@ -198,19 +213,42 @@ void k_decode(DecodeArgs a) {
     return (o.srow + g) * 2;
   };
 
-  u32x4_t bw[TPW];
+  // RING register sets of one item's weight tiles each: the loads of the
+  // next RING - 1 items are in flight while one item is multiplied.
+  u32x4_t bw[RING][TPW];
   // raw bf16 bits, kept 16-bit until use: widening them where the loop
   // carries them would wait for the loads (see load_batch)
-  uint16_t sc[TPW];
+  uint16_t sc[RING][TPW];
+  // WIDE: the item's TPW scales as packed bf16 pairs
+  constexpr int SCW = (TPW + 1) / 2;
+  uint32_t scw[RING][SCW];
+  auto load_scales_wide = [&](int r, const Off& o) {
+    const int off = (o.srow + tile0) * 2;
+    if (SCW == 3) {
+      typedef __attribute__((ext_vector_type(3))) uint32_t u32x3_t;
+      const u32x3_t v = __builtin_bit_cast(u32x3_t, __builtin_amdgcn_raw_buffer_load_b96(ssrc, off, 0, 0));
+      scw[r][0] = v.x; scw[r][SCW > 1 ? 1 : 0] = v.y; scw[r][SCW > 2 ? 2 : 0] = v.z;
+    } else if (SCW == 2) {
+      typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
+      const u32x2_t v = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(ssrc, off, 0, 0));
+      scw[r][0] = v.x; scw[r][SCW > 1 ? 1 : 0] = v.y;
+    } else {
+      scw[r][0] = __builtin_amdgcn_raw_buffer_load_b32(ssrc, off, 0, 0);
+    }
+  };
 
   // All loads of one batch are issued back to back; converting a scale right
   // away would make the wavefront wait for it and -- loads retiring in order --
   // for every weight load before it.
-  auto load_batch = [&](const Off& o, int tb) {
+  auto load_batch = [&](int r, const Off& o, int tb) {
 #pragma unroll
-    for (int i = 0; i < TPW; ++i) bw[i] = buf_ld16(wsrc, o.woff + 64 * tb, 64 * i);
+    for (int i = 0; i < TPW; ++i) bw[r][i] = buf_ld16(wsrc, o.woff + 64 * tb, 64 * i);
+    if (WIDE) {
+      load_scales_wide(r, o);
+    } else {
 #pragma unroll
-    for (int i = 0; i < TPW; ++i) sc[i] = buf_ld_u16(ssrc, scale_off(o, tb + i));
+      for (int i = 0; i < TPW; ++i) sc[r][i] = buf_ld_u16(ssrc, scale_off(o, tb + i));
+    }
     __builtin_amdgcn_sched_barrier(0);
   };
 
@@ -270,8 +308,17 @@ void k_decode(DecodeArgs a) {
   // unconditional (the caller picks the source): a conditional reload makes
   // the compiler merge old and new values with register copies, and copying
   // a register that a load is filling waits for every load in flight.
-  auto mma_batch = [&](int tb, f32x4_t& acc, auto refill_tag, const Off& nx) {
+  auto mma_batch = [&](int r, int tb, f32x4_t& acc, auto refill_tag, const Off& nx) {
     constexpr bool REFILL = decltype(refill_tag)::value;
+    // WIDE: this item's scales leave the registers before the refill below
+    // reuses them (one load, needed by the first tile anyway)
+    float sfw[TPW];
+    if (WIDE) {
+#pragma unroll
+      for (int i = 0; i < TPW; ++i)
+        sfw[i] = (i & 1) ? __uint_as_float(scw[r][i >> 1] & 0xFFFF0000u) : __uint_as_float(scw[r][i >> 1] << 16);
+      if (REFILL) load_scales_wide(r, nx);
+    }
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
       // Tiles past K (the last wavefront's spare slots) run on the last real
@@ -285,22 +332,22 @@ void k_decode(DecodeArgs a) {
       for (int s = 0; s < 4; ++s) A[s] = lds_a[frag_slot(16 * tc + 4 * kb + s, rb, jr_read)];
       // the bias form scales a whole tile, the exact form one lane chunk
       const bool s_ok = t_ok && (BIAS || 4 * t + kb < nchunks);
-      const float sci = s_ok ? bf16_bits_to_f32(sc[i]) : 0.f;
+      const float sci = s_ok ? (WIDE ? sfw[i] : bf16_bits_to_f32(sc[r][i])) : 0.f;
       u32x4_t bv[4];
       if (BIAS) {
-        bv[0] = unpack_bias(bw[i].x, kMask, kBias);
-        bv[1] = unpack_bias(bw[i].y, kMask, kBias);
-        bv[2] = unpack_bias(bw[i].z, kMask, kBias);
-        bv[3] = unpack_bias(bw[i].w, kMask, kBias);
+        bv[0] = unpack_bias(bw[r][i].x, kMask, kBias);
+        bv[1] = unpack_bias(bw[r][i].y, kMask, kBias);
+        bv[2] = unpack_bias(bw[r][i].z, kMask, kBias);
+        bv[3] = unpack_bias(bw[r][i].w, kMask, kBias);
       } else {
-        bv[0] = unpack_exact<false>(bw[i].x, sci);
-        bv[1] = unpack_exact<false>(bw[i].y, sci);
-        bv[2] = unpack_exact<false>(bw[i].z, sci);
-        bv[3] = unpack_exact<false>(bw[i].w, sci);
+        bv[0] = unpack_exact<false>(bw[r][i].x, sci);
+        bv[1] = unpack_exact<false>(bw[r][i].y, sci);
+        bv[2] = unpack_exact<false>(bw[r][i].z, sci);
+        bv[3] = unpack_exact<false>(bw[r][i].w, sci);
       }
       if (REFILL) {
-        bw[i] = buf_ld16(wsrc, nx.woff + 64 * tb, 64 * i);
-        sc[i] = buf_ld_u16(ssrc, scale_off(nx, tc));
+        bw[r][i] = buf_ld16(wsrc, nx.woff + 64 * tb, 64 * i);
+        if (!WIDE) sc[r][i] = buf_ld_u16(ssrc, scale_off(nx, tc));
       }
       if (BIAS) {
         f32x4_t g = {0.f, 0.f, 0.f, 0.f};
@@ -320,86 +367,93 @@ void k_decode(DecodeArgs a) {
     }
   };
 
-  const Off first = off_of(begin);
-  if (!LONGK) load_batch(first, tile0);
+  // item at ring position p of a pass (0 <= p < 2 * per): the refill of the
+  // last items of a pass loads the first items again for the next pass
+  auto item_at = [&](int p) -> int { return begin + (p >= per ? p - per : p); };
+  int rbuf = 0;
+  if (!LONGK) {
+#pragma unroll
+    for (int r = 0; r < RING; ++r) load_batch(r, off_of(begin + r), tile0);
+  }
   for (int mc = 0; mc < rows; mc += rb) {
     const int nr = min(rb, rows - mc);
-    const bool last_pass = __builtin_amdgcn_readfirstlane(mc + rb >= rows) != 0;
     stage(mc, nr);
-    for (int ct = begin; ct < end; ++ct) {
+    for (int c0 = begin; c0 < end_pad; c0 += RING) {
+#pragma unroll
+    for (int r = 0; r < RING; ++r) {
+      const int ct = c0 + r;
       bool col_ok;
       weight_row(ct, &col_ok);
       const int colblk = ct * CG + cg;
-      // the weights that follow this item's: the next item's, or -- after
-      // the last item of a pass that is not the last -- the first item's
-      const Off nx = ct + 1 < end ? off_of(ct + 1) : first;
       f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
       if (!LONGK) {
-        mma_batch(tile0, acc, std::true_type{}, nx);
+        // refill this register set with the item RING positions ahead
+        const Off nx = off_of(item_at(ct - begin + RING));
+        mma_batch(r, tile0, acc, std::true_type{}, nx);
       } else {
         const Off cur = off_of(ct);
         for (int tb = tile0; tb < ntiles; tb += KSPLIT * TPW) {
-          load_batch(cur, tb);
-          mma_batch(tb, acc, std::false_type{}, nx);
+          load_batch(0, cur, tb);
+          mma_batch(0, tb, acc, std::false_type{}, cur);
         }
       }
-      (void)last_pass;
-      // split-K reduction over the KSPLIT wavefronts of this column group
+      // split-K reduction over the KSPLIT wavefronts of this column group:
+      // wavefront ks sums output row q = ks of every lane's four (in
+      // wavefront order) and finishes it, so the epilogue is shared four ways
+      int qlo = 0, qhi = 4;
       f32x4_t v = acc;
-      bool owner = true;
       if (KSPLIT > 1) {
-        red[wave][lane] = acc;
+        red[rbuf][wave][lane] = acc;
         __syncthreads();
-        owner = ks == 0;
-        if (owner) {
+        float sum = 0.f;
 #pragma unroll
-          for (int w = 1; w < KSPLIT; ++w) {
-            const f32x4_t o = red[wave + w][lane];
-            v[0] += o[0]; v[1] += o[1]; v[2] += o[2]; v[3] += o[3];
+        for (int w = 0; w < KSPLIT; ++w) sum += red[rbuf][cg * KSPLIT + w][lane][ks];
+        v[ks] = sum;
+        qlo = ks;
+        qhi = ks + 1;
+        rbuf ^= 1;
+      }
+      // output row 4*kb + q of the MFMA tile is staged row 4*kb + q of this
+      // pass; only the pass's nr rows exist
+      const int ibase = mc + 4 * kb;
+      const int iend = mc + nr;
+      if (MODE == kModeDense) {
+        const int n = colblk * 16 + j;
+        const float bb = (a.bias != nullptr && col_ok) ? bf16_bits_to_f32(a.bias[n]) : 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int i = ibase + q;
+          if (q >= qlo && q < qhi && col_ok && i < iend)
+            a.out[(int64_t)i * a.N + n] = f32_to_bf16_bits(v[q] + bb);
+        }
+      } else if (MODE == kModeGateUp) {
+        // lane j (< 8) holds gate column n0+j, lane j+8 the matching up column
+        const int n0 = colblk * 8;
+        const int pos = BIAS ? ((j & 3) * 2 + ((j >> 2) & 1)) : j;  // bias-order slot
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          if (q < qlo || q >= qhi) continue;  // uniform: whole wavefront
+          const float up = lane_xor8(v[q]);
+          const int i = ibase + q;
+          if (j < 8 && i < iend && col_ok) {
+            const float gate = round_bf16(v[q]);
+            const float act = round_bf16(gelu_tanh_f32(gate));
+            const float h = act * round_bf16(up);
+            a.out[(int64_t)(seg0 + i) * a.I + n0 + pos] = f32_to_bf16_bits(h);
+          }
+        }
+      } else {
+        const int n = colblk * 16 + j;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int i = ibase + q;
+          if (q >= qlo && q < qhi && col_ok && i < iend) {
+            const int64_t orow = a.sorted_pos[seg0 + i];
+            a.out[orow * a.N + n] = f32_to_bf16_bits(v[q]);
           }
         }
       }
-      if (owner) {
-        // output row 4*kb + q of the MFMA tile is staged row 4*kb + q of this
-        // pass; only the pass's nr rows exist
-        const int ibase = mc + 4 * kb;
-        const int iend = mc + nr;
-        if (MODE == kModeDense) {
-          const int n = colblk * 16 + j;
-          const float bb = (a.bias != nullptr && col_ok) ? bf16_bits_to_f32(a.bias[n]) : 0.f;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int i = ibase + q;
-            if (col_ok && i < iend) a.out[(int64_t)i * a.N + n] = f32_to_bf16_bits(v[q] + bb);
-          }
-        } else if (MODE == kModeGateUp) {
-          // lane j (< 8) holds gate column n0+j, lane j+8 the matching up column
-          const int n0 = colblk * 8;
-          const int pos = BIAS ? ((j & 3) * 2 + ((j >> 2) & 1)) : j;  // bias-order slot
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const float up = __shfl_xor(v[q], 8);
-            const int i = ibase + q;
-            if (j < 8 && i < iend && col_ok) {
-              const float gate = round_bf16(v[q]);
-              const float act = round_bf16(gelu_tanh_f32(gate));
-              const float h = act * round_bf16(up);
-              a.out[(int64_t)(seg0 + i) * a.I + n0 + pos] = f32_to_bf16_bits(h);
-            }
-          }
-        } else {
-          const int n = colblk * 16 + j;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int i = ibase + q;
-            if (col_ok && i < iend) {
-              const int64_t orow = a.sorted_pos[seg0 + i];
-              a.out[orow * a.N + n] = f32_to_bf16_bits(v[q]);
-            }
-          }
-        }
-      }
-      if (KSPLIT > 1) __syncthreads();  // red is reused by the next item
+    }
     }
   }
 }
@@ -451,9 +505,9 @@ static size_t stream_lds(const DecodeArgs& a) {
   return (size_t)ntiles * 16 * a.rb * 16 + (size_t)ntiles * 16 * 4;
 }
 
-template <int MODE, bool BIAS, int TPW, int KSPLIT, bool LONGK>
+template <int MODE, bool BIAS, int TPW, int KSPLIT, bool LONGK, bool WIDE = false>
 static hipError_t launch_stream(DecodeArgs a, int max_slots, hipStream_t s) {
-  auto kern = k_decode<MODE, BIAS, TPW, KSPLIT, LONGK>;
+  auto kern = k_decode<MODE, BIAS, TPW, KSPLIT, LONGK, WIDE>;
   // workgroups per expert: fill the chip with the workgroups that fit at
   // once, spread over the experts that can be active, at most one per item
   int per_cu = 0;
@@ -484,7 +538,12 @@ static hipError_t launch_decode_mode(DecodeArgs a, int max_slots, hipStream_t s)
   while (rows_cap < a.rows_hint && rows_cap < 16) rows_cap <<= 1;
   if (a.rb > rows_cap) a.rb = rows_cap;
   const int ntiles = ((a.K >> 5) + 3) >> 2;
-#define W4A16_DEC(T_, K_) return launch_stream<MODE, BIAS, T_, K_, false>(a, max_slots, s)
+  // one load for an item's scales: group size 128 (one group per k tile)
+  // and 4-byte aligned scale rows
+  const bool wide = BIAS && a.G == 128 && (a.ng % 2) == 0;
+#define W4A16_DEC(T_, K_)                                                          \
+  return wide ? launch_stream<MODE, BIAS, T_, K_, false, BIAS>(a, max_slots, s) \
+              : launch_stream<MODE, BIAS, T_, K_, false, false>(a, max_slots, s)
   if (ntiles > 24) return launch_stream<MODE, BIAS, 6, 4, true>(a, max_slots, s);
   if (sh.ksplit == 1) {
     if (sh.tpw == 2) W4A16_DEC(2, 1);
