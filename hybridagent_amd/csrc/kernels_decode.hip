@@ -103,7 +103,10 @@ hipError_t launch_bias_order(const uint16_t* x, uint16_t* xp, int64_t rows, int 
 //   (16*(b/16) + 4*(b%4) + (b/4)%4) * rb + j
 // i.e. grouped by (k tile, lane chunk, MFMA step), so a wavefront's
 // ds_read_b128 of one MFMA step is contiguous and bank-conflict free.
-constexpr int kStreamThreads = 256;
+// Threads per workgroup: K-split shapes run two column groups of four
+// wavefronts each (eight wavefronts share one activation stage), the others
+// four column groups of one wavefront.
+constexpr int stream_threads(int ksplit) { return ksplit == 4 ? 512 : 256; }
 // items whose weight loads are in flight per wavefront (register sets).
 // One set, refilled tile by tile while the item is multiplied, measured
 // fastest: deeper rings slowed the streamer down.
@@ -116,9 +119,11 @@ __device__ __forceinline__ int frag_slot(int b, int rb, int j) {
 // WIDE (group size 128, an even number of groups per row): the scales of one
 // item's TPW tiles are consecutive bf16 values, fetched with one load.
 template <int MODE, bool BIAS, int TPW, int KSPLIT, bool LONGK, bool WIDE>
-__global__ __launch_bounds__(kStreamThreads) __attribute__((amdgpu_waves_per_eu(TPW >= 4 ? 2 : 4, 8)))
+__global__ __launch_bounds__(stream_threads(KSPLIT)) __attribute__((amdgpu_waves_per_eu(TPW >= 4 ? 2 : 4, 8)))
 void k_decode(DecodeArgs a) {
-  constexpr int CG = 4 / KSPLIT;
+  constexpr int kStreamThreads = stream_threads(KSPLIT);
+  constexpr int NWAVES = kStreamThreads / 64;
+  constexpr int CG = NWAVES / KSPLIT;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   u32x4_t* __restrict__ lds_a = reinterpret_cast<u32x4_t*>(smem_raw);
   // per (k tile, staged row) bias correction, after the activation fragments
@@ -127,7 +132,7 @@ void k_decode(DecodeArgs a) {
   static_assert(KSPLIT == 1 || KSPLIT == 4, "the split-K epilogue gives wavefront ks output row ks");
   static_assert(!WIDE || (BIAS && !LONGK), "wide scale loads serve the bias form");
   // split-K partials, double-buffered so one barrier per item suffices
-  __shared__ f32x4_t red[2][4][64];
+  __shared__ f32x4_t red[2][KSPLIT > 1 ? NWAVES : 1][64];
   __shared__ int tok[16];
 
   const int tid = threadIdx.x;
@@ -361,9 +366,6 @@ void k_decode(DecodeArgs a) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) acc = mfma16(A[s], bv[s], acc);
       }
-      // keep the next tile's LDS reads and unpacking from being hoisted
-      // above this one (bounds the live registers to one tile's operands)
-      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
@@ -511,7 +513,8 @@ static hipError_t launch_stream(DecodeArgs a, int max_slots, hipStream_t s) {
   // workgroups per expert: fill the chip with the workgroups that fit at
   // once, spread over the experts that can be active, at most one per item
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kStreamThreads, stream_lds(a)) !=
+  constexpr int threads = stream_threads(KSPLIT);
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, stream_lds(a)) !=
           hipSuccess || per_cu <= 0)
     per_cu = 1;
   const int64_t resident = (int64_t)device_cus() * per_cu;
@@ -521,14 +524,14 @@ static hipError_t launch_stream(DecodeArgs a, int max_slots, hipStream_t s) {
   a.wg_per_slot = (int)wps;
   const int64_t grid = (int64_t)max_slots * wps;
   if (grid <= 0) return hipSuccess;
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kStreamThreads), stream_lds(a), s, a);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(threads), stream_lds(a), s, a);
   return hipGetLastError();
 }
 
 template <int MODE, bool BIAS>
 static hipError_t launch_decode_mode(DecodeArgs a, int max_slots, hipStream_t s) {
   const DecodeShape sh = decode_shape(a.K);
-  const int cg = 4 / sh.ksplit;
+  const int cg = stream_threads(sh.ksplit) / 64 / sh.ksplit;  // column groups per item
   const int ncolblk = MODE == kModeGateUp ? a.I / 8 : (a.N + 15) / 16;
   a.n_ct = (ncolblk + cg - 1) / cg;
   // rows staged per pass: enough for the rows an expert can have (at most
