@@ -37,6 +37,9 @@ inline int router_ksplit(int64_t M) { return M <= 64 ? 8 : 1; }
 // Token counts up to this use the decode kernels; larger batches the
 // prefill grouped-GEMM kernels.
 constexpr int64_t kDecodeMaxM = 256;
+// routed rows up to this run top-k and the expert sort in one workgroup
+// (measured faster than two launches up to M = 8 at top-8; slower from M = 32)
+constexpr int64_t kTopkSortMaxEntries = 64;
 // longest reduction the streaming kernels stage in LDS (one row per pass)
 constexpr int64_t kMaxStreamK = 49152 / 2;
 
@@ -47,6 +50,11 @@ hipError_t launch_router_partials(const uint16_t* hidden, const uint16_t* scale,
                                   float eps, const uint16_t* proj, uint16_t* r, float* partial,
                                   int64_t M, int64_t H, int64_t E, hipStream_t s) {
   const int ks = router_ksplit(M);
+  // decode sizes: the norm inside the logits launch (each workgroup covers
+  // all experts of 16 tokens, so it normalises its rows once)
+  if (ks == 8 && H <= 384 * 8)
+    return launch_router_norm_logits(hidden, scale, root, eps, proj, partial, (int)M, (int)H,
+                                     (int)E, ks, s);
   hipError_t e = launch_router_norm(hidden, scale, root, eps, r, (int)M, (int)H, s);
   if (e == hipSuccess) e = launch_router_logits(r, proj, partial, (int)M, (int)H, (int)E, ks, s);
   return e;
@@ -439,11 +447,19 @@ int moe_layer_forward(const uint16_t* router_in, const uint16_t* router_scale, f
   hipError_t e = launch_router_partials(router_in, router_scale, scalar_root, eps, proj_w, r,
                                         partial, M, H, E, s);
   if (e != hipSuccess) return W4A16_ERR_LAUNCH;
-  e = launch_router_topk(partial, router_ksplit(M), nullptr, per_expert_scale, nullptr, topk_idx,
-                         topk_w, (int)M, (int)E, (int)top_k, s);
-  if (e != hipSuccess) return W4A16_ERR_LAUNCH;
-  st = moe_plan(hidden, topk_idx, M, top_k, E, H, I, group_size, workspace, moe_bytes, stream);
-  if (st != W4A16_OK) return st;
+  if (M * top_k <= kTopkSortMaxEntries) {
+    // small batches: top-k and the expert sort in one workgroup
+    e = launch_topk_sort(partial, router_ksplit(M), per_expert_scale, topk_idx, topk_w, (int)M,
+                         (int)E, (int)top_k, L.sorted_pos, L.offsets, L.desc, L.counters, L.tiles,
+                         kPrefillBM, s);
+    if (e != hipSuccess) return W4A16_ERR_LAUNCH;
+  } else {
+    e = launch_router_topk(partial, router_ksplit(M), nullptr, per_expert_scale, nullptr, topk_idx,
+                           topk_w, (int)M, (int)E, (int)top_k, s);
+    if (e != hipSuccess) return W4A16_ERR_LAUNCH;
+    st = moe_plan(hidden, topk_idx, M, top_k, E, H, I, group_size, workspace, moe_bytes, stream);
+    if (st != W4A16_OK) return st;
+  }
   st = moe_gate_up(hidden, gu_packed, gu_scale, M, top_k, E, H, I, group_size, workspace,
                    moe_bytes, stream);
   if (st == W4A16_OK)

@@ -37,24 +37,71 @@ __global__ __launch_bounds__(256) void k_router_norm(const uint16_t* __restrict_
                                                      const uint16_t* __restrict__ scale,
                                                      float scalar_root, float eps,
                                                      uint16_t* __restrict__ r, int H) {
+  // one pass: each thread keeps its 16-byte chunks (up to kNormChunks) in
+  // registers between the sum of squares and the scaled write
+  constexpr int kNormChunks = 4;  // H <= 256 * 8 * 4 = 8192 in one pass
   const int64_t row = blockIdx.x;
   const uint16_t* hr = h + row * H;
+  const int n8 = H >> 3;
   __shared__ float part[4];
+  u32x4_t v[kNormChunks];
   float ss = 0.f;
-  for (int c = threadIdx.x; c < H; c += 256) {
-    const float v = bf16_bits_to_f32(hr[c]);
-    ss = __builtin_fmaf(v, v, ss);
+#pragma unroll
+  for (int q = 0; q < kNormChunks; ++q) {
+    const int c8 = threadIdx.x + 256 * q;
+    v[q] = c8 < n8 ? ld16(hr + 8 * c8) : u32x4_t{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int q = 0; q < kNormChunks; ++q) {
+    const uint32_t w4[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float lo = bf16_bits_to_f32(w4[t] & 0xFFFFu), hi = bf16_bits_to_f32(w4[t] >> 16);
+      ss = __builtin_fmaf(lo, lo, ss);
+      ss = __builtin_fmaf(hi, hi, ss);
+    }
+  }
+  // rows longer than the register pass (H > 8192): the remaining chunks
+  for (int c8 = threadIdx.x + 256 * kNormChunks; c8 < n8; c8 += 256) {
+    const u32x4_t x = ld16(hr + 8 * c8);
+    const uint32_t w4[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float lo = bf16_bits_to_f32(w4[t] & 0xFFFFu), hi = bf16_bits_to_f32(w4[t] >> 16);
+      ss = __builtin_fmaf(lo, lo, ss);
+      ss = __builtin_fmaf(hi, hi, ss);
+    }
   }
   ss = wave_sum(ss);
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
   __syncthreads();
   const float tot = part[0] + part[1] + part[2] + part[3];
   const float inv = 1.0f / sqrtf(tot / (float)H + eps);
-  for (int c = threadIdx.x; c < H; c += 256) {
-    const float v = round_bf16(bf16_bits_to_f32(hr[c]) * inv);
-    const float v2 = round_bf16(v * bf16_bits_to_f32(scale[c]));
-    r[row * H + c] = f32_to_bf16_bits(v2 * scalar_root);
+  auto emit = [&](int c8, const u32x4_t& xv) {
+    const u32x4_t sv = ld16(scale + 8 * c8);
+    const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w}, sw[4] = {sv.x, sv.y, sv.z, sv.w};
+    uint32_t ow[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      float rr[2];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const float xe = bf16_bits_to_f32(hh ? (xw[t] >> 16) : (xw[t] & 0xFFFFu));
+        const float se = bf16_bits_to_f32(hh ? (sw[t] >> 16) : (sw[t] & 0xFFFFu));
+        const float a1 = round_bf16(xe * inv);
+        const float a2 = round_bf16(a1 * se);
+        rr[hh] = a2 * scalar_root;
+      }
+      ow[t] = pack_bf16x2(rr[0], rr[1]);
+    }
+    st16(r + row * H + 8 * c8, u32x4_t{ow[0], ow[1], ow[2], ow[3]});
+  };
+#pragma unroll
+  for (int q = 0; q < kNormChunks; ++q) {
+    const int c8 = threadIdx.x + 256 * q;
+    if (c8 < n8) emit(c8, v[q]);
   }
+  for (int c8 = threadIdx.x + 256 * kNormChunks; c8 < n8; c8 += 256) emit(c8, ld16(hr + 8 * c8));
 }
 
 hipError_t launch_router_norm(const uint16_t* h, const uint16_t* scale, float scalar_root,
@@ -109,6 +156,145 @@ hipError_t launch_router_logits(const uint16_t* r, const uint16_t* proj, float* 
 }
 
 // ---------------------------------------------------------------------------
+// router RMSNorm + logits in one launch (decode sizes): one workgroup per
+// (16 tokens, K split) covers all experts, so the norm of its rows is computed
+// once per 128 experts.  Phase 1 sums x^2 over whole rows (fixed order: 32
+// threads per row, each over a strided set of 16-byte chunks, then the 32
+// partials in thread order); phase 2 forms r = bf16(bf16(bf16(x * inv) *
+// scale) * root) for the split's k range only, straight into LDS in MFMA
+// A-operand order; phase 3 is 16x16x32 MFMA against the router weights,
+// whose loads are issued first and overlap phases 1-2.
+// ---------------------------------------------------------------------------
+constexpr int kFusedLogitsThreads = 512;
+constexpr int kFusedLogitsMaxSteps = 12;  // 32-wide k steps per split
+
+__global__ __launch_bounds__(kFusedLogitsThreads) void k_router_norm_logits(
+    const uint16_t* __restrict__ h, const uint16_t* __restrict__ scale, float scalar_root,
+    float eps, const uint16_t* __restrict__ proj, float* __restrict__ partial, int M, int H, int E,
+    int steps_per_split) {
+  constexpr int NW = kFusedLogitsThreads / 64;
+  __shared__ u32x4_t afrag[kFusedLogitsMaxSteps][64];
+  __shared__ float s_part[16][33];
+  __shared__ float s_inv[16];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 15, kb = lane >> 4;
+  const int m0 = blockIdx.x * 16;
+  const int ks = blockIdx.y;
+  const int nchunks = H >> 5;
+  const int c0 = ks * steps_per_split;
+  const int nsteps = max(0, min(nchunks, c0 + steps_per_split) - c0);
+
+  // router weight fragments of this wavefront's first 16 experts
+  const int e = wave * 16 + j;
+  const int ec = min(e, E - 1);
+  u32x4_t bv[kFusedLogitsMaxSteps];
+#pragma unroll
+  for (int c = 0; c < kFusedLogitsMaxSteps; ++c)
+    if (c < nsteps) bv[c] = ld16(proj + (int64_t)ec * H + 32 * (c0 + c) + 8 * kb);
+
+  // phase 1: sum of squares of rows m0 .. m0+15; each thread's chunks are
+  // all loaded before the first is used (H <= 384 * 8 -> at most 12 chunks)
+  {
+    constexpr int kChunks = kFusedLogitsMaxSteps;
+    const int i = tid >> 5, sub = tid & 31;
+    const int m = min(m0 + i, M - 1);
+    const uint16_t* row = h + (int64_t)m * H;
+    const int n8 = H >> 3;
+    u32x4_t v[kChunks];
+#pragma unroll
+    for (int q = 0; q < kChunks; ++q) {
+      const int c8 = sub + 32 * q;
+      v[q] = c8 < n8 ? ld16(row + 8 * c8) : u32x4_t{0u, 0u, 0u, 0u};
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int q = 0; q < kChunks; ++q) {
+      const uint32_t w4[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float lo = bf16_bits_to_f32(w4[t] & 0xFFFFu), hi = bf16_bits_to_f32(w4[t] >> 16);
+        ss = __builtin_fmaf(lo, lo, ss);
+        ss = __builtin_fmaf(hi, hi, ss);
+      }
+    }
+    s_part[i][sub] = ss;
+  }
+  __syncthreads();
+  if (tid < 16) {
+    float tot = 0.f;
+    for (int q = 0; q < 32; ++q) tot += s_part[tid][q];
+    s_inv[tid] = 1.0f / sqrtf(tot / (float)H + eps);
+  }
+  __syncthreads();
+
+  // phase 2: r for this split's k range -> afrag[step][lane(j = row, kb)]
+  for (int p = tid; p < nsteps * 64; p += kFusedLogitsThreads) {
+    const int c = p >> 6, l = p & 63;
+    const int rj = l & 15, rkb = l >> 4;
+    const int m = m0 + rj;
+    u32x4_t o = {0u, 0u, 0u, 0u};
+    if (m < M) {
+      const int k0 = 32 * (c0 + c) + 8 * rkb;
+      const u32x4_t xv = ld16(h + (int64_t)m * H + k0);
+      const u32x4_t sv = ld16(scale + k0);
+      const float inv = s_inv[rj];
+      const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w}, sw[4] = {sv.x, sv.y, sv.z, sv.w};
+      uint32_t ow[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float rr[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const float xe = bf16_bits_to_f32(hh ? (xw[q] >> 16) : (xw[q] & 0xFFFFu));
+          const float se = bf16_bits_to_f32(hh ? (sw[q] >> 16) : (sw[q] & 0xFFFFu));
+          const float v = round_bf16(xe * inv);
+          const float v2 = round_bf16(v * se);
+          rr[hh] = v2 * scalar_root;
+        }
+        ow[q] = pack_bf16x2(rr[0], rr[1]);
+      }
+      o = u32x4_t{ow[0], ow[1], ow[2], ow[3]};
+    }
+    afrag[c][l] = o;
+  }
+  __syncthreads();
+
+  // phase 3: logits of 16 tokens x 16 experts per wavefront
+  for (int eb = wave; eb * 16 < E; eb += NW) {
+    const int ee = eb * 16 + j;
+    if (eb != wave) {
+      const int eec = min(ee, E - 1);
+#pragma unroll
+      for (int c = 0; c < kFusedLogitsMaxSteps; ++c)
+        if (c < nsteps) bv[c] = ld16(proj + (int64_t)eec * H + 32 * (c0 + c) + 8 * kb);
+    }
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < kFusedLogitsMaxSteps; ++c)
+      if (c < nsteps) acc = mfma16(afrag[c][lane], bv[c], acc);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int mm = m0 + 4 * kb + q;
+      if (mm < M && ee < E) partial[((int64_t)ks * M + mm) * E + ee] = acc[q];
+    }
+  }
+}
+
+hipError_t launch_router_norm_logits(const uint16_t* h, const uint16_t* scale, float scalar_root,
+                                     float eps, const uint16_t* proj, float* partial, int M,
+                                     int H, int E, int ksplit, hipStream_t s) {
+  if (M == 0) return hipSuccess;
+  const int nchunks = H >> 5;
+  const int per = (nchunks + ksplit - 1) / ksplit;
+  if (per > kFusedLogitsMaxSteps) return hipErrorInvalidValue;
+  dim3 grid((M + 15) / 16, ksplit);
+  hipLaunchKernelGGL(k_router_norm_logits, grid, dim3(kFusedLogitsThreads), 0, s, h, scale,
+                     scalar_root, eps, proj, partial, M, H, E, per);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // softmax / top-k / renormalise: one wavefront per token, E <= 512
 // ---------------------------------------------------------------------------
 constexpr int kTopkPerLane = kMaxExperts / 64;
@@ -117,18 +303,16 @@ constexpr int kRouterMaxSplit = 8;
 // Routing of one token by one wavefront: bf16 logits (from K-split partials
 // or given), softmax denominator, top-k by (logit desc, index asc), weights.
 // Lane i < topk returns selection i in *sel_e / *sel_w.
-// KS = number of K-split partial sums to add (1 or kRouterMaxSplit), or 0 to
-// read finished bf16 logits; each lane holds experts lane + 64 q, q < PER
-// (PER = ceil(E / 64) rounded up to a power of two).  Every load of the token
-// is issued before any is used (addresses clamped into range, out-of-range
-// values masked after).
+// Logits of token m, lane holding experts lane + 64 q, q < PER (PER =
+// ceil(E / 64) rounded up to a power of two).  KS = number of K-split partial
+// sums to add (1 or kRouterMaxSplit), or 0 to read finished bf16 logits.  All
+// loads are issued before any is used (addresses clamped into range,
+// out-of-range values masked after); NaN becomes -inf so it never wins.
 template <int KS, int PER>
-__device__ void route_token(const float* __restrict__ partial,
-                            const uint16_t* __restrict__ logits_in,
-                            const uint16_t* __restrict__ pes, uint16_t* __restrict__ logits_out,
-                            int64_t m, int M, int E, int topk, int lane, int* sel_e,
-                            float* sel_w) {
-  float lg[PER];
+__device__ __forceinline__ void load_logits(const float* __restrict__ partial,
+                                            const uint16_t* __restrict__ logits_in,
+                                            uint16_t* __restrict__ logits_out, int64_t m, int M,
+                                            int E, int lane, float (&lg)[PER]) {
   const int per = (E + 63) >> 6;
   if (KS > 0) {
     float pv[PER][KS > 0 ? KS : 1];
@@ -149,7 +333,7 @@ __device__ void route_token(const float* __restrict__ partial,
       const bool ok = q < per && e < E;
       if (ok && logits_out != nullptr) logits_out[m * E + e] = b;
       const float v = bf16_bits_to_f32(b);
-      lg[q] = (ok && v == v) ? v : -INFINITY;  // NaN never wins a slot
+      lg[q] = (ok && v == v) ? v : -INFINITY;
     }
   } else {
     uint16_t lb[PER];
@@ -162,6 +346,14 @@ __device__ void route_token(const float* __restrict__ partial,
       lg[q] = (ok && v == v) ? v : -INFINITY;
     }
   }
+}
+
+// softmax (fp32) / top-k / renormalise / per_expert_scale of one token whose
+// logits `lg` were loaded by load_logits; lane `it` < topk returns selection it.
+template <int PER>
+__device__ void select_topk(const float (&lg)[PER], const uint16_t* __restrict__ pes, int E,
+                            int topk, int lane, int* sel_e, float* sel_w) {
+  const int per = (E + 63) >> 6;
   // softmax denominator over all experts (fp32)
   float mx = -INFINITY;
 #pragma unroll
@@ -210,6 +402,17 @@ __device__ void route_token(const float* __restrict__ partial,
   }
   *sel_e = my_i;
   *sel_w = (lane < topk) ? (my_p / psum) * bf16_bits_to_f32(pes[my_i]) : 0.f;
+}
+
+template <int KS, int PER>
+__device__ __forceinline__ void route_token(const float* __restrict__ partial,
+                                            const uint16_t* __restrict__ logits_in,
+                                            const uint16_t* __restrict__ pes,
+                                            uint16_t* __restrict__ logits_out, int64_t m, int M,
+                                            int E, int topk, int lane, int* sel_e, float* sel_w) {
+  float lg[PER];
+  load_logits<KS, PER>(partial, logits_in, logits_out, m, M, E, lane, lg);
+  select_topk<PER>(lg, pes, E, topk, lane, sel_e, sel_w);
 }
 
 template <int KS, int PER>
@@ -296,10 +499,13 @@ __device__ int block_excl_scan(int v, int* wsum, int* total) {
   return res;
 }
 
-__global__ __launch_bounds__(kSortThreads) void k_moe_sort(
-    const int64_t* __restrict__ idx_in, int M, int topk, int E, int32_t* __restrict__ sorted_pos,
-    int32_t* __restrict__ offsets, int32_t* __restrict__ desc, int32_t* __restrict__ counters,
-    int32_t* __restrict__ tiles, int BM) {
+// The counting sort, run by one workgroup of kSortThreads threads; expert_of(row)
+// returns the expert of row t*k+j (global memory or this workgroup's LDS).
+template <typename ExpertOf>
+__device__ void moe_sort_body(ExpertOf expert_of, int M, int topk, int E,
+                              int32_t* __restrict__ sorted_pos, int32_t* __restrict__ offsets,
+                              int32_t* __restrict__ desc, int32_t* __restrict__ counters,
+                              int32_t* __restrict__ tiles, int BM) {
   __shared__ int cnt[kMaxExperts];
   __shared__ int run[kMaxExperts];
   __shared__ int wcnt[kSortWaves][kMaxExperts];
@@ -307,7 +513,6 @@ __global__ __launch_bounds__(kSortThreads) void k_moe_sort(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int total = M * topk;
 
-  auto expert_of = [&](int row) -> int64_t { return idx_in[row]; };
 
   for (int e = tid; e < E; e += kSortThreads) {
     cnt[e] = 0;
@@ -385,6 +590,88 @@ __global__ __launch_bounds__(kSortThreads) void k_moe_sort(
     }
     __syncthreads();
   }
+}
+
+__global__ __launch_bounds__(kSortThreads) void k_moe_sort(
+    const int64_t* __restrict__ idx_in, int M, int topk, int E, int32_t* __restrict__ sorted_pos,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ desc, int32_t* __restrict__ counters,
+    int32_t* __restrict__ tiles, int BM) {
+  moe_sort_body([&](int row) -> int64_t { return idx_in[row]; }, M, topk, E, sorted_pos, offsets,
+                desc, counters, tiles, BM);
+}
+
+// Small batches: top-k of every token and the sort in one workgroup (no
+// hand-off between workgroups).  Wavefront w routes tokens w, w + 16, ...;
+// the routing also lands in LDS, which the sort reads.
+constexpr int kTopkSortMaxEntries = 512;
+constexpr int kTopkSortRounds = 4;  // tokens per wavefront: M <= 64
+
+template <int KS, int PER>
+__global__ __launch_bounds__(kSortThreads) void k_router_topk_sort(
+    const float* __restrict__ partial, const uint16_t* __restrict__ pes,
+    int64_t* __restrict__ idx_out, float* __restrict__ w_out, int M, int E, int topk,
+    int32_t* __restrict__ sorted_pos, int32_t* __restrict__ offsets, int32_t* __restrict__ desc,
+    int32_t* __restrict__ counters, int32_t* __restrict__ tiles, int BM) {
+  __shared__ int s_idx[kTopkSortMaxEntries];
+  __shared__ uint16_t s_pes[kMaxExperts];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  for (int e = threadIdx.x; e < E; e += kSortThreads) s_pes[e] = pes[e];
+  // every token of this wavefront (at most kTopkSortRounds) loaded up front
+  float lg[kTopkSortRounds][PER];
+#pragma unroll
+  for (int rr = 0; rr < kTopkSortRounds; ++rr)
+    load_logits<KS, PER>(partial, nullptr, nullptr, min(wave + kSortWaves * rr, M - 1), M, E, lane,
+                         lg[rr]);
+  __syncthreads();  // s_pes
+#pragma unroll
+  for (int rr = 0; rr < kTopkSortRounds; ++rr) {
+    const int m = wave + kSortWaves * rr;
+    if (m >= M) break;  // uniform per wavefront
+    int se;
+    float sw;
+    select_topk<PER>(lg[rr], s_pes, E, topk, lane, &se, &sw);
+    if (lane < topk) {
+      idx_out[(int64_t)m * topk + lane] = se;
+      w_out[(int64_t)m * topk + lane] = sw;
+      s_idx[m * topk + lane] = se;
+    }
+  }
+  __syncthreads();
+  moe_sort_body([&](int row) -> int64_t { return s_idx[row]; }, M, topk, E, sorted_pos, offsets,
+                desc, counters, tiles, BM);
+}
+
+template <int KS>
+static void launch_topk_sort_ks(const float* partial, const uint16_t* pes, int64_t* idx, float* w,
+                                int M, int E, int topk, int32_t* sorted_pos, int32_t* offsets,
+                                int32_t* desc, int32_t* counters, int32_t* tiles, int BM,
+                                hipStream_t s) {
+#define W4A16_TS(P_)                                                                          \
+  hipLaunchKernelGGL((k_router_topk_sort<KS, P_>), dim3(1), dim3(kSortThreads), 0, s, partial, \
+                     pes, idx, w, M, E, topk, sorted_pos, offsets, desc, counters, tiles, BM)
+  if (E <= 64) W4A16_TS(1);
+  else if (E <= 128) W4A16_TS(2);
+  else if (E <= 256) W4A16_TS(4);
+  else W4A16_TS(kTopkPerLane);
+#undef W4A16_TS
+}
+
+hipError_t launch_topk_sort(const float* partial, int ksplit, const uint16_t* per_expert_scale,
+                            int64_t* idx, float* w, int M, int E, int topk, int32_t* sorted_pos,
+                            int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
+                            int BM, hipStream_t s) {
+  if (M == 0) return hipSuccess;
+  if (M * topk > kTopkSortMaxEntries || M > kTopkSortRounds * kSortWaves) return hipErrorInvalidValue;
+  if (ksplit == kRouterMaxSplit)
+    launch_topk_sort_ks<kRouterMaxSplit>(partial, per_expert_scale, idx, w, M, E, topk,
+                                         sorted_pos, offsets, desc, counters, tiles, BM, s);
+  else if (ksplit == 1)
+    launch_topk_sort_ks<1>(partial, per_expert_scale, idx, w, M, E, topk, sorted_pos, offsets,
+                           desc, counters, tiles, BM, s);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
 }
 
 hipError_t launch_sort(const int64_t* idx, int M, int topk, int E, int32_t* sorted_pos,

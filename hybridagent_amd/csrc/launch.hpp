@@ -67,6 +67,16 @@ hipError_t launch_router_norm(const uint16_t* h, const uint16_t* scale, float sc
                               float eps, uint16_t* r, int M, int H, hipStream_t s);
 hipError_t launch_router_logits(const uint16_t* r, const uint16_t* proj, float* partial, int M,
                                 int H, int E, int ksplit, hipStream_t s);
+// RMSNorm + logits partials in one launch; K split by ksplit with at most
+// 12 steps of 32 per split (H <= 384 * ksplit)
+hipError_t launch_router_norm_logits(const uint16_t* h, const uint16_t* scale, float scalar_root,
+                                     float eps, const uint16_t* proj, float* partial, int M,
+                                     int H, int E, int ksplit, hipStream_t s);
+// top-k and expert sort in one workgroup, M * topk <= 512
+hipError_t launch_topk_sort(const float* partial, int ksplit, const uint16_t* per_expert_scale,
+                            int64_t* idx, float* w, int M, int E, int topk, int32_t* sorted_pos,
+                            int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
+                            int BM, hipStream_t s);
 hipError_t launch_router_topk(const float* partial, int ksplit, const uint16_t* logits_in,
                               const uint16_t* per_expert_scale, uint16_t* logits_out,
                               int64_t* idx, float* w, int M, int E, int topk, hipStream_t s);
