@@ -70,13 +70,13 @@ template <int MODE, int BM>
 __global__ __launch_bounds__(kPfThreads) void k_prefill(PrefillArgs a) {
   constexpr int FM = BM / 32;       // 16-row fragments per wavefront
   constexpr int FN = 4;             // 16-column fragments per wavefront
-  constexpr int RB = BM / 64;       // row blocks each thread stages
-  constexpr int AR = 2 * RB;        // A loads per thread per stage
-  constexpr int A_SLOTS = BM * 8;   // 16-byte slots per A stage
+  constexpr int AR = BM / 32;       // A rows each thread stages (one 16-byte chunk each)
+  constexpr int A_PITCH = 9;        // 16-byte slots per A row: 8 chunks + 1 pad
+  constexpr int A_SLOTS = BM * A_PITCH;
   constexpr int B_SLOTS = kPfBN * 8;
   constexpr int STAGE = A_SLOTS + B_SLOTS;
   constexpr int D = kPfDepth;
-  __shared__ u32x4_t lds[2 * STAGE];
+  extern __shared__ u32x4_t lds[];  // 2 * STAGE slots (prefill_lds_bytes)
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -95,10 +95,14 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill(PrefillArgs a) {
   const int chunk = (total + 7) >> 3;
   const int it_end = min(total, (xcd + 1) * chunk);
 
-  // Staging roles, chosen so that each wavefront's 16-byte LDS stores of one
-  // instruction cover one contiguous 1 KiB fragment (no bank conflicts):
-  //  A: row blocks wave + 4 i (i < RB), row (lane & 15), k chunk 4 h + lane/16
-  //  B: tile column (tid & 15) + 16 (tid >> 5), k half (tid >> 4) & 1
+  // Staging roles:
+  //  A: rows (tid >> 3) + 32 i, 16-byte chunk tid & 7 -- one load instruction
+  //     reads 8 whole 128-byte row segments; rows sit in LDS at a pitch of 144
+  //     bytes, so both these stores and the fragment reads below (lane l: row
+  //     l % 16, chunk l / 16) touch distinct banks;
+  //  B: tile column (tid & 15) + 16 (tid >> 5), k half (tid >> 4) & 1, stored
+  //     in fragment order (each store instruction covers 1 KiB contiguously).
+  const int ar0 = tid >> 3, ac = tid & 7;
   const int bn = (tid & 15) + 16 * (tid >> 5);
   const int bh = (tid >> 4) & 1;
   const uint32_t m0f = opaque(0x0F0F0F0Fu);
@@ -113,18 +117,21 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill(PrefillArgs a) {
 
     // activation row sources (rows past the segment repeat its last row;
     // their results are never stored)
-    const uint16_t* arow[RB];
+    const uint16_t* arow[AR];
 #pragma unroll
-    for (int i = 0; i < RB; ++i) {
-      const int rr = min(16 * (wave + 4 * i) + (lane & 15), nrows - 1);
-      const int chunk8 = (lane >> 4) * 8;
+    for (int i = 0; i < AR; ++i) {
+      const int rr = min(ar0 + 32 * i, nrows - 1);
       if (MODE == kModeGateUp) {
         const int tok = a.sorted_pos[seg0 + rr] / a.topk;
-        arow[i] = a.act + (int64_t)tok * K + chunk8;
+        arow[i] = a.act + (int64_t)tok * K + ac * 8;
       } else {
-        arow[i] = a.act + (int64_t)(seg0 + rr) * K + chunk8;
+        arow[i] = a.act + (int64_t)(seg0 + rr) * K + ac * 8;
       }
     }
+    // 16-row fragments of this wavefront that hold real rows: MFMA work on
+    // fragments made only of padding rows is skipped
+    const int nvf = __builtin_amdgcn_readfirstlane(
+        max(0, min(FM, (nrows - wm * (BM / 2) + 15) >> 4)));
     int ncol;
     if (MODE == kModeGateUp)
       ncol = bn < 64 ? nt * 64 + bn : a.I + nt * 64 + (bn - 64);
@@ -139,20 +146,14 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill(PrefillArgs a) {
     uint16_t rs[D];
     auto load_stage = [&](int slot, int ks) {
 #pragma unroll
-      for (int i = 0; i < RB; ++i) {
-        ra[slot][2 * i] = ld16(arow[i] + ks * kPfBK);
-        ra[slot][2 * i + 1] = ld16(arow[i] + ks * kPfBK + 32);
-      }
+      for (int i = 0; i < AR; ++i) ra[slot][i] = ld16(arow[i] + ks * kPfBK);
       rw[slot] = ld16(wsrc + ks * 8);
       rs[slot] = ssrc[(ks * kPfBK + 32 * bh) / a.G];
     };
     auto store_stage = [&](int buf, int slot) {
       u32x4_t* base = lds + buf * STAGE;
 #pragma unroll
-      for (int i = 0; i < RB; ++i) {
-        base[((wave + 4 * i) * 2 + 0) * 64 + lane] = ra[slot][2 * i];
-        base[((wave + 4 * i) * 2 + 1) * 64 + lane] = ra[slot][2 * i + 1];
-      }
+      for (int i = 0; i < AR; ++i) base[(ar0 + 32 * i) * A_PITCH + ac] = ra[slot][i];
       const float sc = bf16_bits_to_f32(rs[slot]);
       const float m8 = -8.0f * sc;
       u32x4_t* bb = base + A_SLOTS + (((bn >> 4) << 1) + bh) * 64 + (bn & 15);
@@ -174,14 +175,18 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill(PrefillArgs a) {
       for (int h = 0; h < 2; ++h) {
         u32x4_t af[FM], bf[FN];
 #pragma unroll
-        for (int i = 0; i < FM; ++i) af[i] = base[((wm * FM + i) * 2 + h) * 64 + lane];
+        for (int i = 0; i < FM; ++i)
+          if (i < nvf)
+            af[i] = base[((wm * FM + i) * 16 + (lane & 15)) * A_PITCH + 4 * h + (lane >> 4)];
 #pragma unroll
         for (int j = 0; j < FN; ++j)
           bf[j] = base[A_SLOTS + (col_block<MODE>(wn, j) * 2 + h) * 64 + lane];
 #pragma unroll
         for (int i = 0; i < FM; ++i)
+          if (i < nvf) {
 #pragma unroll
-          for (int j = 0; j < FN; ++j) acc[i][j] = mfma16(af[i], bf[j], acc[i][j]);
+            for (int j = 0; j < FN; ++j) acc[i][j] = mfma16(af[i], bf[j], acc[i][j]);
+          }
       }
     };
 
@@ -253,27 +258,39 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill(PrefillArgs a) {
   }
 }
 
-int prefill_grid(int max_items) {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0;
-    hipDeviceProp_t p;
-    if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess)
-      cus = p.multiProcessorCount;
-    if (cus <= 0) cus = 256;
-  }
-  int g = cus * 2;  // two workgroups per CU (64 KiB LDS each)
+size_t prefill_lds_bytes(int BM) {
+  return (size_t)2 * (BM * 9 + kPfBN * 8) * 16;
+}
+
+// persistent grid: the workgroups that fit on the device at once (a multiple
+// of the 8 XCDs), at most one per item
+template <typename Kern>
+int prefill_grid(Kern kern, size_t lds, int max_items) {
+  int dev = 0, cus = 256, per_cu = 1;
+  hipDeviceProp_t p;
+  if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess &&
+      p.multiProcessorCount > 0)
+    cus = p.multiProcessorCount;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kPfThreads, lds) != hipSuccess ||
+      per_cu <= 0)
+    per_cu = 1;
+  int g = cus * per_cu;
   if (max_items < g) g = max_items;
   return ((g + 7) / 8) * 8;
 }
 
 hipError_t launch_prefill(int mode, PrefillArgs a, int max_mtiles, hipStream_t s) {
   if (max_mtiles <= 0) return hipSuccess;
-  const int grid = prefill_grid(max_mtiles * a.n_nt);
-  if (mode == kModeGateUp)
-    hipLaunchKernelGGL((k_prefill<kModeGateUp, kPrefillBM>), dim3(grid), dim3(kPfThreads), 0, s, a);
-  else
-    hipLaunchKernelGGL((k_prefill<kModeDown, kPrefillBM>), dim3(grid), dim3(kPfThreads), 0, s, a);
+  const size_t lds = prefill_lds_bytes(kPrefillBM);
+  if (mode == kModeGateUp) {
+    auto kern = k_prefill<kModeGateUp, kPrefillBM>;
+    hipLaunchKernelGGL(kern, dim3(prefill_grid(kern, lds, max_mtiles * a.n_nt)), dim3(kPfThreads),
+                       lds, s, a);
+  } else {
+    auto kern = k_prefill<kModeDown, kPrefillBM>;
+    hipLaunchKernelGGL(kern, dim3(prefill_grid(kern, lds, max_mtiles * a.n_nt)), dim3(kPfThreads),
+                       lds, s, a);
+  }
   return hipGetLastError();
 }
 
