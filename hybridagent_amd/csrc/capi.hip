@@ -37,6 +37,8 @@ inline int router_ksplit(int64_t M) { return M <= 64 ? 8 : 1; }
 // Token counts up to this use the decode kernels; larger batches the
 // prefill grouped-GEMM kernels.
 constexpr int64_t kDecodeMaxM = 256;
+// routed rows above this sort over several workgroups (two launches)
+constexpr int64_t kSortMultiMinRows = 2048;
 // routed rows up to this run top-k and the expert sort in one workgroup
 // (measured faster than two launches up to M = 8 at top-8; slower from M = 32)
 constexpr int64_t kTopkSortMaxEntries = 64;
@@ -67,6 +69,7 @@ struct MoeLayout {
   int32_t* counters;
   int32_t* sorted_pos;
   int32_t* tiles;
+  int32_t* blockcnt;
   uint16_t* inter;
   uint16_t* dn;
   size_t bytes;
@@ -80,6 +83,7 @@ MoeLayout moe_layout(void* ws, int64_t M, int64_t k, int64_t E, int64_t H, int64
   L.counters = c.take<int32_t>(2);
   L.sorted_pos = c.take<int32_t>(M * k);
   L.tiles = c.take<int32_t>(M * k / kPrefillBM + E + 1);
+  L.blockcnt = c.take<int32_t>(size_t(sort_blocks(M * k)) * E);
   L.inter = c.take<uint16_t>(M * k * I);
   L.dn = c.take<uint16_t>(M * k * H);
   L.bytes = c.used;
@@ -203,7 +207,8 @@ int moe_topk_from_logits(const uint16_t* logits, const uint16_t* per_expert_scal
 
 size_t moe_sort_workspace_bytes(int64_t M, int64_t top_k, int64_t E) {
   if (M <= 0 || top_k <= 0 || E <= 0) return 0;
-  return round256(size_t(E) * 16) + round256(8) + round256(size_t(M * top_k / kPrefillBM + E + 1) * 4);
+  return round256(size_t(E) * 16) + round256(8) + round256(size_t(M * top_k / kPrefillBM + E + 1) * 4) +
+         round256(size_t(sort_blocks(M * top_k)) * E * 4);
 }
 
 int moe_sort_permute(const int64_t* topk_idx, int64_t M, int64_t top_k, int64_t E,
@@ -220,9 +225,14 @@ int moe_sort_permute(const int64_t* topk_idx, int64_t M, int64_t top_k, int64_t 
   int32_t* desc = c.take<int32_t>(4 * E);
   int32_t* counters = c.take<int32_t>(2);
   int32_t* tiles = c.take<int32_t>(M * top_k / kPrefillBM + E + 1);
+  int32_t* blockcnt = c.take<int32_t>(size_t(sort_blocks(M * top_k)) * E);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (M * top_k > kSortMultiMinRows)
+    return launch_status(launch_sort_multi(topk_idx, (int)M, (int)top_k, (int)E, sorted_pos,
+                                           expert_offsets, desc, counters, tiles, blockcnt,
+                                           kPrefillBM, s));
   return launch_status(launch_sort(topk_idx, (int)M, (int)top_k, (int)E, sorted_pos,
-                                   expert_offsets, desc, counters, tiles, kPrefillBM,
-                                   static_cast<hipStream_t>(stream)));
+                                   expert_offsets, desc, counters, tiles, kPrefillBM, s));
 }
 
 size_t moe_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I) {
@@ -303,8 +313,12 @@ int moe_plan(const uint16_t* hidden, const int64_t* topk_idx, int64_t M, int64_t
   if (!hidden || !topk_idx) return W4A16_ERR_NULL;
   if (!aligned16(hidden)) return W4A16_ERR_ALIGN;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e = launch_sort(topk_idx, (int)M, (int)top_k, (int)E, L.sorted_pos, L.offsets,
-                             L.desc, L.counters, L.tiles, kPrefillBM, s);
+  hipError_t e =
+      M * top_k > kSortMultiMinRows
+          ? launch_sort_multi(topk_idx, (int)M, (int)top_k, (int)E, L.sorted_pos, L.offsets,
+                              L.desc, L.counters, L.tiles, L.blockcnt, kPrefillBM, s)
+          : launch_sort(topk_idx, (int)M, (int)top_k, (int)E, L.sorted_pos, L.offsets, L.desc,
+                        L.counters, L.tiles, kPrefillBM, s);
   return launch_status(e);
 }
 

@@ -499,6 +499,38 @@ __device__ int block_excl_scan(int v, int* wsum, int* total) {
   return res;
 }
 
+// From the per-expert counts (thread e holds expert e's count c, e < E <= 512):
+// the segment offsets, one work descriptor per active expert and the m-tile
+// list; written when `write` (one workgroup writes them).  Returns thread e's
+// segment start.  All threads of the kSortThreads-thread workgroup call it.
+__device__ int write_plan(int c, int E, int32_t* __restrict__ offsets, int32_t* __restrict__ desc,
+                          int32_t* __restrict__ counters, int32_t* __restrict__ tiles, int BM,
+                          int* wsum, bool write) {
+  const int tid = threadIdx.x;
+  int tot;
+  const int off = block_excl_scan(c, wsum, &tot);
+  int nact;
+  const int apos = block_excl_scan(c > 0 ? 1 : 0, wsum, &nact);
+  const int nt = (c + BM - 1) / BM;
+  int ntiles;
+  const int tpos = block_excl_scan(nt, wsum, &ntiles);
+  if (write) {
+    if (tid < E) offsets[tid] = off;
+    if (tid == 0) {
+      offsets[E] = tot;
+      counters[0] = nact;
+      counters[1] = ntiles;
+    }
+    if (tid < E && c > 0) {
+      const int4 d = make_int4(tid, off, c, 0);
+      *reinterpret_cast<int4*>(desc + 4 * apos) = d;
+    }
+    if (tid < E)
+      for (int i = 0; i < nt; ++i) tiles[tpos + i] = (tid << 16) | i;
+  }
+  return off;
+}
+
 // The counting sort, run by one workgroup of kSortThreads threads; expert_of(row)
 // returns the expert of row t*k+j (global memory or this workgroup's LDS).
 template <typename ExpertOf>
@@ -526,29 +558,9 @@ __device__ void moe_sort_body(ExpertOf expert_of, int M, int topk, int E,
   __syncthreads();
 
   // offsets, work descriptors and tile list (E <= 512 < 1024 threads)
-  const int c = tid < E ? cnt[tid] : 0;
-  int tot;
-  const int off = block_excl_scan(c, wsum, &tot);
-  if (tid < E) {
-    offsets[tid] = off;
-    run[tid] = off;
-  }
-  if (tid == 0) offsets[E] = tot;
-  int nact;
-  const int apos = block_excl_scan(c > 0 ? 1 : 0, wsum, &nact);
-  if (tid < E && c > 0) {
-    const int4 d = make_int4(tid, off, c, 0);
-    *reinterpret_cast<int4*>(desc + 4 * apos) = d;
-  }
-  const int nt = (c + BM - 1) / BM;
-  int ntiles;
-  const int tpos = block_excl_scan(nt, wsum, &ntiles);
-  if (tid < E)
-    for (int i = 0; i < nt; ++i) tiles[tpos + i] = (tid << 16) | i;
-  if (tid == 0) {
-    counters[0] = nact;
-    counters[1] = ntiles;
-  }
+  const int off = write_plan(tid < E ? cnt[tid] : 0, E, offsets, desc, counters, tiles, BM, wsum,
+                             true);
+  if (tid < E) run[tid] = off;
   __syncthreads();
 
   // stable scatter in k-major order p = j*M + t
@@ -671,6 +683,97 @@ hipError_t launch_topk_sort(const float* partial, int ksplit, const uint16_t* pe
                            desc, counters, tiles, BM, s);
   else
     return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+// Large batches: the same stable sort over several workgroups, in two
+// launches.  Workgroup b owns k-major positions [b*kSortThreads,
+// (b+1)*kSortThreads).  k_sort_hist counts its experts; k_sort_scatter
+// derives every expert's segment start and the counts of the blocks before
+// its own from all blocks' histograms, then ranks its entries exactly as the
+// one-workgroup sort does (stable within the block) and scatters them.
+// Workgroup 0 also writes the offsets, descriptors and tile list.
+__global__ __launch_bounds__(kSortThreads) void k_sort_hist(const int64_t* __restrict__ idx,
+                                                           int M, int topk, int E,
+                                                           int32_t* __restrict__ blockcnt) {
+  __shared__ int cnt[kMaxExperts];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += kSortThreads) cnt[e] = 0;
+  __syncthreads();
+  const int total = M * topk;
+  const int p = blockIdx.x * kSortThreads + tid;
+  if (p < total) {
+    const int jj = p / M, t = p - jj * M;
+    const int64_t e = idx[(int64_t)t * topk + jj];
+    if (e >= 0 && e < E) atomicAdd(&cnt[(int)e], 1);
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += kSortThreads) blockcnt[(int64_t)blockIdx.x * E + e] = cnt[e];
+}
+
+__global__ __launch_bounds__(kSortThreads) void k_sort_scatter(
+    const int64_t* __restrict__ idx, int M, int topk, int E, const int32_t* __restrict__ blockcnt,
+    int32_t* __restrict__ sorted_pos, int32_t* __restrict__ offsets, int32_t* __restrict__ desc,
+    int32_t* __restrict__ counters, int32_t* __restrict__ tiles, int BM) {
+  __shared__ int base[kMaxExperts];
+  __shared__ int wcnt[kSortWaves][kMaxExperts];
+  __shared__ int wsum[kSortWaves];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = blockIdx.x, nb = gridDim.x;
+  // expert totals and the counts of the blocks before this one
+  int tot = 0, pre = 0;
+  if (tid < E) {
+    for (int q = 0; q < nb; ++q) {
+      const int c = blockcnt[(int64_t)q * E + tid];
+      tot += c;
+      pre += q < b ? c : 0;
+    }
+  }
+  for (int e = tid; e < E; e += kSortThreads)
+    for (int w = 0; w < kSortWaves; ++w) wcnt[w][e] = 0;
+  const int off = write_plan(tot, E, offsets, desc, counters, tiles, BM, wsum, b == 0);
+  if (tid < E) base[tid] = off + pre;
+  __syncthreads();
+
+  int nbits = 0;
+  while ((1 << nbits) < E) ++nbits;
+  const unsigned long long lt_mask = (1ull << lane) - 1ull;
+  const int total = M * topk;
+  const int p = b * kSortThreads + tid;
+  int e = -1, row = 0;
+  if (p < total) {
+    const int jj = p / M, t = p - jj * M;
+    row = t * topk + jj;
+    const int64_t ev = idx[row];
+    if (ev >= 0 && ev < E) e = (int)ev;
+  }
+  const bool ok = e >= 0;
+  unsigned long long same = __ballot(ok);
+  for (int bit = 0; bit < nbits; ++bit) {
+    const bool on = ok && ((e >> bit) & 1);
+    const unsigned long long bb = __ballot(on);
+    same &= on ? bb : ~bb;
+  }
+  const int rank = __popcll(same & lt_mask);
+  if (ok && (same & lt_mask) == 0ull) wcnt[wave][e] = __popcll(same);
+  __syncthreads();
+  if (ok) {
+    int q = base[e];
+    for (int w = 0; w < wave; ++w) q += wcnt[w][e];
+    sorted_pos[q + rank] = row;
+  }
+}
+
+int sort_blocks(int64_t rows) { return (int)((rows + kSortThreads - 1) / kSortThreads); }
+
+hipError_t launch_sort_multi(const int64_t* idx, int M, int topk, int E, int32_t* sorted_pos,
+                             int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
+                             int32_t* blockcnt, int BM, hipStream_t s) {
+  const int nb = sort_blocks((int64_t)M * topk);
+  if (nb <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_sort_hist, dim3(nb), dim3(kSortThreads), 0, s, idx, M, topk, E, blockcnt);
+  hipLaunchKernelGGL(k_sort_scatter, dim3(nb), dim3(kSortThreads), 0, s, idx, M, topk, E, blockcnt,
+                     sorted_pos, offsets, desc, counters, tiles, BM);
   return hipGetLastError();
 }
 

@@ -63,6 +63,12 @@ hipError_t launch_combine(const uint16_t* dn, const int64_t* idx, const float* w
 hipError_t launch_sort(const int64_t* idx, int M, int topk, int E, int32_t* sorted_pos,
                        int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
                        int BM, hipStream_t s);
+// the sort over several workgroups (large batches); blockcnt holds
+// sort_blocks(M * topk) * E ints
+int sort_blocks(int64_t rows);
+hipError_t launch_sort_multi(const int64_t* idx, int M, int topk, int E, int32_t* sorted_pos,
+                             int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
+                             int32_t* blockcnt, int BM, hipStream_t s);
 hipError_t launch_router_norm(const uint16_t* h, const uint16_t* scale, float scalar_root,
                               float eps, uint16_t* r, int M, int H, hipStream_t s);
 hipError_t launch_router_logits(const uint16_t* r, const uint16_t* proj, float* partial, int M,
