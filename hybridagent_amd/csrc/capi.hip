@@ -57,6 +57,10 @@ hipError_t launch_router_partials(const uint16_t* hidden, const uint16_t* scale,
   if (ks == 8 && H <= 384 * 8)
     return launch_router_norm_logits(hidden, scale, root, eps, proj, partial, (int)M, (int)H,
                                      (int)E, ks, s);
+  // large batches: the norm inside a tiled logits GEMM (64 tokens x 32 experts
+  // per workgroup over the whole K)
+  if (ks == 1 && H % 64 == 0)
+    return launch_router_big(hidden, scale, root, eps, proj, partial, (int)M, (int)H, (int)E, s);
   hipError_t e = launch_router_norm(hidden, scale, root, eps, r, (int)M, (int)H, s);
   if (e == hipSuccess) e = launch_router_logits(r, proj, partial, (int)M, (int)H, (int)E, ks, s);
   return e;

@@ -295,6 +295,177 @@ hipError_t launch_router_norm_logits(const uint16_t* h, const uint16_t* scale, f
 }
 
 // ---------------------------------------------------------------------------
+// router RMSNorm + logits for large batches: one workgroup per (64 tokens, 32
+// experts) over the whole K.  Prologue: the rows' sums of squares (4 threads
+// per row, fixed order, then a quad reduction).  Main loop over 64-wide k
+// stages: r = bf16(bf16(bf16(x * inv) * scale) * root) is formed on the fly
+// into LDS (MFMA A-operand order) next to the stage's router-weight tile;
+// wavefront w multiplies token block w against the two expert blocks.  The
+// next stage's global loads are in flight during the current stage's MFMA.
+// ---------------------------------------------------------------------------
+constexpr int kBigTok = 64, kBigExp = 32, kBigBK = 64, kBigDepth = 4;
+
+__global__ __launch_bounds__(256) void k_router_big(const uint16_t* __restrict__ h,
+                                                   const uint16_t* __restrict__ scale,
+                                                   float scalar_root, float eps,
+                                                   const uint16_t* __restrict__ proj,
+                                                   float* __restrict__ logits, int M, int H,
+                                                   int E) {
+  // fragment order: A [row block 4][k32 2][lane 64], B [col block 2][k32 2][lane 64]
+  __shared__ u32x4_t sa[2][4 * 2 * 64];
+  __shared__ u32x4_t sb[2][2 * 2 * 64];
+  __shared__ float s_inv[kBigTok];
+  __shared__ float s_ss[kBigTok][4];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int m0 = blockIdx.x * kBigTok, e0 = blockIdx.y * kBigExp;
+  const int n8 = H >> 3;
+
+  // prologue: sums of squares, 4 threads per row
+  {
+    const int r = tid >> 2, sub = tid & 3;
+    const uint16_t* row = h + (int64_t)min(m0 + r, M - 1) * H;
+    float ss = 0.f;
+    for (int c8 = sub; c8 < n8; c8 += 4 * 8) {
+      u32x4_t v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int c = c8 + 4 * u;
+        v[u] = c < n8 ? ld16(row + 8 * c) : u32x4_t{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const uint32_t w4[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float lo = bf16_bits_to_f32(w4[t] & 0xFFFFu), hi = bf16_bits_to_f32(w4[t] >> 16);
+          ss = __builtin_fmaf(lo, lo, ss);
+          ss = __builtin_fmaf(hi, hi, ss);
+        }
+      }
+    }
+    // the row's four partials, summed in thread order
+    s_ss[r][sub] = ss;
+    __syncthreads();
+    if (tid < kBigTok) {
+      const float tot = ((s_ss[tid][0] + s_ss[tid][1]) + s_ss[tid][2]) + s_ss[tid][3];
+      s_inv[tid] = 1.0f / sqrtf(tot / (float)H + eps);
+    }
+    __syncthreads();
+  }
+
+  // staging roles: A chunks (row ar, 8-wide k chunk ac) x2, B chunks x1
+  // A: 64 rows x 8 chunks = 512 -> threads tid, tid + 256; B: 32 experts x 8 chunks = 256
+  auto a_role = [&](int q, int* row, int* chunk) {
+    const int id = tid + 256 * q;
+    *row = id >> 3;
+    *chunk = id & 7;
+  };
+  const int br = tid >> 3, bc = tid & 7;
+  const int be = min(e0 + br, E - 1);
+  const bool be_ok = e0 + br < E;
+
+  // kBigDepth stages of global loads in flight (register slots)
+  u32x4_t gx[kBigDepth][2], gs[kBigDepth][2], gp[kBigDepth];
+  auto load_stage = [&](int slot, int ks) {
+    const int kbase = ks * kBigBK;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      int row, chunk;
+      a_role(q, &row, &chunk);
+      const int m = min(m0 + row, M - 1);
+      gx[slot][q] = ld16(h + (int64_t)m * H + kbase + 8 * chunk);
+      gs[slot][q] = ld16(scale + kbase + 8 * chunk);
+    }
+    gp[slot] = ld16(proj + (int64_t)be * H + kbase + 8 * bc);
+  };
+  auto store_stage = [&](int buf, int slot) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      int row, chunk;
+      a_role(q, &row, &chunk);
+      u32x4_t o = {0u, 0u, 0u, 0u};
+      if (m0 + row < M) {
+        const float inv = s_inv[row];
+        const uint32_t xw[4] = {gx[slot][q].x, gx[slot][q].y, gx[slot][q].z, gx[slot][q].w};
+        const uint32_t sw[4] = {gs[slot][q].x, gs[slot][q].y, gs[slot][q].z, gs[slot][q].w};
+        uint32_t ow[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          float rr[2];
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const float xe = bf16_bits_to_f32(hh ? (xw[t] >> 16) : (xw[t] & 0xFFFFu));
+            const float se = bf16_bits_to_f32(hh ? (sw[t] >> 16) : (sw[t] & 0xFFFFu));
+            const float v1 = round_bf16(xe * inv);
+            const float v2 = round_bf16(v1 * se);
+            rr[hh] = v2 * scalar_root;
+          }
+          ow[t] = pack_bf16x2(rr[0], rr[1]);
+        }
+        o = u32x4_t{ow[0], ow[1], ow[2], ow[3]};
+      }
+      // row block row/16, k32 chunk/4, lane (row%16) + 16 (chunk%4)
+      sa[buf][((row >> 4) * 2 + (chunk >> 2)) * 64 + (row & 15) + 16 * (chunk & 3)] = o;
+    }
+    sb[buf][((br >> 4) * 2 + (bc >> 2)) * 64 + (br & 15) + 16 * (bc & 3)] =
+        be_ok ? gp[slot] : u32x4_t{0u, 0u, 0u, 0u};
+  };
+
+  f32x4_t acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  const int nks = H / kBigBK;
+  constexpr int D = kBigDepth;
+#pragma unroll
+  for (int d = 0; d < D; ++d) load_stage(d, min(d, nks - 1));
+  store_stage(0, 0);
+  __syncthreads();
+  // stage s: slot s % D (already in LDS buffer s & 1) is refilled with stage
+  // s + D; stage s + 1 (slot (s + 1) % D) goes to the other buffer.  Stages
+  // past the end reload the last one (in bounds, unused).
+  for (int k0 = 0; k0 < nks; k0 += D) {
+#pragma unroll
+    for (int u = 0; u < D; ++u) {
+      const int ks = k0 + u;
+      if (ks < nks) {
+        const int cur = ks & 1;
+        load_stage(u, min(ks + D, nks - 1));
+#pragma unroll
+        for (int k32 = 0; k32 < 2; ++k32) {
+          const u32x4_t av = sa[cur][(wave * 2 + k32) * 64 + lane];
+#pragma unroll
+          for (int cb = 0; cb < 2; ++cb)
+            acc[cb] = mfma16(av, sb[cur][(cb * 2 + k32) * 64 + lane], acc[cb]);
+        }
+        store_stage(cur ^ 1, (u + 1) % D);
+        __syncthreads();
+      }
+    }
+  }
+  // D lane l: rows 4*(l/16)+q (tokens), column l%16 (experts)
+  const int kb = lane >> 4, j = lane & 15;
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    const int e = e0 + cb * 16 + j;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int m = m0 + wave * 16 + 4 * kb + q;
+      if (m < M && e < E) logits[(int64_t)m * E + e] = acc[cb][q];
+    }
+  }
+}
+
+hipError_t launch_router_big(const uint16_t* h, const uint16_t* scale, float scalar_root,
+                             float eps, const uint16_t* proj, float* logits, int M, int H, int E,
+                             hipStream_t s) {
+  if (M == 0) return hipSuccess;
+  if (H % kBigBK != 0) return hipErrorInvalidValue;
+  dim3 grid((M + kBigTok - 1) / kBigTok, (E + kBigExp - 1) / kBigExp);
+  hipLaunchKernelGGL(k_router_big, grid, dim3(256), 0, s, h, scale, scalar_root, eps, proj,
+                     logits, M, H, E);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // softmax / top-k / renormalise: one wavefront per token, E <= 512
 // ---------------------------------------------------------------------------
 constexpr int kTopkPerLane = kMaxExperts / 64;
