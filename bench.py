@@ -51,6 +51,7 @@ GATEUP_BYTES = 2 * I * H // 2 + 2 * I * math.ceil(H / G) * 2
 ROUTER_BYTES = E * H * 2
 DECODE_MS = (1, 8, 32, 64)
 PREFILL_M = 4096
+LATENT_LAYERS, LATENT_BATCH, LATENT_STEPS = 30, 32, 16
 
 
 def log(msg: str) -> None:
@@ -208,6 +209,34 @@ def calibrate_copy(dev) -> int:
     return 0
 
 
+def latent(dev, steps: int = LATENT_STEPS):
+    """30 MoE layers (h += MoE(RMSNorm(h))) + HybridLink x sqrt(H),
+    batch 32, the output fed back as the next step's input.  One HIP graph
+    replay = one latent step."""
+    from hybridagent_amd.latent import LatentStack
+    st = LatentStack(LATENT_LAYERS, E, H, I, TOPK, G, seed=7777, device=dev)
+    h0 = synth.activations(LATENT_BATCH, H, seed=7778, device=dev)
+    uniq, h = [], h0.clone()
+    for i in range(LATENT_LAYERS):  # distinct experts per layer on the first step
+        h, idx, _ = st.layer(h, i)
+        uniq.append(int(torch.unique(idx).numel()))
+    buf = h0.clone()
+
+    def run():
+        buf.copy_(st.step(buf))
+
+    t = time_graph(run, 1, steps, 4)
+    nbytes = sum(uniq) * EXPERT_BYTES + LATENT_LAYERS * ROUTER_BYTES + 2 * H * H * 2
+    res = {"ms_per_step": t * 1e3, "us_per_token": t * 1e6 / LATENT_BATCH, "layers": LATENT_LAYERS,
+           "batch": LATENT_BATCH, "steps": steps, "unique_experts_per_layer": sum(uniq) / len(uniq),
+           "bytes_per_step": nbytes, "gbps": nbytes / t / 1e9, "frac_hbm": nbytes / t / 1e9 / PEAK_HBM_GBS}
+    log(f"latent stack: {t*1e3:.3f} ms/step ({LATENT_LAYERS} layers + HybridLink, batch {LATENT_BATCH}), "
+        f"{res['us_per_token']:.1f} us/token, {res['gbps']:.0f} GB/s")
+    del st
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(budget_s: float):
     """numpy oracle on this host's cores, bounded decode sample (M=32, one layer)."""
     import numpy as np
@@ -281,6 +310,8 @@ def main(argv=None):
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--only-roofline", action="store_true",
                     help="time only the roofline kernel (for rocprofv3 counter runs)")
+    ap.add_argument("--no-latent", action="store_true", help="skip the 30-layer latent stack (configs[4])")
+    ap.add_argument("--only-latent", action="store_true")
     ap.add_argument("--only-prefill", action="store_true",
                     help="time only the prefill layer (for rocprofv3 counter runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -300,6 +331,9 @@ def main(argv=None):
         return calibrate_copy(dev)
     _lib.load()
     torch.manual_seed(0)
+    if args.only_latent:
+        print(json.dumps({"latent": latent(dev)}), flush=True)
+        return 0
     if args.only_prefill:
         pre = prefill(dev, max(8, args.steps // 4), max(2, args.warmup // 4), min(args.layers, 4))
         print(json.dumps({"prefill": pre}), flush=True)
@@ -320,6 +354,8 @@ def main(argv=None):
 
     pre = None if args.no_prefill else prefill(dev, max(8, args.steps // 4), max(2, args.warmup // 4),
                                                min(args.layers, 4))
+
+    lat = None if args.no_latent else latent(dev)
 
     total_bytes = sum(d["bytes"] for d in dec.values())
     total_t = sum(d["us"] for d in dec.values()) * 1e-6
@@ -351,6 +387,8 @@ def main(argv=None):
                    for M, d in dec.items()},
         "prefill": None if pre is None else {k: (round(v, 4) if isinstance(v, float) else v)
                                              for k, v in pre.items()},
+        "latent": None if lat is None else {k: (round(v, 4) if isinstance(v, float) else v)
+                                            for k, v in lat.items()},
         "cpu_baseline": None if cpu is None else {k: (round(v, 4) if isinstance(v, float) else v)
                                                   for k, v in cpu.items()},
     }

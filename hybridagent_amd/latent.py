@@ -1,0 +1,87 @@
+"""Latent-mode MoE stack: the decode step of the
+HybridAgent latent loop reduced to its MoE layers.
+
+Each layer: ``h <- h + MoE(RMSNorm(h))``, the router reading the residual
+``h`` as in backends.py:111-122 (attention replaced by the identity, the
+shared MLP and post-FFN norms left out, as the config states).  After the
+last layer the HybridLink map R(h) = LN(h + proj2(GELU(proj1(LN(h)))))
+(hybridlink.py:17-28) scaled by sqrt(hidden) gives the next step's input.
+
+The MoE layers run through the HIP library (router + experts in one C-ABI
+call per layer); the norms and the HybridLink MLP are plain torch bf16 ops
+(hipBLASLt GEMMs), which is all that path needs.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib, synth
+
+
+@dataclass
+class _Layer:
+    router: synth.RouterWeights
+    experts: synth.MoEWeights
+    pre_norm: torch.Tensor  # RMSNorm weight of the MoE input (bf16 [H])
+
+
+class LatentStack:
+    def __init__(self, n_layers: int, E: int, H: int, I: int, top_k: int, group_size: int, seed: int,
+                 device, eps: float = 1e-6):
+        self.H, self.top_k, self.G, self.eps = H, top_k, group_size, eps
+        dev = torch.device(device)
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.layers = []
+        for i in range(n_layers):
+            rw = synth.router_weights(E, H, seed=seed + 31 * i, device=dev)
+            ew = synth.moe_weights(E, H, I, group_size, seed=seed + 31 * i + 7, device=dev)
+            pre = (1.0 + 0.05 * torch.randn(H, generator=g, device=dev)).to(torch.bfloat16)
+            self.layers.append(_Layer(rw, ew, pre))
+        std = 1.0 / math.sqrt(H)
+        mk = lambda *s, sc=1.0: (sc * torch.randn(*s, generator=g, device=dev)).to(torch.bfloat16)
+        self.hl = {
+            "ln1w": (1.0 + 0.05 * torch.randn(H, generator=g, device=dev)).to(torch.bfloat16),
+            "ln1b": mk(H, sc=0.02),
+            "p1w": mk(H, H, sc=std), "p1b": mk(H, sc=0.02),
+            "p2w": mk(H, H, sc=std), "p2b": mk(H, sc=0.02),
+            "ln2w": (1.0 + 0.05 * torch.randn(H, generator=g, device=dev)).to(torch.bfloat16),
+            "ln2b": mk(H, sc=0.02),
+        }
+
+    def rms_norm(self, h: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        """fp32 x * rsqrt(mean(x^2) + eps) * w, back to bf16 (TF:modeling_gemma4.py:197-215)."""
+        x = h.float()
+        y = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + self.eps) * w.float()
+        return y.to(torch.bfloat16)
+
+    def moe(self, h: torch.Tensor, i: int):
+        """MoE block of layer i on residual h -> (out, top_k_index, top_k_weights)."""
+        ly = self.layers[i]
+        xin = self.rms_norm(h, ly.pre_norm)
+        rw, ew = ly.router, ly.experts
+        out, w, idx = _lib.moe_layer_forward(h, rw.scale, rw.scalar_root, rw.proj, rw.per_expert_scale,
+                                             rw.eps, self.top_k, xin, ew.gate_up_packed, ew.gate_up_scale,
+                                             ew.down_packed, ew.down_scale, group_size=self.G)
+        return out, idx, w
+
+    def layer(self, h: torch.Tensor, i: int):
+        """One MoE layer; returns (new h, top_k_index, top_k_weights)."""
+        out, idx, w = self.moe(h, i)
+        return h + out, idx, w
+
+    def hybridlink(self, h: torch.Tensor) -> torch.Tensor:
+        p = self.hl
+        a = F.layer_norm(h, (self.H,), p["ln1w"], p["ln1b"])
+        a = F.linear(a, p["p1w"], p["p1b"])
+        a = F.linear(F.gelu(a), p["p2w"], p["p2b"])
+        return F.layer_norm(h + a, (self.H,), p["ln2w"], p["ln2b"])
+
+    def step(self, h: torch.Tensor) -> torch.Tensor:
+        """One latent step: all MoE layers, then HybridLink x sqrt(H)."""
+        for i in range(len(self.layers)):
+            h, _, _ = self.layer(h, i)
+        return self.hybridlink(h) * math.sqrt(self.H)
