@@ -158,16 +158,17 @@ void k_decode(DecodeArgs a) {
     seg0 = __builtin_amdgcn_readfirstlane(d.y);
     rows = __builtin_amdgcn_readfirstlane(d.z);
   }
-  // items per workgroup, a multiple of the register ring depth so every
-  // workgroup walks whole rounds; items past n_ct (the last workgroup's
-  // padding) compute on row 0 and store nothing
+  // Items per workgroup, a multiple of the register ring depth so every
+  // workgroup walks whole rounds.  The expert's workgroups interleave: local
+  // item c of workgroup `part` is item part + c * wg_per_slot, so together
+  // they read the expert's weights as one front moving through memory.
+  // Items past n_ct (padding) compute on row 0 and store nothing.
   constexpr int RING = LONGK ? 1 : kRing;
   int per = (a.n_ct + a.wg_per_slot - 1) / a.wg_per_slot;
   per = (per + RING - 1) / RING * RING;
-  const int begin = part * per;
-  const int end = min(a.n_ct, begin + per);
-  if (begin >= end || rows <= 0) return;
-  const int end_pad = begin + per;
+  if (part >= a.n_ct || rows <= 0) return;
+  const int begin = 0, end_pad = per;
+  auto phys = [&](int c) { return part + c * a.wg_per_slot; };
 
   const int K8 = a.K >> 3;
   const int nchunks = a.K >> 5;
@@ -264,7 +265,11 @@ void k_decode(DecodeArgs a) {
   // bias form subtracts per group.
   auto stage = [&](int mc, int nr) {
     __syncthreads();  // previous readers of lds_a / csum / tok are done
+    // gate_up: token of each staged row; down: the output row t*k+j of each
+    // staged row (read here once, so the epilogue issues no load: a load
+    // there would wait for every weight refill issued before it)
     if (MODE == kModeGateUp && tid < nr) tok[tid] = a.sorted_pos[seg0 + mc + tid] / a.topk;
+    if (MODE == kModeDown && tid < nr) tok[tid] = a.sorted_pos[seg0 + mc + tid];
     __syncthreads();
     for (int q = tid; q < nr * ntiles; q += kStreamThreads) {
       const int jr = q / ntiles;
@@ -375,7 +380,7 @@ void k_decode(DecodeArgs a) {
   int rbuf = 0;
   if (!LONGK) {
 #pragma unroll
-    for (int r = 0; r < RING; ++r) load_batch(r, off_of(begin + r), tile0);
+    for (int r = 0; r < RING; ++r) load_batch(r, off_of(phys(begin + r)), tile0);
   }
   for (int mc = 0; mc < rows; mc += rb) {
     const int nr = min(rb, rows - mc);
@@ -385,15 +390,15 @@ void k_decode(DecodeArgs a) {
     for (int r = 0; r < RING; ++r) {
       const int ct = c0 + r;
       bool col_ok;
-      weight_row(ct, &col_ok);
-      const int colblk = ct * CG + cg;
+      weight_row(phys(ct), &col_ok);
+      const int colblk = phys(ct) * CG + cg;
       f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
       if (!LONGK) {
         // refill this register set with the item RING positions ahead
-        const Off nx = off_of(item_at(ct - begin + RING));
+        const Off nx = off_of(phys(item_at(ct - begin + RING)));
         mma_batch(r, tile0, acc, std::true_type{}, nx);
       } else {
-        const Off cur = off_of(ct);
+        const Off cur = off_of(phys(ct));
         for (int tb = tile0; tb < ntiles; tb += KSPLIT * TPW) {
           load_batch(0, cur, tb);
           mma_batch(0, tb, acc, std::false_type{}, cur);
@@ -450,7 +455,7 @@ void k_decode(DecodeArgs a) {
         for (int q = 0; q < 4; ++q) {
           const int i = ibase + q;
           if (q >= qlo && q < qhi && col_ok && i < iend) {
-            const int64_t orow = a.sorted_pos[seg0 + i];
+            const int64_t orow = tok[i - mc];
             a.out[orow * a.N + n] = f32_to_bf16_bits(v[q]);
           }
         }
