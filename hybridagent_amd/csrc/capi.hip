@@ -32,7 +32,7 @@ struct Carve {
 
 inline int launch_status(hipError_t e) { return e == hipSuccess ? W4A16_OK : W4A16_ERR_LAUNCH; }
 
-inline int router_ksplit(int64_t M) { return M <= 64 ? 8 : 1; }
+inline int router_ksplit(int64_t M) { return M <= 64 ? 16 : 1; }
 
 // Token counts up to this use the decode kernels; larger batches the
 // prefill grouped-GEMM kernels.
@@ -54,7 +54,7 @@ hipError_t launch_router_partials(const uint16_t* hidden, const uint16_t* scale,
   const int ks = router_ksplit(M);
   // decode sizes: the norm inside the logits launch (each workgroup covers
   // all experts of 16 tokens, so it normalises its rows once)
-  if (ks == 8 && H <= 384 * 8)
+  if (ks > 1 && H <= 384 * 8)
     return launch_router_norm_logits(hidden, scale, root, eps, proj, partial, (int)M, (int)H,
                                      (int)E, ks, s);
   // large batches: the norm inside a tiled logits GEMM (64 tokens x 32 experts

@@ -15,6 +15,7 @@
 //   MODE = down   : dn[t*k+j] = inter W_d^T          (quantization.py:122-127)
 //
 // k_bias_order, k_combine and k_dequant are the small helpers around it.
+#include <algorithm>
 #include <type_traits>
 
 #include "common.hpp"
@@ -83,10 +84,12 @@ hipError_t launch_bias_order(const uint16_t* x, uint16_t* xp, int64_t rows, int 
 // k index carried by (l/16, element), so each lane feeds 8 consecutive
 // (bias- or natural-ordered) k values of its own 32-element chunk per step.
 //
-// Work split: every workgroup serves exactly one active expert.  The grid is
-// max_slots x wg_per_slot workgroups; workgroup w takes expert slot
-// w / wg_per_slot (exiting if that slot is not active) and a contiguous run of
-// that expert's column tiles ("items": 4/KSPLIT groups of 16 weight rows).
+// Work split: every workgroup serves exactly one active expert.  The grid
+// holds the workgroups that fit on the chip at once (at least one per
+// possible expert slot); with U experts active, workgroup w takes slot
+// w / wps, wps = grid / U (exiting if that slot is not active), and every
+// wps-th of that expert's column tiles ("items": NWAVES/KSPLIT groups of 16
+// weight rows).
 // It stages the expert's activation rows into LDS once per pass of rb rows
 // (an expert with more than rb rows makes several passes over its weights),
 // then streams its items.  Inside an item, each 16-row column group's K range
@@ -103,10 +106,14 @@ hipError_t launch_bias_order(const uint16_t* x, uint16_t* xp, int64_t rows, int 
 //   (16*(b/16) + 4*(b%4) + (b/4)%4) * rb + j
 // i.e. grouped by (k tile, lane chunk, MFMA step), so a wavefront's
 // ds_read_b128 of one MFMA step is contiguous and bank-conflict free.
-// Threads per workgroup: K-split shapes run two column groups of four
-// wavefronts each (eight wavefronts share one activation stage), the others
-// four column groups of one wavefront.
-constexpr int stream_threads(int ksplit) { return ksplit == 4 ? 512 : 256; }
+// Threads per workgroup: K-split shapes run four column groups of four
+// wavefronts each (sixteen wavefronts, one workgroup per CU, share one
+// activation stage of up to 16 rows), the others four column groups of one
+// wavefront.
+constexpr int stream_threads(int ksplit) { return ksplit == 4 ? 1024 : 256; }
+// LDS bytes for staged activation rows: the K-split workgroup owns its CU's
+// LDS; the others leave room for several workgroups per CU
+constexpr int stage_lds_budget(int ksplit) { return ksplit == 4 ? 98304 : 49152; }
 // items whose weight loads are in flight per wavefront (register sets).
 // One set, refilled tile by tile while the item is multiplied, measured
 // fastest: deeper rings slowed the streamer down.
@@ -146,13 +153,21 @@ void k_decode(DecodeArgs a) {
   const int j = lane & 15;   // MFMA column (weight row in the group) / A row
   const int kb = lane >> 4;  // 32-element chunk of the 128-wide k tile
 
-  // this workgroup's expert and item range
-  const int slot = (int)blockIdx.x / a.wg_per_slot;
-  const int part = (int)blockIdx.x - slot * a.wg_per_slot;
+  // this workgroup's expert and item range.  The grid is spread over the
+  // experts that are active in this batch (known only here): wps
+  // workgroups each, so the chip fills whatever the routing.
+  int wps = a.wg_per_slot;
+  int U = 1;
+  if (MODE != kModeDense) {
+    U = __builtin_amdgcn_readfirstlane(*a.n_active);
+    if (U <= 0) return;
+    wps = max(1, min(a.n_ct, (int)gridDim.x / U));
+  }
+  const int slot = (int)blockIdx.x / wps;
+  const int part = (int)blockIdx.x - slot * wps;
+  if (slot >= U) return;  // uniform across the workgroup
   int e = 0, seg0 = 0, rows = a.M;
   if (MODE != kModeDense) {
-    const int U = __builtin_amdgcn_readfirstlane(*a.n_active);
-    if (slot >= U) return;  // uniform across the workgroup
     const int4 d = *reinterpret_cast<const int4*>(a.desc + 4 * slot);
     e = __builtin_amdgcn_readfirstlane(d.x);
     seg0 = __builtin_amdgcn_readfirstlane(d.y);
@@ -160,15 +175,15 @@ void k_decode(DecodeArgs a) {
   }
   // Items per workgroup, a multiple of the register ring depth so every
   // workgroup walks whole rounds.  The expert's workgroups interleave: local
-  // item c of workgroup `part` is item part + c * wg_per_slot, so together
+  // item c of workgroup `part` is item part + c * wps, so together
   // they read the expert's weights as one front moving through memory.
   // Items past n_ct (padding) compute on row 0 and store nothing.
   constexpr int RING = LONGK ? 1 : kRing;
-  int per = (a.n_ct + a.wg_per_slot - 1) / a.wg_per_slot;
+  int per = (a.n_ct + wps - 1) / wps;
   per = (per + RING - 1) / RING * RING;
   if (part >= a.n_ct || rows <= 0) return;
   const int begin = 0, end_pad = per;
-  auto phys = [&](int c) { return part + c * a.wg_per_slot; };
+  auto phys = [&](int c) { return part + c * wps; };
 
   const int K8 = a.K >> 3;
   const int nchunks = a.K >> 5;
@@ -284,10 +299,14 @@ void k_decode(DecodeArgs a) {
 #pragma unroll
       for (int half = 0; half < 2; ++half) {
         u32x4_t v[8];
+        // all eight loads issued before any is used: addresses clamped into
+        // the row, pieces past it zeroed after the load (a conditional load
+        // would wait for everything in flight, once per piece)
 #pragma unroll
         for (int b8 = 0; b8 < 8; ++b8) {
           const int bb = 8 * half + b8;
-          v[b8] = bb < nb ? ld16(src + 8 * bb) : u32x4_t{0u, 0u, 0u, 0u};
+          const u32x4_t t = ld16(src + 8 * min(bb, nb - 1));
+          v[b8] = bb < nb ? t : u32x4_t{0u, 0u, 0u, 0u};
         }
 #pragma unroll
         for (int b8 = 0; b8 < 8; ++b8) {
@@ -482,12 +501,12 @@ static DecodeShape decode_shape(int K) {
 }
 
 // activation rows staged per LDS pass: the largest power of two <= 16 whose
-// fragment-layout footprint fits 48 KB of LDS
-static int stage_rows(int K) {
+// fragment-layout footprint fits the shape's LDS budget
+static int stage_rows(int K, int ksplit) {
   const int ntiles = ((K >> 5) + 3) >> 2;
   const int bytes_per_row = ntiles * 16 * 16;  // fragment layout pads the last tile
   int rb = 16;
-  while (rb > 1 && rb * bytes_per_row > 49152) rb >>= 1;
+  while (rb > 1 && rb * bytes_per_row > stage_lds_budget(ksplit)) rb >>= 1;
   return rb;
 }
 
@@ -515,19 +534,18 @@ static size_t stream_lds(const DecodeArgs& a) {
 template <int MODE, bool BIAS, int TPW, int KSPLIT, bool LONGK, bool WIDE = false>
 static hipError_t launch_stream(DecodeArgs a, int max_slots, hipStream_t s) {
   auto kern = k_decode<MODE, BIAS, TPW, KSPLIT, LONGK, WIDE>;
-  // workgroups per expert: fill the chip with the workgroups that fit at
-  // once, spread over the experts that can be active, at most one per item
+  // the workgroups that fit on the chip at once, at least one per possible
+  // expert slot and at most one per item; the kernel spreads them over the
+  // experts that turn out active (dense: one slot, wg_per_slot = grid)
   int per_cu = 0;
   constexpr int threads = stream_threads(KSPLIT);
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, stream_lds(a)) !=
           hipSuccess || per_cu <= 0)
     per_cu = 1;
   const int64_t resident = (int64_t)device_cus() * per_cu;
-  int64_t wps = (resident + max_slots - 1) / max_slots;
-  if (wps > a.n_ct) wps = a.n_ct;
-  if (wps < 1) wps = 1;
-  a.wg_per_slot = (int)wps;
-  const int64_t grid = (int64_t)max_slots * wps;
+  int64_t grid = std::min<int64_t>(resident, (int64_t)max_slots * a.n_ct);
+  if (grid < max_slots) grid = max_slots;
+  a.wg_per_slot = (int)std::max<int64_t>(1, grid / max_slots);
   if (grid <= 0) return hipSuccess;
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(threads), stream_lds(a), s, a);
   return hipGetLastError();
@@ -541,7 +559,7 @@ static hipError_t launch_decode_mode(DecodeArgs a, int max_slots, hipStream_t s)
   a.n_ct = (ncolblk + cg - 1) / cg;
   // rows staged per pass: enough for the rows an expert can have (at most
   // the row count of the batch), capped by the LDS budget
-  a.rb = stage_rows(a.K);
+  a.rb = stage_rows(a.K, sh.ksplit);
   int rows_cap = 1;
   while (rows_cap < a.rows_hint && rows_cap < 16) rows_cap <<= 1;
   if (a.rb > rows_cap) a.rb = rows_cap;
@@ -582,6 +600,11 @@ hipError_t launch_decode(int mode, bool bias_form, DecodeArgs a, int max_slots, 
 // Slots whose expert index is outside [0, E) contribute nothing.
 // one thread per (token, 8 columns)
 // ---------------------------------------------------------------------------
+// KMAX > 0: topk <= KMAX; every slot's index, weight and 16-byte piece is
+// loaded before any is used (slots past topk load slot 0 again and are
+// dropped), so a thread waits for memory once instead of twice per slot.
+// KMAX == 0: any topk, one slot after the other.
+template <int KMAX>
 __global__ __launch_bounds__(256) void k_combine(const uint16_t* __restrict__ dn,
                                                  const int64_t* __restrict__ idx,
                                                  const float* __restrict__ w,
@@ -593,17 +616,36 @@ __global__ __launch_bounds__(256) void k_combine(const uint16_t* __restrict__ dn
        i += (int64_t)gridDim.x * blockDim.x) {
     const int t = (int)(i / per_row);
     const int c8 = (int)(i - (int64_t)t * per_row) * 8;
+    const int64_t r0 = (int64_t)t * topk;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int jj = 0; jj < topk; ++jj) {
-      const int64_t ex = idx[(int64_t)t * topk + jj];
-      if (ex < 0 || ex >= E) continue;
-      const float wb = round_bf16(w[(int64_t)t * topk + jj]);
-      const u32x4_t d = ld16(dn + ((int64_t)t * topk + jj) * H + c8);
+    auto add = [&](const u32x4_t& d, float wv) {
+      const float wb = round_bf16(wv);
       const uint32_t dw[4] = {d.x, d.y, d.z, d.w};
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         acc[2 * q] += round_bf16(bf16_bits_to_f32(dw[q] & 0xFFFFu) * wb);
         acc[2 * q + 1] += round_bf16(bf16_bits_to_f32(dw[q] >> 16) * wb);
+      }
+    };
+    if (KMAX > 0) {
+      int64_t ex[KMAX > 0 ? KMAX : 1];
+      float wv[KMAX > 0 ? KMAX : 1];
+      u32x4_t d[KMAX > 0 ? KMAX : 1];
+#pragma unroll
+      for (int jj = 0; jj < KMAX; ++jj) {
+        const int64_t r = r0 + (jj < topk ? jj : 0);
+        ex[jj] = idx[r];
+        wv[jj] = w[r];
+        d[jj] = ld16(dn + r * H + c8);
+      }
+#pragma unroll
+      for (int jj = 0; jj < KMAX; ++jj)
+        if (jj < topk && ex[jj] >= 0 && ex[jj] < E) add(d[jj], wv[jj]);
+    } else {
+      for (int jj = 0; jj < topk; ++jj) {
+        const int64_t ex = idx[r0 + jj];
+        if (ex < 0 || ex >= E) continue;
+        add(ld16(dn + (r0 + jj) * H + c8), w[r0 + jj]);
       }
     }
     u32x4_t o;
@@ -621,8 +663,12 @@ hipError_t launch_combine(const uint16_t* dn, const int64_t* idx, const float* w
   if (total == 0) return hipSuccess;
   int64_t blocks = (total + 255) / 256;
   if (blocks > 65536) blocks = 65536;
-  hipLaunchKernelGGL(k_combine, dim3((unsigned)blocks), dim3(256), 0, s, dn, idx, w, out, M, topk,
-                     E, H);
+  if (topk <= 8)
+    hipLaunchKernelGGL(k_combine<8>, dim3((unsigned)blocks), dim3(256), 0, s, dn, idx, w, out, M,
+                       topk, E, H);
+  else
+    hipLaunchKernelGGL(k_combine<0>, dim3((unsigned)blocks), dim3(256), 0, s, dn, idx, w, out, M,
+                       topk, E, H);
   return hipGetLastError();
 }
 

@@ -21,12 +21,17 @@ namespace w4a16 {
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float wave_sum(float v) { return wave_sum_f32(v); }
 
-__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int u = __shfl_up(v, o);
-    if (lane >= o) v += u;
-  }
+// Inclusive prefix sum over the 64 lanes with DPP: row_shr 1, 2, 4, 8 scan
+// each row of 16 lanes (lanes shifted in from outside the row add the 0
+// passed as `old`); row_bcast:15 then adds row r's total to row r + 1 (rows
+// 1 and 3), row_bcast:31 the total of rows 0-1 to rows 2 and 3.
+__device__ __forceinline__ int wave_incl_scan(int v, int /*lane*/) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31
   return v;
 }
 
@@ -163,7 +168,7 @@ hipError_t launch_router_logits(const uint16_t* r, const uint16_t* proj, float* 
 // partials in thread order); phase 2 forms r = bf16(bf16(bf16(x * inv) *
 // scale) * root) for the split's k range only, straight into LDS in MFMA
 // A-operand order; phase 3 is 16x16x32 MFMA against the router weights,
-// whose loads are issued first and overlap phases 1-2.
+// whose loads are issued right after the rows' and overlap phases 1-2.
 // ---------------------------------------------------------------------------
 constexpr int kFusedLogitsThreads = 512;
 constexpr int kFusedLogitsMaxSteps = 12;  // 32-wide k steps per split
@@ -185,13 +190,23 @@ __global__ __launch_bounds__(kFusedLogitsThreads) void k_router_norm_logits(
   const int c0 = ks * steps_per_split;
   const int nsteps = max(0, min(nchunks, c0 + steps_per_split) - c0);
 
-  // router weight fragments of this wavefront's first 16 experts
-  const int e = wave * 16 + j;
-  const int ec = min(e, E - 1);
   u32x4_t bv[kFusedLogitsMaxSteps];
+
+  // phase 2's activation and scale pieces, loaded now so they arrive with
+  // phase 1's (one memory round trip instead of two); rows past M are
+  // clamped and masked in phase 2
+  constexpr int kP2 = (kFusedLogitsMaxSteps * 64 + kFusedLogitsThreads - 1) / kFusedLogitsThreads;
+  u32x4_t p2x[kP2], p2s[kP2];
 #pragma unroll
-  for (int c = 0; c < kFusedLogitsMaxSteps; ++c)
-    if (c < nsteps) bv[c] = ld16(proj + (int64_t)ec * H + 32 * (c0 + c) + 8 * kb);
+  for (int it = 0; it < kP2; ++it) {
+    const int p = min(tid + it * kFusedLogitsThreads, max(nsteps, 1) * 64 - 1);
+    const int c = p >> 6, l = p & 63;
+    const int cc = nsteps > 0 ? c0 + min(c, nsteps - 1) : 0;  // a chunk inside the row
+    const int k0 = 32 * cc + 8 * (l >> 4);
+    p2x[it] = u32x4_t{0u, 0u, 0u, 0u};
+    if (m0 + (l & 15) < M) p2x[it] = ld16(h + (int64_t)(m0 + (l & 15)) * H + k0);
+    p2s[it] = ld16(scale + k0);
+  }
 
   // phase 1: sum of squares of rows m0 .. m0+15; each thread's chunks are
   // all loaded before the first is used (H <= 384 * 8 -> at most 12 chunks)
@@ -203,10 +218,22 @@ __global__ __launch_bounds__(kFusedLogitsThreads) void k_router_norm_logits(
     const int n8 = H >> 3;
     u32x4_t v[kChunks];
 #pragma unroll
-    for (int q = 0; q < kChunks; ++q) {
-      const int c8 = sub + 32 * q;
-      v[q] = c8 < n8 ? ld16(row + 8 * c8) : u32x4_t{0u, 0u, 0u, 0u};
+    for (int q = 0; q < kChunks; ++q) v[q] = u32x4_t{0u, 0u, 0u, 0u};
+    // rows past M (their sums are never used) issue no loads
+    if (m0 + i < M) {
+#pragma unroll
+      for (int q = 0; q < kChunks; ++q) {
+        const int c8 = sub + 32 * q;
+        if (c8 < n8) v[q] = ld16(row + 8 * c8);
+      }
     }
+    // router weight fragments of this wavefront's first 16 experts, issued
+    // after the rows: loads complete in order, so the sums of squares wait
+    // only for the rows and the weights arrive during phase 2
+    const int ec = min(wave * 16 + j, E - 1);
+#pragma unroll
+    for (int c = 0; c < kFusedLogitsMaxSteps; ++c)
+      if (c < nsteps) bv[c] = ld16(proj + (int64_t)ec * H + 32 * (c0 + c) + 8 * kb);
     float ss = 0.f;
 #pragma unroll
     for (int q = 0; q < kChunks; ++q) {
@@ -229,15 +256,17 @@ __global__ __launch_bounds__(kFusedLogitsThreads) void k_router_norm_logits(
   __syncthreads();
 
   // phase 2: r for this split's k range -> afrag[step][lane(j = row, kb)]
-  for (int p = tid; p < nsteps * 64; p += kFusedLogitsThreads) {
+#pragma unroll
+  for (int it = 0; it < kP2; ++it) {
+    const int p = tid + it * kFusedLogitsThreads;
+    if (p >= nsteps * 64) break;
     const int c = p >> 6, l = p & 63;
-    const int rj = l & 15, rkb = l >> 4;
+    const int rj = l & 15;
     const int m = m0 + rj;
     u32x4_t o = {0u, 0u, 0u, 0u};
     if (m < M) {
-      const int k0 = 32 * (c0 + c) + 8 * rkb;
-      const u32x4_t xv = ld16(h + (int64_t)m * H + k0);
-      const u32x4_t sv = ld16(scale + k0);
+      const u32x4_t xv = p2x[it];
+      const u32x4_t sv = p2s[it];
       const float inv = s_inv[rj];
       const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w}, sw[4] = {sv.x, sv.y, sv.z, sv.w};
       uint32_t ow[4];
@@ -469,7 +498,7 @@ hipError_t launch_router_big(const uint16_t* h, const uint16_t* scale, float sca
 // softmax / top-k / renormalise: one wavefront per token, E <= 512
 // ---------------------------------------------------------------------------
 constexpr int kTopkPerLane = kMaxExperts / 64;
-constexpr int kRouterMaxSplit = 8;
+constexpr int kRouterMaxSplit = 16;
 
 // Routing of one token by one wavefront: bf16 logits (from K-split partials
 // or given), softmax denominator, top-k by (logit desc, index asc), weights.
@@ -550,9 +579,7 @@ __device__ void select_topk(const float (&lg)[PER], const uint16_t* __restrict__
     const uint32_t mono = (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
     key[q] = (q < per && e < E) ? ((mono << 16) | (0xFFFFu - (uint32_t)e)) : 0u;
   }
-  float my_p = 0.f;
-  int my_i = 0;
-  float psum = 0.f;
+  uint32_t my_key = 0u;
   for (int it = 0; it < topk; ++it) {
     uint32_t best = 0u;
 #pragma unroll
@@ -560,19 +587,18 @@ __device__ void select_topk(const float (&lg)[PER], const uint16_t* __restrict__
     const uint32_t kmax = wave_max_u32(best);
 #pragma unroll
     for (int q = 0; q < PER; ++q) key[q] = key[q] == kmax ? 0u : key[q];
-    const int bi = (int)(0xFFFFu - (kmax & 0xFFFFu));
-    const uint32_t mono = kmax >> 16;
-    const uint32_t bb = (mono & 0x8000u) ? (mono & 0x7FFFu) : (~mono & 0xFFFFu);
-    const float bv = bf16_bits_to_f32(bb);
-    const float p = expf(bv - mx) / den;
-    if (lane == it) {
-      my_p = p;
-      my_i = bi;
-    }
-    psum += p;
+    if (lane == it) my_key = kmax;
   }
-  *sel_e = my_i;
-  *sel_w = (lane < topk) ? (my_p / psum) * bf16_bits_to_f32(pes[my_i]) : 0.f;
+  // lane it < topk decodes selection it; the probabilities of all k are
+  // formed at once and summed across the lanes
+  const int bi = (int)(0xFFFFu - (my_key & 0xFFFFu));
+  const uint32_t mono = my_key >> 16;
+  const uint32_t bb = (mono & 0x8000u) ? (mono & 0x7FFFu) : (~mono & 0xFFFFu);
+  const float p = lane < topk ? expf(bf16_bits_to_f32(bb) - mx) / den : 0.f;
+  const float psum = wave_sum_f32(p);
+  const int ei = lane < topk ? bi : 0;
+  *sel_e = ei;
+  *sel_w = (lane < topk) ? (p / psum) * bf16_bits_to_f32(pes[ei]) : 0.f;
 }
 
 template <int KS, int PER>
@@ -702,6 +728,52 @@ __device__ int write_plan(int c, int E, int32_t* __restrict__ offsets, int32_t* 
   return off;
 }
 
+// The plan from the per-expert counts cnt[0..E), by one wavefront (lane l
+// owns the consecutive experts l*pe .. l*pe+pe-1, pe = ceil(E / 64)): segment
+// starts into offsets[] and run[] (LDS), one descriptor per active expert,
+// the m-tile list and the two counters -- the same output as write_plan,
+// without workgroup barriers.
+__device__ void plan_wave(const int* cnt, int* run, int E, int32_t* __restrict__ offsets,
+                          int32_t* __restrict__ desc, int32_t* __restrict__ counters,
+                          int32_t* __restrict__ tiles, int BM) {
+  constexpr int PE = kMaxExperts / 64;
+  const int lane = threadIdx.x & 63;
+  const int pe = (E + 63) >> 6;
+  int c[PE];
+  int cs = 0, as = 0, ts = 0;
+#pragma unroll
+  for (int q = 0; q < PE; ++q) {
+    const int e = lane * pe + q;
+    c[q] = (q < pe && e < E) ? cnt[e] : 0;
+    cs += c[q];
+    as += c[q] > 0 ? 1 : 0;
+    ts += (c[q] + BM - 1) / BM;
+  }
+  const int ci = wave_incl_scan(cs, lane), ai = wave_incl_scan(as, lane), ti = wave_incl_scan(ts, lane);
+  int off = ci - cs, apos = ai - as, tpos = ti - ts;
+#pragma unroll
+  for (int q = 0; q < PE; ++q) {
+    const int e = lane * pe + q;
+    if (q < pe && e < E) {
+      offsets[e] = off;
+      run[e] = off;
+      if (c[q] > 0) {
+        *reinterpret_cast<int4*>(desc + 4 * apos) = make_int4(e, off, c[q], 0);
+        ++apos;
+      }
+      const int nt = (c[q] + BM - 1) / BM;
+      for (int i = 0; i < nt; ++i) tiles[tpos + i] = (e << 16) | i;
+      tpos += nt;
+      off += c[q];
+    }
+  }
+  if (lane == 63) {
+    offsets[E] = ci;
+    counters[0] = ai;
+    counters[1] = ti;
+  }
+}
+
 // The counting sort, run by one workgroup of kSortThreads threads; expert_of(row)
 // returns the expert of row t*k+j (global memory or this workgroup's LDS).
 template <typename ExpertOf>
@@ -712,40 +784,57 @@ __device__ void moe_sort_body(ExpertOf expert_of, int M, int topk, int E,
   __shared__ int cnt[kMaxExperts];
   __shared__ int run[kMaxExperts];
   __shared__ int wcnt[kSortWaves][kMaxExperts];
-  __shared__ int wsum[kSortWaves];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int total = M * topk;
 
+
+  // Entry p (k-major: p = j*M + t) is routed row t*topk + j; thread tid owns
+  // p = tid + kSortThreads * r.  The experts of its first kPre entries are
+  // read once, all before the first is used, and serve both the count and
+  // the scatter (-1: no entry or no expert).
+  constexpr int kPre = 2;  // the scatter below picks pre_e[0] / pre_e[1]
+  auto expert_at = [&](int p) -> int {
+    const int jj = p / M, t = p - jj * M;
+    const int64_t ev = expert_of(t * topk + jj);
+    return (ev >= 0 && ev < E) ? (int)ev : -1;
+  };
+  int pre_e[kPre];
+#pragma unroll
+  for (int r = 0; r < kPre; ++r) {
+    const int p = tid + kSortThreads * r;
+    const int ev = total > 0 ? expert_at(min(p, total - 1)) : -1;
+    pre_e[r] = (p < total) ? ev : -1;
+  }
 
   for (int e = tid; e < E; e += kSortThreads) {
     cnt[e] = 0;
     for (int w = 0; w < kSortWaves; ++w) wcnt[w][e] = 0;
   }
   __syncthreads();
-  for (int p = tid; p < total; p += kSortThreads) {
-    const int64_t e = expert_of(p);
-    if (e >= 0 && e < E) atomicAdd(&cnt[(int)e], 1);
+#pragma unroll
+  for (int r = 0; r < kPre; ++r)
+    if (pre_e[r] >= 0) atomicAdd(&cnt[pre_e[r]], 1);
+  for (int p = tid + kSortThreads * kPre; p < total; p += kSortThreads) {
+    const int e = expert_at(p);
+    if (e >= 0) atomicAdd(&cnt[e], 1);
   }
   __syncthreads();
 
-  // offsets, work descriptors and tile list (E <= 512 < 1024 threads)
-  const int off = write_plan(tid < E ? cnt[tid] : 0, E, offsets, desc, counters, tiles, BM, wsum,
-                             true);
-  if (tid < E) run[tid] = off;
+  // offsets, work descriptors, tile list and scatter bases, by wavefront 0
+  if (wave == 0) plan_wave(cnt, run, E, offsets, desc, counters, tiles, BM);
   __syncthreads();
 
   // stable scatter in k-major order p = j*M + t
   int nbits = 0;
   while ((1 << nbits) < E) ++nbits;
   const unsigned long long lt_mask = (1ull << lane) - 1ull;
-  for (int base = 0; base < total; base += kSortThreads) {
+  for (int base = 0, r = 0; base < total; base += kSortThreads, ++r) {
     const int p = base + tid;
     int e = -1, row = 0;
     if (p < total) {
       const int jj = p / M, t = p - jj * M;
       row = t * topk + jj;
-      const int64_t ev = expert_of(row);
-      if (ev >= 0 && ev < E) e = (int)ev;
+      e = r < kPre ? (r == 0 ? pre_e[0] : pre_e[kPre - 1]) : expert_at(p);
     }
     const bool ok = e >= 0;
     unsigned long long same = __ballot(ok);
@@ -789,7 +878,7 @@ __global__ __launch_bounds__(kSortThreads) void k_moe_sort(
 constexpr int kTopkSortMaxEntries = 512;
 constexpr int kTopkSortRounds = 4;  // tokens per wavefront: M <= 64
 
-template <int KS, int PER>
+template <int KS, int PER, int ROUNDS>
 __global__ __launch_bounds__(kSortThreads) void k_router_topk_sort(
     const float* __restrict__ partial, const uint16_t* __restrict__ pes,
     int64_t* __restrict__ idx_out, float* __restrict__ w_out, int M, int E, int topk,
@@ -800,15 +889,15 @@ __global__ __launch_bounds__(kSortThreads) void k_router_topk_sort(
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   for (int e = threadIdx.x; e < E; e += kSortThreads) s_pes[e] = pes[e];
-  // every token of this wavefront (at most kTopkSortRounds) loaded up front
-  float lg[kTopkSortRounds][PER];
+  // every token of this wavefront (at most ROUNDS) loaded up front
+  float lg[ROUNDS][PER];
 #pragma unroll
-  for (int rr = 0; rr < kTopkSortRounds; ++rr)
+  for (int rr = 0; rr < ROUNDS; ++rr)
     load_logits<KS, PER>(partial, nullptr, nullptr, min(wave + kSortWaves * rr, M - 1), M, E, lane,
                          lg[rr]);
   __syncthreads();  // s_pes
 #pragma unroll
-  for (int rr = 0; rr < kTopkSortRounds; ++rr) {
+  for (int rr = 0; rr < ROUNDS; ++rr) {
     const int m = wave + kSortWaves * rr;
     if (m >= M) break;  // uniform per wavefront
     int se;
@@ -830,13 +919,25 @@ static void launch_topk_sort_ks(const float* partial, const uint16_t* pes, int64
                                 int M, int E, int topk, int32_t* sorted_pos, int32_t* offsets,
                                 int32_t* desc, int32_t* counters, int32_t* tiles, int BM,
                                 hipStream_t s) {
-#define W4A16_TS(P_)                                                                          \
-  hipLaunchKernelGGL((k_router_topk_sort<KS, P_>), dim3(1), dim3(kSortThreads), 0, s, partial, \
-                     pes, idx, w, M, E, topk, sorted_pos, offsets, desc, counters, tiles, BM)
-  if (E <= 64) W4A16_TS(1);
-  else if (E <= 128) W4A16_TS(2);
-  else if (E <= 256) W4A16_TS(4);
-  else W4A16_TS(kTopkPerLane);
+  // one token per wavefront up to M = 16, else up to kTopkSortRounds
+#define W4A16_TS(P_)                                                                            \
+  if (M <= kSortWaves)                                                                          \
+    hipLaunchKernelGGL((k_router_topk_sort<KS, P_, 1>), dim3(1), dim3(kSortThreads), 0, s,       \
+                       partial, pes, idx, w, M, E, topk, sorted_pos, offsets, desc, counters,    \
+                       tiles, BM);                                                               \
+  else                                                                                          \
+    hipLaunchKernelGGL((k_router_topk_sort<KS, P_, kTopkSortRounds>), dim3(1), dim3(kSortThreads), \
+                       0, s, partial, pes, idx, w, M, E, topk, sorted_pos, offsets, desc,         \
+                       counters, tiles, BM)
+  if (E <= 64) {
+    W4A16_TS(1);
+  } else if (E <= 128) {
+    W4A16_TS(2);
+  } else if (E <= 256) {
+    W4A16_TS(4);
+  } else {
+    W4A16_TS(kTopkPerLane);
+  }
 #undef W4A16_TS
 }
 
