@@ -70,6 +70,15 @@ __device__ __forceinline__ u32x4_t unpack_bias(uint32_t w, uint32_t mask, uint32
 }
 
 // Hides a value from constant folding so it stays in a register.
+// p[i] for a wavefront-uniform i, through the scalar data cache (a read of
+// the constant address space): scalar loads are counted apart from vector
+// loads, so the value arrives without waiting for vector loads in flight.
+// Only for data no thread of the running kernel writes.
+__device__ __forceinline__ int32_t ld_uniform(const int32_t* p, int i) {
+  typedef __attribute__((address_space(4))) const int32_t cint32_t;
+  return ((cint32_t*)p)[__builtin_amdgcn_readfirstlane(i)];
+}
+
 __device__ __forceinline__ uint32_t opaque(uint32_t v) {
   asm volatile("" : "+v"(v));
   return v;

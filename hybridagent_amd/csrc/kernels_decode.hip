@@ -159,7 +159,7 @@ void k_decode(DecodeArgs a) {
   int wps = a.wg_per_slot;
   int U = 1;
   if (MODE != kModeDense) {
-    U = __builtin_amdgcn_readfirstlane(*a.n_active);
+    U = ld_uniform(a.n_active, 0);
     if (U <= 0) return;
     wps = max(1, min(a.n_ct, (int)gridDim.x / U));
   }
@@ -168,10 +168,9 @@ void k_decode(DecodeArgs a) {
   if (slot >= U) return;  // uniform across the workgroup
   int e = 0, seg0 = 0, rows = a.M;
   if (MODE != kModeDense) {
-    const int4 d = *reinterpret_cast<const int4*>(a.desc + 4 * slot);
-    e = __builtin_amdgcn_readfirstlane(d.x);
-    seg0 = __builtin_amdgcn_readfirstlane(d.y);
-    rows = __builtin_amdgcn_readfirstlane(d.z);
+    e = ld_uniform(a.desc, 4 * slot);
+    seg0 = ld_uniform(a.desc, 4 * slot + 1);
+    rows = ld_uniform(a.desc, 4 * slot + 2);
   }
   // Items per workgroup, a multiple of the register ring depth so every
   // workgroup walks whole rounds.  The expert's workgroups interleave: local
@@ -277,53 +276,62 @@ void k_decode(DecodeArgs a) {
   // tile): 16 pieces of 16 bytes, reordered for the bias form, stored in
   // fragment order, and -- for the bias form -- summed into
   // csum[t][row] = 136 * (sum of the row's tile elements), the correction the
-  // bias form subtracts per group.
-  auto stage = [&](int mc, int nr) {
+  // bias form subtracts per group.  Every thread has at most one task
+  // (rb * ntiles <= kStreamThreads, from the LDS budget).  `between` runs
+  // after the task's loads are issued and before they are used: the first
+  // pass issues the weight prologue there, so the activations do not queue
+  // behind the weights (loads complete in issue order).
+  auto stage = [&](int mc, int nr, auto&& between) {
     __syncthreads();  // previous readers of lds_a / csum / tok are done
     // gate_up: token of each staged row; down: the output row t*k+j of each
     // staged row (read here once, so the epilogue issues no load: a load
-    // there would wait for every weight refill issued before it)
-    if (MODE == kModeGateUp && tid < nr) tok[tid] = a.sorted_pos[seg0 + mc + tid] / a.topk;
-    if (MODE == kModeDown && tid < nr) tok[tid] = a.sorted_pos[seg0 + mc + tid];
+    // there would wait for every weight refill issued before it).  The
+    // positions are read with scalar loads, which do not wait for the
+    // vector loads in flight.
+    if (MODE != kModeDense) {
+      int sp[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sp[i] = ld_uniform(a.sorted_pos, seg0 + mc + min(i, nr - 1));
+      if (tid < 16) {
+        int v = sp[0];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) v = tid == i ? sp[i] : v;
+        tok[tid] = MODE == kModeGateUp ? v / a.topk : v;
+      }
+    }
     __syncthreads();
-    for (int q = tid; q < nr * ntiles; q += kStreamThreads) {
-      const int jr = q / ntiles;
-      const int t = q - jr * ntiles;
+    const bool has = tid < nr * ntiles;
+    const int jr = tid / ntiles;
+    const int t = tid - jr * ntiles;
+    const int nb = min(16, K8 - 16 * t);
+    u32x4_t v[16];
+    if (has) {
       int64_t row;
       if (MODE == kModeDense) row = mc + jr;
       else if (MODE == kModeGateUp) row = tok[jr];
       else row = seg0 + mc + jr;
       const uint16_t* src = a.act + row * a.K + 128 * t;
-      const int nb = min(16, K8 - 16 * t);
+      // pieces past the row end load the last piece again and are dropped
+#pragma unroll
+      for (int b = 0; b < 16; ++b) v[b] = ld16(src + 8 * min(b, nb - 1));
+    }
+    between();
+    if (has) {
       float sum = 0.f;
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        u32x4_t v[8];
-        // all eight loads issued before any is used: addresses clamped into
-        // the row, pieces past it zeroed after the load (a conditional load
-        // would wait for everything in flight, once per piece)
-#pragma unroll
-        for (int b8 = 0; b8 < 8; ++b8) {
-          const int bb = 8 * half + b8;
-          const u32x4_t t = ld16(src + 8 * min(bb, nb - 1));
-          v[b8] = bb < nb ? t : u32x4_t{0u, 0u, 0u, 0u};
-        }
-#pragma unroll
-        for (int b8 = 0; b8 < 8; ++b8) {
-          const int bb = 8 * half + b8;
-          if (bb < nb) {
-            u32x4_t x = v[b8];
-            // gate_up / dense read caller activations in natural order; down
-            // reads intermediate rows the gate_up epilogue wrote in bias order
-            if (BIAS && MODE != kModeDown) x = to_bias_order(x);
-            if (BIAS) {
-              sum += bf16_bits_to_f32(x.x & 0xFFFFu) + bf16_bits_to_f32(x.x >> 16) +
-                     bf16_bits_to_f32(x.y & 0xFFFFu) + bf16_bits_to_f32(x.y >> 16) +
-                     bf16_bits_to_f32(x.z & 0xFFFFu) + bf16_bits_to_f32(x.z >> 16) +
-                     bf16_bits_to_f32(x.w & 0xFFFFu) + bf16_bits_to_f32(x.w >> 16);
-            }
-            lds_a[frag_slot(16 * t + bb, rb, jr)] = x;
+      for (int b = 0; b < 16; ++b) {
+        if (b < nb) {
+          u32x4_t x = v[b];
+          // gate_up / dense read caller activations in natural order; down
+          // reads intermediate rows the gate_up epilogue wrote in bias order
+          if (BIAS && MODE != kModeDown) x = to_bias_order(x);
+          if (BIAS) {
+            sum += bf16_bits_to_f32(x.x & 0xFFFFu) + bf16_bits_to_f32(x.x >> 16) +
+                   bf16_bits_to_f32(x.y & 0xFFFFu) + bf16_bits_to_f32(x.y >> 16) +
+                   bf16_bits_to_f32(x.z & 0xFFFFu) + bf16_bits_to_f32(x.z >> 16) +
+                   bf16_bits_to_f32(x.w & 0xFFFFu) + bf16_bits_to_f32(x.w >> 16);
           }
+          lds_a[frag_slot(16 * t + b, rb, jr)] = x;
         }
       }
       if (BIAS) csum[t * 16 + jr] = 136.0f * sum;
@@ -397,13 +405,8 @@ void k_decode(DecodeArgs a) {
   // last items of a pass loads the first items again for the next pass
   auto item_at = [&](int p) -> int { return begin + (p >= per ? p - per : p); };
   int rbuf = 0;
-  if (!LONGK) {
-#pragma unroll
-    for (int r = 0; r < RING; ++r) load_batch(r, off_of(phys(begin + r)), tile0);
-  }
-  for (int mc = 0; mc < rows; mc += rb) {
-    const int nr = min(rb, rows - mc);
-    stage(mc, nr);
+  // one pass of rb staged rows over all of this workgroup's items
+  auto pass = [&](int mc, int nr) {
     for (int c0 = begin; c0 < end_pad; c0 += RING) {
 #pragma unroll
     for (int r = 0; r < RING; ++r) {
@@ -481,6 +484,21 @@ void k_decode(DecodeArgs a) {
       }
     }
     }
+  };
+  // The first pass issues the weight prologue between its activation loads
+  // and their use; later passes find the next items' weights in flight (the
+  // refills of a pass's last items load its first items again).
+  stage(0, min(rb, rows), [&] {
+    if (!LONGK) {
+#pragma unroll
+      for (int r = 0; r < RING; ++r) load_batch(r, off_of(phys(begin + r)), tile0);
+    }
+  });
+  pass(0, min(rb, rows));
+  for (int mc = rb; mc < rows; mc += rb) {
+    const int nr = min(rb, rows - mc);
+    stage(mc, nr, [] {});
+    pass(mc, nr);
   }
 }
 
