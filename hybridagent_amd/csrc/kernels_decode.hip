@@ -277,11 +277,13 @@ void k_decode(DecodeArgs a) {
   // fragment order, and -- for the bias form -- summed into
   // csum[t][row] = 136 * (sum of the row's tile elements), the correction the
   // bias form subtracts per group.  Every thread has at most one task
-  // (rb * ntiles <= kStreamThreads, from the LDS budget).  `between` runs
-  // after the task's loads are issued and before they are used: the first
-  // pass issues the weight prologue there, so the activations do not queue
-  // behind the weights (loads complete in issue order).
-  auto stage = [&](int mc, int nr, auto&& between) {
+  // (rb * ntiles <= kStreamThreads, from the LDS budget).  `first` runs
+  // before anything else: the first pass issues the weight prologue there,
+  // as early as the expert is known, so the first items' weights (the bulk
+  // of the start-up traffic) are in flight while the row positions and the
+  // activations are fetched.
+  auto stage = [&](int mc, int nr, auto&& first) {
+    first();
     __syncthreads();  // previous readers of lds_a / csum / tok are done
     // gate_up: token of each staged row; down: the output row t*k+j of each
     // staged row (read here once, so the epilogue issues no load: a load
@@ -315,7 +317,6 @@ void k_decode(DecodeArgs a) {
 #pragma unroll
       for (int b = 0; b < 16; ++b) v[b] = ld16(src + 8 * min(b, nb - 1));
     }
-    between();
     if (has) {
       float sum = 0.f;
 #pragma unroll
@@ -485,9 +486,9 @@ void k_decode(DecodeArgs a) {
     }
     }
   };
-  // The first pass issues the weight prologue between its activation loads
-  // and their use; later passes find the next items' weights in flight (the
-  // refills of a pass's last items load its first items again).
+  // The first pass issues the weight prologue before its staging; later
+  // passes find the next items' weights in flight (the refills of a pass's
+  // last items load its first items again).
   stage(0, min(rb, rows), [&] {
     if (!LONGK) {
 #pragma unroll
