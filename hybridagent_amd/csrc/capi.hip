@@ -4,6 +4,7 @@
 #include "w4a16moe.h"
 
 #include "launch.hpp"
+#include <algorithm>
 
 using namespace w4a16;
 
@@ -76,8 +77,20 @@ struct MoeLayout {
   int32_t* blockcnt;
   uint16_t* inter;
   uint16_t* dn;
+  // bias-form prefill: hidden rows in bias order, their 128-wide k tile
+  // sums, and the intermediate rows' 128-column block sums
+  uint16_t* xb;
+  float* crx;
+  float* crs;
+  float* crh;
   size_t bytes;
 };
+
+// row strides of the bias-form prefill operands: whole 128-wide k tiles
+// plus 64 elements, so consecutive rows start an odd number of 128-byte
+// lines apart
+inline int64_t hidden_ld(int64_t H) { return (H + 127) / 128 * 128 + 64; }
+inline int64_t inter_ld(int64_t I) { return (I + 127) / 128 * 128 + 64; }
 
 MoeLayout moe_layout(void* ws, int64_t M, int64_t k, int64_t E, int64_t H, int64_t I) {
   Carve c(ws);
@@ -88,8 +101,12 @@ MoeLayout moe_layout(void* ws, int64_t M, int64_t k, int64_t E, int64_t H, int64
   L.sorted_pos = c.take<int32_t>(M * k);
   L.tiles = c.take<int32_t>(M * k / kPrefillBM + E + 1);
   L.blockcnt = c.take<int32_t>(size_t(sort_blocks(M * k)) * E);
-  L.inter = c.take<uint16_t>(M * k * I);
+  L.inter = c.take<uint16_t>(M * k * std::max<int64_t>(I, inter_ld(I)));
   L.dn = c.take<uint16_t>(M * k * H);
+  L.xb = c.take<uint16_t>(M * hidden_ld(H));
+  L.crx = c.take<float>(M * ((H + 127) / 128));
+  L.crs = c.take<float>(M * k * ((H + 127) / 128));
+  L.crh = c.take<float>(M * k * ((I + 127) / 128));
   L.bytes = c.used;
   return L;
 }
@@ -270,6 +287,12 @@ inline bool use_prefill(int64_t M, int64_t H, int64_t I) {
   return M > kDecodeMaxM && H % 128 == 0 && I % 64 == 0;
 }
 
+// gate_up and down take the same form (the intermediate layout differs)
+inline bool bias_prefill(int64_t H, int64_t I, int64_t G) {
+  return G % 128 == 0 && prefill_bias_supported((int)((H + G - 1) / G)) &&
+         prefill_bias_supported((int)((I + G - 1) / G));
+}
+
 PrefillArgs prefill_args(const MoeLayout& L, int64_t M, int64_t top_k, int64_t I, int64_t G) {
   PrefillArgs a{};
   a.sorted_pos = L.sorted_pos;
@@ -345,6 +368,23 @@ int moe_gate_up(const uint16_t* hidden, const int32_t* gu_packed, const uint16_t
     p.K = (int)H;
     p.ng = (int)((H + group_size - 1) / group_size);
     p.n_nt = (int)(I / 64);
+    if (bias_prefill(H, I, group_size)) {
+      // bias form: hidden rows reordered once, with their k tile sums
+      hipError_t e = launch_prefill_prep(hidden, L.xb, L.crx, (int)M, (int)H, (int)hidden_ld(H),
+                                         L.sorted_pos, L.offsets + E, (int)top_k, L.crs,
+                                         (int)(M * top_k), s);
+      if (e != hipSuccess) return launch_status(e);
+      p.act = L.xb;
+      p.lda = (int)hidden_ld(H);
+      p.ldo = (int)inter_ld(I);
+      p.ldc = (int)(M * top_k);
+      p.cr = L.crs;
+      p.ncr = (int)((H + 127) / 128);
+      p.cr_out = L.crh;
+      p.ncr_out = (int)((I + 127) / 128);
+      p.n_nt = (int)((I + 127) / 128);  // 128 intermediate columns per item
+      return launch_status(launch_prefill_bias(kModeGateUp, p, max_mtiles(M, top_k, E), s));
+    }
     return launch_status(launch_prefill(kModeGateUp, p, max_mtiles(M, top_k, E), s));
   }
   const int max_slots = (int)(M * top_k < E ? M * top_k : E);
@@ -378,6 +418,15 @@ int moe_down(const int32_t* dn_packed, const uint16_t* dn_scale, int64_t M, int6
     p.K = (int)I;
     p.ng = (int)((I + group_size - 1) / group_size);
     p.n_nt = (int)(H / kPfBN);
+    if (bias_prefill(H, I, group_size)) {
+      // the gate_up epilogue wrote bias-ordered rows and their block sums
+      p.ldc = (int)(M * top_k);
+      p.cr = L.crh;
+      p.ncr = (int)((I + 127) / 128);
+      p.n_nt = (int)((H + 255) / 256);  // 256 output columns per item
+      p.lda = (int)inter_ld(I);
+      return launch_status(launch_prefill_bias(kModeDown, p, max_mtiles(M, top_k, E), s));
+    }
     return launch_status(launch_prefill(kModeDown, p, max_mtiles(M, top_k, E), s));
   }
   const int max_slots = (int)(M * top_k < E ? M * top_k : E);

@@ -69,7 +69,6 @@ __device__ __forceinline__ u32x4_t unpack_bias(uint32_t w, uint32_t mask, uint32
   return r;
 }
 
-// Hides a value from constant folding so it stays in a register.
 // p[i] for a wavefront-uniform i, through the scalar data cache (a read of
 // the constant address space): scalar loads are counted apart from vector
 // loads, so the value arrives without waiting for vector loads in flight.
@@ -79,6 +78,7 @@ __device__ __forceinline__ int32_t ld_uniform(const int32_t* p, int i) {
   return ((cint32_t*)p)[__builtin_amdgcn_readfirstlane(i)];
 }
 
+// Hides a value from constant folding so it stays in a register.
 __device__ __forceinline__ uint32_t opaque(uint32_t v) {
   asm volatile("" : "+v"(v));
   return v;

@@ -49,6 +49,17 @@ struct PrefillArgs {
   const int32_t* counters;    // [1] = number of m-tiles
   int N, K, G, ng, topk, I;
   int n_nt;                   // n-tiles per m-tile
+  // bias form only: 136 * activation sums per (128-wide k tile, segment
+  // row), [ncr][ldc] -- gate_up: of the routed token rows; down: of the
+  // intermediate rows, written by the gate_up epilogue into cr_out
+  const float* cr;
+  float* cr_out;
+  int ncr, ncr_out;
+  // bias form only: row strides (elements) of act and of the gate_up output;
+  // rows hold each 128-wide k tile with its 16-byte chunks transposed
+  // (chunk 4 kb + s of the tile stored at 4 s + kb); ldc = the tile stride
+  // of the correction tables, which are [tile][segment row]
+  int lda, ldo, ldc;
 };
 
 enum DecodeMode { kModeDense = 0, kModeGateUp = 1, kModeDown = 2 };
@@ -92,5 +103,18 @@ hipError_t launch_router_topk(const float* partial, int ksplit, const uint16_t* 
                               int64_t* idx, float* w, int M, int E, int topk, hipStream_t s);
 // prefill grouped GEMM: one launch per stage, items = (m-tile, n-tile)
 hipError_t launch_prefill(int mode, PrefillArgs a, int max_mtiles, hipStream_t s);
+// the bias-form prefill GEMM (group size a multiple of 128) and the pass that
+// writes its gate_up inputs: xb = x in bias order with each 128-wide k tile's
+// chunks transposed, row stride ldx; crx = 136 * the sums of each row's k
+// tiles ([K / 128][M]) and crs = those sums in expert-segment order
+// ([K / 128][ldc]); K a multiple of 128
+hipError_t launch_prefill_prep(const uint16_t* x, uint16_t* xb, float* crx, int M, int K, int ldx,
+                               const int32_t* sorted_pos, const int32_t* rows_total, int topk,
+                               float* crs, int ldc, hipStream_t s);
+// the bias-form prefill kernels stage each item's scales in LDS: they take
+// an even number of scale groups per row, at most 24
+bool prefill_bias_supported(int ng);
+hipError_t launch_prefill_bias(int mode, PrefillArgs a, int max_mtiles, hipStream_t s);
+int prefill_grid_size(const void* kern, int threads, size_t lds, int max_items);
 
 }  // namespace w4a16
