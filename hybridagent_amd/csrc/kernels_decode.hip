@@ -405,9 +405,22 @@ void k_decode(DecodeArgs a) {
   // item at ring position p of a pass (0 <= p < 2 * per): the refill of the
   // last items of a pass loads the first items again for the next pass
   auto item_at = [&](int p) -> int { return begin + (p >= per ? p - per : p); };
+  // After the last pass nothing useful is refilled: every lane of those
+  // loads reads the expert's first bytes (one cache line, a cache hit after
+  // the first wavefront) instead of the first items again, which would
+  // read TPW * 16 bytes per thread from HBM that nobody uses.
+  // MoE outputs (inter or dn rows, M * topk of them) through a buffer
+  // descriptor: masked lanes store past its end, where the hardware drops
+  // the store.  Every wavefront then issues the same stores on every item
+  // (no branch around them), so the compiler can count the memory operations
+  // in flight across the item loop and waits only for the next item's first
+  // weights instead of all of them.
+  const __amdgpu_buffer_rsrc_t osrc =
+      make_rsrc(a.out, (uint32_t)a.M * (uint32_t)a.topk * (uint32_t)(MODE == kModeGateUp ? a.I : a.N) * 2u);
+  constexpr int kNoStore = 0x7FFFFFF0;
   int rbuf = 0;
   // one pass of rb staged rows over all of this workgroup's items
-  auto pass = [&](int mc, int nr) {
+  auto pass = [&](int mc, int nr, bool last) {
     for (int c0 = begin; c0 < end_pad; c0 += RING) {
 #pragma unroll
     for (int r = 0; r < RING; ++r) {
@@ -418,7 +431,12 @@ void k_decode(DecodeArgs a) {
       f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
       if (!LONGK) {
         // refill this register set with the item RING positions ahead
-        const Off nx = off_of(phys(item_at(ct - begin + RING)));
+        // (offsets scaled by 0 or 1: a select here becomes a branch, which
+        // costs the loop a register)
+        const int pn = ct - begin + RING;
+        const int keep = (last && pn >= per) ? 0 : 1;
+        const Off nx0 = off_of(phys(item_at(pn)));
+        const Off nx{nx0.woff * keep, nx0.srow * keep};
         mma_batch(r, tile0, acc, std::true_type{}, nx);
       } else {
         const Off cur = off_of(phys(ct));
@@ -465,22 +483,24 @@ void k_decode(DecodeArgs a) {
           if (q < qlo || q >= qhi) continue;  // uniform: whole wavefront
           const float up = lane_xor8(v[q]);
           const int i = ibase + q;
-          if (j < 8 && i < iend && col_ok) {
-            const float gate = round_bf16(v[q]);
-            const float act = round_bf16(gelu_tanh_f32(gate));
-            const float h = act * round_bf16(up);
-            a.out[(int64_t)(seg0 + i) * a.I + n0 + pos] = f32_to_bf16_bits(h);
-          }
+          const float gate = round_bf16(v[q]);
+          const float act = round_bf16(gelu_tanh_f32(gate));
+          const float h = act * round_bf16(up);
+          const bool ok = j < 8 && i < iend && col_ok;
+          __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(h), osrc,
+                                                ok ? ((seg0 + i) * a.I + n0 + pos) * 2 : kNoStore,
+                                                0, 0);
         }
       } else {
         const int n = colblk * 16 + j;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
+          if (q < qlo || q >= qhi) continue;  // uniform: whole wavefront
           const int i = ibase + q;
-          if (q >= qlo && q < qhi && col_ok && i < iend) {
-            const int64_t orow = tok[i - mc];
-            a.out[orow * a.N + n] = f32_to_bf16_bits(v[q]);
-          }
+          const int orow = tok[i - mc];
+          const bool ok = col_ok && i < iend;
+          __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(v[q]), osrc,
+                                                ok ? (orow * a.N + n) * 2 : kNoStore, 0, 0);
         }
       }
     }
@@ -495,11 +515,11 @@ void k_decode(DecodeArgs a) {
       for (int r = 0; r < RING; ++r) load_batch(r, off_of(phys(begin + r)), tile0);
     }
   });
-  pass(0, min(rb, rows));
+  pass(0, min(rb, rows), rows <= rb);
   for (int mc = rb; mc < rows; mc += rb) {
     const int nr = min(rb, rows - mc);
     stage(mc, nr, [] {});
-    pass(mc, nr);
+    pass(mc, nr, mc + nr >= rows);
   }
 }
 
@@ -603,6 +623,10 @@ static hipError_t launch_decode_mode(DecodeArgs a, int max_slots, hipStream_t s)
 
 hipError_t launch_decode(int mode, bool bias_form, DecodeArgs a, int max_slots, hipStream_t s) {
   if (max_slots <= 0) return hipSuccess;
+  // MoE outputs are addressed by 32-bit byte offsets of one buffer descriptor
+  if (mode != kModeDense &&
+      (int64_t)a.M * a.topk * (mode == kModeGateUp ? a.I : a.N) * 2 >= (int64_t)0x7FFFFFF0)
+    return hipErrorInvalidValue;
   if (mode == kModeDense)
     return bias_form ? launch_decode_mode<kModeDense, true>(a, max_slots, s)
                      : launch_decode_mode<kModeDense, false>(a, max_slots, s);
