@@ -200,13 +200,15 @@ void k_decode(DecodeArgs a) {
 
   const uint32_t kMask = opaque(0x000F000Fu), kBias = opaque(kBiasPair);
 
-  // weight row of this lane's MFMA column for column tile ct
+  // weight row of this lane's MFMA column for column tile ct (gate_up: lanes
+  // j < 8 take gate row n0 + j, lanes j >= 8 up row I + n0 + j - 8)
+  const int jrow_g = (j & 7) + (j >= 8 ? a.I : 0);
   auto weight_row = [&](int ct, bool* ok) -> int {
     const int colblk = ct * CG + cg;
     if (MODE == kModeGateUp) {
       const int n0 = colblk * 8;
       *ok = colblk * 8 + 8 <= a.I;
-      return *ok ? ((j < 8) ? (n0 + j) : (a.I + n0 + (j - 8))) : 0;
+      return *ok ? n0 + jrow_g : 0;
     }
     const int wrow = colblk * 16 + j;
     *ok = wrow < a.N;
@@ -260,14 +262,16 @@ void k_decode(DecodeArgs a) {
   // All loads of one batch are issued back to back; converting a scale right
   // away would make the wavefront wait for it and -- loads retiring in order --
   // for every weight load before it.
+  // In the order of the refills in mma_batch (WIDE: the scales, then the
+  // tiles; otherwise each tile followed by its scale): with one order on
+  // every path into the item loop, the compiler's waits there count only the
+  // loads an item needs first.
   auto load_batch = [&](int r, const Off& o, int tb) {
+    if (WIDE) load_scales_wide(r, o);
 #pragma unroll
-    for (int i = 0; i < TPW; ++i) bw[r][i] = buf_ld16(wsrc, o.woff + 64 * tb, 64 * i);
-    if (WIDE) {
-      load_scales_wide(r, o);
-    } else {
-#pragma unroll
-      for (int i = 0; i < TPW; ++i) sc[r][i] = buf_ld_u16(ssrc, scale_off(o, tb + i));
+    for (int i = 0; i < TPW; ++i) {
+      bw[r][i] = buf_ld16(wsrc, o.woff + 64 * tb, 64 * i);
+      if (!WIDE) sc[r][i] = buf_ld_u16(ssrc, scale_off(o, tb + i));
     }
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -448,42 +452,48 @@ void k_decode(DecodeArgs a) {
       // split-K reduction over the KSPLIT wavefronts of this column group:
       // wavefront ks sums output row q = ks of every lane's four (in
       // wavefront order) and finishes it, so the epilogue is shared four ways
-      int qlo = 0, qhi = 4;
-      f32x4_t v = acc;
+      // wavefront ks finishes output rows qlo .. qlo + QPW - 1 of every
+      // lane's four (all four without a K split): outv[qq] is row qlo + qq
+      constexpr int QPW = 4 / KSPLIT;
+      const int qlo = ks * QPW;
+      float outv[QPW];
       if (KSPLIT > 1) {
         red[rbuf][wave][lane] = acc;
         __syncthreads();
-        float sum = 0.f;
 #pragma unroll
-        for (int w = 0; w < KSPLIT; ++w) sum += red[rbuf][cg * KSPLIT + w][lane][ks];
-        v[ks] = sum;
-        qlo = ks;
-        qhi = ks + 1;
+        for (int qq = 0; qq < QPW; ++qq) {
+          float sum = 0.f;
+#pragma unroll
+          for (int w = 0; w < KSPLIT; ++w) sum += red[rbuf][cg * KSPLIT + w][lane][qlo + qq];
+          outv[qq] = sum;
+        }
         rbuf ^= 1;
+      } else {
+#pragma unroll
+        for (int qq = 0; qq < QPW; ++qq) outv[qq] = acc[qq];
       }
       // output row 4*kb + q of the MFMA tile is staged row 4*kb + q of this
-      // pass; only the pass's nr rows exist
-      const int ibase = mc + 4 * kb;
+      // pass; only the pass's nr rows exist.  Every wavefront stores QPW
+      // values per item, none of them under a branch.
+      const int ibase = mc + 4 * kb + qlo;
       const int iend = mc + nr;
       if (MODE == kModeDense) {
         const int n = colblk * 16 + j;
         const float bb = (a.bias != nullptr && col_ok) ? bf16_bits_to_f32(a.bias[n]) : 0.f;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int i = ibase + q;
-          if (q >= qlo && q < qhi && col_ok && i < iend)
-            a.out[(int64_t)i * a.N + n] = f32_to_bf16_bits(v[q] + bb);
+        for (int qq = 0; qq < QPW; ++qq) {
+          const int i = ibase + qq;
+          if (col_ok && i < iend) a.out[(int64_t)i * a.N + n] = f32_to_bf16_bits(outv[qq] + bb);
         }
       } else if (MODE == kModeGateUp) {
         // lane j (< 8) holds gate column n0+j, lane j+8 the matching up column
         const int n0 = colblk * 8;
         const int pos = BIAS ? ((j & 3) * 2 + ((j >> 2) & 1)) : j;  // bias-order slot
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          if (q < qlo || q >= qhi) continue;  // uniform: whole wavefront
-          const float up = lane_xor8(v[q]);
-          const int i = ibase + q;
-          const float gate = round_bf16(v[q]);
+        for (int qq = 0; qq < QPW; ++qq) {
+          const float up = lane_xor8(outv[qq]);
+          const int i = ibase + qq;
+          const float gate = round_bf16(outv[qq]);
           const float act = round_bf16(gelu_tanh_f32(gate));
           const float h = act * round_bf16(up);
           const bool ok = j < 8 && i < iend && col_ok;
@@ -494,12 +504,11 @@ void k_decode(DecodeArgs a) {
       } else {
         const int n = colblk * 16 + j;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          if (q < qlo || q >= qhi) continue;  // uniform: whole wavefront
-          const int i = ibase + q;
+        for (int qq = 0; qq < QPW; ++qq) {
+          const int i = ibase + qq;
           const int orow = tok[i - mc];
           const bool ok = col_ok && i < iend;
-          __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(v[q]), osrc,
+          __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(outv[qq]), osrc,
                                                 ok ? (orow * a.N + n) * 2 : kNoStore, 0, 0);
         }
       }
