@@ -14,6 +14,12 @@ down [704 -> 2816], all experts W4A16 at group size 128; activations ~N(0,1).
   + router weights (128 * 2816 * 2) + activations in and out (2 * M * 2816 * 2).
 * prefill: M = 4096 tokens, router biased to a Zipf(1.1) expert load with
   empty experts; reported as TFLOP/s over the layer time.
+* dense: the W4A16 linear alone (w4a16_linear, quantization.py
+  Linear4Bit) at M in {1, 4, 16, 64} x (K, N) in {(2816, 2816), (2816, 1408),
+  (704, 2816)}, cycling through enough weight copies that the rotated
+  footprint is >= 512 MiB; bytes = N K / 2 + N ceil(K / 128) 2 + M K 2 + M N 2
+  per call.  One call is one kernel of 1-4 MB, so these rates include the
+  per-launch cost of graph replay.
 
 Weights and inputs are resident in HBM before the timed region; the timed
 region replays a HIP graph of layer forwards that cycles through ``--layers``
@@ -50,6 +56,9 @@ EXPERT_BYTES = (2 * I * H // 2 + 2 * I * math.ceil(H / G) * 2) + (H * I // 2 + H
 GATEUP_BYTES = 2 * I * H // 2 + 2 * I * math.ceil(H / G) * 2
 ROUTER_BYTES = E * H * 2
 DECODE_MS = (1, 8, 32, 64)
+DENSE_SHAPES = ((2816, 2816), (2816, 1408), (704, 2816))
+DENSE_MS = (1, 4, 16, 64)
+DENSE_ROTATE_BYTES = 512 * 2 ** 20  # twice the 256 MB Infinity Cache
 PREFILL_M = 4096
 LATENT_LAYERS, LATENT_BATCH, LATENT_STEPS = 30, 32, 16
 
@@ -143,6 +152,27 @@ def gateup_kernel(layers, dev, M, steps, warmup):
     nbytes = U * GATEUP_BYTES + M * H * 2 + M * TOPK * I * 2
     return {"kernel": "k_decode<gateup,bias> (moe_gate_up)", "M": M, "us": t * 1e6, "bytes": nbytes,
             "gbps": nbytes / t / 1e9}
+
+
+def dense_sweep(dev, steps, warmup):
+    """w4a16_linear over rotated weight copies (>= 512 MiB per shape)."""
+    out = {}
+    for si, (K, N) in enumerate(DENSE_SHAPES):
+        wbytes = N * K // 2 + N * math.ceil(K / G) * 2
+        nrot = math.ceil(DENSE_ROTATE_BYTES / wbytes)
+        packed = synth.packed_int4((nrot, N, K), seed=3000 + si, device=dev)
+        scales = synth.group_scales((nrot, N, K), G, seed=3100 + si, device=dev)
+        for M in DENSE_MS:
+            x = synth.activations(M, K, seed=3200 + M, device=dev)
+            t = time_graph(lambda: [_lib.linear(x, packed[i], scales[i], group_size=G) for i in range(nrot)],
+                           nrot, steps, warmup)
+            nbytes = wbytes + M * K * 2 + M * N * 2
+            out[f"K{K}_N{N}_M{M}"] = {"us": t * 1e6, "bytes": nbytes, "gbps": nbytes / t / 1e9,
+                                      "frac_hbm": nbytes / t / 1e9 / PEAK_HBM_GBS, "copies": nrot}
+            log(f"dense K={K} N={N} M={M}: {t*1e6:.2f} us/call, {nbytes / t / 1e9:.0f} GB/s ({nrot} copies)")
+        del packed, scales
+        torch.cuda.empty_cache()
+    return out
 
 
 def prefill(dev, steps, warmup, n_layers):
@@ -311,6 +341,8 @@ def main(argv=None):
     ap.add_argument("--only-roofline", action="store_true",
                     help="time only the roofline kernel (for rocprofv3 counter runs)")
     ap.add_argument("--no-latent", action="store_true", help="skip the 30-layer latent stack (configs[4])")
+    ap.add_argument("--no-dense", action="store_true", help="skip the dense W4A16 linear sweep (configs[1])")
+    ap.add_argument("--only-dense", action="store_true")
     ap.add_argument("--only-latent", action="store_true")
     ap.add_argument("--only-prefill", action="store_true",
                     help="time only the prefill layer (for rocprofv3 counter runs)")
@@ -334,6 +366,9 @@ def main(argv=None):
     if args.only_latent:
         print(json.dumps({"latent": latent(dev)}), flush=True)
         return 0
+    if args.only_dense:
+        print(json.dumps({"dense": dense_sweep(dev, args.steps, args.warmup)}), flush=True)
+        return 0
     if args.only_prefill:
         pre = prefill(dev, max(8, args.steps // 4), max(2, args.warmup // 4), min(args.layers, 4))
         print(json.dumps({"prefill": pre}), flush=True)
@@ -356,6 +391,8 @@ def main(argv=None):
                                                min(args.layers, 4))
 
     lat = None if args.no_latent else latent(dev)
+
+    dense = None if args.no_dense else dense_sweep(dev, args.steps, args.warmup)
 
     total_bytes = sum(d["bytes"] for d in dec.values())
     total_t = sum(d["us"] for d in dec.values()) * 1e-6
@@ -389,6 +426,8 @@ def main(argv=None):
                                              for k, v in pre.items()},
         "latent": None if lat is None else {k: (round(v, 4) if isinstance(v, float) else v)
                                             for k, v in lat.items()},
+        "dense": None if dense is None else {c: {k: (round(v, 4) if isinstance(v, float) else v)
+                                                 for k, v in d.items()} for c, d in dense.items()},
         "cpu_baseline": None if cpu is None else {k: (round(v, 4) if isinstance(v, float) else v)
                                                   for k, v in cpu.items()},
     }

@@ -156,13 +156,14 @@ void k_decode(DecodeArgs a) {
   // this workgroup's expert and item range.  The grid is spread over the
   // experts that are active in this batch (known only here): wps
   // workgroups each, so the chip fills whatever the routing.
-  int wps = a.wg_per_slot;
-  int U = 1;
+  // Dense: the slots are the groups of rb rows (all of them run at once, so
+  // each workgroup stages its rows once and streams its items once).
+  int U = MODE == kModeDense ? (a.M + a.rb - 1) / a.rb : 1;
   if (MODE != kModeDense) {
     U = ld_uniform(a.n_active, 0);
     if (U <= 0) return;
-    wps = max(1, min(a.n_ct, (int)gridDim.x / U));
   }
+  const int wps = max(1, min(a.n_ct, (int)gridDim.x / U));
   const int slot = (int)blockIdx.x / wps;
   const int part = (int)blockIdx.x - slot * wps;
   if (slot >= U) return;  // uniform across the workgroup
@@ -171,6 +172,9 @@ void k_decode(DecodeArgs a) {
     e = ld_uniform(a.desc, 4 * slot);
     seg0 = ld_uniform(a.desc, 4 * slot + 1);
     rows = ld_uniform(a.desc, 4 * slot + 2);
+  } else {
+    seg0 = slot * a.rb;
+    rows = min(a.rb, a.M - seg0);
   }
   // Items per workgroup, a multiple of the register ring depth so every
   // workgroup walks whole rounds.  The expert's workgroups interleave: local
@@ -313,7 +317,7 @@ void k_decode(DecodeArgs a) {
     u32x4_t v[16];
     if (has) {
       int64_t row;
-      if (MODE == kModeDense) row = mc + jr;
+      if (MODE == kModeDense) row = seg0 + mc + jr;
       else if (MODE == kModeGateUp) row = tok[jr];
       else row = seg0 + mc + jr;
       const uint16_t* src = a.act + row * a.K + 128 * t;
@@ -483,7 +487,7 @@ void k_decode(DecodeArgs a) {
 #pragma unroll
         for (int qq = 0; qq < QPW; ++qq) {
           const int i = ibase + qq;
-          if (col_ok && i < iend) a.out[(int64_t)i * a.N + n] = f32_to_bf16_bits(outv[qq] + bb);
+          if (col_ok && i < iend) a.out[(int64_t)(seg0 + i) * a.N + n] = f32_to_bf16_bits(outv[qq] + bb);
         }
       } else if (MODE == kModeGateUp) {
         // lane j (< 8) holds gate column n0+j, lane j+8 the matching up column
@@ -515,17 +519,15 @@ void k_decode(DecodeArgs a) {
     }
     }
   };
-  // The first pass issues the weight prologue before its staging; later
-  // passes find the next items' weights in flight (the refills of a pass's
-  // last items load its first items again).
-  stage(0, min(rb, rows), [&] {
-    if (!LONGK) {
+  // The weight prologue goes out before the first staging; later passes find
+  // the next items' weights in flight (the refills of a pass's last items
+  // load its first items again).  One loop for every pass: a separate copy
+  // of the pass loop for later passes was compiled with spills.
+  if (!LONGK) {
 #pragma unroll
-      for (int r = 0; r < RING; ++r) load_batch(r, off_of(phys(begin + r)), tile0);
-    }
-  });
-  pass(0, min(rb, rows), rows <= rb);
-  for (int mc = rb; mc < rows; mc += rb) {
+    for (int r = 0; r < RING; ++r) load_batch(r, off_of(phys(begin + r)), tile0);
+  }
+  for (int mc = 0; mc < rows; mc += rb) {
     const int nr = min(rb, rows - mc);
     stage(mc, nr, [] {});
     pass(mc, nr, mc + nr >= rows);
@@ -584,7 +586,7 @@ static hipError_t launch_stream(DecodeArgs a, int max_slots, hipStream_t s) {
   auto kern = k_decode<MODE, BIAS, TPW, KSPLIT, LONGK, WIDE>;
   // the workgroups that fit on the chip at once, at least one per possible
   // expert slot and at most one per item; the kernel spreads them over the
-  // experts that turn out active (dense: one slot, wg_per_slot = grid)
+  // experts that turn out active (dense: the row groups)
   int per_cu = 0;
   constexpr int threads = stream_threads(KSPLIT);
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, stream_lds(a)) !=
@@ -593,7 +595,6 @@ static hipError_t launch_stream(DecodeArgs a, int max_slots, hipStream_t s) {
   const int64_t resident = (int64_t)device_cus() * per_cu;
   int64_t grid = std::min<int64_t>(resident, (int64_t)max_slots * a.n_ct);
   if (grid < max_slots) grid = max_slots;
-  a.wg_per_slot = (int)std::max<int64_t>(1, grid / max_slots);
   if (grid <= 0) return hipSuccess;
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(threads), stream_lds(a), s, a);
   return hipGetLastError();
@@ -611,6 +612,8 @@ static hipError_t launch_decode_mode(DecodeArgs a, int max_slots, hipStream_t s)
   int rows_cap = 1;
   while (rows_cap < a.rows_hint && rows_cap < 16) rows_cap <<= 1;
   if (a.rb > rows_cap) a.rb = rows_cap;
+  // dense: one slot per group of rb rows
+  if (MODE == kModeDense) max_slots = (a.M + a.rb - 1) / a.rb;
   const int ntiles = ((a.K >> 5) + 3) >> 2;
   // one load for an item's scales: group size 128 (one group per k tile)
   // and 4-byte aligned scale rows

@@ -34,7 +34,6 @@ struct DecodeArgs {
   int rb;    // activation rows staged in LDS per pass (<= 16)
   int n_ct;  // work items (column tiles) per expert
   int rows_hint;    // most activation rows one expert can have (set by the caller)
-  int wg_per_slot;  // workgroups sharing one expert's items (set by the launcher)
 };
 
 // Arguments of the prefill-shaped grouped GEMM (kernels_prefill.hip).
