@@ -519,15 +519,19 @@ void k_decode(DecodeArgs a) {
     }
     }
   };
-  // The weight prologue goes out before the first staging; later passes find
-  // the next items' weights in flight (the refills of a pass's last items
-  // load its first items again).  One loop for every pass: a separate copy
-  // of the pass loop for later passes was compiled with spills.
-  if (!LONGK) {
+  // The first pass issues the weight prologue before its staging; later
+  // passes find the next items' weights in flight (the refills of a pass's
+  // last items load its first items again).  (Folding the first pass into
+  // the loop of the later ones was measured twice as slow at decode sizes:
+  // the compiler then waits for the prologue's loads before staging.)
+  stage(0, min(rb, rows), [&] {
+    if (!LONGK) {
 #pragma unroll
-    for (int r = 0; r < RING; ++r) load_batch(r, off_of(phys(begin + r)), tile0);
-  }
-  for (int mc = 0; mc < rows; mc += rb) {
+      for (int r = 0; r < RING; ++r) load_batch(r, off_of(phys(begin + r)), tile0);
+    }
+  });
+  pass(0, min(rb, rows), rows <= rb);
+  for (int mc = rb; mc < rows; mc += rb) {
     const int nr = min(rb, rows - mc);
     stage(mc, nr, [] {});
     pass(mc, nr, mc + nr >= rows);
