@@ -29,6 +29,7 @@ SIGNATURES = {
     "w4a16moe_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "w4a16_dequantize": (ctypes.c_int, [_VP, _VP, _VP, _I64, _I64, _I64, _VP]),
     "w4a16_linear_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
+    "w4a16_add_rms_norm": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _I64, _I64, _F32, _VP]),
     "w4a16_linear": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "moe_router_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
     "moe_router_topk": (ctypes.c_int, [_VP, _VP, _F32, _VP, _VP, _F32, _I64, _I64, _I64, _I64,
@@ -168,6 +169,32 @@ def dequantize(packed: torch.Tensor, scale: torch.Tensor, group_size: int | None
         _check(load().w4a16_dequantize(_ptr(packed), _ptr(scale), _ptr(out), rows, K, G, _stream(dev)),
                "w4a16_dequantize")
     return out
+
+
+def add_rms_norm(h: torch.Tensor, weight: torch.Tensor, eps: float,
+                 delta: torch.Tensor | None = None):
+    """(x, y): x = bf16(h + delta) (h itself without delta), y = RMSNorm(x) * weight in fp32,
+    rounded to bf16 (TF:modeling_gemma4.py:197-215); h, delta [..., H] bf16."""
+    dev = _require_gpu(h, weight, delta)
+    h = _bf16(h, "h")
+    weight = _bf16(weight, "weight")
+    H = h.shape[-1]
+    if weight.shape != (H,):
+        raise ValueError(f"weight must be [{H}]")
+    h2 = h.reshape(-1, H)
+    d2 = None
+    if delta is not None:
+        d2 = _bf16(delta, "delta").reshape(-1, H)
+        if d2.shape != h2.shape:
+            raise ValueError("delta must have the shape of h")
+    M = h2.shape[0]
+    y = torch.empty_like(h2)
+    x = torch.empty_like(h2) if d2 is not None else h2
+    lib = load()
+    with torch.cuda.device(dev):
+        _check(lib.w4a16_add_rms_norm(_ptr(h2), _ptr(d2), _ptr(weight), _ptr(x) if d2 is not None else None,
+                                      _ptr(y), M, H, float(eps), _stream(dev)), "w4a16_add_rms_norm")
+    return x.reshape(h.shape), y.reshape(h.shape)
 
 
 def linear(x: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tensor,

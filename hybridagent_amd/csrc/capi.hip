@@ -141,6 +141,20 @@ int w4a16_dequantize(const int32_t* packed, const uint16_t* scale, uint16_t* out
                                       static_cast<hipStream_t>(stream)));
 }
 
+int w4a16_add_rms_norm(const uint16_t* h, const uint16_t* delta, const uint16_t* weight,
+                       uint16_t* h_out, uint16_t* y, int64_t M, int64_t H, float eps,
+                       void* stream) {
+  if (M < 0 || M > (int64_t(1) << 31) - 1 || H <= 0 || H % 8 != 0 || H > 8192)
+    return W4A16_ERR_SHAPE;
+  if (M == 0) return W4A16_OK;
+  if (!h || !weight || !y || (delta && !h_out)) return W4A16_ERR_NULL;
+  if (!aligned16(h) || !aligned16(weight) || !aligned16(y) || (delta && !aligned16(delta)) ||
+      (h_out && !aligned16(h_out)))
+    return W4A16_ERR_ALIGN;
+  return launch_status(launch_add_rms_norm(h, delta, weight, h_out, y, M, (int)H, eps,
+                                           static_cast<hipStream_t>(stream)));
+}
+
 size_t w4a16_linear_workspace_bytes(int64_t M, int64_t K, int64_t group_size) {
   (void)M;
   (void)K;

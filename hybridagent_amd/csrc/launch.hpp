@@ -68,6 +68,10 @@ hipError_t launch_dequant(const int32_t* packed, const uint16_t* scale, uint16_t
 hipError_t launch_bias_order(const uint16_t* x, uint16_t* xp, int64_t rows, int K, hipStream_t s);
 // max_slots: upper bound of active experts (1 for dense)
 hipError_t launch_decode(int mode, bool bias_form, DecodeArgs a, int max_slots, hipStream_t s);
+// x = bf16(h + delta) -> h_out (delta may be null), y = bf16(rms_norm(x) * w)
+hipError_t launch_add_rms_norm(const uint16_t* h, const uint16_t* delta, const uint16_t* w,
+                               uint16_t* h_out, uint16_t* y, int64_t M, int H, float eps,
+                               hipStream_t s);
 hipError_t launch_combine(const uint16_t* dn, const int64_t* idx, const float* w, uint16_t* out,
                           int M, int topk, int E, int H, hipStream_t s);
 hipError_t launch_sort(const int64_t* idx, int M, int topk, int E, int32_t* sorted_pos,

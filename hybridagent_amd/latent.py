@@ -8,7 +8,9 @@ last layer the HybridLink map R(h) = LN(h + proj2(GELU(proj1(LN(h)))))
 (hybridlink.py:17-28) scaled by sqrt(hidden) gives the next step's input.
 
 The MoE layers run through the HIP library (router + experts in one C-ABI
-call per layer); the norms and the HybridLink MLP are plain torch bf16 ops
+call per layer), and so do the residual add and RMSNorm in front of each
+(one w4a16_add_rms_norm launch: the previous layer's MoE output is added to
+the residual while it is normalised); the HybridLink MLP is plain torch bf16
 (hipBLASLt GEMMs), which is all that path needs.
 """
 from __future__ import annotations
@@ -54,14 +56,15 @@ class LatentStack:
 
     def rms_norm(self, h: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
         """fp32 x * rsqrt(mean(x^2) + eps) * w, back to bf16 (TF:modeling_gemma4.py:197-215)."""
-        x = h.float()
-        y = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + self.eps) * w.float()
-        return y.to(torch.bfloat16)
+        return _lib.add_rms_norm(h, w, self.eps)[1]
 
     def moe(self, h: torch.Tensor, i: int):
         """MoE block of layer i on residual h -> (out, top_k_index, top_k_weights)."""
+        return self.moe_on(h, self.rms_norm(h, self.layers[i].pre_norm), i)
+
+    def moe_on(self, h: torch.Tensor, xin: torch.Tensor, i: int):
+        """MoE block of layer i: router on the residual h, experts on xin = RMSNorm(h)."""
         ly = self.layers[i]
-        xin = self.rms_norm(h, ly.pre_norm)
         rw, ew = ly.router, ly.experts
         out, w, idx = _lib.moe_layer_forward(h, rw.scale, rw.scalar_root, rw.proj, rw.per_expert_scale,
                                              rw.eps, self.top_k, xin, ew.gate_up_packed, ew.gate_up_scale,
@@ -81,7 +84,11 @@ class LatentStack:
         return F.layer_norm(h + a, (self.H,), p["ln2w"], p["ln2b"])
 
     def step(self, h: torch.Tensor) -> torch.Tensor:
-        """One latent step: all MoE layers, then HybridLink x sqrt(H)."""
-        for i in range(len(self.layers)):
-            h, _, _ = self.layer(h, i)
-        return self.hybridlink(h) * math.sqrt(self.H)
+        """One latent step: all MoE layers, then HybridLink x sqrt(H).  The same
+        arithmetic as calling layer() in turn: layer i's output is added to the
+        residual inside layer i + 1's norm launch."""
+        out = None
+        for i, ly in enumerate(self.layers):
+            h, xin = _lib.add_rms_norm(h, ly.pre_norm, self.eps, delta=out)
+            out, _, _ = self.moe_on(h, xin, i)
+        return self.hybridlink(h + out) * math.sqrt(self.H)

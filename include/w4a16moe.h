@@ -70,6 +70,19 @@ W4A16_API int w4a16_linear(const uint16_t* x, const int32_t* w_packed, const uin
                  const uint16_t* bias, uint16_t* y, int64_t M, int64_t N, int64_t K,
                  int64_t group_size, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Residual add + RMSNorm of the MoE input in the latent harness (config 4):
+ * RMSNorm -- transformers/models/gemma4/modeling_gemma4.py:197-215 (fp32
+ * x * rsqrt(mean(x^2) + eps) * weight, back to bf16); the add is the
+ * harness's h <- h + MoE(...).
+ *   x      = bf16(h + delta)       written to h_out; delta NULL: x = h and
+ *                                  h_out is not written (may be NULL)
+ *   y      = bf16((x * rsqrt(mean(x^2) + eps)) * weight)
+ * h, delta, h_out, y [M, H] bf16; weight [H] bf16.  H % 8 == 0, H <= 8192;
+ * 16-byte aligned pointers.  No workspace.                                  */
+W4A16_API int w4a16_add_rms_norm(const uint16_t* h, const uint16_t* delta, const uint16_t* weight,
+                       uint16_t* h_out, uint16_t* y, int64_t M, int64_t H, float eps,
+                       void* stream);
+
 /* Router  -- backends.py:111-117 (HF Gemma4TextRouter.forward,
  * transformers/models/gemma4/modeling_gemma4.py:1335-1356):
  *   r       = bf16(bf16(rms_norm(hidden) * router_scale) * scalar_root)

@@ -58,6 +58,17 @@ def test_linear_host_validation(lib):
     assert lib.w4a16_linear(ctypes.c_void_p(4098), fake, fake, NULL, fake, 4, 16, 64, 32, NULL, 0, NULL) == 4
     # the dense path needs no scratch memory
     assert lib.w4a16_linear_workspace_bytes(4, 256, 128) == 0
+
+
+def test_add_rms_norm_host_validation(lib):
+    fake = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    f = lib.w4a16_add_rms_norm
+    assert f(fake, NULL, fake, NULL, fake, 4, 12, 1e-6, NULL) == 2       # H % 8
+    assert f(fake, NULL, fake, NULL, fake, 4, 8200, 1e-6, NULL) == 2     # H > 8192
+    assert f(NULL, NULL, fake, NULL, fake, 4, 64, 1e-6, NULL) == 1       # h missing
+    assert f(fake, fake, fake, NULL, fake, 4, 64, 1e-6, NULL) == 1       # delta without h_out
+    assert f(ctypes.c_void_p(4098), NULL, fake, NULL, fake, 4, 64, 1e-6, NULL) == 4
+    assert f(NULL, NULL, NULL, NULL, NULL, 0, 64, 1e-6, NULL) == 0       # nothing to do
     # K beyond what one LDS pass stages
     assert lib.w4a16_linear(fake, fake, fake, NULL, fake, 4, 16, 32768, 128, NULL, 0, NULL) == 2
     # M == 0 is a no-op

@@ -4,6 +4,8 @@ Bars: bit-exact for dequantised weights, routing indices (given identical
 logits) and the token permutation; max_abs_rel <= 1e-2 for layer outputs
 (``max|y - y_ref| / max|y_ref|``, the tolerance the north star states).
 """
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -413,5 +415,31 @@ def test_latent_stack_layers_and_hybridlink(dev):
     p = {key: _np(v) for key, v in st.hl.items()}
     ref = oracle.hybridlink(_np(h), p["p1w"], p["p1b"], p["p2w"], p["p2b"], p["ln1w"], p["ln1b"], p["ln2w"], p["ln2b"])
     assert oracle.max_abs_rel(_np(st.hybridlink(h)), ref) <= 2 * TOL
-    out = st.step(synth.activations(6, h_, seed=902, device=dev))
+    h0 = synth.activations(6, h_, seed=902, device=dev)
+    out = st.step(h0)
     assert out.shape == (6, h_) and torch.isfinite(out.float()).all()
+    # step() adds each layer's output inside the next layer's norm launch:
+    # bit-identical to the layers one after the other
+    hs = h0
+    for li in range(len(st.layers)):
+        hs, _, _ = st.layer(hs, li)
+    assert torch.equal(out, st.hybridlink(hs) * math.sqrt(h_))
+
+
+@pytest.mark.parametrize("M,H", [(1, 2816), (32, 2816), (5, 8), (3, 8192), (7, 1000)])
+def test_add_rms_norm(dev, M, H):
+    # x = bf16(h + delta) bit-exact against torch's bf16 add; y within one
+    # bf16 ulp of the oracle's RMSNorm (fp32 reduction order)
+    g = torch.Generator().manual_seed(M * 7 + H)
+    h = torch.randn(M, H, generator=g).to(torch.bfloat16)
+    d = (0.5 * torch.randn(M, H, generator=g)).to(torch.bfloat16)
+    w = (1.0 + 0.05 * torch.randn(H, generator=g)).to(torch.bfloat16)
+    x, y = _lib.add_rms_norm(h.to(dev), w.to(dev), 1e-6, delta=d.to(dev))
+    assert torch.equal(x.cpu(), h + d)
+    ref = oracle.rms_norm(_np(h + d), _np(w), 1e-6)
+    ulp = np.abs(oracle.to_bf16_bits(_np(y)).astype(np.int32) - oracle.to_bf16_bits(ref).astype(np.int32))
+    assert ulp.max() <= 1
+    x2, y2 = _lib.add_rms_norm(h.to(dev), w.to(dev), 1e-6)
+    assert torch.equal(x2.cpu(), h)
+    ref2 = oracle.rms_norm(_np(h), _np(w), 1e-6)
+    assert np.abs(oracle.to_bf16_bits(_np(y2)).astype(np.int32) - oracle.to_bf16_bits(ref2).astype(np.int32)).max() <= 1
