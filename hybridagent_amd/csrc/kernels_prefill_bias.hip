@@ -21,8 +21,10 @@
 //      XOR-swizzled by row), unpacked per wavefront with four v_and_or_b32
 //      per word into (128 + u) bf16 pairs;
 //   c  the rows' activation sums for the tile.
-// The MFMAs accumulate g = sum x (128 + u) over the tile, which is folded
-// into the fp32 accumulator as acc += s (g - 136 c) (the tables hold 136 c).
+// The tables hold -136 c; the tile's first MFMAs take it as their
+// accumulator input, so the MFMAs produce g = sum x (128 + u) - 136 c
+// = sum x (u - 8) over the tile and the fold is one fma per accumulator
+// element: acc += s g.
 // A ring of three k tiles
 // keeps two in flight while one is multiplied; the waits count loads (every
 // wavefront issues the same ones), and the barriers wait only for LDS.
@@ -84,7 +86,7 @@ __device__ __forceinline__ int bias_pos(int c) { return ((c & 3) << 1) | ((c >> 
 // ---------------------------------------------------------------------------
 // hidden rows -> bias order with each 128-wide k tile's 16-byte chunks
 // transposed (chunk 4 kb + s stored at 4 s + kb, so MFMA steps 2h, 2h + 1
-// are 128 contiguous bytes of a row), and 136 * (the sum of each row's k
+// are 128 contiguous bytes of a row), and -136 * (the sum of each row's k
 // tile) into crx[t][row].  16 lanes (one DPP row) per (row, tile); lane c
 // owns chunk c.
 // ---------------------------------------------------------------------------
@@ -107,7 +109,7 @@ __global__ __launch_bounds__(256) void k_prefill_prep(const uint16_t* __restrict
   sum = __uint_as_float(dpp_row_reduce(__float_as_uint(sum), [](uint32_t a, uint32_t b) {
     return __float_as_uint(__uint_as_float(a) + __uint_as_float(b));
   }));
-  if (c == 0) crx[(int64_t)t * M + row] = 136.0f * sum;
+  if (c == 0) crx[(int64_t)t * M + row] = -136.0f * sum;
 }
 
 // the tile sums in expert-segment order: crs[t][s] = crx[t][token of row s]
@@ -315,11 +317,13 @@ void k_prefill_bias(PrefillArgs a) {
 #pragma unroll
       for (int f = 0; f < 4; ++f)
         bw[f] = bbuf[r * kPbBStage + brow[f] * 4 + (kb ^ (brow[f] & 3))];
-      f32x4_t g[4][4];
+      // -136 * the tile sums of this lane's output rows (4 kb .. 4 kb + 3 of
+      // m-tile i): the accumulator input of the tile's first MFMAs
+      f32x4_t ncr[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int f = 0; f < 4; ++f) g[i][f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        ncr[i] = *reinterpret_cast<const f32x4_t*>(crbuf + r * kPbBM + 16 * (wm * 4 + i) + 4 * kb);
+      f32x4_t g[4][4];
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         u32x4_t af[4], bv[4];
@@ -333,20 +337,17 @@ void k_prefill_bias(PrefillArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-          for (int f = 0; f < 4; ++f) g[i][f] = mfma16(af[i], bv[f], g[i][f]);
+          for (int f = 0; f < 4; ++f) g[i][f] = mfma16(af[i], bv[f], s == 0 ? ncr[i] : g[i][f]);
         __builtin_amdgcn_sched_barrier(0);
         issue_part(tn, rn, s);
         __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        // rows 4 kb .. 4 kb + 3 of m-tile i: this lane's output rows
-        const f32x4_t cr = *reinterpret_cast<const f32x4_t*>(crbuf + r * kPbBM + 16 * (wm * 4 + i) + 4 * kb);
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
 #pragma unroll
-          for (int f = 0; f < 4; ++f) acc[i][f][q] = __builtin_fmaf(sf[f], g[i][f][q] - cr[q], acc[i][f][q]);
-      }
+          for (int f = 0; f < 4; ++f) acc[i][f][q] = __builtin_fmaf(sf[f], g[i][f][q], acc[i][f][q]);
     };
     // k tile t + 1 must have landed; t + 2 may still be loading
     auto wait_next = [&]() {
@@ -440,7 +441,7 @@ void k_prefill_bias(PrefillArgs a) {
       lds_barrier();
       if (tid < kPbBM && tid < nrows)
         a.cr_out[(int64_t)nt * a.ldc + seg0 + tid] =
-            136.0f * (((red[tid] + red[kPbBM + tid]) + red[2 * kPbBM + tid]) + red[3 * kPbBM + tid]);
+            -136.0f * (((red[tid] + red[kPbBM + tid]) + red[2 * kPbBM + tid]) + red[3 * kPbBM + tid]);
     } else {
       constexpr int PITCH = 72;
       uint16_t* ob = reinterpret_cast<uint16_t*>(smem) + wave * 64 * PITCH;
