@@ -297,6 +297,20 @@ def _skewed_route(M, seed, hot=8):
     return idx, (w / w.sum(1, keepdim=True)).float()
 
 
+@pytest.mark.parametrize("M", [48, 200])
+def test_moe_decode_experts_over_16_rows(dev, moe128, M):
+    # decode sizes with every token on the same 8 experts: each expert has M
+    # rows, more than one staging pass (16 rows) of the streaming kernels
+    cpu, gpu = moe128
+    x = synth.activations(M, H, seed=240 + M)
+    idx, w = _skewed_route(M, seed=340 + M)
+    y = _moe_gpu(x, idx, w, gpu, dev)
+    rows = np.arange(0, M, max(1, M // 24))
+    err = oracle.max_abs_rel(_np(y)[rows], _moe_ref(x, idx, w, cpu, 128, rows=rows))
+    print(f"moe decode skewed M={M} sampled max_abs_rel={err:.2e}")
+    assert err <= TOL
+
+
 @pytest.mark.parametrize("M", [257, 300])
 def test_moe_prefill_skewed_segments(dev, moe128, M):
     cpu, gpu = moe128
