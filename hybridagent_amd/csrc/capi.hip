@@ -33,7 +33,9 @@ struct Carve {
 
 inline int launch_status(hipError_t e) { return e == hipSuccess ? W4A16_OK : W4A16_ERR_LAUNCH; }
 
-inline int router_ksplit(int64_t M) { return M <= 64 ? 16 : 1; }
+// K splits of the router logits: decode sizes 16, large batches what the
+// large-batch router picks for its grid
+inline int router_ksplit(int64_t M, int64_t E) { return M <= 64 ? 16 : router_tok_splits(M, E); }
 
 // Token counts up to this use the decode kernels; larger batches the
 // prefill grouped-GEMM kernels.
@@ -46,22 +48,24 @@ constexpr int64_t kTopkSortMaxEntries = 64;
 // longest reduction the streaming kernels stage in LDS (one row per pass)
 constexpr int64_t kMaxStreamK = 49152 / 2;
 
-// Router partial logits: a normalisation pass into r, then the K-split
-// MFMA logits.  (Normalising inside the logits kernel was measured slower:
-// every wavefront then re-reads whole rows.)
+// Router partial logits.  `r` is workspace of M * H bf16: the normalised
+// rows on the generic path, the rows' inverse norms (M floats) on the
+// large-batch path.
 hipError_t launch_router_partials(const uint16_t* hidden, const uint16_t* scale, float root,
                                   float eps, const uint16_t* proj, uint16_t* r, float* partial,
                                   int64_t M, int64_t H, int64_t E, hipStream_t s) {
-  const int ks = router_ksplit(M);
+  const int ks = router_ksplit(M, E);
+  // large batches: inverse norms, then logits with r formed in registers
+  if (M > 64)
+    return launch_router_tok(hidden, scale, root, eps, proj, reinterpret_cast<float*>(r), partial,
+                             (int)M, (int)H, (int)E, s);
   // decode sizes: the norm inside the logits launch (each workgroup covers
   // all experts of 16 tokens, so it normalises its rows once)
-  if (ks > 1 && H <= 384 * 8)
+  if (H <= 384 * 8)
     return launch_router_norm_logits(hidden, scale, root, eps, proj, partial, (int)M, (int)H,
                                      (int)E, ks, s);
-  // large batches: the norm inside a tiled logits GEMM (64 tokens x 32 experts
-  // per workgroup over the whole K)
-  if (ks == 1 && H % 64 == 0)
-    return launch_router_big(hidden, scale, root, eps, proj, partial, (int)M, (int)H, (int)E, s);
+  // long rows at decode sizes: a normalisation pass into r, then the K-split
+  // MFMA logits
   hipError_t e = launch_router_norm(hidden, scale, root, eps, r, (int)M, (int)H, s);
   if (e == hipSuccess) e = launch_router_logits(r, proj, partial, (int)M, (int)H, (int)E, ks, s);
   return e;
@@ -196,7 +200,7 @@ int w4a16_linear(const uint16_t* x, const int32_t* w_packed, const uint16_t* w_s
 
 size_t moe_router_workspace_bytes(int64_t M, int64_t H, int64_t E) {
   if (M <= 0 || H <= 0 || E <= 0) return 0;
-  return round256(size_t(M) * H * 2) + round256(size_t(router_ksplit(M)) * M * E * 4);
+  return round256(size_t(M) * H * 2) + round256(size_t(router_ksplit(M, E)) * M * E * 4);
 }
 
 int moe_router_topk(const uint16_t* hidden, const uint16_t* router_scale, float scalar_root,
@@ -217,7 +221,7 @@ int moe_router_topk(const uint16_t* hidden, const uint16_t* router_scale, float 
   hipStream_t s = static_cast<hipStream_t>(stream);
   Carve c(workspace);
   uint16_t* r = c.take<uint16_t>(M * H);
-  const int ks = router_ksplit(M);
+  const int ks = router_ksplit(M, E);
   float* partial = c.take<float>(size_t(ks) * M * E);
   hipError_t e = launch_router_partials(hidden, router_scale, scalar_root, eps, proj_w, r, partial,
                                         M, H, E, s);
@@ -524,18 +528,18 @@ int moe_layer_forward(const uint16_t* router_in, const uint16_t* router_scale, f
   hipStream_t s = static_cast<hipStream_t>(stream);
   Carve c(static_cast<char*>(workspace) + moe_bytes);
   uint16_t* r = c.take<uint16_t>(M * H);
-  float* partial = c.take<float>(size_t(router_ksplit(M)) * M * E);
+  float* partial = c.take<float>(size_t(router_ksplit(M, E)) * M * E);
   hipError_t e = launch_router_partials(router_in, router_scale, scalar_root, eps, proj_w, r,
                                         partial, M, H, E, s);
   if (e != hipSuccess) return W4A16_ERR_LAUNCH;
   if (M * top_k <= kTopkSortMaxEntries) {
     // small batches: top-k and the expert sort in one workgroup
-    e = launch_topk_sort(partial, router_ksplit(M), per_expert_scale, topk_idx, topk_w, (int)M,
+    e = launch_topk_sort(partial, router_ksplit(M, E), per_expert_scale, topk_idx, topk_w, (int)M,
                          (int)E, (int)top_k, L.sorted_pos, L.offsets, L.desc, L.counters, L.tiles,
                          kPrefillBM, s);
     if (e != hipSuccess) return W4A16_ERR_LAUNCH;
   } else {
-    e = launch_router_topk(partial, router_ksplit(M), nullptr, per_expert_scale, nullptr, topk_idx,
+    e = launch_router_topk(partial, router_ksplit(M, E), nullptr, per_expert_scale, nullptr, topk_idx,
                            topk_w, (int)M, (int)E, (int)top_k, s);
     if (e != hipSuccess) return W4A16_ERR_LAUNCH;
     st = moe_plan(hidden, topk_idx, M, top_k, E, H, I, group_size, workspace, moe_bytes, stream);

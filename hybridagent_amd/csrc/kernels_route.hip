@@ -324,173 +324,172 @@ hipError_t launch_router_norm_logits(const uint16_t* h, const uint16_t* scale, f
 }
 
 // ---------------------------------------------------------------------------
-// router RMSNorm + logits for large batches: one workgroup per (64 tokens, 32
-// experts) over the whole K.  Prologue: the rows' sums of squares (4 threads
-// per row, fixed order, then a quad reduction).  Main loop over 64-wide k
-// stages: r = bf16(bf16(bf16(x * inv) * scale) * root) is formed on the fly
-// into LDS (MFMA A-operand order) next to the stage's router-weight tile;
-// wavefront w multiplies token block w against the two expert blocks.  The
-// next stage's global loads are in flight during the current stage's MFMA.
+// router for large batches, two launches.
+//   k_router_inv   inv[m] = 1 / sqrt(mean(h[m]^2) + eps): one wavefront per
+//                  row, each lane's chunks in order, then the wave sum
+//   k_router_tok   partial[ks][m][e]: wavefront w of a workgroup owns 16
+//                  tokens and 128 experts over split ks's k range.  r = bf16(bf16(bf16(x * inv) * scale) * root) is
+//                  formed in registers as the MFMA A operand, so every
+//                  element of h is read and normalised once.  The router
+//                  weights of up to 12 steps are staged in LDS per chunk
+//                  (one barrier pair per chunk; one chunk at H = 2816 and 8
+//                  splits), and all of a chunk's activation loads are issued
+//                  before its first MFMA.
+// Rows past M and experts past E read clamped (in-bounds) addresses; MFMA
+// rows and columns are independent, so their results are simply not stored.
 // ---------------------------------------------------------------------------
-constexpr int kBigTok = 64, kBigExp = 32, kBigBK = 64, kBigDepth = 4;
+__global__ __launch_bounds__(256) void k_router_inv(const uint16_t* __restrict__ h,
+                                                    float eps, float* __restrict__ inv, int M,
+                                                    int H) {
+  constexpr int kChunks = 8;  // H <= 64 * 8 * 8 = 4096 in one batch of loads
+  const int lane = threadIdx.x & 63;
+  const int64_t m = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= M) return;  // uniform per wavefront
+  const uint16_t* row = h + m * H;
+  const int n8 = H >> 3;
+  float ss = 0.f;
+  for (int b = 0; b < n8; b += 64 * kChunks) {
+    u32x4_t v[kChunks];
+#pragma unroll
+    for (int q = 0; q < kChunks; ++q) {
+      const int c8 = b + lane + 64 * q;
+      v[q] = c8 < n8 ? ld16(row + 8 * c8) : u32x4_t{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int q = 0; q < kChunks; ++q) {
+      const uint32_t w4[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float lo = bf16_bits_to_f32(w4[t] & 0xFFFFu), hi = bf16_bits_to_f32(w4[t] >> 16);
+        ss = __builtin_fmaf(lo, lo, ss);
+        ss = __builtin_fmaf(hi, hi, ss);
+      }
+    }
+  }
+  const float tot = wave_sum(ss);
+  if (lane == 0) inv[m] = 1.0f / sqrtf(tot / (float)H + eps);
+}
 
-__global__ __launch_bounds__(256) void k_router_big(const uint16_t* __restrict__ h,
-                                                   const uint16_t* __restrict__ scale,
-                                                   float scalar_root, float eps,
-                                                   const uint16_t* __restrict__ proj,
-                                                   float* __restrict__ logits, int M, int H,
-                                                   int E) {
-  // fragment order: A [row block 4][k32 2][lane 64], B [col block 2][k32 2][lane 64]
-  __shared__ u32x4_t sa[2][4 * 2 * 64];
-  __shared__ u32x4_t sb[2][2 * 2 * 64];
-  __shared__ float s_inv[kBigTok];
-  __shared__ float s_ss[kBigTok][4];
+constexpr int kTokExperts = 128;  // experts per workgroup (8 MFMA column tiles)
+constexpr int kTokLdsSteps = 12;  // k steps of 32 whose router weights sit in LDS at once
+constexpr int kTokWaves = 8;      // wavefronts per workgroup, 16 tokens each
+constexpr int kTokThreads = 64 * kTokWaves;
+constexpr int kTokRows = 16 * kTokWaves;
+
+// LDS bytes of k_router_tok for `steps` steps per chunk: the weight fragments
+// [step][column tile][lane] and the scale chunks [step][kb], 16 bytes each
+size_t router_tok_lds(int steps) { return (size_t)steps * (kTokExperts / 16 * 64 + 4) * 16; }
+
+__global__ __launch_bounds__(kTokThreads) void k_router_tok(const uint16_t* __restrict__ h,
+                                                            const float* __restrict__ inv,
+                                                            const uint16_t* __restrict__ scale,
+                                                            float scalar_root,
+                                                            const uint16_t* __restrict__ proj,
+                                                            float* __restrict__ partial, int M,
+                                                            int H, int E, int steps_per_split,
+                                                            int lds_steps) {
+  constexpr int NF = kTokExperts / 16;
+  static_assert(kTokThreads == kTokExperts * 4, "one staging thread per (expert, 8-wide chunk)");
+  extern __shared__ u32x4_t lds[];
+  u32x4_t* sb = lds;                         // [lds_steps][NF][64]
+  u32x4_t* ss = lds + lds_steps * NF * 64;   // [lds_steps][4]
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int m0 = blockIdx.x * kBigTok, e0 = blockIdx.y * kBigExp;
-  const int n8 = H >> 3;
+  const int j = lane & 15, kb = lane >> 4;
+  const int ks = blockIdx.y;
+  const int mw = blockIdx.x * kTokRows + wave * 16;
+  const int eg = blockIdx.z * kTokExperts;
+  const int c0 = ks * steps_per_split;
+  const int c1 = min(H >> 5, c0 + steps_per_split);
 
-  // prologue: sums of squares, 4 threads per row
-  {
-    const int r = tid >> 2, sub = tid & 3;
-    const uint16_t* row = h + (int64_t)min(m0 + r, M - 1) * H;
-    float ss = 0.f;
-    for (int c8 = sub; c8 < n8; c8 += 4 * 8) {
-      u32x4_t v[8];
+  const int m = min(mw + j, M - 1);
+  const uint16_t* xrow = h + (int64_t)m * H + 8 * kb;
+  const float rinv = inv[m];
+  // staging role: expert se, 8-wide chunk sq of each step; its LDS slot is
+  // column tile se / 16, lane (se % 16) + 16 sq (a wavefront's 64 stores
+  // fill one contiguous kilobyte)
+  const int se = tid >> 2, sq = tid & 3;
+  const uint16_t* wrow = proj + (int64_t)min(eg + se, E - 1) * H + 8 * sq;
+  const int sslot = (se >> 4) * 64 + (se & 15) + 16 * sq;
+  f32x4_t acc[NF];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int c = c8 + 4 * u;
-        v[u] = c < n8 ? ld16(row + 8 * c) : u32x4_t{0u, 0u, 0u, 0u};
-      }
+  for (int f = 0; f < NF; ++f) acc[f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int cc = c0; cc < c1; cc += lds_steps) {
+    const int ns = min(lds_steps, c1 - cc);
+    // the chunk's router weights first, then its activation rows and
+    // scales, which stay in flight through the LDS stores and the barrier
+    u32x4_t st[kTokLdsSteps];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const uint32_t w4[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+    for (int s2 = 0; s2 < kTokLdsSteps; ++s2) st[s2] = ld16(wrow + 32 * (cc + min(s2, ns - 1)));
+    const u32x4_t sc = ld16(scale + 32 * cc + 8 * min(tid, ns * 4 - 1));
+    u32x4_t xv[kTokLdsSteps];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const float lo = bf16_bits_to_f32(w4[t] & 0xFFFFu), hi = bf16_bits_to_f32(w4[t] >> 16);
-          ss = __builtin_fmaf(lo, lo, ss);
-          ss = __builtin_fmaf(hi, hi, ss);
-        }
-      }
-    }
-    // the row's four partials, summed in thread order
-    s_ss[r][sub] = ss;
+    for (int s2 = 0; s2 < kTokLdsSteps; ++s2) xv[s2] = ld16(xrow + 32 * (cc + min(s2, ns - 1)));
+    if (cc != c0) __syncthreads();  // the previous chunk's fragments are consumed
+#pragma unroll
+    for (int s2 = 0; s2 < kTokLdsSteps; ++s2)
+      if (s2 < ns) sb[s2 * NF * 64 + sslot] = st[s2];
+    if (tid < ns * 4) ss[tid] = sc;
     __syncthreads();
-    if (tid < kBigTok) {
-      const float tot = ((s_ss[tid][0] + s_ss[tid][1]) + s_ss[tid][2]) + s_ss[tid][3];
-      s_inv[tid] = 1.0f / sqrtf(tot / (float)H + eps);
-    }
-    __syncthreads();
-  }
-
-  // staging roles: A chunks (row ar, 8-wide k chunk ac) x2, B chunks x1
-  // A: 64 rows x 8 chunks = 512 -> threads tid, tid + 256; B: 32 experts x 8 chunks = 256
-  auto a_role = [&](int q, int* row, int* chunk) {
-    const int id = tid + 256 * q;
-    *row = id >> 3;
-    *chunk = id & 7;
-  };
-  const int br = tid >> 3, bc = tid & 7;
-  const int be = min(e0 + br, E - 1);
-  const bool be_ok = e0 + br < E;
-
-  // kBigDepth stages of global loads in flight (register slots)
-  u32x4_t gx[kBigDepth][2], gs[kBigDepth][2], gp[kBigDepth];
-  auto load_stage = [&](int slot, int ks) {
-    const int kbase = ks * kBigBK;
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      int row, chunk;
-      a_role(q, &row, &chunk);
-      const int m = min(m0 + row, M - 1);
-      gx[slot][q] = ld16(h + (int64_t)m * H + kbase + 8 * chunk);
-      gs[slot][q] = ld16(scale + kbase + 8 * chunk);
-    }
-    gp[slot] = ld16(proj + (int64_t)be * H + kbase + 8 * bc);
-  };
-  auto store_stage = [&](int buf, int slot) {
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      int row, chunk;
-      a_role(q, &row, &chunk);
-      u32x4_t o = {0u, 0u, 0u, 0u};
-      if (m0 + row < M) {
-        const float inv = s_inv[row];
-        const uint32_t xw[4] = {gx[slot][q].x, gx[slot][q].y, gx[slot][q].z, gx[slot][q].w};
-        const uint32_t sw[4] = {gs[slot][q].x, gs[slot][q].y, gs[slot][q].z, gs[slot][q].w};
+    for (int s2 = 0; s2 < kTokLdsSteps; ++s2) {
+      if (s2 < ns) {
+        const u32x4_t sv = ss[s2 * 4 + kb];
+        const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+        const uint32_t xw[4] = {xv[s2].x, xv[s2].y, xv[s2].z, xv[s2].w};
         uint32_t ow[4];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
+        for (int q = 0; q < 4; ++q) {
           float rr[2];
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh) {
-            const float xe = bf16_bits_to_f32(hh ? (xw[t] >> 16) : (xw[t] & 0xFFFFu));
-            const float se = bf16_bits_to_f32(hh ? (sw[t] >> 16) : (sw[t] & 0xFFFFu));
-            const float v1 = round_bf16(xe * inv);
-            const float v2 = round_bf16(v1 * se);
+            const float xe = bf16_bits_to_f32(hh ? (xw[q] >> 16) : (xw[q] & 0xFFFFu));
+            const float sf = bf16_bits_to_f32(hh ? (sw[q] >> 16) : (sw[q] & 0xFFFFu));
+            const float v1 = round_bf16(xe * rinv);
+            const float v2 = round_bf16(v1 * sf);
             rr[hh] = v2 * scalar_root;
           }
-          ow[t] = pack_bf16x2(rr[0], rr[1]);
+          ow[q] = pack_bf16x2(rr[0], rr[1]);
         }
-        o = u32x4_t{ow[0], ow[1], ow[2], ow[3]};
-      }
-      // row block row/16, k32 chunk/4, lane (row%16) + 16 (chunk%4)
-      sa[buf][((row >> 4) * 2 + (chunk >> 2)) * 64 + (row & 15) + 16 * (chunk & 3)] = o;
-    }
-    sb[buf][((br >> 4) * 2 + (bc >> 2)) * 64 + (br & 15) + 16 * (bc & 3)] =
-        be_ok ? gp[slot] : u32x4_t{0u, 0u, 0u, 0u};
-  };
-
-  f32x4_t acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-  const int nks = H / kBigBK;
-  constexpr int D = kBigDepth;
+        const u32x4_t a = {ow[0], ow[1], ow[2], ow[3]};
 #pragma unroll
-  for (int d = 0; d < D; ++d) load_stage(d, min(d, nks - 1));
-  store_stage(0, 0);
-  __syncthreads();
-  // stage s: slot s % D (already in LDS buffer s & 1) is refilled with stage
-  // s + D; stage s + 1 (slot (s + 1) % D) goes to the other buffer.  Stages
-  // past the end reload the last one (in bounds, unused).
-  for (int k0 = 0; k0 < nks; k0 += D) {
-#pragma unroll
-    for (int u = 0; u < D; ++u) {
-      const int ks = k0 + u;
-      if (ks < nks) {
-        const int cur = ks & 1;
-        load_stage(u, min(ks + D, nks - 1));
-#pragma unroll
-        for (int k32 = 0; k32 < 2; ++k32) {
-          const u32x4_t av = sa[cur][(wave * 2 + k32) * 64 + lane];
-#pragma unroll
-          for (int cb = 0; cb < 2; ++cb)
-            acc[cb] = mfma16(av, sb[cur][(cb * 2 + k32) * 64 + lane], acc[cb]);
-        }
-        store_stage(cur ^ 1, (u + 1) % D);
-        __syncthreads();
+        for (int f = 0; f < NF; ++f) acc[f] = mfma16(a, sb[(s2 * NF + f) * 64 + lane], acc[f]);
       }
     }
   }
   // D lane l: rows 4*(l/16)+q (tokens), column l%16 (experts)
-  const int kb = lane >> 4, j = lane & 15;
 #pragma unroll
-  for (int cb = 0; cb < 2; ++cb) {
-    const int e = e0 + cb * 16 + j;
+  for (int f = 0; f < NF; ++f) {
+    const int e = eg + 16 * f + j;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int m = m0 + wave * 16 + 4 * kb + q;
-      if (m < M && e < E) logits[(int64_t)m * E + e] = acc[cb][q];
+      const int mm = mw + 4 * kb + q;
+      if (mm < M && e < E) partial[((int64_t)ks * M + mm) * E + e] = acc[f][q];
     }
   }
 }
 
-hipError_t launch_router_big(const uint16_t* h, const uint16_t* scale, float scalar_root,
-                             float eps, const uint16_t* proj, float* logits, int M, int H, int E,
-                             hipStream_t s) {
+// K splits of the large-batch router: enough workgroups to cover the chip
+// (at least 256) with 4, 8 or 16 splits
+int router_tok_splits(int64_t M, int64_t E) {
+  const int64_t wgs = (M + kTokRows - 1) / kTokRows * ((E + kTokExperts - 1) / kTokExperts);
+  return wgs * 4 >= 256 ? 4 : wgs * 8 >= 256 ? 8 : 16;
+}
+
+hipError_t launch_router_tok(const uint16_t* h, const uint16_t* scale, float scalar_root,
+                             float eps, const uint16_t* proj, float* inv, float* partial, int M,
+                             int H, int E, hipStream_t s) {
   if (M == 0) return hipSuccess;
-  if (H % kBigBK != 0) return hipErrorInvalidValue;
-  dim3 grid((M + kBigTok - 1) / kBigTok, (E + kBigExp - 1) / kBigExp);
-  hipLaunchKernelGGL(k_router_big, grid, dim3(256), 0, s, h, scale, scalar_root, eps, proj,
-                     logits, M, H, E);
+  const int ks = router_tok_splits(M, E);
+  const int nch = H >> 5;
+  const int per = (nch + ks - 1) / ks;
+  hipLaunchKernelGGL(k_router_inv, dim3((M + 3) / 4), dim3(256), 0, s, h, eps, inv, M, H);
+  // splits whose k range is empty (per * ks > nch) still store zeros
+  const int lsteps = min(per, kTokLdsSteps);
+  const dim3 grid((M + kTokRows - 1) / kTokRows, ks, (E + kTokExperts - 1) / kTokExperts);
+  hipLaunchKernelGGL(k_router_tok, grid, dim3(kTokThreads), router_tok_lds(lsteps), s, h, inv,
+                     scale, scalar_root, proj, partial, M, H, E, per, lsteps);
   return hipGetLastError();
 }
 
@@ -505,7 +504,7 @@ constexpr int kRouterMaxSplit = 16;
 // Lane i < topk returns selection i in *sel_e / *sel_w.
 // Logits of token m, lane holding experts lane + 64 q, q < PER (PER =
 // ceil(E / 64) rounded up to a power of two).  KS = number of K-split partial
-// sums to add (1 or kRouterMaxSplit), or 0 to read finished bf16 logits.  All
+// sums to add (1, 4, 8 or kRouterMaxSplit), or 0 to read finished bf16 logits.  All
 // loads are issued before any is used (addresses clamped into range,
 // out-of-range values masked after); NaN becomes -inf so it never wins.
 template <int KS, int PER>
@@ -660,6 +659,10 @@ hipError_t launch_router_topk(const float* partial, int ksplit, const uint16_t* 
   else if (ksplit == kRouterMaxSplit)
     launch_topk_ks<kRouterMaxSplit>(partial, logits_in, per_expert_scale, logits_out, idx, w, M,
                                     E, topk, s);
+  else if (ksplit == 8)
+    launch_topk_ks<8>(partial, logits_in, per_expert_scale, logits_out, idx, w, M, E, topk, s);
+  else if (ksplit == 4)
+    launch_topk_ks<4>(partial, logits_in, per_expert_scale, logits_out, idx, w, M, E, topk, s);
   else if (ksplit == 1)
     launch_topk_ks<1>(partial, logits_in, per_expert_scale, logits_out, idx, w, M, E, topk, s);
   else

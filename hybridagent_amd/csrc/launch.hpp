@@ -92,10 +92,12 @@ hipError_t launch_router_logits(const uint16_t* r, const uint16_t* proj, float* 
 hipError_t launch_router_norm_logits(const uint16_t* h, const uint16_t* scale, float scalar_root,
                                      float eps, const uint16_t* proj, float* partial, int M,
                                      int H, int E, int ksplit, hipStream_t s);
-// RMSNorm + fp32 logits [M, E] for large batches (H % 64 == 0)
-hipError_t launch_router_big(const uint16_t* h, const uint16_t* scale, float scalar_root,
-                             float eps, const uint16_t* proj, float* logits, int M, int H, int E,
-                             hipStream_t s);
+// large batches: row inverse norms into inv[M], then K-split logits partials
+// [router_tok_splits(M, E)][M][E]
+int router_tok_splits(int64_t M, int64_t E);
+hipError_t launch_router_tok(const uint16_t* h, const uint16_t* scale, float scalar_root,
+                             float eps, const uint16_t* proj, float* inv, float* partial, int M,
+                             int H, int E, hipStream_t s);
 // top-k and expert sort in one workgroup, M * topk <= 512
 hipError_t launch_topk_sort(const float* partial, int ksplit, const uint16_t* per_expert_scale,
                             int64_t* idx, float* w, int M, int E, int topk, int32_t* sorted_pos,

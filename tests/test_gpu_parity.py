@@ -111,7 +111,9 @@ def test_topk_tie_rule(dev):
     assert idx.cpu().tolist() == [[1, 2, 4, 7, 3]]
 
 
-@pytest.mark.parametrize("M", [1, 32, 257])
+# M > 64 runs the large-batch router (128 tokens per workgroup): 257 and
+# 1000 with 16 K splits, 4096 with 8, 8193 with 4 and a ragged last block
+@pytest.mark.parametrize("M", [1, 32, 257, 1000, 4096, 8193])
 def test_router_end_to_end(dev, M):
     h, rw = _router_inputs(M, seed=50)
     w, idx, lg = _lib.router_topk(h.to(dev), rw.scale.to(dev), rw.scalar_root, rw.proj.to(dev),
