@@ -76,6 +76,7 @@ struct MoeLayout {
   int32_t* offsets;
   int32_t* desc;
   int32_t* counters;
+  int32_t* queues;  // prefill work queues: gate_up [0, 16), down [16, 32)
   int32_t* sorted_pos;
   int32_t* tiles;
   int32_t* blockcnt;
@@ -102,6 +103,7 @@ MoeLayout moe_layout(void* ws, int64_t M, int64_t k, int64_t E, int64_t H, int64
   L.offsets = c.take<int32_t>(E + 1);
   L.desc = c.take<int32_t>(4 * E);
   L.counters = c.take<int32_t>(2);
+  L.queues = c.take<int32_t>(kPrefillQueueInts);
   L.sorted_pos = c.take<int32_t>(M * k);
   L.tiles = c.take<int32_t>(M * k / kPrefillBM + E + 1);
   L.blockcnt = c.take<int32_t>(size_t(sort_blocks(M * k)) * E);
@@ -390,7 +392,7 @@ int moe_gate_up(const uint16_t* hidden, const int32_t* gu_packed, const uint16_t
       // bias form: hidden rows reordered once, with their k tile sums
       hipError_t e = launch_prefill_prep(hidden, L.xb, L.crx, (int)M, (int)H, (int)hidden_ld(H),
                                          L.sorted_pos, L.offsets + E, (int)top_k, L.crs,
-                                         (int)(M * top_k), s);
+                                         (int)(M * top_k), L.queues, s);
       if (e != hipSuccess) return launch_status(e);
       p.act = L.xb;
       p.lda = (int)hidden_ld(H);
@@ -401,6 +403,7 @@ int moe_gate_up(const uint16_t* hidden, const int32_t* gu_packed, const uint16_t
       p.cr_out = L.crh;
       p.ncr_out = (int)((I + 127) / 128);
       p.n_nt = (int)((I + 127) / 128);  // 128 intermediate columns per item
+      p.queues = L.queues;
       return launch_status(launch_prefill_bias(kModeGateUp, p, max_mtiles(M, top_k, E), s));
     }
     return launch_status(launch_prefill(kModeGateUp, p, max_mtiles(M, top_k, E), s));
@@ -442,6 +445,7 @@ int moe_down(const int32_t* dn_packed, const uint16_t* dn_scale, int64_t M, int6
       p.cr = L.crh;
       p.ncr = (int)((I + 127) / 128);
       p.n_nt = (int)((H + 255) / 256);  // 256 output columns per item
+      p.queues = L.queues + kPrefillQueueInts / 2;
       p.lda = (int)inter_ld(I);
       return launch_status(launch_prefill_bias(kModeDown, p, max_mtiles(M, top_k, E), s));
     }

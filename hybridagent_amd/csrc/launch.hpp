@@ -59,6 +59,9 @@ struct PrefillArgs {
   // (chunk 4 kb + s of the tile stored at 4 s + kb); ldc = the tile stride
   // of the correction tables, which are [tile][segment row]
   int lda, ldo, ldc;
+  // bias form only: the work queues of this launch, 9 ints (one counter
+  // per XCD, then the count of workgroups that have left), zero at launch
+  int32_t* queues;
 };
 
 enum DecodeMode { kModeDense = 0, kModeGateUp = 1, kModeDown = 2 };
@@ -113,9 +116,12 @@ hipError_t launch_prefill(int mode, PrefillArgs a, int max_mtiles, hipStream_t s
 // chunks transposed, row stride ldx; crx = 136 * the sums of each row's k
 // tiles ([K / 128][M]) and crs = those sums in expert-segment order
 // ([K / 128][ldc]); K a multiple of 128
+// It also zeroes `queues` (kPrefillQueueInts ints: the gate_up and down
+// kernels' work queues).
+constexpr int kPrefillQueueInts = 32;
 hipError_t launch_prefill_prep(const uint16_t* x, uint16_t* xb, float* crx, int M, int K, int ldx,
                                const int32_t* sorted_pos, const int32_t* rows_total, int topk,
-                               float* crs, int ldc, hipStream_t s);
+                               float* crs, int ldc, int32_t* queues, hipStream_t s);
 // the bias-form prefill kernels stage each item's scales in LDS: they take
 // an even number of scale groups per row, at most 24
 bool prefill_bias_supported(int ng);

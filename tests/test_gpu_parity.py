@@ -358,6 +358,40 @@ def test_moe_prefill_groups(dev, G):
     assert err <= TOL
 
 
+# (640, 320, 128): odd group counts -> the exact-form kernels; (896, 960,
+# 256) and (1024, 704, 128): the bias-form kernels with half-width last
+# n-tiles (gate_up when I % 128 == 64, down when H % 256 == 128)
+@pytest.mark.parametrize("h,i,G", [(640, 320, 128), (896, 960, 256), (1024, 704, 128)])
+def test_moe_prefill_half_items(dev, h, i, G):
+    # items of at most 64 rows and half-width last n-tiles run with all eight
+    # wavefronts on half the tile; segment sizes chosen to give tails of 122,
+    # 2, 64, 40, 33, 20, 1 and 62 rows
+    e, k = 8, 2
+    wts = synth.moe_weights(e, h, i, G, seed=760)
+    counts = [250, 130, 64, 40, 33, 20, 1, 62]
+    M = sum(counts) // k
+    x = synth.activations(M, h, seed=761)
+    slots = np.repeat(np.arange(e), counts)
+    idx = np.stack([slots[:M], slots[M:]], 1)
+    assert (idx[:, 0] != idx[:, 1]).all()
+    idx = torch.from_numpy(idx[np.random.default_rng(762).permutation(M)]).long()
+    w = torch.rand(M, k, generator=torch.Generator().manual_seed(763)).float()
+    y = _lib.moe_forward(x.to(dev), idx.to(dev), w.to(dev), wts.gate_up_packed.to(dev), wts.gate_up_scale.to(dev),
+                         wts.down_packed.to(dev), wts.down_scale.to(dev))
+    rows = np.arange(0, M, 3)
+    ref = oracle.moe_forward(_np(x)[rows], idx.numpy()[rows], w.numpy()[rows], wts.gate_up_packed.numpy(),
+                             _bits(wts.gate_up_scale), wts.down_packed.numpy(), _bits(wts.down_scale), G)
+    err = oracle.max_abs_rel(_np(y)[rows], ref)
+    print(f"moe prefill half items h={h} i={i} G={G} max_abs_rel={err:.2e}")
+    assert err <= TOL
+    # a token's output does not depend on the tile shape its rows land in
+    # (270 tokens: still above the decode threshold, other segment tails)
+    sub = torch.tensor([t for t in range(M) if t % 10 != 0])
+    y_sub = _lib.moe_forward(x[sub].to(dev), idx[sub].to(dev), w[sub].to(dev), wts.gate_up_packed.to(dev),
+                             wts.gate_up_scale.to(dev), wts.down_packed.to(dev), wts.down_scale.to(dev))
+    assert torch.equal(y_sub.cpu(), y.cpu()[sub])
+
+
 def test_moe_large_batch_untiled_shape(dev):
     # H not a multiple of 128 / I not a multiple of 64: large batches stay on
     # the streaming kernels and must still match
