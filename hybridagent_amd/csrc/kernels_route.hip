@@ -995,33 +995,42 @@ __global__ __launch_bounds__(kSortThreads) void k_sort_scatter(
   __shared__ int wsum[kSortWaves];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int b = blockIdx.x, nb = gridDim.x;
-  // expert totals and the counts of the blocks before this one
+  // this thread's entry, loaded first so its latency overlaps the counts'
+  const int total = M * topk;
+  const int p = b * kSortThreads + tid;
+  int e = -1, row = 0;
+  int64_t ev = -1;
+  if (p < total) {
+    const int jj = p / M, t = p - jj * M;
+    row = t * topk + jj;
+    ev = idx[row];
+  }
+  // expert totals and the counts of the blocks before this one, 32 blocks'
+  // counts per batch of loads (one memory round trip up to 32768 entries)
   int tot = 0, pre = 0;
   if (tid < E) {
-    for (int q = 0; q < nb; ++q) {
-      const int c = blockcnt[(int64_t)q * E + tid];
-      tot += c;
-      pre += q < b ? c : 0;
+    constexpr int U = 32;
+    for (int q0 = 0; q0 < nb; q0 += U) {
+      int cv[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) cv[u] = q0 + u < nb ? blockcnt[(int64_t)(q0 + u) * E + tid] : 0;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        tot += cv[u];
+        pre += q0 + u < b ? cv[u] : 0;
+      }
     }
   }
-  for (int e = tid; e < E; e += kSortThreads)
-    for (int w = 0; w < kSortWaves; ++w) wcnt[w][e] = 0;
+  for (int x = tid; x < E; x += kSortThreads)
+    for (int w = 0; w < kSortWaves; ++w) wcnt[w][x] = 0;
   const int off = write_plan(tot, E, offsets, desc, counters, tiles, BM, wsum, b == 0);
   if (tid < E) base[tid] = off + pre;
   __syncthreads();
+  if (ev >= 0 && ev < E) e = (int)ev;
 
   int nbits = 0;
   while ((1 << nbits) < E) ++nbits;
   const unsigned long long lt_mask = (1ull << lane) - 1ull;
-  const int total = M * topk;
-  const int p = b * kSortThreads + tid;
-  int e = -1, row = 0;
-  if (p < total) {
-    const int jj = p / M, t = p - jj * M;
-    row = t * topk + jj;
-    const int64_t ev = idx[row];
-    if (ev >= 0 && ev < E) e = (int)ev;
-  }
   const bool ok = e >= 0;
   unsigned long long same = __ballot(ok);
   for (int bit = 0; bit < nbits; ++bit) {
