@@ -143,6 +143,32 @@ def test_router_end_to_end(dev, M):
     np.testing.assert_allclose(w.cpu().numpy(), w2, rtol=2e-6, atol=1e-7)
 
 
+# other router shapes: expert counts that are not a multiple of 16 or that
+# need several 128-expert groups, rows too long for the fused decode-size
+# kernel (H > 3072: normalisation pass + K-split logits), and the
+# large-batch kernels at those shapes
+@pytest.mark.parametrize("M,Hr,Er", [(8, 4096, 200), (300, 4096, 200), (300, 1056, 64), (70, 2816, 512)])
+def test_router_other_shapes(dev, M, Hr, Er):
+    rw = synth.router_weights(Er, Hr, seed=60 + Er)
+    g = torch.Generator().manual_seed(61 + Hr)
+    rw.scale = (1 + 0.05 * torch.randn(Hr, generator=g)).to(torch.bfloat16)
+    rw.per_expert_scale = (1 + 0.05 * torch.randn(Er, generator=g)).to(torch.bfloat16)
+    h = synth.activations(M, Hr, seed=62 + M)
+    w, idx, lg = _lib.router_topk(h.to(dev), rw.scale.to(dev), rw.scalar_root, rw.proj.to(dev),
+                                  rw.per_expert_scale.to(dev), rw.eps, K_TOP, return_logits=True)
+    ref_lg = oracle.router_logits(_np(h), _np(rw.scale), rw.scalar_root, _np(rw.proj), rw.eps)
+    got_lg = _np(lg)
+    ulp = np.abs(oracle.to_bf16_bits(got_lg).astype(np.int32) - oracle.to_bf16_bits(ref_lg).astype(np.int32))
+    scale = np.abs(ref_lg).max()
+    big = np.abs(ref_lg) > 0.25 * scale
+    assert ulp[big].max() <= 1 and (ulp > 0).mean() < 0.05
+    assert np.abs(got_lg - ref_lg).max() <= 2.0 ** -8 * scale
+    # selection and weights are bit-exact against the kernel's own logits
+    idx2, w2 = oracle.topk_from_logits(got_lg, _np(rw.per_expert_scale), K_TOP)
+    assert np.array_equal(idx.cpu().numpy(), idx2)
+    np.testing.assert_allclose(w.cpu().numpy(), w2, rtol=2e-6, atol=1e-7)
+
+
 # ------------------------------------------------------------------ sort / permute
 
 @pytest.mark.parametrize("M", [1, 8, 64, 777, 4096])
