@@ -330,11 +330,11 @@ hipError_t launch_router_norm_logits(const uint16_t* h, const uint16_t* scale, f
 //   k_router_tok   partial[ks][m][e]: wavefront w of a workgroup owns 16
 //                  tokens and 128 experts over split ks's k range.  r = bf16(bf16(bf16(x * inv) * scale) * root) is
 //                  formed in registers as the MFMA A operand, so every
-//                  element of h is read and normalised once.  The router
-//                  weights of up to 12 steps are staged in LDS per chunk
-//                  (one barrier pair per chunk; one chunk at H = 2816 and 8
-//                  splits), and all of a chunk's activation loads are issued
-//                  before its first MFMA.
+//                  element of h is read and normalised once.  The split's
+//                  k range goes in chunks of 4 steps: the 128 experts'
+//                  router weights (and the scales, as fp32) of a chunk sit in
+//                  one of two LDS buffers, and the next chunk's loads are in
+//                  flight while a chunk is multiplied (one barrier per chunk).
 // Rows past M and experts past E read clamped (in-bounds) addresses; MFMA
 // rows and columns are independent, so their results are simply not stored.
 // ---------------------------------------------------------------------------
@@ -371,14 +371,15 @@ __global__ __launch_bounds__(256) void k_router_inv(const uint16_t* __restrict__
 }
 
 constexpr int kTokExperts = 128;  // experts per workgroup (8 MFMA column tiles)
-constexpr int kTokLdsSteps = 12;  // k steps of 32 whose router weights sit in LDS at once
+constexpr int kTokChunk = 4;      // k steps of 32 per LDS chunk (double-buffered)
 constexpr int kTokWaves = 8;      // wavefronts per workgroup, 16 tokens each
 constexpr int kTokThreads = 64 * kTokWaves;
 constexpr int kTokRows = 16 * kTokWaves;
-
-// LDS bytes of k_router_tok for `steps` steps per chunk: the weight fragments
-// [step][column tile][lane] and the scale chunks [step][kb], 16 bytes each
-size_t router_tok_lds(int steps) { return (size_t)steps * (kTokExperts / 16 * 64 + 4) * 16; }
+constexpr int kTokNF = kTokExperts / 16;
+// LDS of one chunk: weight fragments [step][column tile][lane] (16 bytes
+// each), then the scales in fp32 [step][kb][8]
+constexpr int kTokBSlots = kTokChunk * kTokNF * 64;
+constexpr int kTokSFloats = kTokChunk * 32;
 
 __global__ __launch_bounds__(kTokThreads) void k_router_tok(const uint16_t* __restrict__ h,
                                                             const float* __restrict__ inv,
@@ -386,13 +387,11 @@ __global__ __launch_bounds__(kTokThreads) void k_router_tok(const uint16_t* __re
                                                             float scalar_root,
                                                             const uint16_t* __restrict__ proj,
                                                             float* __restrict__ partial, int M,
-                                                            int H, int E, int steps_per_split,
-                                                            int lds_steps) {
-  constexpr int NF = kTokExperts / 16;
+                                                            int H, int E, int steps_per_split) {
+  constexpr int NF = kTokNF;
   static_assert(kTokThreads == kTokExperts * 4, "one staging thread per (expert, 8-wide chunk)");
-  extern __shared__ u32x4_t lds[];
-  u32x4_t* sb = lds;                         // [lds_steps][NF][64]
-  u32x4_t* ss = lds + lds_steps * NF * 64;   // [lds_steps][4]
+  __shared__ u32x4_t sb[2][kTokBSlots];
+  __shared__ __align__(16) float ssf[2][kTokSFloats];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int j = lane & 15, kb = lane >> 4;
@@ -401,60 +400,104 @@ __global__ __launch_bounds__(kTokThreads) void k_router_tok(const uint16_t* __re
   const int eg = blockIdx.z * kTokExperts;
   const int c0 = ks * steps_per_split;
   const int c1 = min(H >> 5, c0 + steps_per_split);
+  const int nq = (c1 - c0 + kTokChunk - 1) / kTokChunk;  // chunks (<= 0: empty split)
 
   const int m = min(mw + j, M - 1);
   const uint16_t* xrow = h + (int64_t)m * H + 8 * kb;
   const float rinv = inv[m];
   // staging role: expert se, 8-wide chunk sq of each step; its LDS slot is
   // column tile se / 16, lane (se % 16) + 16 sq (a wavefront's 64 stores
-  // fill one contiguous kilobyte)
+  // fill one contiguous kilobyte); threads below 4 kTokChunk also bring in
+  // one 8-wide scale chunk (step tid / 4, kb tid % 4) as fp32
   const int se = tid >> 2, sq = tid & 3;
   const uint16_t* wrow = proj + (int64_t)min(eg + se, E - 1) * H + 8 * sq;
   const int sslot = (se >> 4) * 64 + (se & 15) + 16 * sq;
+  const int sstep = min(tid >> 2, kTokChunk - 1), skb = tid & 3;
   f32x4_t acc[NF];
 #pragma unroll
   for (int f = 0; f < NF; ++f) acc[f] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  for (int cc = c0; cc < c1; cc += lds_steps) {
-    const int ns = min(lds_steps, c1 - cc);
-    // the chunk's router weights first, then its activation rows and
-    // scales, which stay in flight through the LDS stores and the barrier
-    u32x4_t st[kTokLdsSteps];
+  // Loads of chunk q (clamped into the split, so every chunk issues the
+  // same loads; a reload of the last chunk is unused): weights, scale,
+  // then activations, so waiting for the weights leaves the activations in
+  // flight.
+  u32x4_t st[kTokChunk], scv, xv[2][kTokChunk];
+  auto step_of = [&](int q, int s2) { return min(c0 + kTokChunk * q + s2, c1 - 1); };
+  auto load_w = [&](int q) {
 #pragma unroll
-    for (int s2 = 0; s2 < kTokLdsSteps; ++s2) st[s2] = ld16(wrow + 32 * (cc + min(s2, ns - 1)));
-    const u32x4_t sc = ld16(scale + 32 * cc + 8 * min(tid, ns * 4 - 1));
-    u32x4_t xv[kTokLdsSteps];
+    for (int s2 = 0; s2 < kTokChunk; ++s2) st[s2] = ld16(wrow + 32 * step_of(q, s2));
+    scv = ld16(scale + 32 * step_of(q, sstep) + 8 * skb);
+  };
+  auto load_x = [&](int q, int buf) {
 #pragma unroll
-    for (int s2 = 0; s2 < kTokLdsSteps; ++s2) xv[s2] = ld16(xrow + 32 * (cc + min(s2, ns - 1)));
-    if (cc != c0) __syncthreads();  // the previous chunk's fragments are consumed
+    for (int s2 = 0; s2 < kTokChunk; ++s2) xv[buf][s2] = ld16(xrow + 32 * step_of(q, s2));
+  };
+  auto stage = [&](int buf) {
 #pragma unroll
-    for (int s2 = 0; s2 < kTokLdsSteps; ++s2)
-      if (s2 < ns) sb[s2 * NF * 64 + sslot] = st[s2];
-    if (tid < ns * 4) ss[tid] = sc;
-    __syncthreads();
+    for (int s2 = 0; s2 < kTokChunk; ++s2) sb[buf][s2 * NF * 64 + sslot] = st[s2];
+    if (tid < 4 * kTokChunk) {
+      const uint32_t w4[4] = {scv.x, scv.y, scv.z, scv.w};
+      f32x4_t lo, hi;
 #pragma unroll
-    for (int s2 = 0; s2 < kTokLdsSteps; ++s2) {
+      for (int t = 0; t < 2; ++t) {
+        lo[2 * t] = bf16_bits_to_f32(w4[t] & 0xFFFFu);
+        lo[2 * t + 1] = bf16_bits_to_f32(w4[t] >> 16);
+        hi[2 * t] = bf16_bits_to_f32(w4[t + 2] & 0xFFFFu);
+        hi[2 * t + 1] = bf16_bits_to_f32(w4[t + 2] >> 16);
+      }
+      *reinterpret_cast<f32x4_t*>(&ssf[buf][8 * tid]) = lo;
+      *reinterpret_cast<f32x4_t*>(&ssf[buf][8 * tid + 4]) = hi;
+    }
+  };
+  auto compute = [&](int q, int buf, int xb) {
+    const int ns = min(kTokChunk, c1 - c0 - kTokChunk * q);
+#pragma unroll
+    for (int s2 = 0; s2 < kTokChunk; ++s2) {
       if (s2 < ns) {
-        const u32x4_t sv = ss[s2 * 4 + kb];
-        const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
-        const uint32_t xw[4] = {xv[s2].x, xv[s2].y, xv[s2].z, xv[s2].w};
+        const f32x4_t sl = *reinterpret_cast<const f32x4_t*>(&ssf[buf][(s2 * 4 + kb) * 8]);
+        const f32x4_t sh = *reinterpret_cast<const f32x4_t*>(&ssf[buf][(s2 * 4 + kb) * 8 + 4]);
+        const float sf[8] = {sl[0], sl[1], sl[2], sl[3], sh[0], sh[1], sh[2], sh[3]};
+        const uint32_t xw[4] = {xv[xb][s2].x, xv[xb][s2].y, xv[xb][s2].z, xv[xb][s2].w};
         uint32_t ow[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int t = 0; t < 4; ++t) {
           float rr[2];
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh) {
-            const float xe = bf16_bits_to_f32(hh ? (xw[q] >> 16) : (xw[q] & 0xFFFFu));
-            const float sf = bf16_bits_to_f32(hh ? (sw[q] >> 16) : (sw[q] & 0xFFFFu));
+            const float xe = bf16_bits_to_f32(hh ? (xw[t] >> 16) : (xw[t] & 0xFFFFu));
             const float v1 = round_bf16(xe * rinv);
-            const float v2 = round_bf16(v1 * sf);
+            const float v2 = round_bf16(v1 * sf[2 * t + hh]);
             rr[hh] = v2 * scalar_root;
           }
-          ow[q] = pack_bf16x2(rr[0], rr[1]);
+          ow[t] = pack_bf16x2(rr[0], rr[1]);
         }
         const u32x4_t a = {ow[0], ow[1], ow[2], ow[3]};
 #pragma unroll
-        for (int f = 0; f < NF; ++f) acc[f] = mfma16(a, sb[(s2 * NF + f) * 64 + lane], acc[f]);
+        for (int f = 0; f < NF; ++f) acc[f] = mfma16(a, sb[buf][(s2 * NF + f) * 64 + lane], acc[f]);
+      }
+    }
+  };
+
+  if (nq > 0) {
+    load_w(0);
+    load_x(0, 0);
+    stage(0);
+    __syncthreads();
+    // chunk q: chunk q + 1's loads in flight during its multiplication, then
+    // staged into the other buffer (whose last readers, chunk q - 1, all
+    // passed the previous barrier); one barrier per chunk
+    for (int q = 0; q < nq; q += 2) {
+      load_w(q + 1);
+      load_x(q + 1, 1);
+      compute(q, 0, 0);
+      stage(1);
+      __syncthreads();
+      if (q + 1 < nq) {
+        load_w(q + 2);
+        load_x(q + 2, 0);
+        compute(q + 1, 1, 1);
+        stage(0);
+        __syncthreads();
       }
     }
   }
@@ -486,10 +529,9 @@ hipError_t launch_router_tok(const uint16_t* h, const uint16_t* scale, float sca
   const int per = (nch + ks - 1) / ks;
   hipLaunchKernelGGL(k_router_inv, dim3((M + 3) / 4), dim3(256), 0, s, h, eps, inv, M, H);
   // splits whose k range is empty (per * ks > nch) still store zeros
-  const int lsteps = min(per, kTokLdsSteps);
   const dim3 grid((M + kTokRows - 1) / kTokRows, ks, (E + kTokExperts - 1) / kTokExperts);
-  hipLaunchKernelGGL(k_router_tok, grid, dim3(kTokThreads), router_tok_lds(lsteps), s, h, inv,
-                     scale, scalar_root, proj, partial, M, H, E, per, lsteps);
+  hipLaunchKernelGGL(k_router_tok, grid, dim3(kTokThreads), 0, s, h, inv, scale, scalar_root,
+                     proj, partial, M, H, E, per);
   return hipGetLastError();
 }
 
