@@ -959,14 +959,90 @@ __global__ __launch_bounds__(kSortThreads) void k_router_topk_sort(
                 desc, counters, tiles, BM);
 }
 
+// The same for at most 64 routed rows (decode sizes): eight wavefronts do the
+// top-k (ROUNDS tokens each), then one wavefront sorts the rows -- one row
+// per lane: expert counts by LDS atomics, plan_wave, the stable rank among
+// lower lanes of the same expert by ballots -- with no workgroup barrier
+// after the top-k (a wavefront's LDS operations complete in order).
+constexpr int kSmallSortWaves = 8;
+template <int KS, int PER, int ROUNDS>
+__global__ __launch_bounds__(64 * kSmallSortWaves) void k_router_topk_sort_small(
+    const float* __restrict__ partial, const uint16_t* __restrict__ pes,
+    int64_t* __restrict__ idx_out, float* __restrict__ w_out, int M, int E, int topk,
+    int32_t* __restrict__ sorted_pos, int32_t* __restrict__ offsets, int32_t* __restrict__ desc,
+    int32_t* __restrict__ counters, int32_t* __restrict__ tiles, int BM) {
+  __shared__ int s_idx[64];
+  __shared__ uint16_t s_pes[kMaxExperts];
+  __shared__ int cnt[kMaxExperts];
+  __shared__ int run[kMaxExperts];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  for (int e = threadIdx.x; e < E; e += 64 * kSmallSortWaves) {
+    s_pes[e] = pes[e];
+    cnt[e] = 0;
+  }
+  float lg[ROUNDS][PER];
+#pragma unroll
+  for (int rr = 0; rr < ROUNDS; ++rr)
+    load_logits<KS, PER>(partial, nullptr, nullptr, min(wave + kSmallSortWaves * rr, M - 1), M, E,
+                         lane, lg[rr]);
+  __syncthreads();  // s_pes, cnt
+#pragma unroll
+  for (int rr = 0; rr < ROUNDS; ++rr) {
+    const int m = wave + kSmallSortWaves * rr;
+    if (m >= M) break;  // uniform per wavefront
+    int se;
+    float sw;
+    select_topk<PER>(lg[rr], s_pes, E, topk, lane, &se, &sw);
+    if (lane < topk) {
+      idx_out[(int64_t)m * topk + lane] = se;
+      w_out[(int64_t)m * topk + lane] = sw;
+      s_idx[m * topk + lane] = se;
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  // lane p < M * topk holds k-major entry p = j*M + t, routed row t*topk + j
+  const int total = M * topk;
+  int e = -1, row = 0;
+  if (lane < total) {
+    const int jj = lane / M, t = lane - jj * M;
+    row = t * topk + jj;
+    const int ev = s_idx[row];
+    if (ev >= 0 && ev < E) e = ev;
+  }
+  const bool ok = e >= 0;
+  if (ok) atomicAdd(&cnt[e], 1);
+  plan_wave(cnt, run, E, offsets, desc, counters, tiles, BM);
+  int nbits = 0;
+  while ((1 << nbits) < E) ++nbits;
+  unsigned long long same = __ballot(ok);
+  for (int b = 0; b < nbits; ++b) {
+    const bool on = ok && ((e >> b) & 1);
+    const unsigned long long bb = __ballot(on);
+    same &= on ? bb : ~bb;
+  }
+  const int rank = __popcll(same & ((1ull << lane) - 1ull));
+  if (ok) sorted_pos[run[e] + rank] = row;
+}
+
 template <int KS>
 static void launch_topk_sort_ks(const float* partial, const uint16_t* pes, int64_t* idx, float* w,
                                 int M, int E, int topk, int32_t* sorted_pos, int32_t* offsets,
                                 int32_t* desc, int32_t* counters, int32_t* tiles, int BM,
                                 hipStream_t s) {
-  // one token per wavefront up to M = 16, else up to kTopkSortRounds
+  // at most 64 rows: eight wavefronts, one of them sorting; else one token
+  // per wavefront up to M = 16, else up to kTopkSortRounds
 #define W4A16_TS(P_)                                                                            \
-  if (M <= kSortWaves)                                                                          \
+  if (M * topk <= 64 && M <= kSmallSortWaves)                                                   \
+    hipLaunchKernelGGL((k_router_topk_sort_small<KS, P_, 1>), dim3(1), dim3(64 * kSmallSortWaves), \
+                       0, s, partial, pes, idx, w, M, E, topk, sorted_pos, offsets, desc,         \
+                       counters, tiles, BM);                                                     \
+  else if (M * topk <= 64)                                                                      \
+    hipLaunchKernelGGL((k_router_topk_sort_small<KS, P_, 64 / kSmallSortWaves>), dim3(1),        \
+                       dim3(64 * kSmallSortWaves), 0, s, partial, pes, idx, w, M, E, topk,        \
+                       sorted_pos, offsets, desc, counters, tiles, BM);                          \
+  else if (M <= kSortWaves)                                                                     \
     hipLaunchKernelGGL((k_router_topk_sort<KS, P_, 1>), dim3(1), dim3(kSortThreads), 0, s,       \
                        partial, pes, idx, w, M, E, topk, sorted_pos, offsets, desc, counters,    \
                        tiles, BM);                                                               \
