@@ -10,7 +10,12 @@
 //                    top_k_index by expert -> per-expert segments in the
 //                    reference's visiting order (quantization.py:266-276),
 //                    plus one work descriptor per active expert and the
-//                    prefill tile list.
+//                    prefill tile list (k_sort_hist + k_sort_scatter: the
+//                    same over several workgroups)
+//   large batches    k_router_inv + k_router_tok (the norm folded into the
+//                    logits kernel's A operand)
+//   decode sizes     k_router_norm_logits (norm + logits in one launch),
+//                    k_router_topk_sort[_small] (top-k + sort in one launch)
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -328,7 +333,8 @@ hipError_t launch_router_norm_logits(const uint16_t* h, const uint16_t* scale, f
 //   k_router_inv   inv[m] = 1 / sqrt(mean(h[m]^2) + eps): one wavefront per
 //                  row, each lane's chunks in order, then the wave sum
 //   k_router_tok   partial[ks][m][e]: wavefront w of a workgroup owns 16
-//                  tokens and 128 experts over split ks's k range.  r = bf16(bf16(bf16(x * inv) * scale) * root) is
+//                  tokens and 128 experts over split ks's k range.
+//                  r = bf16(bf16(bf16(x * inv) * scale) * root) is
 //                  formed in registers as the MFMA A operand, so every
 //                  element of h is read and normalised once.  The split's
 //                  k range goes in chunks of 4 steps: the 128 experts'
