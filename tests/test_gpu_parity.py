@@ -519,3 +519,60 @@ def test_add_rms_norm(dev, M, H):
     assert torch.equal(x2.cpu(), h)
     ref2 = oracle.rms_norm(_np(h), _np(w), 1e-6)
     assert np.abs(oracle.to_bf16_bits(_np(y2)).astype(np.int32) - oracle.to_bf16_bits(ref2).astype(np.int32)).max() <= 1
+
+
+# ------------------------------------------------------------ HIP graph replay
+# The layer is captured once and replayed several times with other eager work
+# (another batch size through the same kernels) and synchronisations in
+# between; every replay must reproduce the eager result bit for bit.  This
+# covers state that lives across launches: the prefill work queues (zeroed by
+# k_prefill_prep, reset by the last workgroup of each launch) and the plan.
+
+def _replays_match(capture, eager, disturb, n=3):
+    ref = eager()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        capture()  # warm-up outside the graph
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = capture()
+    for i in range(n):
+        g.replay()
+        torch.cuda.synchronize()
+        for o, r in zip(outs, ref):
+            assert torch.equal(o, r), f"replay {i} differs from the eager result"
+        disturb()
+        torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("M", [512, 4096])
+def test_graph_replay_prefill_experts(dev, moe128, M):
+    cpu, gpu = moe128
+    x = synth.activations(M, H, seed=800 + M).to(dev)
+    idx, w = _route(M, seed=801 + M)
+    idx, w = idx.to(dev), w.to(dev)
+    args = (gpu["gate_up_packed"], gpu["gate_up_scale"], gpu["down_packed"], gpu["down_scale"])
+    fwd = lambda: (_lib.moe_forward(x, idx, w, *args),)
+    x2 = synth.activations(300, H, seed=802).to(dev)
+    i2, w2 = _route(300, seed=803)
+    i2, w2 = i2.to(dev), w2.to(dev)
+    _replays_match(fwd, fwd, lambda: _lib.moe_forward(x2, i2, w2, *args))
+
+
+@pytest.mark.parametrize("M", [8, 64])
+def test_graph_replay_decode_layer(dev, moe128, M):
+    cpu, gpu = moe128
+    h, rw = _router_inputs(M, seed=810 + M)
+    x = synth.activations(M, H, seed=811 + M).to(dev)
+    rargs = (h.to(dev), rw.scale.to(dev), rw.scalar_root, rw.proj.to(dev), rw.per_expert_scale.to(dev),
+             rw.eps, K_TOP)
+    eargs = (gpu["gate_up_packed"], gpu["gate_up_scale"], gpu["down_packed"], gpu["down_scale"])
+    fwd = lambda: _lib.moe_layer_forward(*rargs, x, *eargs)
+    h2, _ = _router_inputs(33, seed=812)
+    x2 = synth.activations(33, H, seed=813).to(dev)
+    rargs2 = (h2.to(dev),) + rargs[1:]
+    _replays_match(fwd, fwd, lambda: _lib.moe_layer_forward(*rargs2, x2, *eargs))
