@@ -31,6 +31,9 @@ HIP events on the stream the kernels run on.
 decode M, about two thirds of the decode bytes), timed alone the same way.
 ``cpu_baseline`` times the numpy oracle (``oracle/``, the CPU restatement of
 the reference path) on a bounded decode sample on this host.
+``latent`` is BASELINE configs[4] (30 MoE layers + HybridLink per step, batch
+32); ``hybridlink`` times the HybridLink map alone at that batch (weights
+rotated through HBM).
 """
 from __future__ import annotations
 
@@ -239,6 +242,24 @@ def calibrate_copy(dev) -> int:
     return 0
 
 
+def hybridlink_leg(dev, steps: int = 64):
+    """The HybridLink map alone (hybridlink.py:17-28) at the latent loop's
+    batch: LayerNorm, proj1 + GELU, proj2 + residual, LayerNorm through
+    w4a16_hybridlink.  Ten parameter sets (317 MB) are rotated so the weights
+    come from HBM, not the 256 MB last-level cache."""
+    from hybridagent_amd.latent import LatentStack
+    sets = [LatentStack(0, E, H, I, TOPK, G, seed=8800 + i, device=dev) for i in range(10)]
+    x = synth.activations(LATENT_BATCH, H, seed=8899, device=dev)
+    t = time_graph(lambda: [st.hybridlink(x) for st in sets], len(sets), steps, 8)
+    nbytes = 2 * H * H * 2 + 6 * H * 2 + 2 * LATENT_BATCH * H * 2
+    res = {"us": t * 1e6, "batch": LATENT_BATCH, "bytes": nbytes, "gbps": nbytes / t / 1e9,
+           "frac_hbm": nbytes / t / 1e9 / PEAK_HBM_GBS}
+    log(f"hybridlink B={LATENT_BATCH}: {t*1e6:.2f} us/call, {res['gbps']:.0f} GB/s")
+    del sets
+    torch.cuda.empty_cache()
+    return res
+
+
 def latent(dev, steps: int = LATENT_STEPS):
     """30 MoE layers (h += MoE(RMSNorm(h))) + HybridLink x sqrt(H),
     batch 32, the output fed back as the next step's input.  One HIP graph
@@ -391,6 +412,7 @@ def main(argv=None):
                                                min(args.layers, 4))
 
     lat = None if args.no_latent else latent(dev)
+    hl = None if args.no_latent else hybridlink_leg(dev)
 
     dense = None if args.no_dense else dense_sweep(dev, args.steps, args.warmup)
 
@@ -426,6 +448,8 @@ def main(argv=None):
                                              for k, v in pre.items()},
         "latent": None if lat is None else {k: (round(v, 4) if isinstance(v, float) else v)
                                             for k, v in lat.items()},
+        "hybridlink": None if hl is None else {k: (round(v, 4) if isinstance(v, float) else v)
+                                               for k, v in hl.items()},
         "dense": None if dense is None else {c: {k: (round(v, 4) if isinstance(v, float) else v)
                                                  for k, v in d.items()} for c, d in dense.items()},
         "cpu_baseline": None if cpu is None else {k: (round(v, 4) if isinstance(v, float) else v)

@@ -31,6 +31,9 @@ SIGNATURES = {
     "w4a16_linear_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
     "w4a16_add_rms_norm": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _I64, _I64, _F32, _VP]),
     "w4a16_linear": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
+    "w4a16_hybridlink_workspace_bytes": (_SZ, [_I64, _I64]),
+    "w4a16_hybridlink": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64,
+                                        _F32, _VP, _SZ, _VP]),
     "moe_router_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
     "moe_router_topk": (ctypes.c_int, [_VP, _VP, _F32, _VP, _VP, _F32, _I64, _I64, _I64, _I64,
                                        _VP, _VP, _VP, _VP, _SZ, _VP]),
@@ -195,6 +198,34 @@ def add_rms_norm(h: torch.Tensor, weight: torch.Tensor, eps: float,
         _check(lib.w4a16_add_rms_norm(_ptr(h2), _ptr(d2), _ptr(weight), _ptr(x) if d2 is not None else None,
                                       _ptr(y), M, H, float(eps), _stream(dev)), "w4a16_add_rms_norm")
     return x.reshape(h.shape), y.reshape(h.shape)
+
+
+def hybridlink(h: torch.Tensor, ln1_w: torch.Tensor, ln1_b: torch.Tensor, p1_w: torch.Tensor,
+               p1_b: torch.Tensor, p2_w: torch.Tensor, p2_b: torch.Tensor, ln2_w: torch.Tensor,
+               ln2_b: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
+    """HybridLink R(h) = post_ln(h + proj2(GELU(proj1(pre_ln(h)))))  (hybridlink.py:17-28);
+    h [..., H] bf16, LayerNorm/Linear parameters bf16 in the nn.Module layout."""
+    params = (ln1_w, ln1_b, p1_w, p1_b, p2_w, p2_b, ln2_w, ln2_b)
+    dev = _require_gpu(h, *params)
+    h = _bf16(h, "h")
+    H = h.shape[-1]
+    names = ("pre_ln weight", "pre_ln bias", "proj1 weight", "proj1 bias", "proj2 weight",
+             "proj2 bias", "post_ln weight", "post_ln bias")
+    params = tuple(_bf16(p, n) for p, n in zip(params, names))
+    for p, n in zip(params, names):
+        want = (H, H) if n.endswith("weight") and n.startswith("proj") else (H,)
+        if tuple(p.shape) != want:
+            raise ValueError(f"{n} must be {list(want)}, got {list(p.shape)}")
+    h2 = h.reshape(-1, H)
+    B = h2.shape[0]
+    out = torch.empty_like(h2)
+    lib = load()
+    ws = _workspace(lib.w4a16_hybridlink_workspace_bytes(B, H), dev)
+    with torch.cuda.device(dev):
+        _check(lib.w4a16_hybridlink(_ptr(h2), *[_ptr(p) for p in params], _ptr(out), B, H, float(eps),
+                                    _ptr(ws), 0 if ws is None else ws.numel(), _stream(dev)),
+               "w4a16_hybridlink")
+    return out.reshape(h.shape)
 
 
 def linear(x: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tensor,

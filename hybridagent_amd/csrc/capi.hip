@@ -161,6 +161,37 @@ int w4a16_add_rms_norm(const uint16_t* h, const uint16_t* delta, const uint16_t*
                                            static_cast<hipStream_t>(stream)));
 }
 
+size_t w4a16_hybridlink_workspace_bytes(int64_t B, int64_t H) {
+  if (B <= 0 || H <= 0) return 0;
+  return 2 * round256(size_t(B) * H * 2);
+}
+
+int w4a16_hybridlink(const uint16_t* h, const uint16_t* ln1_w, const uint16_t* ln1_b,
+                     const uint16_t* p1_w, const uint16_t* p1_b, const uint16_t* p2_w,
+                     const uint16_t* p2_b, const uint16_t* ln2_w, const uint16_t* ln2_b,
+                     uint16_t* out, int64_t B, int64_t H, float eps, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  if (B < 0 || B > (int64_t(1) << 24) || H <= 0 || H % 32 != 0 || H > 3072) return W4A16_ERR_SHAPE;
+  if (B == 0) return W4A16_OK;
+  if (!h || !ln1_w || !ln1_b || !p1_w || !p1_b || !p2_w || !p2_b || !ln2_w || !ln2_b || !out)
+    return W4A16_ERR_NULL;
+  if (!aligned16(h) || !aligned16(ln1_w) || !aligned16(ln1_b) || !aligned16(p1_w) ||
+      !aligned16(p2_w) || !aligned16(ln2_w) || !aligned16(ln2_b) || !aligned16(out))
+    return W4A16_ERR_ALIGN;
+  if (workspace == nullptr || workspace_bytes < w4a16_hybridlink_workspace_bytes(B, H))
+    return W4A16_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return W4A16_ERR_ALIGN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Carve c(workspace);
+  uint16_t* t0 = c.take<uint16_t>(B * H);  // pre_ln(h), later h + proj2(...)
+  uint16_t* t1 = c.take<uint16_t>(B * H);  // GELU(proj1(...))
+  hipError_t e = launch_layer_norm(h, ln1_w, ln1_b, t0, B, (int)H, eps, s);
+  if (e == hipSuccess) e = launch_linear_bf16(kLinGelu, t0, p1_w, p1_b, nullptr, t1, B, (int)H, (int)H, s);
+  if (e == hipSuccess) e = launch_linear_bf16(kLinResidual, t1, p2_w, p2_b, h, t0, B, (int)H, (int)H, s);
+  if (e == hipSuccess) e = launch_layer_norm(t0, ln2_w, ln2_b, out, B, (int)H, eps, s);
+  return launch_status(e);
+}
+
 size_t w4a16_linear_workspace_bytes(int64_t M, int64_t K, int64_t group_size) {
   (void)M;
   (void)K;

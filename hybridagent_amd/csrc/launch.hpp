@@ -109,6 +109,18 @@ hipError_t launch_topk_sort(const float* partial, int ksplit, const uint16_t* pe
 hipError_t launch_router_topk(const float* partial, int ksplit, const uint16_t* logits_in,
                               const uint16_t* per_expert_scale, uint16_t* logits_out,
                               int64_t* idx, float* w, int M, int E, int topk, hipStream_t s);
+// HybridLink pieces (kernels_hybridlink.hip): nn.LayerNorm with bf16 affine
+// parameters (H % 8 == 0, H <= 8192) and the bf16-weight linear for small
+// batches (K % 32 == 0, K <= 3072: at most 12 k steps of 32 per wavefront)
+// with a fused epilogue:
+//   kLinGelu      out = bf16(GELU_erf(bf16(x W^T + b)))
+//   kLinResidual  out = bf16(res + bf16(x W^T + b))
+enum LinearEpilogue { kLinGelu = 0, kLinResidual = 1 };
+hipError_t launch_layer_norm(const uint16_t* x, const uint16_t* w, const uint16_t* b, uint16_t* y,
+                             int64_t M, int H, float eps, hipStream_t s);
+hipError_t launch_linear_bf16(int epi, const uint16_t* x, const uint16_t* W, const uint16_t* bias,
+                              const uint16_t* res, uint16_t* out, int64_t M, int N, int K,
+                              hipStream_t s);
 // prefill grouped GEMM: one launch per stage, items = (m-tile, n-tile)
 hipError_t launch_prefill(int mode, PrefillArgs a, int max_mtiles, hipStream_t s);
 // the bias-form prefill GEMM (group size a multiple of 128) and the pass that

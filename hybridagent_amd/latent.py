@@ -10,8 +10,9 @@ last layer the HybridLink map R(h) = LN(h + proj2(GELU(proj1(LN(h)))))
 The MoE layers run through the HIP library (router + experts in one C-ABI
 call per layer), and so do the residual add and RMSNorm in front of each
 (one w4a16_add_rms_norm launch: the previous layer's MoE output is added to
-the residual while it is normalised); the HybridLink MLP is plain torch bf16
-(hipBLASLt GEMMs), which is all that path needs.
+the residual while it is normalised), and so does the HybridLink map
+(w4a16_hybridlink: two LayerNorm launches and two bf16 weight-streaming
+linear launches with the bias, GELU and residual fused).
 """
 from __future__ import annotations
 
@@ -19,7 +20,6 @@ import math
 from dataclasses import dataclass
 
 import torch
-import torch.nn.functional as F
 
 from . import _lib, synth
 
@@ -78,10 +78,8 @@ class LatentStack:
 
     def hybridlink(self, h: torch.Tensor) -> torch.Tensor:
         p = self.hl
-        a = F.layer_norm(h, (self.H,), p["ln1w"], p["ln1b"])
-        a = F.linear(a, p["p1w"], p["p1b"])
-        a = F.linear(F.gelu(a), p["p2w"], p["p2b"])
-        return F.layer_norm(h + a, (self.H,), p["ln2w"], p["ln2b"])
+        return _lib.hybridlink(h, p["ln1w"], p["ln1b"], p["p1w"], p["p1b"], p["p2w"], p["p2b"],
+                               p["ln2w"], p["ln2b"])
 
     def step(self, h: torch.Tensor) -> torch.Tensor:
         """One latent step: all MoE layers, then HybridLink x sqrt(H).  The same

@@ -83,6 +83,24 @@ W4A16_API int w4a16_add_rms_norm(const uint16_t* h, const uint16_t* delta, const
                        uint16_t* h_out, uint16_t* y, int64_t M, int64_t H, float eps,
                        void* stream);
 
+/* HybridLink latent map -- hybridlink.py:17-28 (HybridLink.forward; the
+ * latent loop applies it to the last hidden state, engine.py:381-390):
+ *   a   = LayerNorm(h; ln1_w, ln1_b)                     (pre_ln)
+ *   g   = bf16(GELU_erf(bf16(a p1_w^T + p1_b)))          (proj1, act)
+ *   r   = bf16(h + bf16(g p2_w^T + p2_b))                (proj2, residual)
+ *   out = LayerNorm(r; ln2_w, ln2_b)                     (post_ln)
+ * LayerNorm: fp32 mean and variance, (x - mean) * rsqrt(var + eps) * w + b,
+ * bf16 out (nn.LayerNorm, eps = 1e-5 in the reference module).
+ * h, out [B, H] bf16; ln*_w, ln*_b, p*_b [H] bf16; p1_w, p2_w [H, H] bf16
+ * (nn.Linear layout, out x in).  H % 32 == 0, H <= 3072; 16-byte aligned
+ * h, out, weights, LayerNorm parameters and workspace.                     */
+W4A16_API size_t w4a16_hybridlink_workspace_bytes(int64_t B, int64_t H);
+W4A16_API int w4a16_hybridlink(const uint16_t* h, const uint16_t* ln1_w, const uint16_t* ln1_b,
+                     const uint16_t* p1_w, const uint16_t* p1_b, const uint16_t* p2_w,
+                     const uint16_t* p2_b, const uint16_t* ln2_w, const uint16_t* ln2_b,
+                     uint16_t* out, int64_t B, int64_t H, float eps, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
 /* Router  -- backends.py:111-117 (HF Gemma4TextRouter.forward,
  * transformers/models/gemma4/modeling_gemma4.py:1335-1356):
  *   r       = bf16(bf16(rms_norm(hidden) * router_scale) * scalar_root)

@@ -75,6 +75,20 @@ def test_add_rms_norm_host_validation(lib):
     assert lib.w4a16_linear(NULL, NULL, NULL, NULL, NULL, 0, 16, 64, 32, NULL, 0, NULL) == 0
 
 
+def test_hybridlink_host_validation(lib):
+    fake = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    p = [fake] * 9
+    need = lib.w4a16_hybridlink_workspace_bytes(32, 2816)
+    assert need >= 2 * 32 * 2816 * 2
+    f = lib.w4a16_hybridlink
+    assert f(*p, fake, 32, 2800, 1e-5, fake, need, NULL) == 2      # H % 32
+    assert f(*p, fake, 32, 4096, 1e-5, fake, need, NULL) == 2      # H > 3072
+    assert f(*p[:8], NULL, fake, 32, 2816, 1e-5, fake, need, NULL) == 1   # post_ln bias missing
+    assert f(*p, fake, 32, 2816, 1e-5, fake, need - 1, NULL) == 5  # workspace too small
+    assert f(ctypes.c_void_p(4098), *p[1:], fake, 32, 2816, 1e-5, fake, need, NULL) == 4
+    assert f(*([NULL] * 10), 0, 2816, 1e-5, NULL, 0, NULL) == 0    # nothing to do
+
+
 def test_moe_host_validation(lib):
     fake = ctypes.c_void_p(4096)
     args = [fake] * 8

@@ -576,3 +576,43 @@ def test_graph_replay_decode_layer(dev, moe128, M):
     x2 = synth.activations(33, H, seed=813).to(dev)
     rargs2 = (h2.to(dev),) + rargs[1:]
     _replays_match(fwd, fwd, lambda: _lib.moe_layer_forward(*rargs2, x2, *eargs))
+
+
+# ---------------------------------------------------- HybridLink (hybridlink.py)
+
+def _hybridlink_params(H, seed, dev):
+    g = torch.Generator().manual_seed(seed)
+    std = 1.0 / math.sqrt(H)
+    mk = lambda *s, sc=1.0: (sc * torch.randn(*s, generator=g)).to(torch.bfloat16).to(dev)
+    return {"ln1w": (1.0 + 0.05 * torch.randn(H, generator=g)).to(torch.bfloat16).to(dev), "ln1b": mk(H, sc=0.02),
+            "p1w": mk(H, H, sc=std), "p1b": mk(H, sc=0.02), "p2w": mk(H, H, sc=std), "p2b": mk(H, sc=0.02),
+            "ln2w": (1.0 + 0.05 * torch.randn(H, generator=g)).to(torch.bfloat16).to(dev), "ln2b": mk(H, sc=0.02)}
+
+
+# batch 32 at H = 2816 is the latent loop's shape; 1 / 17 / 100 cover one,
+# two and several row tiles (ragged); H = 32 leaves seven of the eight
+# K-split wavefronts without k steps
+@pytest.mark.parametrize("B,Hh", [(32, 2816), (1, 2816), (17, 256), (100, 1024), (5, 32)])
+def test_hybridlink(dev, B, Hh):
+    p = _hybridlink_params(Hh, seed=900 + Hh, dev=dev)
+    h = synth.activations(B, Hh, seed=901 + B, device=dev)
+    got = _lib.hybridlink(h, p["ln1w"], p["ln1b"], p["p1w"], p["p1b"], p["p2w"], p["p2b"], p["ln2w"], p["ln2b"])
+    q = {key: _np(v) for key, v in p.items()}
+    ref = oracle.hybridlink(_np(h), q["p1w"], q["p1b"], q["p2w"], q["p2b"], q["ln1w"], q["ln1b"], q["ln2w"], q["ln2b"])
+    err = oracle.max_abs_rel(_np(got), ref)
+    print(f"hybridlink B={B} H={Hh} max_abs_rel={err:.2e}")
+    assert err <= 2 * TOL
+    # the torch bf16 module (the reference's own arithmetic, torch CPU in fp32
+    # per op with bf16 rounding between the ops) agrees as closely
+    hc = h.cpu().float()
+    pc = {key: v.cpu().float() for key, v in p.items()}
+    rb = lambda t: t.to(torch.bfloat16).float()
+    a = rb(torch.nn.functional.layer_norm(hc, (Hh,), pc["ln1w"], pc["ln1b"]))
+    a = rb(torch.nn.functional.gelu(rb(a @ pc["p1w"].T + pc["p1b"])))
+    r = rb(hc + rb(a @ pc["p2w"].T + pc["p2b"]))
+    tref = rb(torch.nn.functional.layer_norm(r, (Hh,), pc["ln2w"], pc["ln2b"]))
+    assert oracle.max_abs_rel(_np(got), tref.numpy()) <= TOL
+    # rows are independent: a sub-batch gives the same bits
+    got_sub = _lib.hybridlink(h[: max(1, B // 2)], p["ln1w"], p["ln1b"], p["p1w"], p["p1b"], p["p2w"], p["p2b"],
+                              p["ln2w"], p["ln2b"])
+    assert torch.equal(got_sub, got[: max(1, B // 2)])
