@@ -53,6 +53,15 @@ __global__ __launch_bounds__(kLnThreads) void k_layer_norm(const uint16_t* __res
   const int n8 = H >> 3;
   float v[kLnChunks][8];
   float s = 0.f;
+  // the affine parameters are loaded with the row, so the row's statistics
+  // and the parameters arrive in one memory round trip
+  u32x4_t wv[kLnChunks], bv[kLnChunks];
+#pragma unroll
+  for (int q = 0; q < kLnChunks; ++q) {
+    const int c8 = min(threadIdx.x + kLnThreads * q, n8 - 1);
+    wv[q] = ld16(w + 8 * c8);
+    bv[q] = ld16(b + 8 * c8);
+  }
 #pragma unroll
   for (int q = 0; q < kLnChunks; ++q) {
     const int c8 = threadIdx.x + kLnThreads * q;
@@ -84,8 +93,8 @@ __global__ __launch_bounds__(kLnThreads) void k_layer_norm(const uint16_t* __res
   for (int q = 0; q < kLnChunks; ++q) {
     const int c8 = threadIdx.x + kLnThreads * q;
     if (c8 < n8) {
-      const u32x4_t wv = ld16(w + 8 * c8), bv = ld16(b + 8 * c8);
-      const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w}, bw[4] = {bv.x, bv.y, bv.z, bv.w};
+      const uint32_t ww[4] = {wv[q].x, wv[q].y, wv[q].z, wv[q].w};
+      const uint32_t bw[4] = {bv[q].x, bv[q].y, bv[q].z, bv[q].w};
       uint32_t o[4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
