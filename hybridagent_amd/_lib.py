@@ -327,8 +327,9 @@ def moe_forward(hidden_states: torch.Tensor, top_k_index: torch.Tensor, top_k_we
     dev = _require_gpu(hidden_states, top_k_index, top_k_weights, gu_packed, gu_scale, dn_packed, dn_scale)
     H = hidden_states.shape[-1]
     x = _bf16(hidden_states, "hidden_states").reshape(-1, H)
-    idx = top_k_index.reshape(x.shape[0], -1).to(torch.int64).contiguous()
-    w = top_k_weights.reshape(x.shape[0], -1).to(torch.float32).contiguous()
+    # explicit widths: reshape(0, -1) is ambiguous for an empty batch
+    idx = top_k_index.reshape(x.shape[0], top_k_index.shape[-1]).to(torch.int64).contiguous()
+    w = top_k_weights.reshape(x.shape[0], top_k_weights.shape[-1]).to(torch.float32).contiguous()
     gu_packed = _i32(gu_packed, "gate_up_packed")
     dn_packed = _i32(dn_packed, "down_packed")
     gu_scale = _bf16(gu_scale, "gate_up_scale")

@@ -18,6 +18,11 @@ inline bool valid_group(int64_t G) { return G >= 32 && G <= (1 << 20) && (G & (G
 
 inline size_t round256(size_t b) { return (b + 255) & ~size_t(255); }
 
+// Row-per-workgroup launches (256 threads) keep rows * 256 below 2^32.
+constexpr int64_t kMaxRowLaunches = (int64_t(1) << 24) - 1;
+// HybridLink: the linears' grid.y = ceil(B / 64) stays <= 65535
+constexpr int64_t kMaxHybridLinkRows = int64_t(65535) * 64;
+
 // Bump allocator over a caller-provided workspace.
 struct Carve {
   char* base;
@@ -150,8 +155,8 @@ int w4a16_dequantize(const int32_t* packed, const uint16_t* scale, uint16_t* out
 int w4a16_add_rms_norm(const uint16_t* h, const uint16_t* delta, const uint16_t* weight,
                        uint16_t* h_out, uint16_t* y, int64_t M, int64_t H, float eps,
                        void* stream) {
-  if (M < 0 || M > (int64_t(1) << 31) - 1 || H <= 0 || H % 8 != 0 || H > 8192)
-    return W4A16_ERR_SHAPE;
+  // one 256-thread workgroup per row: M * 256 work-items must fit in 32 bits
+  if (M < 0 || M > kMaxRowLaunches || H <= 0 || H % 8 != 0 || H > 8192) return W4A16_ERR_SHAPE;
   if (M == 0) return W4A16_OK;
   if (!h || !weight || !y || (delta && !h_out)) return W4A16_ERR_NULL;
   if (!aligned16(h) || !aligned16(weight) || !aligned16(y) || (delta && !aligned16(delta)) ||
@@ -171,7 +176,8 @@ int w4a16_hybridlink(const uint16_t* h, const uint16_t* ln1_w, const uint16_t* l
                      const uint16_t* p2_b, const uint16_t* ln2_w, const uint16_t* ln2_b,
                      uint16_t* out, int64_t B, int64_t H, float eps, void* workspace,
                      size_t workspace_bytes, void* stream) {
-  if (B < 0 || B > (int64_t(1) << 24) || H <= 0 || H % 32 != 0 || H > 3072) return W4A16_ERR_SHAPE;
+  // LayerNorm: one 256-thread workgroup per row; the linears: grid.y = ceil(B / 64) <= 65535
+  if (B < 0 || B > kMaxHybridLinkRows || H <= 0 || H % 32 != 0 || H > 3072) return W4A16_ERR_SHAPE;
   if (B == 0) return W4A16_OK;
   if (!h || !ln1_w || !ln1_b || !p1_w || !p1_b || !p2_w || !p2_b || !ln2_w || !ln2_b || !out)
     return W4A16_ERR_NULL;
@@ -205,6 +211,8 @@ int w4a16_linear(const uint16_t* x, const int32_t* w_packed, const uint16_t* w_s
   if (M < 0 || N <= 0 || K <= 0 || K % 32 != 0 || K > (1 << 24) || N > (1 << 24) ||
       M > (1 << 24))
     return W4A16_ERR_SHAPE;
+  // the packed matrix is addressed by 32-bit byte offsets of one buffer descriptor
+  if (N * K / 2 >= (int64_t(1) << 31)) return W4A16_ERR_SHAPE;
   if (!valid_group(group_size)) return W4A16_ERR_GROUP;
   if (M == 0) return W4A16_OK;
   if (!x || !w_packed || !w_scale || !y) return W4A16_ERR_NULL;

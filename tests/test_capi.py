@@ -87,6 +87,21 @@ def test_hybridlink_host_validation(lib):
     assert f(*p, fake, 32, 2816, 1e-5, fake, need - 1, NULL) == 5  # workspace too small
     assert f(ctypes.c_void_p(4098), *p[1:], fake, 32, 2816, 1e-5, fake, need, NULL) == 4
     assert f(*([NULL] * 10), 0, 2816, 1e-5, NULL, 0, NULL) == 0    # nothing to do
+    # batch limit: the linears' grid.y = ceil(B / 64) must stay <= 65535
+    big = 65535 * 64
+    assert f(*p, fake, big + 1, 2816, 1e-5, fake, 1 << 62, NULL) == 2
+
+
+def test_row_launch_limits(lib):
+    fake = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    # one 256-thread workgroup per row: rows * 256 must stay below 2^32
+    assert lib.w4a16_add_rms_norm(fake, NULL, fake, NULL, fake, 1 << 24, 64, 1e-6, NULL) == 2
+    # dense weights whose packed bytes reach 2 GiB would overflow the 32-bit
+    # buffer offsets: rejected instead of reading the wrong rows
+    assert lib.w4a16_linear(fake, fake, fake, NULL, fake, 4, 1 << 20, 4096, 128, NULL, 0, NULL) == 2
+    # just below the limit the shape passes (and the missing x is reported)
+    assert lib.w4a16_linear(NULL, fake, fake, NULL, fake, 4, (1 << 20) - 8, 4096, 128, NULL, 0,
+                            NULL) == 1
 
 
 def test_moe_host_validation(lib):
