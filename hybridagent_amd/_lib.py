@@ -43,6 +43,8 @@ SIGNATURES = {
     "moe_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
     "moe_forward": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64,
                                    _I64, _I64, _VP, _SZ, _VP]),
+    "moe_forward_static": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64,
+                                          _I64, _I64, _VP]),
     "moe_plan": (ctypes.c_int, [_VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "moe_gate_up": (ctypes.c_int, [_VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "moe_down": (ctypes.c_int, [_VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),

@@ -5,6 +5,8 @@
 
 #include "launch.hpp"
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 
 using namespace w4a16;
 
@@ -537,6 +539,70 @@ int moe_forward(const uint16_t* hidden, const int64_t* topk_idx, const float* to
     st = moe_combine(topk_idx, topk_w, out, M, top_k, E, H, I, workspace, workspace_bytes,
                      stream);
   return st;
+}
+
+}  // extern "C"
+
+// moe_forward_static's scratch: one array per GPU the library runs on, held
+// until the process ends.  Host code never uses this name as an address (on
+// the host it is a stand-in, not device memory): static_scratch() looks up
+// each device's copy once, with that device current, and every later use
+// goes through the pointer it returns.
+static __device__ __align__(256) unsigned char scratch[W4A16_STATIC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// The current device's address of `scratch` (the kernels' workspace for
+// moe_forward_static); fails if the stream belongs to another device.
+int static_scratch(hipStream_t stream, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return W4A16_ERR_LAUNCH;
+  if (stream != nullptr) {
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(stream, &sdev) != hipSuccess || sdev != dev) return W4A16_ERR_LAUNCH;
+  }
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr)
+        return W4A16_ERR_LAUNCH;
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return W4A16_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe_forward_static(const uint16_t* hidden, const int64_t* topk_idx, const float* topk_w,
+                       const int32_t* gu_packed, const uint16_t* gu_scale,
+                       const int32_t* dn_packed, const uint16_t* dn_scale, uint16_t* out,
+                       int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I,
+                       int64_t group_size, void* stream) {
+  // the shape checks of moe_forward (with no workspace, valid shapes report
+  // W4A16_ERR_WORKSPACE), then the scratch limit
+  MoeLayout none{};
+  int st = moe_check(M, top_k, E, H, I, group_size, nullptr, 0, &none);
+  if (st != W4A16_OK && st != W4A16_ERR_WORKSPACE) return st;
+  if (M == 0) return W4A16_OK;
+  if (moe_workspace_bytes(M, top_k, E, H, I) > W4A16_STATIC_SCRATCH_BYTES) return W4A16_ERR_SHAPE;
+  if (!hidden || !topk_idx || !topk_w || !gu_packed || !gu_scale || !dn_packed || !dn_scale ||
+      !out)
+    return W4A16_ERR_NULL;
+  void* ws = nullptr;
+  st = static_scratch(static_cast<hipStream_t>(stream), &ws);
+  if (st != W4A16_OK) return st;
+  return moe_forward(hidden, topk_idx, topk_w, gu_packed, gu_scale, dn_packed, dn_scale, out, M,
+                     top_k, E, H, I, group_size, ws, W4A16_STATIC_SCRATCH_BYTES, stream);
 }
 
 size_t moe_layer_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I) {

@@ -152,6 +152,26 @@ W4A16_API int moe_forward(const uint16_t* hidden, const int64_t* topk_idx, const
                 int64_t H, int64_t I, int64_t group_size, void* workspace,
                 size_t workspace_bytes, void* stream);
 
+/* moe_forward without a workspace and without allocating -- no counterpart
+ * in the reference.  For callers that cannot allocate device memory at call
+ * time (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments and results as moe_forward minus the
+ * workspace: the scratch is a file-scope device array of
+ * W4A16_STATIC_SCRATCH_BYTES per GPU, which each GPU the library runs on
+ * holds until the process ends; its address is looked up once per device,
+ * on the first call there.  Sizes whose moe_workspace_bytes() exceeds the
+ * array are rejected with W4A16_ERR_SHAPE (16 MiB covers every decode size,
+ * M <= 256, at the Gemma-4-26B-A4B shape).  The stream must belong to the
+ * current device (W4A16_ERR_LAUNCH otherwise).  Every call on a GPU shares
+ * that GPU's array: calls that overlap on one GPU (other streams, other
+ * threads) race.  Nothing in the array needs to start at zero; it keeps the
+ * last call's contents.                                                    */
+#define W4A16_STATIC_SCRATCH_BYTES ((size_t)16 << 20)
+W4A16_API int moe_forward_static(const uint16_t* hidden, const int64_t* topk_idx, const float* topk_w,
+                       const int32_t* gu_packed, const uint16_t* gu_scale, const int32_t* dn_packed,
+                       const uint16_t* dn_scale, uint16_t* out, int64_t M, int64_t top_k,
+                       int64_t E, int64_t H, int64_t I, int64_t group_size, void* stream);
+
 /* The four stages of moe_forward, for callers that schedule or time them
  * separately.  They share one workspace of moe_workspace_bytes(M, top_k, E,
  * H, I) bytes that carries the routing plan and the intermediate

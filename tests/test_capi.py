@@ -137,6 +137,22 @@ def test_moe_host_validation(lib):
     assert lib.moe_layer_forward(*largs, 8, 8, 128, 2816, 704, 128, fake, lw, NULL) == 4
 
 
+def test_moe_forward_static_host_validation(lib):
+    fake = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    args = [fake] * 8
+    f = lib.moe_forward_static
+    # needs more scratch than the static array holds
+    assert lib.moe_workspace_bytes(4096, 8, 128, 2816, 704) > (16 << 20)
+    assert f(*args, 4096, 8, 128, 2816, 704, 128, NULL) == 2
+    # the shape checks of moe_forward
+    assert f(*args, 8, 8, 128, 2816, 700, 128, NULL) == 2
+    assert f(*args, 8, 8, 128, 2816, 704, 96, NULL) == 3
+    bad = list(args)
+    bad[0] = NULL
+    assert f(*bad, 8, 8, 128, 2816, 704, 128, NULL) == 1
+    assert f(*([NULL] * 8), 0, 8, 128, 2816, 704, 128, NULL) == 0   # nothing to do
+
+
 def test_dequant_host_validation(lib):
     fake = ctypes.c_void_p(4096)
     assert lib.w4a16_dequantize(fake, fake, fake, 4, 12, 32, NULL) == 2
