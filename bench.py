@@ -23,14 +23,20 @@ down [704 -> 2816], all experts W4A16 at group size 128; activations ~N(0,1).
 
 Weights and inputs are resident in HBM before the timed region; the timed
 region replays a HIP graph of layer forwards that cycles through ``--layers``
-independent layer copies (default 8 x 393 MB = 3.1 GB, far above the 256 MB
-Infinity Cache) so every call streams its experts from HBM.  Times come from
-HIP events on the stream the kernels run on.
+independent layer copies (default 24 x 393 MB = 9.4 GB; even at M = 1, where
+a call touches only its 8 experts, one pass over the copies reads 590 MB,
+more than twice the 256 MB Infinity Cache) so every call streams its experts
+from HBM.  Times come from HIP events on the stream the kernels run on.
 
-``roofline`` is the dominant kernel (the grouped gate_up GEMM at the largest
-decode M, about two thirds of the decode bytes), timed alone the same way.
-``cpu_baseline`` times the numpy oracle (``oracle/``, the CPU restatement of
-the reference path) on a bounded decode sample on this host.
+``roofline`` is the dominant decode kernel (the grouped gate_up GEMM at the
+largest decode M, about two thirds of the decode bytes), timed alone the same
+way; ``roofline_prefill`` the dominant prefill kernel (the gate_up stage at
+M = 4096) against the bf16 MFMA peak, with the MFMA-busy fraction of the
+committed counter summary.  ``g32`` repeats decode (M = 1, 64) and prefill at
+group size 32, the released checkpoints'.
+``cpu_baseline`` times the torch-CPU restatement of the reference's CPU path
+(``oracle/torch_cpu.py``) on this host's cores: one decode layer at each M of
+the sweep, and configs[0] (the dense W4A16 linear at M = 16).
 ``latent`` is BASELINE configs[4] (30 MoE layers + HybridLink per step, batch
 32); ``hybridlink`` times the HybridLink map alone at that batch (weights
 rotated through HBM).
@@ -70,13 +76,19 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def expert_bytes(g: int) -> int:
+    """Packed weights + bf16 scales of one expert (gate_up and down) at group size g."""
+    return (2 * I * H // 2 + 2 * I * math.ceil(H / g) * 2) + (H * I // 2 + H * math.ceil(I / g) * 2)
+
+
 class Layer:
     """One MoE layer's device-resident weights (router + experts)."""
 
-    def __init__(self, seed: int, dev, zipf: bool = False):
+    def __init__(self, seed: int, dev, zipf: bool = False, g: int = G):
+        self.g = g
         self.rw = (synth.zipf_router_weights(E, H, seed=seed, device=dev) if zipf
                    else synth.router_weights(E, H, seed=seed, device=dev))
-        self.ew = synth.moe_weights(E, H, I, G, seed=seed + 1000, device=dev)
+        self.ew = synth.moe_weights(E, H, I, g, seed=seed + 1000, device=dev)
 
     def route(self, x):
         rw = self.rw
@@ -87,7 +99,7 @@ class Layer:
         rw, ew = self.rw, self.ew
         out, _, _ = _lib.moe_layer_forward(x, rw.scale, rw.scalar_root, rw.proj, rw.per_expert_scale,
                                            rw.eps, TOPK, x, ew.gate_up_packed, ew.gate_up_scale,
-                                           ew.down_packed, ew.down_scale, group_size=G)
+                                           ew.down_packed, ew.down_scale, group_size=self.g)
         return out
 
 
@@ -117,9 +129,10 @@ def time_graph(fn, calls_per_replay: int, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) * 1e-3 / (replays * calls_per_replay)
 
 
-def decode_sweep(layers, dev, steps, warmup):
+def decode_sweep(layers, dev, steps, warmup, ms=DECODE_MS):
     out = {}
-    for M in DECODE_MS:
+    g = layers[0].g
+    for M in ms:
         x = synth.activations(M, H, seed=7000 + M, device=dev)
         uniq = []
         for ly in layers:
@@ -127,10 +140,11 @@ def decode_sweep(layers, dev, steps, warmup):
             uniq.append(int(torch.unique(idx).numel()))
         U = sum(uniq) / len(uniq)
         t = time_graph(lambda: [ly.forward(x) for ly in layers], len(layers), steps, warmup)
-        nbytes = U * EXPERT_BYTES + ROUTER_BYTES + 2 * M * H * 2
+        nbytes = U * expert_bytes(g) + ROUTER_BYTES + 2 * M * H * 2
         out[M] = {"us": t * 1e6, "unique_experts": U, "bytes": nbytes, "gbps": nbytes / t / 1e9,
-                  "frac_hbm": nbytes / t / 1e9 / PEAK_HBM_GBS}
-        log(f"decode M={M}: {t*1e6:.1f} us/layer, U={U:.1f}, {out[M]['gbps']:.0f} GB/s")
+                  "frac_hbm": nbytes / t / 1e9 / PEAK_HBM_GBS,
+                  "distinct_bytes_per_replay": len(layers) * U * expert_bytes(g)}
+        log(f"decode G={g} M={M}: {t*1e6:.1f} us/layer, U={U:.1f}, {out[M]['gbps']:.0f} GB/s")
     return out
 
 
@@ -178,21 +192,79 @@ def dense_sweep(dev, steps, warmup):
     return out
 
 
-def prefill(dev, steps, warmup, n_layers):
-    layers = [Layer(seed=9000 + 17 * i, dev=dev, zipf=True) for i in range(n_layers)]
+def prefill(dev, steps, warmup, n_layers, g: int = G, stages: bool = True):
+    """the whole layer (router + sort + gate_up + down + combine) at
+    M = 4096 with Zipf routing; with ``stages`` also the gate_up stage alone
+    (prefill prep + the grouped gate_up GEMM, the dominant kernel)."""
+    layers = [Layer(seed=9000 + 17 * i, dev=dev, zipf=True, g=g) for i in range(n_layers)]
     x = synth.zipf_activations(PREFILL_M, H, seed=9999, device=dev)
     _, idx = layers[0].route(x)
     counts = torch.bincount(idx.flatten(), minlength=E).cpu()
     t = time_graph(lambda: [ly.forward(x) for ly in layers], len(layers), steps, warmup)
     flops = 2.0 * PREFILL_M * TOPK * (H * 2 * I + I * H) + 2.0 * PREFILL_M * H * E
     srt = torch.sort(counts, descending=True).values
-    res = {"ms": t * 1e3, "tflops": flops / t / 1e12, "frac_mfma": flops / t / 1e12 / PEAK_BF16_TFLOPS,
-           "gflop": flops / 1e9, "empty_experts": int((counts == 0).sum()),
-           "hot_expert_rows": srt[:4].tolist()}
-    log(f"prefill M={PREFILL_M}: {t*1e3:.3f} ms/layer, {res['tflops']:.1f} TFLOP/s, "
+    res = {"group_size": g, "ms": t * 1e3, "tflops": flops / t / 1e12,
+           "frac_mfma": flops / t / 1e12 / PEAK_BF16_TFLOPS, "gflop": flops / 1e9,
+           "empty_experts": int((counts == 0).sum()), "hot_expert_rows": srt[:4].tolist()}
+    log(f"prefill G={g} M={PREFILL_M}: {t*1e3:.3f} ms/layer, {res['tflops']:.1f} TFLOP/s, "
         f"empty={res['empty_experts']} hot={res['hot_expert_rows']}")
+    if stages:
+        sts = []
+        for ly in layers:
+            _, li = ly.route(x)
+            st = _lib.MoEStages(PREFILL_M, TOPK, E, H, I, g, dev)
+            st.plan(x, li)
+            sts.append(st)
+        torch.cuda.synchronize()
+
+        def run():
+            for ly, st in zip(layers, sts):
+                st.gate_up(x, ly.ew.gate_up_packed, ly.ew.gate_up_scale)
+
+        tg = time_graph(run, len(layers), steps, warmup)
+        gflop = 2.0 * PREFILL_M * TOPK * H * 2 * I
+        res["gate_up_stage"] = {"us": tg * 1e6, "tflops": gflop / tg / 1e12, "gflop": gflop / 1e9}
+        log(f"prefill G={g} gate_up stage: {tg*1e6:.1f} us, {gflop / tg / 1e12:.1f} TFLOP/s")
+        del sts
     del layers
+    torch.cuda.empty_cache()
     return res
+
+
+PREFILL_COUNTERS_FILE = os.path.join(ROOT, "profiles", "prefill_M4096_counters.md")
+
+
+def counter_summary(path, key):
+    """A ``key: value`` line of a committed counter summary (None if absent)."""
+    try:
+        with open(path) as f:
+            for ln in f:
+                if ln.startswith(key + ":"):
+                    return float(ln.split(":", 1)[1].strip())
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def roofline_prefill(pre):
+    """The prefill's dominant kernel against the bf16 MFMA peak: the gate_up
+    stage (k_prefill_prep + k_prefill_cr_gather + k_prefill_bias<gateup>; the
+    GEMM is all but a few us of it), algorithmic flops 2 * 4096 * 8 * 2816 *
+    1408 per launch over its HIP-event time."""
+    st = pre["gate_up_stage"]
+    return {
+        "bound": "mfma",
+        "kernel": "k_prefill_bias<gateup> (moe_gate_up stage, prep included)",
+        "M": PREFILL_M,
+        "achieved": round(st["tflops"], 2),
+        "peak": PEAK_BF16_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(st["tflops"] / PEAK_BF16_TFLOPS, 4),
+        "us_per_launch": round(st["us"], 3),
+        "algorithmic_gflop_per_launch": round(st["gflop"], 3),
+        "mfma_busy_frac_counter": counter_summary(PREFILL_COUNTERS_FILE, "mfma_busy_frac_gate_up"),
+        "counter_source": os.path.relpath(PREFILL_COUNTERS_FILE, ROOT),
+    }
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gateup_decode_M64_traffic.md")
@@ -288,66 +360,111 @@ def latent(dev, steps: int = LATENT_STEPS):
     return res
 
 
-def cpu_baseline(budget_s: float):
-    """numpy oracle on this host's cores, bounded decode sample (M=32, one layer)."""
-    import numpy as np
-    import oracle
-    try:
-        from threadpoolctl import threadpool_info, threadpool_limits
-    except ImportError:  # pragma: no cover
-        threadpool_info = threadpool_limits = None
-    ncores = len(os.sched_getaffinity(0))
+def _host_cores() -> int:
+    n = len(os.sched_getaffinity(0))
     if os.environ.get("OMP_NUM_THREADS", "").isdigit():
-        ncores = min(ncores, int(os.environ["OMP_NUM_THREADS"]))
-    M = 32
-    ly_seed = 4242
-    ew = synth.moe_weights(E, H, I, G, seed=ly_seed + 1000)
-    rw = synth.router_weights(E, H, seed=ly_seed)
-    x = synth.activations(M, H, seed=7000 + M)
-    bits = lambda t: t.view(torch.int16).numpy().view(np.uint16)
-    args = (ew.gate_up_packed.numpy(), bits(ew.gate_up_scale), ew.down_packed.numpy(), bits(ew.down_scale))
-    xf = x.float().numpy()
+        n = min(n, int(os.environ["OMP_NUM_THREADS"]))
+    return max(1, n)
 
-    def run():
-        _, idx, w = oracle.router(xf, rw.scale.float().numpy(), rw.scalar_root, rw.proj.float().numpy(),
-                                  rw.per_expert_scale.float().numpy(), rw.eps, TOPK)
-        oracle.moe_forward(xf, idx, w, *args, G)
-        return idx
 
-    import contextlib
-    ctx = threadpool_limits(limits=ncores) if threadpool_limits else contextlib.nullcontext()
-    with ctx:
-        idx = run()  # warm-up
-        U = len(np.unique(idx))
-        times = []
-        t_all = time.perf_counter()
-        while len(times) < 3 or (time.perf_counter() - t_all < budget_s and len(times) < 10):
-            t0 = time.perf_counter()
-            run()
-            times.append(time.perf_counter() - t0)
-            if time.perf_counter() - t_all > 3 * budget_s:
-                break
-        threads = ncores
-        if threadpool_info:
-            blas = [p["num_threads"] for p in threadpool_info() if p.get("user_api") == "blas"]
-            threads = max(blas) if blas else 1
-    t = sorted(times)[len(times) // 2]
-    nbytes = U * EXPERT_BYTES + ROUTER_BYTES + 2 * M * H * 2
-    cpu_model = ""
+def _cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
             for ln in f:
                 if ln.startswith("model name"):
-                    cpu_model = ln.split(":", 1)[1].strip()
-                    break
+                    return ln.split(":", 1)[1].strip()
     except OSError:
         pass
-    return {"value": nbytes / t / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": (f"numpy oracle (oracle/w4a16_oracle.py: router + fused-path MoE) on one "
-                       f"decode layer at M={M} (U={U} experts, {nbytes/1e6:.0f} MB algorithmic), "
-                       f"median of {len(times)} reps, {t:.2f} s/layer; dequant in single-threaded numpy, "
-                       f"matmuls in BLAS with {threads} threads; host {cpu_model}, {ncores} cores available"),
-            "seconds_per_layer": t}
+    return ""
+
+
+def _median_time(fn, budget_s: float, min_reps: int = 3, max_reps: int = 10) -> tuple[float, int]:
+    fn()  # warm-up
+    times, t_all = [], time.perf_counter()
+    while len(times) < min_reps or (time.perf_counter() - t_all < budget_s and len(times) < max_reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_all > 3 * budget_s:
+            break
+    return sorted(times)[len(times) // 2], len(times)
+
+
+def cpu_baseline(budget_s: float):
+    """The reference's CPU path (oracle/torch_cpu.py: the torch ops of
+    quantization.py:132-137,171-175,241-294 and the router of backends.py:111-117)
+    on this host's cores: one decode layer (router + experts) at each M of the
+    decode sweep, value = sum of algorithmic bytes / sum of times as for the
+    GPU; and configs[0], Linear4Bit.forward at M = 16, K = N = 2816, G = 128."""
+    from oracle import torch_cpu
+    ncores = _host_cores()
+    prev_threads = torch.get_num_threads()
+    torch.set_num_threads(ncores)
+    try:
+        ew = synth.moe_weights(E, H, I, G, seed=5242)
+        rw = synth.router_weights(E, H, seed=4242)
+        per_m, tot_b, tot_t, reps = {}, 0.0, 0.0, []
+        for M in DECODE_MS:
+            x = synth.activations(M, H, seed=7000 + M)
+
+            def layer():
+                w, idx, _ = torch_cpu.router(x, rw.scale, rw.scalar_root, rw.proj, rw.per_expert_scale, rw.eps,
+                                             TOPK)
+                torch_cpu.experts(x, idx, w, ew.gate_up_packed, ew.gate_up_scale, ew.down_packed,
+                                  ew.down_scale, G)
+                return idx
+
+            U = int(torch.unique(layer()).numel())
+            t, n = _median_time(layer, budget_s / len(DECODE_MS))
+            nbytes = U * EXPERT_BYTES + ROUTER_BYTES + 2 * M * H * 2
+            per_m[str(M)] = {"ms": t * 1e3, "gbps": nbytes / t / 1e9, "unique_experts": U, "reps": n}
+            tot_b += nbytes
+            tot_t += t
+            reps.append(n)
+            log(f"cpu baseline decode M={M}: {t*1e3:.1f} ms/layer, {nbytes / t / 1e9:.2f} GB/s ({ncores} threads)")
+        # configs[0]: the dense W4A16 linear on the reference CPU path
+        x0 = synth.activations(16, 2816, seed=11)
+        p0 = synth.packed_int4((2816, 2816), seed=12)
+        s0 = synth.group_scales((2816, 2816), G, seed=13)
+        t0, n0 = _median_time(lambda: torch_cpu.linear4bit(x0, p0, s0, G), 2.0)
+        b0 = 2816 * 2816 // 2 + 2816 * 22 * 2 + 16 * 2816 * 2 * 2
+        f0 = 2.0 * 16 * 2816 * 2816
+        log(f"cpu baseline configs[0] dense M=16: {t0*1e3:.2f} ms, {f0 / t0 / 1e9:.1f} GFLOP/s")
+    finally:
+        torch.set_num_threads(prev_threads)
+    return {"value": tot_b / tot_t / 1e9, "unit": "GB/s", "cores": ncores, "kind": "port",
+            "sample": (f"torch-CPU restatement of the reference CPU path (oracle/torch_cpu.py: router, "
+                       f"quantization.py T==1 path at M=1 and the per-expert loop at M>1), one decode layer "
+                       f"at each M in {list(DECODE_MS)} (median of {min(reps)}-{max(reps)} reps each), "
+                       f"torch {torch.__version__} with {ncores} threads on {_cpu_model()}"),
+            "decode": per_m,
+            "config0_dense": {"M": 16, "K": 2816, "N": 2816, "group_size": G, "ms": t0 * 1e3, "reps": n0,
+                              "gbps": b0 / t0 / 1e9, "gflops": f0 / t0 / 1e9}}
+
+
+def _rounded(v):
+    """Floats rounded to 4 decimals, recursively (None passes through)."""
+    if isinstance(v, float):
+        return round(v, 4)
+    if isinstance(v, dict):
+        return {k: _rounded(x) for k, x in v.items()}
+    if isinstance(v, list):
+        return [_rounded(x) for x in v]
+    return v
+
+
+def g32_leg(dev, args):
+    """Group size 32, the released checkpoints' (quantization.py:19): decode at
+    M = 1 and 64 over the same rotation of layer copies, and the prefill layer."""
+    layers = [Layer(seed=200 + 17 * i, dev=dev, g=32) for i in range(args.layers)]
+    torch.cuda.synchronize()
+    dec = decode_sweep(layers, dev, args.steps, args.warmup, ms=(1, 64))
+    del layers
+    torch.cuda.empty_cache()
+    pre = None if args.no_prefill else prefill(dev, max(8, args.steps // 4), max(2, args.warmup // 4), 4,
+                                               g=32, stages=False)
+    return {"group_size": 32, "expert_bytes": expert_bytes(32),
+            "decode": {str(M): d for M, d in dec.items()}, "prefill": pre}
 
 
 def main(argv=None):
@@ -355,7 +472,9 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=16)
-    ap.add_argument("--layers", type=int, default=8, help="independent layer copies cycled per graph")
+    ap.add_argument("--layers", type=int, default=24,
+                    help="independent decode layer copies cycled per graph (24 x 393 MB: at M = 1 the "
+                         "8 experts of each copy add up to 590 MB, above twice the 256 MB Infinity Cache)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true")
@@ -367,6 +486,8 @@ def main(argv=None):
     ap.add_argument("--only-latent", action="store_true")
     ap.add_argument("--only-prefill", action="store_true",
                     help="time only the prefill layer (for rocprofv3 counter runs)")
+    ap.add_argument("--no-g32", action="store_true",
+                    help="skip the group-size-32 leg (the released checkpoints' group size)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run a plain 256 MiB device copy 8 times (counter calibration) and exit")
     args = ap.parse_args(argv)
@@ -391,8 +512,8 @@ def main(argv=None):
         print(json.dumps({"dense": dense_sweep(dev, args.steps, args.warmup)}), flush=True)
         return 0
     if args.only_prefill:
-        pre = prefill(dev, max(8, args.steps // 4), max(2, args.warmup // 4), min(args.layers, 4))
-        print(json.dumps({"prefill": pre}), flush=True)
+        pre = prefill(dev, max(8, args.steps // 4), max(2, args.warmup // 4), 4)
+        print(json.dumps({"prefill": pre, "roofline_prefill": roofline_prefill(pre)}), flush=True)
         return 0
 
     log(f"building {args.layers} decode layers ({args.layers * (E * EXPERT_BYTES + ROUTER_BYTES) / 1e9:.2f} GB)")
@@ -408,8 +529,8 @@ def main(argv=None):
     del layers
     torch.cuda.empty_cache()
 
-    pre = None if args.no_prefill else prefill(dev, max(8, args.steps // 4), max(2, args.warmup // 4),
-                                               min(args.layers, 4))
+    pre = None if args.no_prefill else prefill(dev, max(8, args.steps // 4), max(2, args.warmup // 4), 4)
+    g32 = None if args.no_g32 else g32_leg(dev, args)
 
     lat = None if args.no_latent else latent(dev)
     hl = None if args.no_latent else hybridlink_leg(dev)
@@ -442,6 +563,7 @@ def main(argv=None):
             "layers_rotated": args.layers, "timing": "HIP graph replay, HIP events",
         },
         "roofline": roofline(kern),
+        "roofline_prefill": None if pre is None else _rounded(roofline_prefill(pre)),
         "decode": {str(M): {k: (round(v, 4) if isinstance(v, float) else v) for k, v in d.items()}
                    for M, d in dec.items()},
         "prefill": None if pre is None else {k: (round(v, 4) if isinstance(v, float) else v)
@@ -452,8 +574,8 @@ def main(argv=None):
                                                for k, v in hl.items()},
         "dense": None if dense is None else {c: {k: (round(v, 4) if isinstance(v, float) else v)
                                                  for k, v in d.items()} for c, d in dense.items()},
-        "cpu_baseline": None if cpu is None else {k: (round(v, 4) if isinstance(v, float) else v)
-                                                  for k, v in cpu.items()},
+        "g32": _rounded(g32),
+        "cpu_baseline": _rounded(cpu),
     }
     print(json.dumps(result), flush=True)
     return 0

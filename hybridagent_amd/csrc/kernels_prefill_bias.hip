@@ -319,23 +319,27 @@ __device__ __forceinline__ void pb_item(const PrefillArgs& a, unsigned char* sme
     for (int i = 0; i < MI; ++i)
       ncr[i] = *reinterpret_cast<const f32x4_t*>(crbuf + r * kPbBM + 16 * (wm * MI + i) + 4 * kb);
     f32x4_t g[MI][NF];
+    // B fragments of step 0; each later step's fragment f is unpacked as
+    // soon as the MI MFMAs of the current step have read fragment f, so the
+    // unpack (VALU) of one column block runs beside the MFMAs of the next
+    u32x4_t bv[NF];
+#pragma unroll
+    for (int f = 0; f < NF; ++f) bv[f] = unpack_bias(bw[f].x, kMask, kBias);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      u32x4_t af[MI], bv[NF];
+      u32x4_t af[MI];
 #pragma unroll
       for (int i = 0; i < MI; ++i) af[i] = abuf[r * kPbAStage + (wm * MI + i) * 256 + a_slot[s]];
 #pragma unroll
       for (int f = 0; f < NF; ++f) {
-        const uint32_t wd = s == 0 ? bw[f].x : s == 1 ? bw[f].y : s == 2 ? bw[f].z : bw[f].w;
-        bv[f] = unpack_bias(wd, kMask, kBias);
+#pragma unroll
+        for (int i = 0; i < MI; ++i) g[i][f] = mfma16(af[i], bv[f], s == 0 ? ncr[i] : g[i][f]);
+        if (s < 3) {
+          const uint32_t wd = s == 0 ? bw[f].y : s == 1 ? bw[f].z : bw[f].w;
+          bv[f] = unpack_bias(wd, kMask, kBias);
+        }
       }
-#pragma unroll
-      for (int i = 0; i < MI; ++i)
-#pragma unroll
-        for (int f = 0; f < NF; ++f) g[i][f] = mfma16(af[i], bv[f], s == 0 ? ncr[i] : g[i][f]);
-      __builtin_amdgcn_sched_barrier(0);
       issue_part(tn, rn, s);
-      __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int i = 0; i < MI; ++i)

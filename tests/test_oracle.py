@@ -355,3 +355,73 @@ def test_hybridlink_vs_torch_modules():
     got = oracle.hybridlink(p(h), p(lin1.weight), p(lin1.bias), p(lin2.weight), p(lin2.bias),
                             p(ln1.weight), p(ln1.bias), p(ln2.weight), p(ln2.bias))
     np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-5)
+
+
+# ----------------------------------------------- torch-CPU restatement (CPU baseline)
+# oracle/torch_cpu.py restates the reference's CPU torch path; bench.py times
+# it.  Pinned here against the numpy oracle on identical inputs.
+
+def _ref_inputs(M, E=8, H=256, I=96, G=32, seed=0):
+    from hybridagent_amd import synth
+    w = synth.moe_weights(E, H, I, G, seed=seed)
+    x = synth.activations(M, H, seed=seed + 1)
+    g = torch.Generator().manual_seed(seed + 2)
+    idx = torch.stack([torch.randperm(E, generator=g)[:4] for _ in range(M)])
+    tw = torch.rand(M, 4, generator=g) + 0.05
+    return w, x, idx, (tw / tw.sum(1, keepdim=True)).float()
+
+
+def _b(t):
+    return t.view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("K,G", [(256, 32), (704, 128), (2816, 128)])
+def test_torch_cpu_dequant_bit_exact(K, G):
+    from oracle import torch_cpu
+    from hybridagent_amd import synth
+    p = synth.packed_int4((24, K), seed=5)
+    s = synth.group_scales((24, K), G, seed=6)
+    got = torch_cpu.dequantize(p, s, G)
+    assert np.array_equal(_b(got), to_bf16_bits(oracle.dequantize(p.numpy(), _b(s), G)))
+
+
+def test_torch_cpu_linear4bit_vs_oracle():
+    from oracle import torch_cpu
+    from hybridagent_amd import synth
+    x = synth.activations(16, 704, seed=7)
+    p = synth.packed_int4((96, 704), seed=8)
+    s = synth.group_scales((96, 704), 128, seed=9)
+    b = synth.activations(1, 96, seed=10)[0]
+    got = torch_cpu.linear4bit(x, p, s, 128, b)
+    ref = oracle.linear(x.float().numpy(), p.numpy(), _b(s), 128, bias=b.float().numpy())
+    assert oracle.max_abs_rel(got.float().numpy(), ref) <= 1e-2
+
+
+@pytest.mark.parametrize("M", [1, 9])
+def test_torch_cpu_experts_vs_oracle(M):
+    # M == 1: the single-token path (quantization.py:241-263); M > 1 the loop
+    from oracle import torch_cpu
+    w, x, idx, tw = _ref_inputs(M)
+    got = torch_cpu.experts(x, idx, tw, w.gate_up_packed, w.gate_up_scale, w.down_packed, w.down_scale, 32)
+    path = "fused" if M == 1 else "loop"
+    ref = oracle.moe_forward(x.float().numpy(), idx.numpy(), tw.numpy(), w.gate_up_packed.numpy(),
+                             _b(w.gate_up_scale), w.down_packed.numpy(), _b(w.down_scale), 32, path=path)
+    assert oracle.max_abs_rel(got.float().numpy(), ref) <= 1e-2
+
+
+def test_torch_cpu_router_vs_oracle():
+    from oracle import torch_cpu
+    from hybridagent_amd import synth
+    rw = synth.router_weights(64, 512, seed=11)
+    h = synth.activations(200, 512, seed=12)
+    tw, ti, lg = torch_cpu.router(h, rw.scale, rw.scalar_root, rw.proj, rw.per_expert_scale, rw.eps, 8)
+    ref_lg, ref_idx, ref_w = oracle.router(h.float().numpy(), rw.scale.float().numpy(), rw.scalar_root,
+                                           rw.proj.float().numpy(), rw.per_expert_scale.float().numpy(),
+                                           rw.eps, 8)
+    assert _ulp_diff_bf16(lg.float().numpy(), ref_lg).max() <= 1
+    # torch.topk's tie order is its own: compare index sets where no tie
+    # touches the boundary, and the weights of those rows
+    srt = -np.sort(-ref_lg, 1)
+    ok = (srt[:, 7] > srt[:, 8]) & (np.abs(lg.float().numpy() - ref_lg).max(1) == 0)
+    assert ok.mean() > 0.5
+    assert np.array_equal(np.sort(ti.numpy()[ok], 1), np.sort(ref_idx[ok], 1))
