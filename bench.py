@@ -37,6 +37,8 @@ group size 32, the released checkpoints'.
 ``cpu_baseline`` times the torch-CPU restatement of the reference's CPU path
 (``oracle/torch_cpu.py``) on this host's cores: one decode layer at each M of
 the sweep, and configs[0] (the dense W4A16 linear at M = 16).
+``ffn_block`` times the whole post-attention FFN block (backends.py:77-126:
+norms, shared bf16 MLP, router, experts) per decoder layer at M = 1 and 32.
 ``latent`` is BASELINE configs[4] (30 MoE layers + HybridLink per step, batch
 32); ``hybridlink`` times the HybridLink map alone at that batch (weights
 rotated through HBM).
@@ -442,6 +444,57 @@ def cpu_baseline(budget_s: float):
                               "gbps": b0 / t0 / 1e9, "gflops": f0 / t0 / 1e9}}
 
 
+FFN_IM = 2112  # shared-MLP intermediate size assumed for Gemma-4-26B-A4B (config.json absent)
+FFN_MS = (1, 32)
+
+
+class FfnLayer:
+    """One decoder layer's FFN-block weights: norms, shared bf16 MLP, router, experts."""
+
+    def __init__(self, seed: int, dev):
+        g = torch.Generator(device=dev).manual_seed(seed)
+        nrm = lambda: (1 + 0.1 * torch.randn(H, generator=g, device=dev)).to(torch.bfloat16)
+        lin = lambda o, i: (torch.randn(o, i, generator=g, device=dev) / math.sqrt(i)).to(torch.bfloat16)
+        self.moe = Layer(seed, dev)
+        rw, ew = self.moe.rw, self.moe.ew
+        self.args = dict(post_attn_ln_w=nrm(), pre_ff_ln_w=nrm(), mlp_gate_w=lin(FFN_IM, H),
+                         mlp_up_w=lin(FFN_IM, H), mlp_down_w=lin(H, FFN_IM), post_ff_ln1_w=nrm(),
+                         router_scale=rw.scale, router_scalar_root=rw.scalar_root, router_proj_w=rw.proj,
+                         router_per_expert_scale=rw.per_expert_scale, pre_ff_ln2_w=nrm(),
+                         gu_packed=ew.gate_up_packed, gu_scale=ew.gate_up_scale, dn_packed=ew.down_packed,
+                         dn_scale=ew.down_scale, post_ff_ln2_w=nrm(), post_ff_ln_w=nrm(),
+                         layer_scalar=torch.ones(1, dtype=torch.bfloat16, device=dev), eps=1e-6, top_k=TOPK)
+
+    def forward(self, residual, attn_out):
+        return _lib.ffn_block(residual, attn_out, **self.args, group_size=G)
+
+
+def ffn_leg(dev, steps, warmup, n_layers):
+    """The whole post-attention FFN block (backends.py:77-126) per decoder layer at
+    decode sizes, cycling through ``n_layers`` independent layer copies (HBM-cold).
+    Bytes per call: shared MLP weights 3 * Im * H * 2, the U routed experts,
+    router weights, seven norm weights, residual + attn_out in and the output."""
+    layers = [FfnLayer(seed=600 + 13 * i, dev=dev) for i in range(n_layers)]
+    torch.cuda.synchronize()
+    out = {}
+    for M in FFN_MS:
+        res = synth.activations(M, H, seed=6100 + M, device=dev)
+        att = synth.activations(M, H, seed=6200 + M, device=dev)
+        uniq = []
+        for ly in layers:
+            _, idx = ly.moe.route(res)
+            uniq.append(int(torch.unique(idx).numel()))
+        U = sum(uniq) / len(uniq)
+        t = time_graph(lambda: [ly.forward(res, att) for ly in layers], len(layers), steps, warmup)
+        nbytes = (3 * FFN_IM * H * 2 + U * EXPERT_BYTES + ROUTER_BYTES + 7 * H * 2 + 3 * M * H * 2)
+        out[str(M)] = {"us": t * 1e6, "unique_experts": U, "bytes": nbytes, "gbps": nbytes / t / 1e9,
+                       "frac_hbm": nbytes / t / 1e9 / PEAK_HBM_GBS, "shared_mlp_intermediate": FFN_IM}
+        log(f"ffn block M={M}: {t*1e6:.1f} us/layer, U={U:.1f}, {nbytes / t / 1e9:.0f} GB/s")
+    del layers
+    torch.cuda.empty_cache()
+    return out
+
+
 def _rounded(v):
     """Floats rounded to 4 decimals, recursively (None passes through)."""
     if isinstance(v, float):
@@ -486,6 +539,8 @@ def main(argv=None):
     ap.add_argument("--only-latent", action="store_true")
     ap.add_argument("--only-prefill", action="store_true",
                     help="time only the prefill layer (for rocprofv3 counter runs)")
+    ap.add_argument("--no-ffn", action="store_true", help="skip the FFN-block leg")
+    ap.add_argument("--only-ffn", action="store_true")
     ap.add_argument("--no-g32", action="store_true",
                     help="skip the group-size-32 leg (the released checkpoints' group size)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -507,6 +562,9 @@ def main(argv=None):
     torch.manual_seed(0)
     if args.only_latent:
         print(json.dumps({"latent": latent(dev)}), flush=True)
+        return 0
+    if args.only_ffn:
+        print(json.dumps({"ffn_block": _rounded(ffn_leg(dev, args.steps, args.warmup, args.layers))}), flush=True)
         return 0
     if args.only_dense:
         print(json.dumps({"dense": dense_sweep(dev, args.steps, args.warmup)}), flush=True)
@@ -531,6 +589,7 @@ def main(argv=None):
 
     pre = None if args.no_prefill else prefill(dev, max(8, args.steps // 4), max(2, args.warmup // 4), 4)
     g32 = None if args.no_g32 else g32_leg(dev, args)
+    ffn = None if args.no_ffn else ffn_leg(dev, args.steps, args.warmup, args.layers)
 
     lat = None if args.no_latent else latent(dev)
     hl = None if args.no_latent else hybridlink_leg(dev)
@@ -575,6 +634,7 @@ def main(argv=None):
         "dense": None if dense is None else {c: {k: (round(v, 4) if isinstance(v, float) else v)
                                                  for k, v in d.items()} for c, d in dense.items()},
         "g32": _rounded(g32),
+        "ffn_block": _rounded(ffn),
         "cpu_baseline": _rounded(cpu),
     }
     print(json.dumps(result), flush=True)

@@ -50,6 +50,10 @@ SIGNATURES = {
     "moe_down": (ctypes.c_int, [_VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "moe_combine": (ctypes.c_int, [_VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "moe_layer_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
+    "moe_ffn_block_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64]),
+    "moe_ffn_block_forward": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _F32, _VP, _VP, _VP,
+                                             _VP, _VP, _VP, _VP, _VP, _VP, _VP, _F32, _VP, _I64, _I64, _I64,
+                                             _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "moe_layer_forward": (ctypes.c_int, [_VP, _VP, _F32, _VP, _VP, _F32, _VP, _VP, _VP, _VP, _VP, _VP,
                                          _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
 }
@@ -398,6 +402,66 @@ def moe_layer_forward(router_in: torch.Tensor, router_scale: torch.Tensor, scala
                                      0 if ws is None else ws.numel(), _stream(dev)),
                "moe_layer_forward")
     return out.reshape(*hidden_states.shape[:-1], H), w, idx
+
+
+def ffn_block(residual: torch.Tensor, attn_out: torch.Tensor, post_attn_ln_w: torch.Tensor,
+              pre_ff_ln_w: torch.Tensor, mlp_gate_w: torch.Tensor, mlp_up_w: torch.Tensor,
+              mlp_down_w: torch.Tensor, post_ff_ln1_w: torch.Tensor, router_scale: torch.Tensor,
+              router_scalar_root: float, router_proj_w: torch.Tensor, router_per_expert_scale: torch.Tensor,
+              pre_ff_ln2_w: torch.Tensor, gu_packed: torch.Tensor, gu_scale: torch.Tensor,
+              dn_packed: torch.Tensor, dn_scale: torch.Tensor, post_ff_ln2_w: torch.Tensor,
+              post_ff_ln_w: torch.Tensor, layer_scalar: torch.Tensor, eps: float, top_k: int,
+              group_size: int | None = None) -> torch.Tensor:
+    """The post-attention FFN block ``_ffn_moe_4bit_step`` (backends.py:77-126), same
+    arguments in the same order: residual / attn_out [..., H] bf16 -> [..., H] bf16."""
+    dense = (post_attn_ln_w, pre_ff_ln_w, mlp_gate_w, mlp_up_w, mlp_down_w, post_ff_ln1_w, router_scale,
+             router_proj_w, router_per_expert_scale, pre_ff_ln2_w, post_ff_ln2_w, post_ff_ln_w)
+    dev = _require_gpu(residual, attn_out, *dense, gu_packed, gu_scale, dn_packed, dn_scale, layer_scalar)
+    H = residual.shape[-1]
+    res = _bf16(residual, "residual").reshape(-1, H)
+    att = _bf16(attn_out, "attn_out").reshape(-1, H)
+    if att.shape != res.shape:
+        raise ValueError("attn_out must have the shape of residual")
+    names = ("post_attention_layernorm", "pre_feedforward_layernorm", "mlp.gate_proj", "mlp.up_proj",
+             "mlp.down_proj", "post_feedforward_layernorm_1", "router.scale", "router.proj",
+             "router.per_expert_scale", "pre_feedforward_layernorm_2", "post_feedforward_layernorm_2",
+             "post_feedforward_layernorm")
+    dense = tuple(_bf16(t, n) for t, n in zip(dense, names))
+    (post_attn_ln_w, pre_ff_ln_w, mlp_gate_w, mlp_up_w, mlp_down_w, post_ff_ln1_w, router_scale,
+     router_proj_w, router_per_expert_scale, pre_ff_ln2_w, post_ff_ln2_w, post_ff_ln_w) = dense
+    # layer_scalar is a bf16 buffer once the model is loaded in bf16; other
+    # dtypes are rounded to it (the product is a bf16 tensor either way)
+    ls = layer_scalar.reshape(-1)[:1].to(torch.bfloat16).contiguous()
+    for t, n in ((post_attn_ln_w, names[0]), (pre_ff_ln_w, names[1]), (post_ff_ln1_w, names[5]),
+                 (router_scale, names[6]), (pre_ff_ln2_w, names[9]), (post_ff_ln2_w, names[10]),
+                 (post_ff_ln_w, names[11])):
+        if tuple(t.shape) != (H,):
+            raise ValueError(f"{n} weight must be [{H}]")
+    Im = mlp_gate_w.shape[0]
+    if tuple(mlp_gate_w.shape) != (Im, H) or tuple(mlp_up_w.shape) != (Im, H) or tuple(mlp_down_w.shape) != (H, Im):
+        raise ValueError("shared MLP weights must be gate/up [Im, H] and down [H, Im]")
+    gu_packed, dn_packed = _i32(gu_packed, "gate_up_packed"), _i32(dn_packed, "down_packed")
+    gu_scale, dn_scale = _bf16(gu_scale, "gate_up_scale"), _bf16(dn_scale, "down_scale")
+    E, two_i, h8 = gu_packed.shape
+    I = two_i // 2
+    if h8 * 8 != H or dn_packed.shape != (E, H, I // 8) or router_proj_w.shape != (E, H):
+        raise ValueError("router / expert weight shapes do not match the hidden size")
+    G = group_size or infer_group_size(H, gu_scale.shape[-1])
+    if gu_scale.shape != (E, two_i, -(-H // G)) or dn_scale.shape != (E, H, -(-I // G)):
+        raise ValueError(f"scale shapes do not match group size {G}")
+    M = res.shape[0]
+    out = torch.empty((M, H), dtype=torch.bfloat16, device=dev)
+    lib = load()
+    ws = _workspace(lib.moe_ffn_block_workspace_bytes(max(M, 1), top_k, E, H, I, Im), dev)
+    with torch.cuda.device(dev):
+        _check(lib.moe_ffn_block_forward(
+            _ptr(res), _ptr(att), _ptr(post_attn_ln_w), _ptr(pre_ff_ln_w), _ptr(mlp_gate_w), _ptr(mlp_up_w),
+            _ptr(mlp_down_w), _ptr(post_ff_ln1_w), _ptr(router_scale), float(router_scalar_root),
+            _ptr(router_proj_w), _ptr(router_per_expert_scale), _ptr(pre_ff_ln2_w), _ptr(gu_packed),
+            _ptr(gu_scale), _ptr(dn_packed), _ptr(dn_scale), _ptr(post_ff_ln2_w), _ptr(post_ff_ln_w), _ptr(ls),
+            float(eps), _ptr(out), M, int(top_k), E, H, I, Im, G, _ptr(ws), 0 if ws is None else ws.numel(),
+            _stream(dev)), "moe_ffn_block_forward")
+    return out.reshape(residual.shape)
 
 
 class MoEStages:

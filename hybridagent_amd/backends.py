@@ -85,6 +85,81 @@ def moe_router(
                           float(eps), int(top_k))
 
 
+def ffn_moe_4bit_step(
+    residual: torch.Tensor,
+    attn_out: torch.Tensor,
+    post_attn_ln_w: torch.Tensor,
+    pre_ff_ln_w: torch.Tensor,
+    mlp_gate_w: torch.Tensor,
+    mlp_up_w: torch.Tensor,
+    mlp_down_w: torch.Tensor,
+    post_ff_ln1_w: torch.Tensor,
+    router_scale: torch.Tensor,
+    router_scalar_root: float,
+    router_proj_w: torch.Tensor,
+    router_per_expert_scale: torch.Tensor,
+    pre_ff_ln2_w: torch.Tensor,
+    gu_packed: torch.Tensor,
+    gu_scale: torch.Tensor,
+    dn_packed: torch.Tensor,
+    dn_scale: torch.Tensor,
+    post_ff_ln2_w: torch.Tensor,
+    post_ff_ln_w: torch.Tensor,
+    layer_scalar: torch.Tensor,
+    eps: float,
+    top_k: int,
+) -> torch.Tensor:
+    """``_ffn_moe_4bit_step`` (backends.py:77-126) with the same 22 arguments: the
+    post-attention RMSNorm and residual, the shared bf16 MLP, the router, the
+    W4A16 experts, the four FFN RMSNorms and ``layer_scalar`` in one C-ABI call
+    (``moe_ffn_block_forward``: two row kernels, two shared-MLP linears and the
+    MoE layer's launches), no host synchronisation."""
+    return _lib.ffn_block(residual, attn_out, post_attn_ln_w, pre_ff_ln_w, mlp_gate_w, mlp_up_w, mlp_down_w,
+                          post_ff_ln1_w, router_scale, router_scalar_root, router_proj_w,
+                          router_per_expert_scale, pre_ff_ln2_w, gu_packed, gu_scale, dn_packed, dn_scale,
+                          post_ff_ln2_w, post_ff_ln_w, layer_scalar, eps, top_k)
+
+
+def patch_ffn_4bit(backbone: torch.nn.Module) -> int:
+    """Route every 4-bit MoE decoder layer's FFN block through ``ffn_moe_4bit_step``,
+    the counterpart of ``patch_compiled_ffn_4bit`` (backends.py:132-201): the layer
+    keeps its input RMSNorm and attention; everything after attention runs in
+    the HIP library.  Returns the number of layers patched."""
+    from .quantization import Gemma4TextExperts4Bit
+
+    text_model = getattr(backbone.model, "language_model", backbone.model)
+    patched = 0
+    for layer in getattr(text_model, "layers", []):
+        if not isinstance(getattr(layer, "experts", None), Gemma4TextExperts4Bit):
+            continue
+        eps = float(layer.input_layernorm.eps)
+        top_k = int(layer.router.config.top_k_experts)
+        scalar_root = float(layer.router.scalar_root_size)
+
+        def _make_layer_fwd(lyr, _eps=eps, _top_k=top_k, _sr=scalar_root):
+            def _fwd(hidden_states, per_layer_input=None, shared_kv_states=None, position_embeddings=None,
+                     attention_mask=None, position_ids=None, past_key_values=None, **kwargs):
+                residual = hidden_states
+                hidden_states = lyr.input_layernorm(hidden_states)
+                hidden_states, _ = lyr.self_attn(
+                    hidden_states=hidden_states, position_embeddings=position_embeddings,
+                    attention_mask=attention_mask, shared_kv_states=shared_kv_states,
+                    position_ids=position_ids, past_key_values=past_key_values, **kwargs)
+                return ffn_moe_4bit_step(
+                    residual, hidden_states, lyr.post_attention_layernorm.weight,
+                    lyr.pre_feedforward_layernorm.weight, lyr.mlp.gate_proj.weight, lyr.mlp.up_proj.weight,
+                    lyr.mlp.down_proj.weight, lyr.post_feedforward_layernorm_1.weight, lyr.router.scale, _sr,
+                    lyr.router.proj.weight, lyr.router.per_expert_scale, lyr.pre_feedforward_layernorm_2.weight,
+                    lyr.experts.gate_up_packed, lyr.experts.gate_up_scale, lyr.experts.down_packed,
+                    lyr.experts.down_scale, lyr.post_feedforward_layernorm_2.weight,
+                    lyr.post_feedforward_layernorm.weight, lyr.layer_scalar, _eps, _top_k)
+            return _fwd
+
+        layer.forward = _make_layer_fwd(layer)
+        patched += 1
+    return patched
+
+
 def moe_block(residual: torch.Tensor, h2_in: torch.Tensor, router, experts) -> torch.Tensor:
     """Router on ``residual`` + experts on ``h2_in`` (backends.py:111-122):
     ``router`` is a Gemma4TextRouter-like module (``scale``, ``proj``,

@@ -179,7 +179,7 @@ int w4a16_hybridlink(const uint16_t* h, const uint16_t* ln1_w, const uint16_t* l
                      uint16_t* out, int64_t B, int64_t H, float eps, void* workspace,
                      size_t workspace_bytes, void* stream) {
   // LayerNorm: one 256-thread workgroup per row; the linears: grid.y = ceil(B / 64) <= 65535
-  if (B < 0 || B > kMaxHybridLinkRows || H <= 0 || H % 32 != 0 || H > 3072) return W4A16_ERR_SHAPE;
+  if (B < 0 || B > kMaxHybridLinkRows || H <= 0 || H % 32 != 0 || H > 8192) return W4A16_ERR_SHAPE;
   if (B == 0) return W4A16_OK;
   if (!h || !ln1_w || !ln1_b || !p1_w || !p1_b || !p2_w || !p2_b || !ln2_w || !ln2_b || !out)
     return W4A16_ERR_NULL;
@@ -194,8 +194,8 @@ int w4a16_hybridlink(const uint16_t* h, const uint16_t* ln1_w, const uint16_t* l
   uint16_t* t0 = c.take<uint16_t>(B * H);  // pre_ln(h), later h + proj2(...)
   uint16_t* t1 = c.take<uint16_t>(B * H);  // GELU(proj1(...))
   hipError_t e = launch_layer_norm(h, ln1_w, ln1_b, t0, B, (int)H, eps, s);
-  if (e == hipSuccess) e = launch_linear_bf16(kLinGelu, t0, p1_w, p1_b, nullptr, t1, B, (int)H, (int)H, s);
-  if (e == hipSuccess) e = launch_linear_bf16(kLinResidual, t1, p2_w, p2_b, h, t0, B, (int)H, (int)H, s);
+  if (e == hipSuccess) e = launch_linear_bf16(kLinGelu, t0, p1_w, nullptr, p1_b, nullptr, t1, B, (int)H, (int)H, s);
+  if (e == hipSuccess) e = launch_linear_bf16(kLinResidual, t1, p2_w, nullptr, p2_b, h, t0, B, (int)H, (int)H, s);
   if (e == hipSuccess) e = launch_layer_norm(t0, ln2_w, ln2_b, out, B, (int)H, eps, s);
   return launch_status(e);
 }
@@ -539,6 +539,107 @@ int moe_forward(const uint16_t* hidden, const int64_t* topk_idx, const float* to
     st = moe_combine(topk_idx, topk_w, out, M, top_k, E, H, I, workspace, workspace_bytes,
                      stream);
   return st;
+}
+
+}  // extern "C"
+
+namespace {
+
+// The FFN block's workspace: its row buffers, the routing, then the MoE
+// layer's workspace.
+struct FfnLayout {
+  uint16_t* res;    // residual + rms_norm(attn_out)
+  uint16_t* h_ff;   // shared-MLP input
+  uint16_t* h2_in;  // experts' input
+  uint16_t* inter;  // shared-MLP intermediate [M, Im]
+  uint16_t* h_mlp;  // shared-MLP output
+  uint16_t* moe;    // experts' output
+  int64_t* idx;
+  float* w;
+  void* moe_ws;
+  size_t moe_bytes;
+  size_t bytes;
+};
+
+FfnLayout ffn_layout(void* ws, int64_t M, int64_t k, int64_t E, int64_t H, int64_t I, int64_t Im) {
+  Carve c(ws);
+  FfnLayout L;
+  L.res = c.take<uint16_t>(M * H);
+  L.h_ff = c.take<uint16_t>(M * H);
+  L.h2_in = c.take<uint16_t>(M * H);
+  L.inter = c.take<uint16_t>(M * Im);
+  L.h_mlp = c.take<uint16_t>(M * H);
+  L.moe = c.take<uint16_t>(M * H);
+  L.idx = c.take<int64_t>(M * k);
+  L.w = c.take<float>(M * k);
+  L.moe_bytes = moe_layer_workspace_bytes(M, k, E, H, I);
+  L.moe_ws = c.take<unsigned char>(L.moe_bytes);
+  L.bytes = c.used;
+  return L;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t moe_ffn_block_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I,
+                                     int64_t Im) {
+  if (M <= 0 || top_k <= 0 || E <= 0 || H <= 0 || I <= 0 || Im <= 0) return 0;
+  return ffn_layout(nullptr, M, top_k, E, H, I, Im).bytes;
+}
+
+int moe_ffn_block_forward(const uint16_t* residual, const uint16_t* attn_out,
+                          const uint16_t* post_attn_ln_w, const uint16_t* pre_ff_ln_w,
+                          const uint16_t* mlp_gate_w, const uint16_t* mlp_up_w,
+                          const uint16_t* mlp_down_w, const uint16_t* post_ff_ln1_w,
+                          const uint16_t* router_scale, float router_scalar_root,
+                          const uint16_t* router_proj_w, const uint16_t* router_per_expert_scale,
+                          const uint16_t* pre_ff_ln2_w, const int32_t* gu_packed,
+                          const uint16_t* gu_scale, const int32_t* dn_packed,
+                          const uint16_t* dn_scale, const uint16_t* post_ff_ln2_w,
+                          const uint16_t* post_ff_ln_w, const uint16_t* layer_scalar, float eps,
+                          uint16_t* out, int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I,
+                          int64_t Im, int64_t group_size, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  // row kernels: H <= 8192, one workgroup per row; shared-MLP linears:
+  // K % 32 == 0 and ceil(M / 64) <= 65535 row tiles
+  if (M < 0 || M > kMaxHybridLinkRows || top_k <= 0 || top_k > E || H <= 0 || H % 32 != 0 || H > 8192 ||
+      Im <= 0 || Im % 32 != 0 || Im > (1 << 16))
+    return W4A16_ERR_SHAPE;
+  MoeLayout none{};
+  int st = moe_check(M, top_k, E, H, I, group_size, nullptr, 0, &none);
+  if (st != W4A16_OK && st != W4A16_ERR_WORKSPACE) return st;
+  if (M == 0) return W4A16_OK;
+  if (!residual || !attn_out || !post_attn_ln_w || !pre_ff_ln_w || !mlp_gate_w || !mlp_up_w ||
+      !mlp_down_w || !post_ff_ln1_w || !router_scale || !router_proj_w || !router_per_expert_scale ||
+      !pre_ff_ln2_w || !gu_packed || !gu_scale || !dn_packed || !dn_scale || !post_ff_ln2_w ||
+      !post_ff_ln_w || !layer_scalar || !out)
+    return W4A16_ERR_NULL;
+  const void* a16[] = {residual, attn_out, post_attn_ln_w, pre_ff_ln_w, mlp_gate_w, mlp_up_w,
+                       mlp_down_w, post_ff_ln1_w, router_scale, router_proj_w, pre_ff_ln2_w,
+                       gu_packed, dn_packed, post_ff_ln2_w, post_ff_ln_w, out};
+  for (const void* p : a16)
+    if (!aligned16(p)) return W4A16_ERR_ALIGN;
+  if (workspace == nullptr || workspace_bytes < moe_ffn_block_workspace_bytes(M, top_k, E, H, I, Im))
+    return W4A16_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return W4A16_ERR_ALIGN;
+  const FfnLayout L = ffn_layout(workspace, M, top_k, E, H, I, Im);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = launch_ffn_pre(attn_out, residual, post_attn_ln_w, pre_ff_ln_w, pre_ff_ln2_w, L.res,
+                                L.h_ff, L.h2_in, M, (int)H, eps, s);
+  if (e == hipSuccess)
+    e = launch_linear_bf16(kLinGateUp, L.h_ff, mlp_gate_w, mlp_up_w, nullptr, nullptr, L.inter, M, (int)Im,
+                           (int)H, s);
+  if (e == hipSuccess)
+    e = launch_linear_bf16(kLinPlain, L.inter, mlp_down_w, nullptr, nullptr, nullptr, L.h_mlp, M, (int)H,
+                           (int)Im, s);
+  if (e != hipSuccess) return W4A16_ERR_LAUNCH;
+  st = moe_layer_forward(L.res, router_scale, router_scalar_root, router_proj_w, router_per_expert_scale,
+                         eps, L.h2_in, gu_packed, gu_scale, dn_packed, dn_scale, L.moe, L.idx, L.w, M,
+                         top_k, E, H, I, group_size, L.moe_ws, L.moe_bytes, stream);
+  if (st != W4A16_OK) return st;
+  return launch_status(launch_ffn_post(L.h_mlp, L.moe, L.res, post_ff_ln1_w, post_ff_ln2_w, post_ff_ln_w,
+                                       layer_scalar, out, M, (int)H, eps, s));
 }
 
 }  // extern "C"

@@ -110,17 +110,33 @@ hipError_t launch_router_topk(const float* partial, int ksplit, const uint16_t* 
                               const uint16_t* per_expert_scale, uint16_t* logits_out,
                               int64_t* idx, float* w, int M, int E, int topk, hipStream_t s);
 // HybridLink pieces (kernels_hybridlink.hip): nn.LayerNorm with bf16 affine
-// parameters (H % 8 == 0, H <= 8192) and the bf16-weight linear for small
-// batches (K % 32 == 0, K <= 3072: at most 12 k steps of 32 per wavefront)
-// with a fused epilogue:
-//   kLinGelu      out = bf16(GELU_erf(bf16(x W^T + b)))
-//   kLinResidual  out = bf16(res + bf16(x W^T + b))
-enum LinearEpilogue { kLinGelu = 0, kLinResidual = 1 };
+// parameters (H % 8 == 0, H <= 8192)
 hipError_t launch_layer_norm(const uint16_t* x, const uint16_t* w, const uint16_t* b, uint16_t* y,
                              int64_t M, int H, float eps, hipStream_t s);
-hipError_t launch_linear_bf16(int epi, const uint16_t* x, const uint16_t* W, const uint16_t* bias,
-                              const uint16_t* res, uint16_t* out, int64_t M, int N, int K,
-                              hipStream_t s);
+// bf16-weight linear for small batches (kernels_linear_bf16.hip), K % 32 ==
+// 0, with a fused epilogue:
+//   kLinGelu      out = bf16(GELU_erf(bf16(x W^T + b)))
+//   kLinResidual  out = bf16(res + bf16(x W^T + b))
+//   kLinGateUp    out = bf16(bf16(gelu_tanh(bf16(x W^T))) * bf16(x W2^T))
+//   kLinPlain     out = bf16(x W^T)
+// M rows in tiles of up to 64 (ceil(M / 64) <= 65535).
+enum LinearEpilogue { kLinGelu = 0, kLinResidual = 1, kLinGateUp = 2, kLinPlain = 3 };
+hipError_t launch_linear_bf16(int epi, const uint16_t* x, const uint16_t* W, const uint16_t* W2,
+                              const uint16_t* bias, const uint16_t* res, uint16_t* out, int64_t M, int N,
+                              int K, hipStream_t s);
+// FFN block row kernels (kernels_ffn.hip), one workgroup per row, H % 8 == 0,
+// H <= 8192:
+//   pre : h = rms(attn) * w_pa; res_out = bf16(res + h);
+//         h_ff = rms(res_out) * w_pf; h2_in = rms(res_out) * w_pf2
+//   post: h1 = rms(mlp) * w1; h2 = rms(moe) * w2; c = rms(bf16(h1 + h2)) * w3;
+//         out = bf16(bf16(res + c) * layer_scalar)
+hipError_t launch_ffn_pre(const uint16_t* attn, const uint16_t* res, const uint16_t* w_pa,
+                          const uint16_t* w_pf, const uint16_t* w_pf2, uint16_t* res_out, uint16_t* h_ff,
+                          uint16_t* h2_in, int64_t M, int H, float eps, hipStream_t s);
+hipError_t launch_ffn_post(const uint16_t* mlp, const uint16_t* moe, const uint16_t* res,
+                           const uint16_t* w1, const uint16_t* w2, const uint16_t* w3,
+                           const uint16_t* layer_scalar, uint16_t* out, int64_t M, int H, float eps,
+                           hipStream_t s);
 // prefill grouped GEMM: one launch per stage, items = (m-tile, n-tile)
 hipError_t launch_prefill(int mode, PrefillArgs a, int max_mtiles, hipStream_t s);
 // the bias-form prefill GEMM (group size a multiple of 128) and the pass that

@@ -92,7 +92,7 @@ W4A16_API int w4a16_add_rms_norm(const uint16_t* h, const uint16_t* delta, const
  * LayerNorm: fp32 mean and variance, (x - mean) * rsqrt(var + eps) * w + b,
  * bf16 out (nn.LayerNorm, eps = 1e-5 in the reference module).
  * h, out [B, H] bf16; ln*_w, ln*_b, p*_b [H] bf16; p1_w, p2_w [H, H] bf16
- * (nn.Linear layout, out x in).  H % 32 == 0, H <= 3072; 16-byte aligned
+ * (nn.Linear layout, out x in).  H % 32 == 0, H <= 8192; 16-byte aligned
  * h, out, weights, LayerNorm parameters and workspace.                     */
 W4A16_API size_t w4a16_hybridlink_workspace_bytes(int64_t B, int64_t H);
 W4A16_API int w4a16_hybridlink(const uint16_t* h, const uint16_t* ln1_w, const uint16_t* ln1_b,
@@ -209,6 +209,39 @@ W4A16_API int moe_layer_forward(const uint16_t* router_in, const uint16_t* route
                       int64_t* topk_idx, float* topk_w, int64_t M, int64_t top_k, int64_t E,
                       int64_t H, int64_t I, int64_t group_size, void* workspace,
                       size_t workspace_bytes, void* stream);
+
+/* The post-attention FFN block of a Gemma-4 MoE decoder layer,
+ * _ffn_moe_4bit_step  -- backends.py:77-126 (installed per layer by
+ * patch_compiled_ffn_4bit, backends.py:132-201):
+ *   h      = rms_norm(attn_out) * post_attn_ln_w;  res = residual + h
+ *   h_ff   = rms_norm(res) * pre_ff_ln_w
+ *   h_mlp  = down(gelu_tanh(gate(h_ff)) * up(h_ff))        (shared bf16 MLP)
+ *   h_1    = rms_norm(h_mlp) * post_ff_ln1_w
+ *   router on res (moe_router_topk semantics), experts on
+ *   h2_in  = rms_norm(res) * pre_ff_ln2_w (moe_forward semantics)
+ *   h_2    = rms_norm(moe_out) * post_ff_ln2_w
+ *   h_comb = rms_norm(h_1 + h_2) * post_ff_ln_w
+ *   out    = (res + h_comb) * layer_scalar
+ * bf16 rounding after every op (the eager torch ops' rounding points).
+ * residual, attn_out, out [M, H] bf16; the norm weights [H] bf16;
+ * mlp_gate_w, mlp_up_w [Im, H], mlp_down_w [H, Im] bf16 (nn.Linear layout);
+ * router and expert tensors as for moe_layer_forward; layer_scalar: one bf16
+ * value in device memory.  H % 32 == 0, H <= 8192, Im % 32 == 0.          */
+W4A16_API size_t moe_ffn_block_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t H,
+                                               int64_t I, int64_t Im);
+W4A16_API int moe_ffn_block_forward(const uint16_t* residual, const uint16_t* attn_out,
+                          const uint16_t* post_attn_ln_w, const uint16_t* pre_ff_ln_w,
+                          const uint16_t* mlp_gate_w, const uint16_t* mlp_up_w,
+                          const uint16_t* mlp_down_w, const uint16_t* post_ff_ln1_w,
+                          const uint16_t* router_scale, float router_scalar_root,
+                          const uint16_t* router_proj_w, const uint16_t* router_per_expert_scale,
+                          const uint16_t* pre_ff_ln2_w, const int32_t* gu_packed,
+                          const uint16_t* gu_scale, const int32_t* dn_packed,
+                          const uint16_t* dn_scale, const uint16_t* post_ff_ln2_w,
+                          const uint16_t* post_ff_ln_w, const uint16_t* layer_scalar, float eps,
+                          uint16_t* out, int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I,
+                          int64_t Im, int64_t group_size, void* workspace, size_t workspace_bytes,
+                          void* stream);
 
 #ifdef __cplusplus
 }

@@ -21,7 +21,8 @@ Restated from (``hybrid_agent/`` in the reference repository):
                          bf16 index_add_);
 * ``router``             backends.py:111-117 (RMSNorm * scale * scalar_root,
                          F.linear logits, fp32 softmax, top-k, renormalise,
-                         per_expert_scale).
+                         per_expert_scale);
+* ``ffn_block``          backends.py:101-126 (_ffn_moe_4bit_step in eager ops).
 
 All tensors are CPU torch tensors in the reference's dtypes (bf16
 activations and scales, int32 packed weights, fp32 routing weights).
@@ -118,3 +119,27 @@ def router(h: torch.Tensor, scale: torch.Tensor, scalar_root: float, proj_w: tor
     tw = tw / tw.sum(dim=-1, keepdim=True)
     tw = tw * per_expert_scale[ti]
     return tw, ti, scores
+
+
+def ffn_block(residual, attn_out, post_attn_ln_w, pre_ff_ln_w, mlp_gate_w, mlp_up_w, mlp_down_w,
+              post_ff_ln1_w, router_scale, router_scalar_root, router_proj_w, router_per_expert_scale,
+              pre_ff_ln2_w, gu_packed, gu_scale, dn_packed, dn_scale, post_ff_ln2_w, post_ff_ln_w,
+              layer_scalar, eps, top_k, G):
+    """_ffn_moe_4bit_step (backends.py:101-126) in eager torch CPU ops, the 4-bit
+    experts on the reference CPU path (``experts`` above)."""
+    D = residual.shape[-1]
+    h = F.rms_norm(attn_out, (D,), post_attn_ln_w, eps)
+    residual = residual + h
+    h_ff = F.rms_norm(residual, (D,), pre_ff_ln_w, eps)
+    gate = F.gelu(F.linear(h_ff, mlp_gate_w), approximate="tanh")
+    up = F.linear(h_ff, mlp_up_w)
+    h_mlp = F.linear(gate * up, mlp_down_w)
+    h_1 = F.rms_norm(h_mlp, (D,), post_ff_ln1_w, eps)
+    h_flat = residual.reshape(-1, D)
+    tw, ti, _ = router(h_flat, router_scale, router_scalar_root, router_proj_w, router_per_expert_scale, eps,
+                       top_k)
+    h_2_in = F.rms_norm(h_flat, (D,), pre_ff_ln2_w, eps)
+    h_2 = experts(h_2_in, ti, tw, gu_packed, gu_scale, dn_packed, dn_scale, G).reshape(residual.shape)
+    h_2 = F.rms_norm(h_2, (D,), post_ff_ln2_w, eps)
+    h_comb = F.rms_norm(h_1 + h_2, (D,), post_ff_ln_w, eps)
+    return (residual + h_comb) * layer_scalar

@@ -43,6 +43,10 @@ Pinning (what checks this restatement, see ``tests/test_oracle.py``):
   linearity of the combine in the routing weights.
 * ``hybridlink`` / ``rms_norm`` (config-4 harness only): torch ``nn.LayerNorm``,
   ``nn.GELU``, ``nn.Linear`` on identical inputs.
+* ``ffn_block``: the same lines of ``_ffn_moe_4bit_step`` written with torch CPU
+  ``F.rms_norm`` / ``F.linear`` / ``F.gelu`` / ``softmax`` + ``topk`` and the
+  torch-CPU experts (``oracle/torch_cpu.py``) on identical inputs; a
+  ``layer_scalar`` of 2 doubles the output exactly.
 
 The reference ships no golden vectors or known-answer tests for this path, so
 no reference-produced fixture pins any function; the checks above are the
@@ -60,7 +64,7 @@ __all__ = [
     "pack_int4", "unpack_int4", "dequantize", "linear", "gelu_tanh",
     "rms_norm", "router_logits", "topk_from_logits", "router",
     "sort_permute", "moe_forward", "max_abs_rel", "hybridlink",
-    "layer_norm", "gelu_erf",
+    "layer_norm", "gelu_erf", "ffn_block",
 ]
 
 
@@ -215,6 +219,42 @@ def layer_norm(x, weight, bias, eps: float = 1e-5) -> np.ndarray:
     mu = x.mean(-1, keepdims=True, dtype=np.float32)
     var = ((x - mu) ** 2).mean(-1, keepdims=True, dtype=np.float32)
     return (x - mu) / np.sqrt(var + np.float32(eps)) * weight + bias
+
+
+def ffn_block(residual, attn_out, post_attn_ln_w, pre_ff_ln_w, mlp_gate_w, mlp_up_w, mlp_down_w,
+              post_ff_ln1_w, router_scale, router_scalar_root, router_proj_w, router_per_expert_scale,
+              pre_ff_ln2_w, gu_packed, gu_scale, dn_packed, dn_scale, post_ff_ln2_w, post_ff_ln_w,
+              layer_scalar, eps, top_k, G, return_routing: bool = False):
+    """The post-attention FFN block ``_ffn_moe_4bit_step`` (backends.py:101-126), bf16
+    rounding after every op as the eager torch ops round:
+
+    * h = rms_norm(attn_out) * w; residual = bf16(residual + h)         (:102-103)
+    * shared MLP: down(bf16(bf16(gelu_tanh(gate(h_ff))) * up(h_ff)))  (:105-108)
+    * h_1 = rms_norm(h_mlp, post_ff_ln1)                                (:109)
+    * router on the residual, MoE on rms_norm(residual, pre_ff_ln2)     (:111-122)
+    * h_2 = rms_norm(moe_out, post_ff_ln2); h_comb = rms_norm(bf16(h_1 + h_2), post_ff_ln)
+    * out = bf16(bf16(residual + h_comb) * layer_scalar)               (:123-126)
+
+    Dense weights are bf16 values [out, in] (nn.Linear layout); ``layer_scalar``
+    is one bf16 value.  Inputs/outputs are bf16 values held as float32.
+    """
+    h = rms_norm(attn_out, post_attn_ln_w, eps)
+    res = bf16_round(np.asarray(residual, np.float32) + h)
+    h_ff = rms_norm(res, pre_ff_ln_w, eps)
+    gate = gelu_tanh(_matmul_bf16(h_ff, mlp_gate_w))
+    up = _matmul_bf16(h_ff, mlp_up_w)
+    h_mlp = _matmul_bf16(bf16_round(gate * up), mlp_down_w)
+    h_1 = rms_norm(h_mlp, post_ff_ln1_w, eps)
+    _, idx, w = router(res, router_scale, router_scalar_root, router_proj_w, router_per_expert_scale, eps,
+                       top_k)
+    h_2_in = rms_norm(res, pre_ff_ln2_w, eps)
+    h_2 = moe_forward(h_2_in, idx, w, gu_packed, gu_scale, dn_packed, dn_scale, G)
+    h_2 = rms_norm(h_2, post_ff_ln2_w, eps)
+    h_comb = rms_norm(bf16_round(h_1 + h_2), post_ff_ln_w, eps)
+    out = bf16_round(bf16_round(res + h_comb) * np.float32(layer_scalar))
+    if return_routing:
+        return out, idx, w
+    return out
 
 
 def hybridlink(h, p1w, p1b, p2w, p2b, ln1w, ln1b, ln2w, ln2b) -> np.ndarray:

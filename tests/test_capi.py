@@ -82,7 +82,7 @@ def test_hybridlink_host_validation(lib):
     assert need >= 2 * 32 * 2816 * 2
     f = lib.w4a16_hybridlink
     assert f(*p, fake, 32, 2800, 1e-5, fake, need, NULL) == 2      # H % 32
-    assert f(*p, fake, 32, 4096, 1e-5, fake, need, NULL) == 2      # H > 3072
+    assert f(*p, fake, 32, 8224, 1e-5, fake, need, NULL) == 2      # H > 8192
     assert f(*p[:8], NULL, fake, 32, 2816, 1e-5, fake, need, NULL) == 1   # post_ln bias missing
     assert f(*p, fake, 32, 2816, 1e-5, fake, need - 1, NULL) == 5  # workspace too small
     assert f(ctypes.c_void_p(4098), *p[1:], fake, 32, 2816, 1e-5, fake, need, NULL) == 4

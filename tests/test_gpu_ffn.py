@@ -1,0 +1,185 @@
+"""The post-attention FFN block (backends.py:77-126, installed per layer by
+backends.py:132-201) on the GPU: ``moe_ffn_block_forward`` through the C ABI
+against the oracle, and the installer against transformers' own
+``Gemma4TextDecoderLayer.forward`` (the layer whose FFN half the reference's
+compiled step replaces).
+
+The oracle routes on its own residual; a row whose 8th and 9th router logits
+lie within two bf16 ulps may legitimately pick the other expert (one ulp of
+fp32 reduction order), which changes that row's MoE output entirely, so
+those rows are reported and left out of the tolerance check.
+"""
+import math
+import types
+from unittest import mock
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from hybridagent_amd import _lib, synth
+from hybridagent_amd import backends
+from hybridagent_amd import quantization as q
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _bits(t):
+    return t.detach().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.fixture(scope="module")
+def dev():
+    assert _lib.available(), "libw4a16moe.so must be built"
+    return torch.device("cuda:0")
+
+
+def _block_inputs(M, H, I, Im, E, G, seed, dev, layer_scalar=1.0):
+    g = torch.Generator().manual_seed(seed)
+    nrm = lambda: (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16).to(dev)
+    lin = lambda o, i: (torch.randn(o, i, generator=g) / math.sqrt(i)).to(torch.bfloat16).to(dev)
+    w = synth.moe_weights(E, H, I, G, seed=seed + 1, device=dev)
+    rw = synth.router_weights(E, H, seed=seed + 2, device=dev)
+    return dict(
+        residual=synth.activations(M, H, seed=seed + 3, device=dev),
+        attn_out=synth.activations(M, H, seed=seed + 4, device=dev),
+        post_attn_ln_w=nrm(), pre_ff_ln_w=nrm(), mlp_gate_w=lin(Im, H), mlp_up_w=lin(Im, H),
+        mlp_down_w=lin(H, Im), post_ff_ln1_w=nrm(), router_scale=nrm(), router_scalar_root=H ** -0.5,
+        router_proj_w=rw.proj, router_per_expert_scale=rw.per_expert_scale, pre_ff_ln2_w=nrm(),
+        gu_packed=w.gate_up_packed, gu_scale=w.gate_up_scale, dn_packed=w.down_packed, dn_scale=w.down_scale,
+        post_ff_ln2_w=nrm(), post_ff_ln_w=nrm(),
+        layer_scalar=torch.tensor([layer_scalar], dtype=torch.bfloat16, device=dev), eps=1e-6)
+
+
+def _oracle_rows(a, rows, top_k, G):
+    conv = {}
+    for k, v in a.items():
+        if isinstance(v, torch.Tensor):
+            if v.dtype == torch.int32:
+                conv[k] = v.cpu().numpy()
+            elif k in ("gu_scale", "dn_scale"):
+                conv[k] = _bits(v)
+            elif k in ("residual", "attn_out"):
+                conv[k] = _np(v)[rows]
+            else:
+                conv[k] = _np(v)
+        else:
+            conv[k] = v
+    conv["layer_scalar"] = float(conv["layer_scalar"].reshape(-1)[0])
+    out = oracle.ffn_block(**conv, top_k=top_k, G=G)
+    # the oracle router's margin on those rows (residual as the oracle forms it)
+    res = oracle.bf16_round(conv["residual"] + oracle.rms_norm(conv["attn_out"], conv["post_attn_ln_w"], conv["eps"]))
+    lg = oracle.router_logits(res, conv["router_scale"], conv["router_scalar_root"], conv["router_proj_w"],
+                              conv["eps"])
+    srt = -np.sort(-lg, axis=1)
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(srt[:, top_k - 1]), 1e-30))) - 7)
+    clear = srt[:, top_k - 1] - srt[:, top_k] > 2 * ulp
+    return out, clear
+
+
+def _check(got, a, rows, top_k, G, what):
+    ref, clear = _oracle_rows(a, rows, top_k, G)
+    g = _np(got)[rows]
+    assert np.isfinite(g).all()
+    err = oracle.max_abs_rel(g[clear], ref[clear])
+    print(f"{what}: max_abs_rel={err:.2e} on {clear.sum()}/{len(rows)} rows with a clear routing margin")
+    assert clear.mean() >= 0.5
+    assert err <= TOL
+
+
+# Gemma-4-26B-A4B shape; the shared MLP's intermediate size (2112) is an
+# assumption: the checkpoint's config.json is not available here
+@pytest.mark.parametrize("M", [1, 32, 300])
+def test_ffn_block_gemma_shape(dev, M):
+    H, I, Im, E, K, G = 2816, 704, 2112, 128, 8, 128
+    a = _block_inputs(max(M, 8), H, I, Im, E, G, seed=2000 + M, dev=dev)
+    if M == 1:
+        # one token: the first of eight candidates whose routing margin is clear
+        _, clear = _oracle_rows(a, np.arange(8), K, G)
+        t = int(np.nonzero(clear)[0][0])
+        a = dict(a, residual=a["residual"][t:t + 1].contiguous(), attn_out=a["attn_out"][t:t + 1].contiguous())
+    out = backends.ffn_moe_4bit_step(**a, top_k=K)
+    assert out.dtype == torch.bfloat16 and tuple(out.shape) == (M, H)
+    rows = np.arange(M) if M <= 32 else np.r_[0:6, 150, M - 6:M]
+    _check(out, a, rows, K, G, f"ffn block M={M}")
+
+
+@pytest.mark.parametrize("G,ls", [(32, 0.5), (128, 2.0)])
+def test_ffn_block_small_shapes(dev, G, ls):
+    H, I, Im, E, K, M = 512, 192, 384, 16, 4, 5
+    a = _block_inputs(M, H, I, Im, E, G, seed=2100 + G, dev=dev, layer_scalar=ls)
+    out = backends.ffn_moe_4bit_step(**a, top_k=K)
+    _check(out, a, np.arange(M), K, G, f"ffn block G={G} layer_scalar={ls}")
+    # the block is row-independent: a sub-batch gives the same bits
+    sub = dict(a, residual=a["residual"][1:4], attn_out=a["attn_out"][1:4])
+    assert torch.equal(backends.ffn_moe_4bit_step(**sub, top_k=K), out[1:4])
+
+
+class _AttnStub(torch.nn.Module):
+    """Stands in for self-attention (attention is outside this path): a fixed
+    elementwise map of the normalised input."""
+
+    def forward(self, hidden_states, **kwargs):
+        return hidden_states * 0.5 + 0.25, None
+
+
+def test_patch_ffn_4bit_matches_hf_decoder_layer(dev):
+    pytest.importorskip("transformers.models.gemma4")
+    from transformers.models.gemma4 import configuration_gemma4 as c, modeling_gemma4 as mg
+    H, Im, E, I, K, G, M = 256, 320, 16, 128, 4, 32, 6
+    cfg = c.Gemma4TextConfig(hidden_size=H, intermediate_size=Im, num_hidden_layers=1, num_attention_heads=2,
+                             num_key_value_heads=1, head_dim=64, vocab_size=128, hidden_size_per_layer_input=0,
+                             enable_moe_block=True, num_experts=E, top_k_experts=K, moe_intermediate_size=I,
+                             layer_types=["full_attention"], max_position_embeddings=64)
+
+    class _Experts(q.Gemma4TextExperts4Bit):
+        def __init__(self, config):
+            super().__init__(config, group_size=G)
+
+    with mock.patch.object(mg, "Gemma4TextExperts", _Experts):
+        layer = mg.Gemma4TextDecoderLayer(cfg, 0)
+    assert isinstance(layer.experts, q.Gemma4TextExperts4Bit)
+    layer.self_attn = _AttnStub()
+    gen = torch.Generator().manual_seed(2200)
+    with torch.no_grad():
+        for name, p in layer.named_parameters():
+            if p.dim() == 1:
+                p.copy_(1 + 0.1 * torch.randn(p.shape, generator=gen))
+            else:
+                p.copy_(torch.randn(p.shape, generator=gen) / math.sqrt(p.shape[-1]))
+        w = synth.moe_weights(E, H, I, G, seed=2201)
+        for name in ("gate_up_packed", "gate_up_scale", "down_packed", "down_scale"):
+            getattr(layer.experts, name).copy_(getattr(w, name))
+        layer.layer_scalar.fill_(0.75)
+    layer = layer.to(device=dev, dtype=torch.bfloat16)
+    x = synth.activations(M, H, seed=2202, device=dev).reshape(1, M, H)
+    with torch.no_grad():
+        ref = layer(x)                      # transformers' decoder layer, our experts module inside
+        ref = ref[0] if isinstance(ref, tuple) else ref
+        backbone = types.SimpleNamespace(model=types.SimpleNamespace(language_model=types.SimpleNamespace(
+            layers=[layer])))
+        assert backends.patch_ffn_4bit(backbone) == 1
+        got = layer(x)
+        # the router's margin on the residual the layer routes on (rows whose
+        # k-th and (k+1)-th probabilities lie within two bf16 ulps may pick
+        # the other expert under either router)
+        res = x + layer.post_attention_layernorm(layer.self_attn(layer.input_layernorm(x))[0])
+        rt = layer.router
+        lg = rt.proj(rt.norm(res.reshape(-1, H)) * rt.scale * rt.scalar_root_size)
+    srt = -np.sort(-_np(lg), axis=1)
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(srt[:, K - 1]), 1e-30))) - 7)
+    clear = srt[:, K - 1] - srt[:, K] > 2 * ulp
+    assert got.shape == ref.shape and got.dtype == torch.bfloat16
+    g, r = _np(got).reshape(M, H), _np(ref).reshape(M, H)
+    assert np.isfinite(g).all() and clear.sum() >= M // 2
+    err = oracle.max_abs_rel(g[clear], r[clear])
+    print(f"patched layer vs transformers' Gemma4TextDecoderLayer: max_abs_rel={err:.2e} "
+          f"on {clear.sum()}/{M} rows with a clear routing margin")
+    assert err <= TOL

@@ -425,3 +425,55 @@ def test_torch_cpu_router_vs_oracle():
     ok = (srt[:, 7] > srt[:, 8]) & (np.abs(lg.float().numpy() - ref_lg).max(1) == 0)
     assert ok.mean() > 0.5
     assert np.array_equal(np.sort(ti.numpy()[ok], 1), np.sort(ref_idx[ok], 1))
+
+
+def _ffn_inputs(M, H=256, I=96, Im=160, E=8, G=32, seed=30):
+    from hybridagent_amd import synth
+    g = torch.Generator().manual_seed(seed)
+    nrm = lambda: (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16)
+    lin = lambda o, i: (torch.randn(o, i, generator=g) / math.sqrt(i)).to(torch.bfloat16)
+    w = synth.moe_weights(E, H, I, G, seed=seed + 1)
+    rw = synth.router_weights(E, H, seed=seed + 2)
+    args = dict(
+        residual=synth.activations(M, H, seed=seed + 3), attn_out=synth.activations(M, H, seed=seed + 4),
+        post_attn_ln_w=nrm(), pre_ff_ln_w=nrm(), mlp_gate_w=lin(Im, H), mlp_up_w=lin(Im, H),
+        mlp_down_w=lin(H, Im), post_ff_ln1_w=nrm(), router_scale=nrm(), router_scalar_root=H ** -0.5,
+        router_proj_w=rw.proj, router_per_expert_scale=rw.per_expert_scale, pre_ff_ln2_w=nrm(),
+        gu_packed=w.gate_up_packed, gu_scale=w.gate_up_scale, dn_packed=w.down_packed, dn_scale=w.down_scale,
+        post_ff_ln2_w=nrm(), post_ff_ln_w=nrm(), layer_scalar=torch.tensor([1.0], dtype=torch.bfloat16),
+        eps=1e-6, top_k=4)
+    return args, G
+
+
+def _ffn_np(args, G, **over):
+    a = dict(args, **over)
+    conv = {}
+    for k, v in a.items():
+        if isinstance(v, torch.Tensor):
+            if v.dtype == torch.int32:
+                conv[k] = v.numpy()
+            elif k in ("gu_scale", "dn_scale"):
+                conv[k] = _b(v)
+            else:
+                conv[k] = v.float().numpy()
+        else:
+            conv[k] = v
+    conv["layer_scalar"] = float(conv["layer_scalar"].reshape(-1)[0])
+    return oracle.ffn_block(**conv, G=G)
+
+
+@pytest.mark.parametrize("M", [1, 7])
+def test_ffn_block_vs_torch_ops(M):
+    from oracle import torch_cpu
+    args, G = _ffn_inputs(M)
+    ref = torch_cpu.ffn_block(**args, G=G)
+    got = _ffn_np(args, G)
+    err = oracle.max_abs_rel(got, ref.float().numpy())
+    assert err <= 1e-2, err
+
+
+def test_ffn_block_layer_scalar_scales_exactly():
+    args, G = _ffn_inputs(3)
+    one = _ffn_np(args, G)
+    two = _ffn_np(args, G, layer_scalar=torch.tensor([2.0], dtype=torch.bfloat16))
+    assert np.array_equal(two, 2 * one)
