@@ -39,6 +39,8 @@ group size 32, the released checkpoints'.
 the sweep, and configs[0] (the dense W4A16 linear at M = 16).
 ``ffn_block`` times the whole post-attention FFN block (backends.py:77-126:
 norms, shared bf16 MLP, router, experts) per decoder layer at M = 1 and 32.
+``bf16_experts`` times the unquantised-experts path (backends.py:209-283) at
+M = 1, 8, 64 over 8 rotated copies of a layer's bf16 experts.
 ``latent`` is BASELINE configs[4] (30 MoE layers + HybridLink per step, batch
 32); ``hybridlink`` times the HybridLink map alone at that batch (weights
 rotated through HBM).
@@ -495,6 +497,35 @@ def ffn_leg(dev, steps, warmup, n_layers):
     return out
 
 
+BF16_MS = (1, 8, 64)
+BF16_COPIES = 8  # 8 x 1.52 GB; at M = 1 one pass reads 8 x 8 experts x 11.9 MB = 761 MB
+
+
+def bf16_experts_leg(dev, steps, warmup):
+    """The BF16 experts path (backends.py:209-283) at decode sizes over rotated
+    copies of a whole layer's bf16 experts; bytes per call = U distinct
+    experts x (2I x H + H x I) x 2 + activations in and out."""
+    g = torch.Generator(device=dev).manual_seed(1700)
+    copies = [((torch.randn(E, 2 * I, H, generator=g, device=dev) / math.sqrt(H)).to(torch.bfloat16),
+               (torch.randn(E, H, I, generator=g, device=dev) / math.sqrt(I)).to(torch.bfloat16))
+              for _ in range(BF16_COPIES)]
+    rw = synth.router_weights(E, H, seed=1701, device=dev)
+    out = {}
+    for M in BF16_MS:
+        x = synth.activations(M, H, seed=1710 + M, device=dev)
+        w, idx = _lib.router_topk(x, rw.scale, rw.scalar_root, rw.proj, rw.per_expert_scale, rw.eps, TOPK)
+        U = int(torch.unique(idx).numel())
+        t = time_graph(lambda: [_lib.bf16_experts_forward(x, idx, w, gu, dn) for gu, dn in copies],
+                       len(copies), steps, warmup)
+        nbytes = U * (3 * I * H * 2) + 2 * M * H * 2
+        out[str(M)] = {"us": t * 1e6, "unique_experts": U, "bytes": nbytes, "gbps": nbytes / t / 1e9,
+                       "frac_hbm": nbytes / t / 1e9 / PEAK_HBM_GBS}
+        log(f"bf16 experts M={M}: {t*1e6:.1f} us/call, U={U}, {nbytes / t / 1e9:.0f} GB/s")
+    del copies
+    torch.cuda.empty_cache()
+    return out
+
+
 def _rounded(v):
     """Floats rounded to 4 decimals, recursively (None passes through)."""
     if isinstance(v, float):
@@ -540,6 +571,8 @@ def main(argv=None):
     ap.add_argument("--only-prefill", action="store_true",
                     help="time only the prefill layer (for rocprofv3 counter runs)")
     ap.add_argument("--no-ffn", action="store_true", help="skip the FFN-block leg")
+    ap.add_argument("--no-bf16", action="store_true", help="skip the BF16-experts leg")
+    ap.add_argument("--only-bf16", action="store_true")
     ap.add_argument("--only-ffn", action="store_true")
     ap.add_argument("--no-g32", action="store_true",
                     help="skip the group-size-32 leg (the released checkpoints' group size)")
@@ -562,6 +595,9 @@ def main(argv=None):
     torch.manual_seed(0)
     if args.only_latent:
         print(json.dumps({"latent": latent(dev)}), flush=True)
+        return 0
+    if args.only_bf16:
+        print(json.dumps({"bf16_experts": _rounded(bf16_experts_leg(dev, args.steps, args.warmup))}), flush=True)
         return 0
     if args.only_ffn:
         print(json.dumps({"ffn_block": _rounded(ffn_leg(dev, args.steps, args.warmup, args.layers))}), flush=True)
@@ -590,6 +626,7 @@ def main(argv=None):
     pre = None if args.no_prefill else prefill(dev, max(8, args.steps // 4), max(2, args.warmup // 4), 4)
     g32 = None if args.no_g32 else g32_leg(dev, args)
     ffn = None if args.no_ffn else ffn_leg(dev, args.steps, args.warmup, args.layers)
+    bf16 = None if args.no_bf16 else bf16_experts_leg(dev, args.steps, args.warmup)
 
     lat = None if args.no_latent else latent(dev)
     hl = None if args.no_latent else hybridlink_leg(dev)
@@ -635,6 +672,7 @@ def main(argv=None):
                                                  for k, v in d.items()} for c, d in dense.items()},
         "g32": _rounded(g32),
         "ffn_block": _rounded(ffn),
+        "bf16_experts": _rounded(bf16),
         "cpu_baseline": _rounded(cpu),
     }
     print(json.dumps(result), flush=True)

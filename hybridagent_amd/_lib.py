@@ -50,6 +50,9 @@ SIGNATURES = {
     "moe_down": (ctypes.c_int, [_VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "moe_combine": (ctypes.c_int, [_VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "moe_layer_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
+    "moe_bf16_experts_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
+    "moe_bf16_experts_forward": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64,
+                                                _VP, _SZ, _VP]),
     "moe_ffn_block_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "moe_ffn_block_forward": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _F32, _VP, _VP, _VP,
                                              _VP, _VP, _VP, _VP, _VP, _VP, _VP, _F32, _VP, _I64, _I64, _I64,
@@ -402,6 +405,34 @@ def moe_layer_forward(router_in: torch.Tensor, router_scale: torch.Tensor, scala
                                      0 if ws is None else ws.numel(), _stream(dev)),
                "moe_layer_forward")
     return out.reshape(*hidden_states.shape[:-1], H), w, idx
+
+
+def bf16_experts_forward(hidden_states: torch.Tensor, top_k_index: torch.Tensor, top_k_weights: torch.Tensor,
+                         gate_up_proj: torch.Tensor, down_proj: torch.Tensor) -> torch.Tensor:
+    """MoE output [T, H] with unquantised bf16 experts (backends.py:209-283):
+    gate_up_proj [E, 2I, H], down_proj [E, H, I] (Gemma4TextExperts parameters)."""
+    dev = _require_gpu(hidden_states, top_k_index, top_k_weights, gate_up_proj, down_proj)
+    H = hidden_states.shape[-1]
+    x = _bf16(hidden_states, "hidden_states").reshape(-1, H)
+    idx = top_k_index.reshape(x.shape[0], top_k_index.shape[-1]).to(torch.int64).contiguous()
+    w = top_k_weights.reshape(x.shape[0], top_k_weights.shape[-1]).to(torch.float32).contiguous()
+    gu = _bf16(gate_up_proj, "gate_up_proj")
+    dn = _bf16(down_proj, "down_proj")
+    E, two_i, h = gu.shape
+    I = two_i // 2
+    if h != H or two_i % 2 or dn.shape != (E, H, I):
+        raise ValueError(f"expert weight shapes {tuple(gu.shape)} / {tuple(dn.shape)} do not match hidden size {H}")
+    if w.shape != idx.shape:
+        raise ValueError("top_k_weights and top_k_index shapes differ")
+    M, k = idx.shape
+    out = torch.empty((M, H), dtype=torch.bfloat16, device=dev)
+    lib = load()
+    ws = _workspace(lib.moe_bf16_experts_workspace_bytes(max(M, 1), k, E, H, I), dev)
+    with torch.cuda.device(dev):
+        _check(lib.moe_bf16_experts_forward(_ptr(x), _ptr(idx), _ptr(w), _ptr(gu), _ptr(dn), _ptr(out), M, k, E,
+                                            H, I, _ptr(ws), 0 if ws is None else ws.numel(), _stream(dev)),
+               "moe_bf16_experts_forward")
+    return out.reshape(*hidden_states.shape[:-1], H)
 
 
 def ffn_block(residual: torch.Tensor, attn_out: torch.Tensor, post_attn_ln_w: torch.Tensor,

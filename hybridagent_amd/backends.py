@@ -160,6 +160,33 @@ def patch_ffn_4bit(backbone: torch.nn.Module) -> int:
     return patched
 
 
+def bf16_experts_fast_forward(self, hidden_states: torch.Tensor, top_k_index: torch.Tensor,
+                              top_k_weights: torch.Tensor) -> torch.Tensor:
+    """``_bf16_experts_fast_forward`` (backends.py:209-283) for transformers'
+    BF16 ``Gemma4TextExperts`` (parameters ``gate_up_proj`` [E, 2I, H] and
+    ``down_proj`` [E, H, I]): the expert sort, the two grouped bf16 GEMMs (gated
+    GELU fused) and the weighted top-k sum on the HIP library, at every batch
+    size, with no host synchronisation."""
+    out = _lib.bf16_experts_forward(hidden_states, top_k_index, top_k_weights, self.gate_up_proj,
+                                    self.down_proj)
+    return out.to(hidden_states.dtype)
+
+
+def patch_bf16_experts_fastpath(backbone: torch.nn.Module) -> int:
+    """Bind ``bf16_experts_fast_forward`` to every BF16 ``Gemma4TextExperts`` module
+    (backends.py:286-298); returns the number of modules patched."""
+    import types
+
+    from .quantization import Gemma4TextExperts4Bit
+
+    patched = 0
+    for mod in backbone.modules():
+        if mod.__class__.__name__ == "Gemma4TextExperts" and not isinstance(mod, Gemma4TextExperts4Bit):
+            mod.forward = types.MethodType(bf16_experts_fast_forward, mod)
+            patched += 1
+    return patched
+
+
 def moe_block(residual: torch.Tensor, h2_in: torch.Tensor, router, experts) -> torch.Tensor:
     """Router on ``residual`` + experts on ``h2_in`` (backends.py:111-122):
     ``router`` is a Gemma4TextRouter-like module (``scale``, ``proj``,

@@ -642,6 +642,56 @@ int moe_ffn_block_forward(const uint16_t* residual, const uint16_t* attn_out,
                                        layer_scalar, out, M, (int)H, eps, s));
 }
 
+size_t moe_bf16_experts_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I) {
+  return moe_workspace_bytes(M, top_k, E, H, I);
+}
+
+int moe_bf16_experts_forward(const uint16_t* hidden, const int64_t* topk_idx, const float* topk_w,
+                             const uint16_t* gate_up_proj, const uint16_t* down_proj, uint16_t* out,
+                             int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+  // the MoE shape checks (group size unused: any valid one)
+  MoeLayout L{};
+  int st = moe_check(M, top_k, E, H, I, 128, workspace, workspace_bytes, &L);
+  if (st != W4A16_OK || M == 0) return st;
+  if (!hidden || !topk_idx || !topk_w || !gate_up_proj || !down_proj || !out) return W4A16_ERR_NULL;
+  if (!aligned16(hidden) || !aligned16(gate_up_proj) || !aligned16(down_proj) || !aligned16(out))
+    return W4A16_ERR_ALIGN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e =
+      M * top_k > kSortMultiMinRows
+          ? launch_sort_multi(topk_idx, (int)M, (int)top_k, (int)E, L.sorted_pos, L.offsets, L.desc,
+                              L.counters, L.tiles, L.blockcnt, kPrefillBM, s)
+          : launch_sort(topk_idx, (int)M, (int)top_k, (int)E, L.sorted_pos, L.offsets, L.desc,
+                        L.counters, L.tiles, kPrefillBM, s);
+  const int max_slots = (int)(M * top_k < E ? M * top_k : E);
+  Bf16ExpertArgs a{};
+  a.sorted_pos = L.sorted_pos;
+  a.desc = L.desc;
+  a.n_active = L.counters;
+  a.I = (int)I;
+  a.topk = (int)top_k;
+  a.rows_total = (int)(M * top_k);
+  if (e == hipSuccess) {
+    a.act = hidden;
+    a.W = gate_up_proj;
+    a.out = L.inter;
+    a.N = (int)(2 * I);
+    a.K = (int)H;
+    e = launch_bf16_experts(kModeGateUp, a, max_slots, s);
+  }
+  if (e == hipSuccess) {
+    a.act = L.inter;
+    a.W = down_proj;
+    a.out = L.dn;
+    a.N = (int)H;
+    a.K = (int)I;
+    e = launch_bf16_experts(kModeDown, a, max_slots, s);
+  }
+  if (e == hipSuccess) e = launch_combine(L.dn, topk_idx, topk_w, out, (int)M, (int)top_k, (int)E, (int)H, s);
+  return launch_status(e);
+}
+
 }  // extern "C"
 
 // moe_forward_static's scratch: one array per GPU the library runs on, held

@@ -66,6 +66,18 @@ struct PrefillArgs {
 
 enum DecodeMode { kModeDense = 0, kModeGateUp = 1, kModeDown = 2 };
 
+// Arguments of the BF16 experts' grouped GEMMs (kernels_bf16_experts.hip).
+struct Bf16ExpertArgs {
+  const uint16_t* act;        // gate_up: hidden [M, K]; down: inter [M*k, K] in segment order
+  const uint16_t* W;          // bf16 weights [E, N, K]
+  uint16_t* out;              // gate_up: inter [M*k, I] (segment order); down: dn rows t*k+j [M*k, N]
+  const int32_t* sorted_pos;  // [M*k] rows t*k+j in expert-segment order
+  const int32_t* desc;        // [E][4] (expert, segment start, rows, 0) per active slot
+  const int32_t* n_active;    // [1]
+  int N, K, I, topk;
+  int rows_total;             // M * topk routed rows (sets the row-chunk size)
+};
+
 hipError_t launch_dequant(const int32_t* packed, const uint16_t* scale, uint16_t* out,
                           int64_t rows, int K, int G, hipStream_t s);
 hipError_t launch_bias_order(const uint16_t* x, uint16_t* xp, int64_t rows, int K, hipStream_t s);
@@ -137,6 +149,8 @@ hipError_t launch_ffn_post(const uint16_t* mlp, const uint16_t* moe, const uint1
                            const uint16_t* w1, const uint16_t* w2, const uint16_t* w3,
                            const uint16_t* layer_scalar, uint16_t* out, int64_t M, int H, float eps,
                            hipStream_t s);
+// BF16 experts: grid (column tile, active slot), max_slots <= 65535
+hipError_t launch_bf16_experts(int mode, Bf16ExpertArgs a, int max_slots, hipStream_t s);
 // prefill grouped GEMM: one launch per stage, items = (m-tile, n-tile)
 hipError_t launch_prefill(int mode, PrefillArgs a, int max_mtiles, hipStream_t s);
 // the bias-form prefill GEMM (group size a multiple of 128) and the pass that

@@ -210,6 +210,23 @@ W4A16_API int moe_layer_forward(const uint16_t* router_in, const uint16_t* route
                       int64_t H, int64_t I, int64_t group_size, void* workspace,
                       size_t workspace_bytes, void* stream);
 
+/* The BF16 experts (unquantised Gemma4TextExperts weights) on the same
+ * routing machinery: _bf16_experts_fast_forward  -- backends.py:209-283
+ * (installed on every BF16 experts module by patch_bf16_experts_fastpath,
+ * backends.py:286-298):
+ *   out[t] = sum_j bf16(topk_w[t,j]) * down_e(gelu_tanh(gate_e(x)) * up_e(x)),
+ * e = topk_idx[t, j], bf16 rounding after every op.
+ * hidden [M, H] bf16; gate_up_proj [E, 2I, H] bf16 (gate rows first);
+ * down_proj [E, H, I] bf16; topk as for moe_forward; slots outside [0, E)
+ * contribute nothing.  Workspace: moe_bf16_experts_workspace_bytes().    */
+W4A16_API size_t moe_bf16_experts_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t H,
+                                                  int64_t I);
+W4A16_API int moe_bf16_experts_forward(const uint16_t* hidden, const int64_t* topk_idx,
+                             const float* topk_w, const uint16_t* gate_up_proj,
+                             const uint16_t* down_proj, uint16_t* out, int64_t M, int64_t top_k,
+                             int64_t E, int64_t H, int64_t I, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
 /* The post-attention FFN block of a Gemma-4 MoE decoder layer,
  * _ffn_moe_4bit_step  -- backends.py:77-126 (installed per layer by
  * patch_compiled_ffn_4bit, backends.py:132-201):

@@ -22,7 +22,8 @@ Restated from (``hybrid_agent/`` in the reference repository):
 * ``router``             backends.py:111-117 (RMSNorm * scale * scalar_root,
                          F.linear logits, fp32 softmax, top-k, renormalise,
                          per_expert_scale);
-* ``ffn_block``          backends.py:101-126 (_ffn_moe_4bit_step in eager ops).
+* ``ffn_block``          backends.py:101-126 (_ffn_moe_4bit_step in eager ops);
+* ``bf16_experts``       backends.py:209-283 (the BF16 experts' three branches).
 
 All tensors are CPU torch tensors in the reference's dtypes (bf16
 activations and scales, int32 packed weights, fp32 routing weights).
@@ -143,3 +144,41 @@ def ffn_block(residual, attn_out, post_attn_ln_w, pre_ff_ln_w, mlp_gate_w, mlp_u
     h_2 = F.rms_norm(h_2, (D,), post_ff_ln2_w, eps)
     h_comb = F.rms_norm(h_1 + h_2, (D,), post_ff_ln_w, eps)
     return (residual + h_comb) * layer_scalar
+
+
+def bf16_experts(h: torch.Tensor, idx: torch.Tensor, w: torch.Tensor, gate_up_proj: torch.Tensor,
+                 down_proj: torch.Tensor) -> torch.Tensor:
+    """_bf16_experts_fast_forward (backends.py:209-283) on CPU tensors: the
+    T == 1 branch (index_select, mv, bmm), the T <= 8 branch (einsum) and the
+    per-expert loop (F.linear, bf16 index_add_) above that."""
+    T = h.shape[0]
+    H = h.shape[-1]
+    E, two_i, _ = gate_up_proj.shape
+    if T == 1:
+        e = idx[0]
+        gu = torch.mv(gate_up_proj.index_select(0, e).view(-1, H), h[0]).view(e.shape[0], two_i)
+        gate, up = gu.chunk(2, dim=-1)
+        inter = _gelu_tanh(gate) * up
+        out = torch.bmm(down_proj.index_select(0, e), inter.unsqueeze(-1)).squeeze(-1)
+        return (out * w[0, :, None].to(out.dtype)).sum(dim=0, keepdim=True).to(h.dtype)
+    if T <= 8:
+        B, K = idx.shape
+        flat = idx.reshape(-1)
+        gu = torch.einsum("bkih,bh->bki", gate_up_proj.index_select(0, flat).view(B, K, two_i, H), h)
+        gate, up = gu.chunk(2, dim=-1)
+        inter = _gelu_tanh(gate) * up
+        out = torch.einsum("bkhi,bki->bkh", down_proj.index_select(0, flat).view(B, K, H, two_i // 2), inter)
+        return (out * w.unsqueeze(-1).to(out.dtype)).sum(dim=1).to(h.dtype)
+    final = torch.zeros_like(h)
+    with torch.no_grad():
+        mask = F.one_hot(idx, num_classes=E + 1).permute(2, 1, 0)
+        hit = torch.greater(mask.sum(dim=(-1, -2)), 0).nonzero()
+    for ex in hit:
+        ex = ex[0]
+        if ex == E:
+            continue
+        kpos, tok = torch.where(mask[ex])
+        gate, up = F.linear(h[tok], gate_up_proj[ex]).chunk(2, dim=-1)
+        a = F.linear(_gelu_tanh(gate) * up, down_proj[ex]) * w[tok, kpos, None]
+        final.index_add_(0, tok, a.to(final.dtype))
+    return final

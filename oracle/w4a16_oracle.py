@@ -43,6 +43,10 @@ Pinning (what checks this restatement, see ``tests/test_oracle.py``):
   linearity of the combine in the routing weights.
 * ``hybridlink`` / ``rms_norm`` (config-4 harness only): torch ``nn.LayerNorm``,
   ``nn.GELU``, ``nn.Linear`` on identical inputs.
+* ``moe_forward_bf16``: with the dequantised 4-bit weights as its bf16
+  weights it equals ``moe_forward`` bit for bit (the dequantise-then-matmul
+  identity); the torch CPU restatement of ``_bf16_experts_fast_forward``
+  (``oracle/torch_cpu.py``) on identical inputs.
 * ``ffn_block``: the same lines of ``_ffn_moe_4bit_step`` written with torch CPU
   ``F.rms_norm`` / ``F.linear`` / ``F.gelu`` / ``softmax`` + ``topk`` and the
   torch-CPU experts (``oracle/torch_cpu.py``) on identical inputs; a
@@ -64,7 +68,7 @@ __all__ = [
     "pack_int4", "unpack_int4", "dequantize", "linear", "gelu_tanh",
     "rms_norm", "router_logits", "topk_from_logits", "router",
     "sort_permute", "moe_forward", "max_abs_rel", "hybridlink",
-    "layer_norm", "gelu_erf", "ffn_block",
+    "layer_norm", "gelu_erf", "ffn_block", "moe_forward_bf16",
 ]
 
 
@@ -342,35 +346,26 @@ def sort_permute(idx, E: int):
 # MoE forward  (quantization.py:88-129, 241-263, 265-294)
 # ---------------------------------------------------------------------------
 
-def moe_forward(hidden, idx, weights, gu_packed, gu_scale, dn_packed, dn_scale, G: int,
-                path: str = "fused", return_intermediates: bool = False):
-    """W4A16 MoE layer output (bf16 values as float32) [M, H].
-
-    ``path="fused"``: rounding points of ``fused_triton_4bit_moe_forward``
-    (quantization.py:112-129) and of the single-token path (:241-263).
-    ``path="loop"``: the per-expert loop (quantization.py:265-294), bf16
-    ``index_add_`` accumulation in ascending expert order.
-    """
+def _moe_core(hidden, idx, weights, E, I, H, proj_gu, proj_dn, path, return_intermediates=False):
+    """The routing, activation and combine of the MoE forward around two
+    projections: ``proj_gu(e, x_rows)`` -> bf16 [rows, 2I] and
+    ``proj_dn(e, a_rows)`` -> bf16 [rows, H] of expert e."""
     x = np.asarray(hidden, np.float32)
     idx = np.asarray(idx, np.int64)
     w = np.asarray(weights, np.float32)
     M, k = idx.shape
-    E, two_i, _ = gu_packed.shape
-    I = two_i // 2
-    H = dn_packed.shape[1]
     if path == "fused":
-        gu = np.zeros((M * k, two_i), np.float32)
+        gu = np.zeros((M * k, 2 * I), np.float32)
         inter = np.zeros((M * k, I), np.float32)
         dn = np.zeros((M, k, H), np.float32)
         for e in np.unique(idx):
             rows = np.nonzero(idx.reshape(-1) == e)[0]          # t*k + j
             tok = rows // k
-            g = linear(x[tok], gu_packed[e], gu_scale[e], G)   # :114-118
+            g = proj_gu(e, x[tok])                              # :114-118
             gu[rows] = g
             a = bf16_round(gelu_tanh(g[:, :I]) * g[:, I:])     # :119-120
             inter[rows] = a
-            d = linear(a, dn_packed[e], dn_scale[e], G)        # :123-127
-            dn[tok, rows % k] = d
+            dn[tok, rows % k] = proj_dn(e, a)                   # :123-127
         wb = bf16_round(w)                                       # :128
         prod = bf16_round(dn * wb[:, :, None])                   # :129
         y = bf16_round(prod.sum(axis=1, dtype=np.float32))
@@ -385,10 +380,39 @@ def moe_forward(hidden, idx, weights, gu_packed, gu_scale, dn_packed, dn_scale, 
                 mask[idx[t, j], j, t] = True
         for e in np.nonzero(mask.any(axis=(1, 2)))[0]:           # :270-275
             kpos, tok = np.nonzero(mask[e])                       # :276
-            g = linear(x[tok], gu_packed[e], gu_scale[e], G)     # :278-281
+            g = proj_gu(e, x[tok])                                # :278-281
             a = bf16_round(gelu_tanh(g[:, :I]) * g[:, I:])       # :281-282
-            d = linear(a, dn_packed[e], dn_scale[e], G)          # :283-286
+            d = proj_dn(e, a)                                     # :283-286
             c = bf16_round(d * w[tok, kpos][:, None])            # :287-291
             final[tok] = bf16_round(final[tok] + c)              # :290-292
         return final
     raise ValueError(f"unknown path {path!r}")
+
+
+def moe_forward(hidden, idx, weights, gu_packed, gu_scale, dn_packed, dn_scale, G: int,
+                path: str = "fused", return_intermediates: bool = False):
+    """W4A16 MoE layer output (bf16 values as float32) [M, H].
+
+    ``path="fused"``: rounding points of ``fused_triton_4bit_moe_forward``
+    (quantization.py:112-129) and of the single-token path (:241-263).
+    ``path="loop"``: the per-expert loop (quantization.py:265-294), bf16
+    ``index_add_`` accumulation in ascending expert order.
+    """
+    E, two_i, _ = gu_packed.shape
+    return _moe_core(hidden, idx, weights, E, two_i // 2, dn_packed.shape[1],
+                     lambda e, xr: linear(xr, gu_packed[e], gu_scale[e], G),
+                     lambda e, ar: linear(ar, dn_packed[e], dn_scale[e], G), path, return_intermediates)
+
+
+def moe_forward_bf16(hidden, idx, weights, gate_up_proj, down_proj, path: str = "fused"):
+    """The BF16 experts (_bf16_experts_fast_forward, backends.py:209-283):
+    the same forward with unquantised bf16 weights ``gate_up_proj`` [E, 2I, H]
+    and ``down_proj`` [E, H, I] (bf16 values as float32).  ``path="fused"``:
+    the T == 1 and T <= 8 branches (bmm / einsum, then a bf16 weighted sum);
+    ``path="loop"``: the T > 8 per-expert loop with bf16 ``index_add_``."""
+    gate_up_proj = np.asarray(gate_up_proj, np.float32)
+    down_proj = np.asarray(down_proj, np.float32)
+    E, two_i, _ = gate_up_proj.shape
+    return _moe_core(hidden, idx, weights, E, two_i // 2, down_proj.shape[1],
+                     lambda e, xr: _matmul_bf16(xr, gate_up_proj[e]),
+                     lambda e, ar: _matmul_bf16(ar, down_proj[e]), path)

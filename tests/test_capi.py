@@ -184,3 +184,30 @@ def test_python_ops_refuse_cpu_tensors():
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(RuntimeError, match="not built"):
         _lib.load(tmp_path / "libw4a16moe.so")
+
+
+def test_ffn_block_and_bf16_experts_host_validation(lib):
+    fake = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    # moe_bf16_experts_forward: hidden, idx, w, gate_up_proj, down_proj, out
+    f = lib.moe_bf16_experts_forward
+    need = lib.moe_bf16_experts_workspace_bytes(8, 8, 128, 2816, 704)
+    assert need == lib.moe_workspace_bytes(8, 8, 128, 2816, 704)
+    assert f(fake, fake, fake, fake, fake, fake, 8, 8, 128, 2816, 700, fake, need, NULL) == 2  # I % 32
+    assert f(fake, fake, fake, fake, fake, fake, 8, 8, 128, 2816, 704, fake, need - 1, NULL) == 5
+    assert f(fake, fake, fake, NULL, fake, fake, 8, 8, 128, 2816, 704, fake, need, NULL) == 1
+    assert f(ctypes.c_void_p(4098), fake, fake, fake, fake, fake, 8, 8, 128, 2816, 704, fake, need, NULL) == 4
+    assert f(*([NULL] * 6), 0, 8, 128, 2816, 704, NULL, 0, NULL) == 0
+    # moe_ffn_block_forward: 9 pointers, root, 10 pointers, eps, out, sizes
+    g = lib.moe_ffn_block_forward
+    wsb = lib.moe_ffn_block_workspace_bytes(8, 8, 128, 2816, 704, 2112)
+    assert wsb > lib.moe_layer_workspace_bytes(8, 8, 128, 2816, 704)
+    p9, p10 = [fake] * 9, [fake] * 10
+    ok = (8, 8, 128, 2816, 704, 2112, 128)
+    assert g(*p9, 0.1, *p10, 1e-6, fake, 8, 8, 128, 2816, 704, 2100, 128, fake, wsb, NULL) == 2  # Im % 32
+    assert g(*p9, 0.1, *p10, 1e-6, fake, 8, 8, 128, 8224, 704, 2112, 128, fake, wsb, NULL) == 2  # H > 8192
+    assert g(*p9, 0.1, *p10, 1e-6, fake, *ok, fake, wsb - 1, NULL) == 5
+    assert g(*p9, 0.1, *p10, 1e-6, fake, 8, 8, 128, 2816, 704, 2112, 96, fake, wsb, NULL) == 3
+    bad = list(p10)
+    bad[9] = NULL                       # layer_scalar
+    assert g(*p9, 0.1, *bad, 1e-6, fake, *ok, fake, wsb, NULL) == 1
+    assert g(*p9, 0.1, *p10, 1e-6, ctypes.c_void_p(4098), *ok, fake, wsb, NULL) == 4

@@ -477,3 +477,33 @@ def test_ffn_block_layer_scalar_scales_exactly():
     one = _ffn_np(args, G)
     two = _ffn_np(args, G, layer_scalar=torch.tensor([2.0], dtype=torch.bfloat16))
     assert np.array_equal(two, 2 * one)
+
+
+# ------------------------------------------------------ BF16 experts (backends.py:209-283)
+
+@pytest.mark.parametrize("path", ["fused", "loop"])
+def test_moe_bf16_equals_moe_on_dequantised_weights(path):
+    # dequantise-then-matmul: the BF16 forward on the dequantised 4-bit
+    # weights is the 4-bit forward, bit for bit
+    w, x, idx, tw = _ref_inputs(6)
+    gu = oracle.dequantize(w.gate_up_packed.numpy(), _b(w.gate_up_scale), 32)
+    dn = oracle.dequantize(w.down_packed.numpy(), _b(w.down_scale), 32)
+    a = oracle.moe_forward_bf16(x.float().numpy(), idx.numpy(), tw.numpy(), gu, dn, path=path)
+    b = oracle.moe_forward(x.float().numpy(), idx.numpy(), tw.numpy(), w.gate_up_packed.numpy(),
+                           _b(w.gate_up_scale), w.down_packed.numpy(), _b(w.down_scale), 32, path=path)
+    assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("M", [1, 5, 12])
+def test_moe_bf16_vs_torch_cpu_branches(M):
+    # M = 1, M <= 8 and M > 8 take the reference's three branches
+    from oracle import torch_cpu
+    g = torch.Generator().manual_seed(40 + M)
+    E, H, I = 8, 256, 96
+    gu = (0.05 * torch.randn(E, 2 * I, H, generator=g)).to(torch.bfloat16)
+    dn = (0.05 * torch.randn(E, H, I, generator=g)).to(torch.bfloat16)
+    _, x, idx, tw = _ref_inputs(M)
+    got = torch_cpu.bf16_experts(x, idx, tw, gu, dn)
+    ref = oracle.moe_forward_bf16(x.float().numpy(), idx.numpy(), tw.numpy(), gu.float().numpy(),
+                                  dn.float().numpy(), path="fused" if M <= 8 else "loop")
+    assert oracle.max_abs_rel(got.float().numpy(), ref) <= 1e-2
