@@ -41,6 +41,9 @@ the sweep, and configs[0] (the dense W4A16 linear at M = 16).
 norms, shared bf16 MLP, router, experts) per decoder layer at M = 1 and 32.
 ``bf16_experts`` times the unquantised-experts path (backends.py:209-283) at
 M = 1, 8, 64 over 8 rotated copies of a layer's bf16 experts.
+``loader`` times checkpoint loading (quantization.py:325-430) of a synthetic
+4-layer pack-quantized checkpoint: the reference's host flow against the
+device-direct loader.
 ``latent`` is BASELINE configs[4] (30 MoE layers + HybridLink per step, batch
 32); ``hybridlink`` times the HybridLink map alone at that batch (weights
 rotated through HBM).
@@ -526,6 +529,90 @@ def bf16_experts_leg(dev, steps, warmup):
     return out
 
 
+LOADER_LAYERS, LOADER_SHARDS = 4, 2
+
+
+def loader_leg(dev, tmpdir: str | None = None):
+    """Checkpoint loading (quantization.py:325-430): a synthetic pack-quantized
+    checkpoint of LOADER_LAYERS layers x 128 experts at the Gemma shape (1.57 GB,
+    LOADER_SHARDS shards, page-cached after writing) loaded into device-resident
+    experts modules by (a) the reference's flow -- safetensors load_file on the
+    host, per-layer torch.stack / torch.cat of the experts on the host, copy into
+    the device buffers -- and (b) the device-direct loader (one pinned read and
+    one host-to-device copy per shard, experts written in place on the device).
+    GB/s = checkpoint bytes / wall time; the better of two runs each."""
+    import shutil
+    import tempfile
+    import types as _types
+
+    from safetensors.torch import load_file, save_file
+
+    from hybridagent_amd import loader as ld
+    from hybridagent_amd.quantization import Gemma4TextExperts4Bit
+
+    d = tempfile.mkdtemp(prefix="w4a16ckpt_", dir=tmpdir)
+    try:
+        cfg = _types.SimpleNamespace(num_experts=E, hidden_size=H, moe_intermediate_size=I,
+                                     hidden_activation="gelu_pytorch_tanh")
+        files, nbytes = [], 0
+        per = LOADER_LAYERS // LOADER_SHARDS
+        for si in range(LOADER_SHARDS):
+            sd = {}
+            for ly in range(si * per, (si + 1) * per):
+                w = synth.moe_weights(E, H, I, G, seed=8100 + ly)
+                for e in range(E):
+                    pre = f"model.language_model.layers.{ly}.experts.{e}"
+                    parts = {"gate_proj": (w.gate_up_packed[e, :I], w.gate_up_scale[e, :I]),
+                             "up_proj": (w.gate_up_packed[e, I:], w.gate_up_scale[e, I:]),
+                             "down_proj": (w.down_packed[e], w.down_scale[e])}
+                    for proj, (pk, sc) in parts.items():
+                        sd[f"{pre}.{proj}.weight_packed"] = pk.contiguous()
+                        sd[f"{pre}.{proj}.weight_scale"] = sc.contiguous()
+            path = os.path.join(d, f"model-{si:05d}-of-{LOADER_SHARDS:05d}.safetensors")
+            save_file(sd, path)
+            files.append(path)
+            nbytes += sum(t.numel() * t.element_size() for t in sd.values())
+            del sd
+        mods = [Gemma4TextExperts4Bit(cfg, group_size=G).to(dev) for _ in range(LOADER_LAYERS)]
+
+        def reference_flow():
+            for path in files:
+                sd = load_file(path, device="cpu")
+                layers = sorted({ld.parse_expert_key(k)[0] for k in sd})
+                for ly in layers:
+                    get = lambda proj, kind: torch.stack(
+                        [sd[f"model.language_model.layers.{ly}.experts.{e}.{proj}.{kind}"] for e in range(E)])
+                    m = mods[ly]
+                    m.gate_up_packed.copy_(torch.cat([get("gate_proj", "weight_packed"),
+                                                      get("up_proj", "weight_packed")], dim=1))
+                    m.gate_up_scale.copy_(torch.cat([get("gate_proj", "weight_scale"),
+                                                     get("up_proj", "weight_scale")], dim=1))
+                    m.down_packed.copy_(get("down_proj", "weight_packed"))
+                    m.down_scale.copy_(get("down_proj", "weight_scale"))
+                del sd
+
+        def device_direct():
+            ld.stream_shards(files, ld.ExpertPlacer(mods), {}, dev)
+
+        res = {"layers": LOADER_LAYERS, "shards": LOADER_SHARDS, "checkpoint_bytes": nbytes}
+        for name, fn in (("reference_flow", reference_flow), ("device_direct", device_direct)):
+            best = float("inf")
+            for _ in range(2):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                fn()
+                torch.cuda.synchronize()
+                best = min(best, time.perf_counter() - t0)
+            res[name] = {"s": best, "gbps": nbytes / best / 1e9}
+            log(f"loader {name}: {best:.3f} s for {nbytes / 1e9:.2f} GB, {nbytes / best / 1e9:.2f} GB/s")
+        res["speedup"] = res["reference_flow"]["s"] / res["device_direct"]["s"]
+        del mods
+        torch.cuda.empty_cache()
+        return res
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+
+
 def _rounded(v):
     """Floats rounded to 4 decimals, recursively (None passes through)."""
     if isinstance(v, float):
@@ -572,6 +659,8 @@ def main(argv=None):
                     help="time only the prefill layer (for rocprofv3 counter runs)")
     ap.add_argument("--no-ffn", action="store_true", help="skip the FFN-block leg")
     ap.add_argument("--no-bf16", action="store_true", help="skip the BF16-experts leg")
+    ap.add_argument("--no-loader", action="store_true", help="skip the checkpoint-loading leg")
+    ap.add_argument("--only-loader", action="store_true")
     ap.add_argument("--only-bf16", action="store_true")
     ap.add_argument("--only-ffn", action="store_true")
     ap.add_argument("--no-g32", action="store_true",
@@ -595,6 +684,9 @@ def main(argv=None):
     torch.manual_seed(0)
     if args.only_latent:
         print(json.dumps({"latent": latent(dev)}), flush=True)
+        return 0
+    if args.only_loader:
+        print(json.dumps({"loader": _rounded(loader_leg(dev))}), flush=True)
         return 0
     if args.only_bf16:
         print(json.dumps({"bf16_experts": _rounded(bf16_experts_leg(dev, args.steps, args.warmup))}), flush=True)
@@ -627,6 +719,7 @@ def main(argv=None):
     g32 = None if args.no_g32 else g32_leg(dev, args)
     ffn = None if args.no_ffn else ffn_leg(dev, args.steps, args.warmup, args.layers)
     bf16 = None if args.no_bf16 else bf16_experts_leg(dev, args.steps, args.warmup)
+    ldr = None if args.no_loader else loader_leg(dev)
 
     lat = None if args.no_latent else latent(dev)
     hl = None if args.no_latent else hybridlink_leg(dev)
@@ -673,6 +766,7 @@ def main(argv=None):
         "g32": _rounded(g32),
         "ffn_block": _rounded(ffn),
         "bf16_experts": _rounded(bf16),
+        "loader": _rounded(ldr),
         "cpu_baseline": _rounded(cpu),
     }
     print(json.dumps(result), flush=True)

@@ -25,7 +25,7 @@ from unittest import mock
 import torch
 import torch.nn as nn
 
-from . import _lib
+from . import _lib, loader
 
 GROUP_SIZE = 32  # quantization.py:19 (the released 4-bit checkpoints)
 
@@ -166,51 +166,9 @@ def is_pack_quantized_dir(model_dir: Path) -> bool:
     return q.get("format") == "pack-quantized" or q.get("quant_method") == "compressed-tensors"
 
 
-_PROJ_TAGS = {
-    ("gate_proj", "weight_packed"): "gp", ("gate_proj", "weight_scale"): "gs",
-    ("up_proj", "weight_packed"): "up", ("up_proj", "weight_scale"): "us",
-    ("down_proj", "weight_packed"): "dp", ("down_proj", "weight_scale"): "ds",
-}
-
-
-class _ExpertShardCollector:
-    """Collects per-expert tensors of one layer across shards and writes the
-    stacked buffers once every expert of a projection pair has arrived
-    (gate rows before up rows, quantization.py:404-421)."""
-
-    def __init__(self, module: Gemma4TextExperts4Bit, dtype: torch.dtype):
-        self.m = module
-        self.dtype = dtype
-        self.parts: dict[str, dict[int, torch.Tensor]] = {t: {} for t in ("gp", "gs", "up", "us", "dp", "ds")}
-        self.gate_up_done = False
-        self.down_done = False
-
-    def add(self, tag: str, expert: int, t: torch.Tensor) -> None:
-        self.parts[tag][expert] = t
-        E = self.m.num_experts
-        if not self.gate_up_done and all(len(self.parts[k]) == E for k in ("gp", "up", "gs", "us")):
-            take = lambda k: torch.stack([self.parts[k].pop(e) for e in range(E)])
-            self.m.gate_up_packed.copy_(torch.cat([take("gp"), take("up")], dim=1))
-            self.m.gate_up_scale.copy_(torch.cat([take("gs"), take("us")], dim=1).to(self.dtype))
-            self.gate_up_done = True
-        if not self.down_done and all(len(self.parts[k]) == E for k in ("dp", "ds")):
-            take = lambda k: torch.stack([self.parts[k].pop(e) for e in range(E)])
-            self.m.down_packed.copy_(take("dp"))
-            self.m.down_scale.copy_(take("ds").to(self.dtype))
-            self.down_done = True
-
-
 def _parse_expert_key(key: str):
     """model.language_model.layers.{l}.experts.{e}.{proj}.{kind} -> (l, e, tag) or None."""
-    if ".experts." not in key or not key.startswith("model.language_model.layers."):
-        return None
-    parts = key.split(".")
-    if len(parts) != 8:
-        return None
-    tag = _PROJ_TAGS.get((parts[6], parts[7]))
-    if tag is None:
-        return None
-    return int(parts[3]), int(parts[5]), tag
+    return loader.parse_expert_key(key)
 
 
 def load_pack_quantized_backbone(
@@ -218,13 +176,18 @@ def load_pack_quantized_backbone(
     *,
     dtype: torch.dtype = torch.bfloat16,
     trust_remote_code: bool = False,
+    device: str | torch.device | None = None,
 ) -> nn.Module:
     """Instantiate Gemma4ForConditionalGeneration with 4-bit experts and stream the
-    compressed-tensors shards into it on the CPU (quantization.py:325-430).
+    compressed-tensors shards into it (quantization.py:325-430).
 
     The group size comes from ``quantization_config`` (default ``GROUP_SIZE``).
+    With ``device`` (e.g. ``"cuda:0"``) the model is built on that device and
+    each shard is read into pinned host memory, copied to the device whole and
+    written from there into the module tensors (experts straight into their
+    slices of the stacked buffers); without it everything stays on the CPU,
+    as in the reference.
     """
-    from safetensors.torch import load_file
     from transformers import AutoConfig, AutoModelForCausalLM
     from transformers.models.gemma4 import modeling_gemma4
 
@@ -245,35 +208,17 @@ def load_pack_quantized_backbone(
             return
         orig_init_weights(self, module)
 
+    dev = torch.device(device) if device is not None else torch.device("cpu")
     with mock.patch.object(modeling_gemma4, "Gemma4TextExperts", _ExpertsCls), \
-            mock.patch.object(modeling_gemma4.Gemma4PreTrainedModel, "_init_weights", _skip_init):
+            mock.patch.object(modeling_gemma4.Gemma4PreTrainedModel, "_init_weights", _skip_init), \
+            torch.device(dev):
         backbone = AutoModelForCausalLM.from_config(config, dtype=dtype, trust_remote_code=trust_remote_code)
 
-    index_file = model_dir / "model.safetensors.index.json"
-    if index_file.is_file():
-        weight_map = json.loads(index_file.read_text(encoding="utf-8"))["weight_map"]
-        shard_files = sorted(set(weight_map.values()))
-    else:
-        shard_files = ["model.safetensors"]
-
     layers = backbone.model.language_model.layers
-    collectors = [_ExpertShardCollector(ly.experts, dtype) for ly in layers]
+    placer = loader.ExpertPlacer([ly.experts for ly in layers])
     targets = dict(backbone.named_parameters())
     targets.update(dict(backbone.named_buffers()))
-
-    for shard in shard_files:
-        sd = load_file(str(model_dir / shard), device="cpu")
-        for key in list(sd.keys()):
-            val = sd.pop(key)
-            if key.endswith(".weight_shape"):
-                continue
-            parsed = _parse_expert_key(key)
-            if parsed is not None:
-                l_idx, e_idx, tag = parsed
-                collectors[l_idx].add(tag, e_idx, val)
-            elif key in targets:
-                tgt = targets[key]
-                tgt.data.copy_(val.to(tgt.dtype) if val.is_floating_point() else val)
+    loader.stream_shards(loader.shard_files(model_dir), placer, targets, dev)
     if getattr(config, "tie_word_embeddings", True):
         backbone.tie_weights()
     return backbone

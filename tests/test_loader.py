@@ -96,3 +96,38 @@ def test_parse_expert_key():
     assert q._parse_expert_key("model.language_model.layers.3.experts.17.up_proj.weight_scale") == (3, 17, "us")
     assert q._parse_expert_key("model.language_model.layers.3.mlp.up_proj.weight") is None
     assert q._parse_expert_key("model.language_model.layers.3.experts.1.up_proj.weight_shape") is None
+
+
+def test_shard_reader_matches_safetensors(tmp_path):
+    from hybridagent_amd import loader
+    from safetensors.torch import load_file
+    g = torch.Generator().manual_seed(9)
+    sd = {
+        "a.odd_bf16": torch.randn(3, generator=g).to(torch.bfloat16),   # 6 bytes: the next tensor starts unaligned
+        "b.i32": torch.randint(-100, 100, (5, 7), generator=g, dtype=torch.int32),
+        "c.f32": torch.randn(4, 2, generator=g),
+        "d.i64": torch.arange(6, dtype=torch.int64).reshape(2, 3),
+    }
+    path = tmp_path / "x.safetensors"
+    save_file(sd, str(path))
+    ref = load_file(str(path))
+    got = loader.ShardReader("cpu").open(path)
+    assert set(got) == set(ref)
+    for k in ref:
+        assert got[k].dtype == ref[k].dtype and torch.equal(got[k], ref[k]), k
+
+
+def test_placer_rejects_wrong_group_size_and_missing_experts():
+    from hybridagent_amd import loader
+    import types as _t
+    cfg = _t.SimpleNamespace(num_experts=2, hidden_size=64, moe_intermediate_size=32,
+                             hidden_activation="gelu_pytorch_tanh")
+    m = q.Gemma4TextExperts4Bit(cfg, group_size=32)
+    placer = loader.ExpertPlacer([m])
+    with pytest.raises(ValueError, match="does not match"):
+        placer.place(0, 0, "gs", torch.zeros(32, 4, dtype=torch.bfloat16))   # G = 16 scales
+    placer.place(0, 0, "gp", torch.zeros(32, 8, dtype=torch.int32))
+    with pytest.raises(ValueError, match="missing"):
+        placer.check_complete()
+    with pytest.raises(ValueError, match="outside"):
+        placer.place(0, 5, "gp", torch.zeros(32, 8, dtype=torch.int32))
