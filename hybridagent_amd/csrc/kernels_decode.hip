@@ -284,8 +284,7 @@ void k_decode(DecodeArgs a) {
   // tile): 16 pieces of 16 bytes, reordered for the bias form, stored in
   // fragment order, and -- for the bias form -- summed into
   // csum[t][row] = 136 * (sum of the row's tile elements), the correction the
-  // bias form subtracts per group.  Every thread has at most one task
-  // (rb * ntiles <= kStreamThreads, from the LDS budget).  `first` runs
+  // bias form subtracts per group.  Each task is split over two threads.  `first` runs
   // before anything else: the first pass issues the weight prologue there,
   // as early as the expert is known, so the first items' weights (the bulk
   // of the start-up traffic) are in flight while the row positions and the
@@ -310,40 +309,77 @@ void k_decode(DecodeArgs a) {
       }
     }
     __syncthreads();
-    const bool has = tid < nr * ntiles;
-    const int jr = tid / ntiles;
-    const int t = tid - jr * ntiles;
-    const int nb = min(16, K8 - 16 * t);
-    u32x4_t v[16];
-    if (has) {
-      int64_t row;
-      if (MODE == kModeDense) row = seg0 + mc + jr;
-      else if (MODE == kModeGateUp) row = tok[jr];
-      else row = seg0 + mc + jr;
-      const uint16_t* src = a.act + row * a.K + 128 * t;
-      // pieces past the row end load the last piece again and are dropped
-#pragma unroll
-      for (int b = 0; b < 16; ++b) v[b] = ld16(src + 8 * min(b, nb - 1));
-    }
-    if (has) {
-      float sum = 0.f;
-#pragma unroll
-      for (int b = 0; b < 16; ++b) {
-        if (b < nb) {
-          u32x4_t x = v[b];
-          // gate_up / dense read caller activations in natural order; down
-          // reads intermediate rows the gate_up epilogue wrote in bias order
-          if (BIAS && MODE != kModeDown) x = to_bias_order(x);
-          if (BIAS) {
-            sum += bf16_bits_to_f32(x.x & 0xFFFFu) + bf16_bits_to_f32(x.x >> 16) +
-                   bf16_bits_to_f32(x.y & 0xFFFFu) + bf16_bits_to_f32(x.y >> 16) +
-                   bf16_bits_to_f32(x.z & 0xFFFFu) + bf16_bits_to_f32(x.z >> 16) +
-                   bf16_bits_to_f32(x.w & 0xFFFFu) + bf16_bits_to_f32(x.w >> 16);
-          }
-          lds_a[frag_slot(16 * t + b, rb, jr)] = x;
-        }
+    // One thread per (row, k tile) task, or -- without a K split -- two,
+    // each taking half of its 16 pieces (adjacent lanes, which add their
+    // sums with one DPP swap).  The LDS budget keeps the task count within
+    // the thread count.  Without a K split the staging registers (16 bytes a
+    // piece, all loads issued before any is used) next to the weight
+    // prologue overflow the register budget unless the task is split; the
+    // K-split shapes keep whole tasks (split, or in a task loop, the compiler
+    // recomputes addresses inside their item loop instead).
+    auto to_lds = [&](const u32x4_t& x0, int t, int b, int jr, float& sum) {
+      u32x4_t x = x0;
+      // gate_up / dense read caller activations in natural order; down
+      // reads intermediate rows the gate_up epilogue wrote in bias order
+      if (BIAS && MODE != kModeDown) x = to_bias_order(x);
+      if (BIAS) {
+        sum += bf16_bits_to_f32(x.x & 0xFFFFu) + bf16_bits_to_f32(x.x >> 16) +
+               bf16_bits_to_f32(x.y & 0xFFFFu) + bf16_bits_to_f32(x.y >> 16) +
+               bf16_bits_to_f32(x.z & 0xFFFFu) + bf16_bits_to_f32(x.z >> 16) +
+               bf16_bits_to_f32(x.w & 0xFFFFu) + bf16_bits_to_f32(x.w >> 16);
       }
-      if (BIAS) csum[t * 16 + jr] = 136.0f * sum;
+      lds_a[frag_slot(16 * t + b, rb, jr)] = x;
+    };
+    auto row_of = [&](int jr) -> int64_t {
+      if (MODE == kModeGateUp) return tok[jr];
+      return seg0 + mc + jr;
+    };
+    if constexpr (KSPLIT != 1) {
+      const bool has = tid < nr * ntiles;
+      const int jr = tid / ntiles;
+      const int t = tid - jr * ntiles;
+      const int nb = min(16, K8 - 16 * t);
+      u32x4_t v[16];
+      if (has) {
+        const uint16_t* src = a.act + row_of(jr) * a.K + 128 * t;
+        // pieces past the row end load the last piece again and are dropped
+#pragma unroll
+        for (int b = 0; b < 16; ++b) v[b] = ld16(src + 8 * min(b, nb - 1));
+      }
+      if (has) {
+        float sum = 0.f;
+#pragma unroll
+        for (int b = 0; b < 16; ++b)
+          if (b < nb) to_lds(v[b], t, b, jr, sum);
+        if (BIAS) csum[t * 16 + jr] = 136.0f * sum;
+      }
+    } else {
+      const int task = tid;
+      const bool has = task < 2 * nr * ntiles;  // equal for both halves
+      const int hf = task & 1;
+      const int rt = task >> 1;
+      const int jr = rt / ntiles;
+      const int t = rt - jr * ntiles;
+      const int nb = min(16, K8 - 16 * t);
+      u32x4_t v[8];
+      if (has) {
+        const uint16_t* src = a.act + row_of(jr) * a.K + 128 * t;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) v[b] = ld16(src + 8 * min(8 * hf + b, nb - 1));
+      }
+      float sum = 0.f;
+      if (has) {
+#pragma unroll
+        for (int b = 0; b < 8; ++b)
+          if (8 * hf + b < nb) to_lds(v[b], t, 8 * hf + b, jr, sum);
+      }
+      if (BIAS) {
+        // lanes 2i, 2i + 1 hold the halves; both add in the same order
+        const float other =
+            __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0xB1, 0xF, 0xF, false));
+        const float tot = hf == 0 ? sum + other : other + sum;
+        if (has && hf == 0) csum[t * 16 + jr] = 136.0f * tot;
+      }
     }
     __syncthreads();
   };
