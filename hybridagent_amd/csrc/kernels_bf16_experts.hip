@@ -7,15 +7,18 @@
 //                   (backends.py:224-232, 243-252, 274-276), rows s in segment order
 //   MODE = down   : dn[sorted_pos[s]] = bf16(inter[s] W_d^T)   (:234-237, 254-259, 277)
 //
-// then k_combine forms the weighted top-k sum.  Grid (column tile, active
-// expert slot); a workgroup whose slot is past the active count leaves at
-// once.  Its eight wavefronts split K (the weights stream once per chunk of
-// 16, 32 or 64 rows of the expert's segment, sized from the mean rows per
-// expert, read through 16-byte loads, every load of a
-// 12-step chunk of k issued before its first MFMA), the partial tiles are
-// summed in LDS in wavefront order, and the epilogue writes bf16 rows.
-// gate_up tiles pair 8 gate columns with the same 8 up columns, so the gated
-// GELU is formed in registers.
+// then k_combine forms the weighted top-k sum.  Grid (group of CB column
+// blocks, active expert slot); a workgroup whose slot is past the active
+// count leaves at once.  Its eight wavefronts are CB column blocks x KS = 8 /
+// CB ranges of K: each streams its block's weights over its K range (16-byte
+// loads, every load of a 12-step chunk of k issued before its first MFMA)
+// once per chunk of 16, 32 or 64 rows of the expert's segment (sized from
+// the mean rows per expert); the KS partial tiles of a block are summed in
+// LDS in K order and the epilogue writes bf16 rows.  gate_up blocks pair 8
+// gate columns with the same 8 up columns, so the gated GELU is formed in
+// registers.  Several blocks per workgroup amortise its fixed costs (the
+// row positions, the reduction, the epilogue) over more weight bytes: down
+// (K = 704) takes 4 blocks of 2 K ranges, gate_up 2 blocks of 4.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -29,9 +32,11 @@ constexpr int kBfMaxSteps = 12;  // 32-wide k steps per wavefront per chunk
 }  // namespace
 
 // MT: 16-row m-tiles per row chunk, chosen from the expected rows per expert
-// (the activation fragments of a chunk live in registers: 48 MT VGPRs)
-template <int MODE, int MT>
+// (the activation fragments of a chunk live in registers: 48 MT VGPRs);
+// CB: column blocks per workgroup (KS = 8 / CB wavefronts per block split K)
+template <int MODE, int MT, int CB>
 __global__ __launch_bounds__(64 * kBfWaves) void k_bf16_expert(Bf16ExpertArgs a) {
+  constexpr int KS = kBfWaves / CB;
   __shared__ f32x4_t red[kBfWaves][MT][64];
   __shared__ int rowsrc[16 * MT];
   const int slot = blockIdx.y;
@@ -41,16 +46,19 @@ __global__ __launch_bounds__(64 * kBfWaves) void k_bf16_expert(Bf16ExpertArgs a)
   const int rows = ld_uniform(a.desc, 4 * slot + 2);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int cb = wave / KS, ks = wave - cb * KS;
   const int j = lane & 15, kb = lane >> 4;
   constexpr bool GU = MODE == kModeGateUp;
-  // gate_up: lanes j < 8 take gate row n0 + j, lanes j >= 8 up row I + n0 + j - 8
-  const int n0 = blockIdx.x * (GU ? 8 : 16);
+  const int ncols = GU ? a.I : a.N;  // output columns
+  // this wavefront's block: gate_up lanes j < 8 take gate row n0 + j, lanes
+  // j >= 8 up row I + n0 + j - 8; blocks past the matrix read its last row
+  // and store nothing
+  const int n0 = (blockIdx.x * CB + cb) * (GU ? 8 : 16);
   const int K = a.K;
   const int nsteps = K >> 5;
-  const int per = (nsteps + kBfWaves - 1) / kBfWaves;
-  const int c0 = wave * per;
+  const int per = (nsteps + KS - 1) / KS;
+  const int c0 = ks * per;
   const int c1 = min(nsteps, c0 + per);
-  const int ncols = GU ? a.I : a.N;  // output columns
   const int wr = GU ? (j < 8 ? n0 + j : a.I + n0 + (j - 8)) : n0 + j;
   const uint16_t* wrow = a.W + ((int64_t)e * a.N + min(wr, a.N - 1)) * K + 8 * kb;
   for (int r0 = 0; r0 < rows; r0 += 16 * MT) {
@@ -68,9 +76,9 @@ __global__ __launch_bounds__(64 * kBfWaves) void k_bf16_expert(Bf16ExpertArgs a)
     f32x4_t acc[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    for (int cb = c0; cb < c1; cb += kBfMaxSteps) {
-      const int ce = min(c1, cb + kBfMaxSteps);
-      auto step_at = [&](int c) { return min(cb + c, ce - 1); };
+    for (int cc = c0; cc < c1; cc += kBfMaxSteps) {
+      const int ce = min(c1, cc + kBfMaxSteps);
+      auto step_at = [&](int c) { return min(cc + c, ce - 1); };
       u32x4_t wv[kBfMaxSteps];
 #pragma unroll
       for (int c = 0; c < kBfMaxSteps; ++c) wv[c] = ld16(wrow + 32 * step_at(c));
@@ -81,7 +89,7 @@ __global__ __launch_bounds__(64 * kBfWaves) void k_bf16_expert(Bf16ExpertArgs a)
         for (int i = 0; i < MT; ++i) av[c][i] = ld16(xrow[i] + 32 * step_at(c));
 #pragma unroll
       for (int c = 0; c < kBfMaxSteps; ++c) {
-        if (cb + c < ce) {
+        if (cc + c < ce) {
 #pragma unroll
           for (int i = 0; i < MT; ++i) acc[i] = mfma16(av[c][i], wv[c], acc[i]);
         }
@@ -90,12 +98,12 @@ __global__ __launch_bounds__(64 * kBfWaves) void k_bf16_expert(Bf16ExpertArgs a)
 #pragma unroll
     for (int i = 0; i < MT; ++i) red[wave][i][lane] = acc[i];
     __syncthreads();
-    // wavefront w < MT finishes m-tile w: partials summed in wavefront order
-    if (wave < MT) {
-      const int i = wave;
-      f32x4_t t = red[0][i][lane];
+    // wavefront (cb, ks) finishes m-tiles i = ks, ks + KS, ... of its block:
+    // the block's partials summed in K order
+    for (int i = ks; i < MT; i += KS) {
+      f32x4_t t = red[cb * KS][i][lane];
 #pragma unroll
-      for (int w = 1; w < kBfWaves; ++w) t += red[w][i][lane];
+      for (int w = 1; w < KS; ++w) t += red[cb * KS + w][i][lane];
       if (GU) {
         float up[4];
 #pragma unroll
@@ -129,7 +137,9 @@ __global__ __launch_bounds__(64 * kBfWaves) void k_bf16_expert(Bf16ExpertArgs a)
 hipError_t launch_bf16_experts(int mode, Bf16ExpertArgs a, int max_slots, hipStream_t s) {
   if (max_slots <= 0) return hipSuccess;
   if (a.K % 32 != 0 || a.K <= 0 || max_slots > 65535) return hipErrorInvalidValue;
-  const int cols = mode == kModeGateUp ? 8 : 16;
+  // column blocks per workgroup: down 4 (K splits of 2), gate_up 2 (of 4)
+  const int cbk = mode == kModeGateUp ? 2 : 4;
+  const int cols = (mode == kModeGateUp ? 8 : 16) * cbk;
   const int ncols = mode == kModeGateUp ? a.I : a.N;
   const dim3 grid((ncols + cols - 1) / cols, (unsigned)max_slots), block(64 * kBfWaves);
   // rows per expert on average: M * topk / E (the sort's segments)
@@ -137,9 +147,9 @@ hipError_t launch_bf16_experts(int mode, Bf16ExpertArgs a, int max_slots, hipStr
 #define W4A16_BF(MT_)                                                                   \
   do {                                                                                  \
     if (mode == kModeGateUp)                                                            \
-      hipLaunchKernelGGL((k_bf16_expert<kModeGateUp, MT_>), grid, block, 0, s, a);      \
+      hipLaunchKernelGGL((k_bf16_expert<kModeGateUp, MT_, 2>), grid, block, 0, s, a);   \
     else                                                                                \
-      hipLaunchKernelGGL((k_bf16_expert<kModeDown, MT_>), grid, block, 0, s, a);        \
+      hipLaunchKernelGGL((k_bf16_expert<kModeDown, MT_, 4>), grid, block, 0, s, a);     \
   } while (0)
   if (avg <= 16)
     W4A16_BF(1);
