@@ -285,12 +285,13 @@ void k_decode(DecodeArgs a) {
   // fragment order, and -- for the bias form -- summed into
   // csum[t][row] = 136 * (sum of the row's tile elements), the correction the
   // bias form subtracts per group.  Each task is split over two threads.  `first` runs
-  // before anything else: the first pass issues the weight prologue there,
-  // as early as the expert is known, so the first items' weights (the bulk
-  // of the start-up traffic) are in flight while the row positions and the
-  // activations are fetched.
+  // right after the activation loads are issued: the first pass issues the
+  // weight prologue there.  Loads complete in order, so waiting for the
+  // activations then does not wait for the first items' weights (at kernel
+  // start every CU requests those at once); the stage completes while they
+  // stream in, and the first item's MFMAs -- and the refills for the next
+  // item -- start as soon as its weights land.
   auto stage = [&](int mc, int nr, auto&& first) {
-    first();
     __syncthreads();  // previous readers of lds_a / csum / tok are done
     // gate_up: token of each staged row; down: the output row t*k+j of each
     // staged row (read here once, so the epilogue issues no load: a load
@@ -346,6 +347,7 @@ void k_decode(DecodeArgs a) {
 #pragma unroll
         for (int b = 0; b < 16; ++b) v[b] = ld16(src + 8 * min(b, nb - 1));
       }
+      first();
       if (has) {
         float sum = 0.f;
 #pragma unroll
@@ -367,6 +369,7 @@ void k_decode(DecodeArgs a) {
 #pragma unroll
         for (int b = 0; b < 8; ++b) v[b] = ld16(src + 8 * min(8 * hf + b, nb - 1));
       }
+      first();
       float sum = 0.f;
       if (has) {
 #pragma unroll
@@ -555,7 +558,7 @@ void k_decode(DecodeArgs a) {
     }
     }
   };
-  // The first pass issues the weight prologue before its staging; later
+  // The first pass issues the weight prologue during its staging; later
   // passes find the next items' weights in flight (the refills of a pass's
   // last items load its first items again).  (Folding the first pass into
   // the loop of the later ones was measured twice as slow at decode sizes:
