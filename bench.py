@@ -641,8 +641,10 @@ def g32_leg(dev, args):
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=64)
-    ap.add_argument("--warmup", type=int, default=16)
+    # layer calls per M; multiples of the 24 rotated layers each graph replay
+    # issues, so exactly K calls are timed after W untimed ones
+    ap.add_argument("--steps", type=int, default=480)
+    ap.add_argument("--warmup", type=int, default=96)
     ap.add_argument("--layers", type=int, default=24,
                     help="independent decode layer copies cycled per graph (24 x 393 MB: at M = 1 the "
                          "8 experts of each copy add up to 590 MB, above twice the 256 MB Infinity Cache)")
