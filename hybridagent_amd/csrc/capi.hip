@@ -348,6 +348,17 @@ inline bool use_prefill(int64_t M, int64_t H, int64_t I) {
   return M > kDecodeMaxM && H % 128 == 0 && I % 64 == 0;
 }
 
+// the exact-form prefill GEMM serves group sizes that are powers of two
+// >= 32; the bias form and the older exact kernel the rest
+inline bool x_prefill(int64_t M, int64_t H, int64_t I, int64_t G) {
+  return use_prefill(M, H, I) && prefill_x_supported(H, I, G);
+}
+
+// m-tile of the prefill tile list the expert sort writes
+inline int plan_bm(int64_t M, int64_t H, int64_t I, int64_t G) {
+  return x_prefill(M, H, I, G) ? kPrefillXBM : kPrefillBM;
+}
+
 // gate_up and down take the same form (the intermediate layout differs)
 inline bool bias_prefill(int64_t H, int64_t I, int64_t G) {
   return G % 128 == 0 && prefill_bias_supported((int)((H + G - 1) / G)) &&
@@ -369,9 +380,15 @@ PrefillArgs prefill_args(const MoeLayout& L, int64_t M, int64_t top_k, int64_t I
 
 // most m-tiles the sort can emit: one partial tile per active expert plus
 // the full ones
-inline int max_mtiles(int64_t M, int64_t top_k, int64_t E) {
+inline int max_mtiles(int64_t M, int64_t top_k, int64_t E, int bm = kPrefillBM) {
   const int64_t rows = M * top_k;
-  return (int)(rows / kPrefillBM + (rows < E ? rows : E));
+  return (int)(rows / bm + (rows < E ? rows : E));
+}
+
+inline int log2_int(int64_t v) {
+  int r = 0;
+  while ((int64_t(1) << (r + 1)) <= v) ++r;
+  return r;
 }
 
 DecodeArgs expert_args(const MoeLayout& L, int64_t M, int64_t top_k, int64_t I, int64_t G) {
@@ -401,12 +418,13 @@ int moe_plan(const uint16_t* hidden, const int64_t* topk_idx, int64_t M, int64_t
   if (!hidden || !topk_idx) return W4A16_ERR_NULL;
   if (!aligned16(hidden)) return W4A16_ERR_ALIGN;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const int bm = plan_bm(M, H, I, group_size);
   hipError_t e =
       M * top_k > kSortMultiMinRows
           ? launch_sort_multi(topk_idx, (int)M, (int)top_k, (int)E, L.sorted_pos, L.offsets,
-                              L.desc, L.counters, L.tiles, L.blockcnt, kPrefillBM, s)
+                              L.desc, L.counters, L.tiles, L.blockcnt, bm, s, L.queues)
           : launch_sort(topk_idx, (int)M, (int)top_k, (int)E, L.sorted_pos, L.offsets, L.desc,
-                        L.counters, L.tiles, kPrefillBM, s);
+                        L.counters, L.tiles, bm, s, L.queues);
   return launch_status(e);
 }
 
@@ -419,6 +437,25 @@ int moe_gate_up(const uint16_t* hidden, const int32_t* gu_packed, const uint16_t
   if (!hidden || !gu_packed || !gu_scale) return W4A16_ERR_NULL;
   if (!aligned16(hidden) || !aligned16(gu_packed)) return W4A16_ERR_ALIGN;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (x_prefill(M, H, I, group_size)) {
+    // exact form: natural hidden rows in, natural intermediate rows out
+    PrefillArgs p = prefill_args(L, M, top_k, I, group_size);
+    p.act = hidden;
+    p.act_bytes = M * H * 2;
+    p.lda = (int)H;
+    p.wp = gu_packed;
+    p.ws = gu_scale;
+    p.out = L.inter;
+    p.ldo = (int)I;
+    p.N = (int)(2 * I);
+    p.K = (int)H;
+    p.ng = (int)((H + group_size - 1) / group_size);
+    p.gshift = log2_int(group_size);
+    p.rows_total = (int)(M * top_k);
+    p.n_nt = (int)((I + 127) / 128);  // 128 intermediate columns per item
+    p.queues = L.queues;
+    return launch_status(launch_prefill_x(kModeGateUp, p, max_mtiles(M, top_k, E, kPrefillXBM), s));
+  }
   if (use_prefill(M, H, I)) {
     PrefillArgs p = prefill_args(L, M, top_k, I, group_size);
     p.act = hidden;
@@ -470,6 +507,23 @@ int moe_down(const int32_t* dn_packed, const uint16_t* dn_scale, int64_t M, int6
   if (!dn_packed || !dn_scale) return W4A16_ERR_NULL;
   if (!aligned16(dn_packed)) return W4A16_ERR_ALIGN;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (x_prefill(M, H, I, group_size)) {
+    PrefillArgs p = prefill_args(L, M, top_k, I, group_size);
+    p.act = L.inter;
+    p.act_bytes = M * top_k * I * 2;
+    p.lda = (int)I;
+    p.wp = dn_packed;
+    p.ws = dn_scale;
+    p.out = L.dn;
+    p.N = (int)H;
+    p.K = (int)I;
+    p.ng = (int)((I + group_size - 1) / group_size);
+    p.gshift = log2_int(group_size);
+    p.rows_total = (int)(M * top_k);
+    p.n_nt = (int)((H + 255) / 256);  // 256 output columns per item
+    p.queues = L.queues + kPrefillQueueInts / 2;
+    return launch_status(launch_prefill_x(kModeDown, p, max_mtiles(M, top_k, E, kPrefillXBM), s));
+  }
   if (use_prefill(M, H, I)) {
     PrefillArgs p = prefill_args(L, M, top_k, I, group_size);
     p.act = L.inter;

@@ -723,7 +723,10 @@ hipError_t launch_router_topk(const float* partial, int ksplit, const uint16_t* 
 //   desc[4*u .. 4*u+3] = (expert, segment start, segment rows, 0) for the u-th
 //     active expert in ascending expert order
 //   counters[0] = number of active experts, counters[1] = number of prefill tiles
-//   tiles[i] = (expert << 16) | m_tile for the i-th (expert, m-tile) pair
+//   tiles[i] = (expert << 16) | m_tile for the i-th (expert, m-tile) pair:
+//     first every tile of more than BM / 2 rows (expert order), then the
+//     segment tails of at most BM / 2 rows (expert order), so work queues
+//     that hand tiles out in list order start with the large ones
 // ---------------------------------------------------------------------------
 constexpr int kSortThreads = 1024;
 constexpr int kSortWaves = kSortThreads / 64;
@@ -759,22 +762,27 @@ __device__ int write_plan(int c, int E, int32_t* __restrict__ offsets, int32_t* 
   const int off = block_excl_scan(c, wsum, &tot);
   int nact;
   const int apos = block_excl_scan(c > 0 ? 1 : 0, wsum, &nact);
-  const int nt = (c + BM - 1) / BM;
-  int ntiles;
-  const int tpos = block_excl_scan(nt, wsum, &ntiles);
+  const int rem = c % BM;
+  const int nsmall = (rem > 0 && rem <= BM / 2) ? 1 : 0;
+  const int nbig = (c + BM - 1) / BM - nsmall;
+  int nbig_tot, nsmall_tot;
+  const int bpos = block_excl_scan(nbig, wsum, &nbig_tot);
+  const int spos = block_excl_scan(nsmall, wsum, &nsmall_tot);
   if (write) {
     if (tid < E) offsets[tid] = off;
     if (tid == 0) {
       offsets[E] = tot;
       counters[0] = nact;
-      counters[1] = ntiles;
+      counters[1] = nbig_tot + nsmall_tot;
     }
     if (tid < E && c > 0) {
       const int4 d = make_int4(tid, off, c, 0);
       *reinterpret_cast<int4*>(desc + 4 * apos) = d;
     }
-    if (tid < E)
-      for (int i = 0; i < nt; ++i) tiles[tpos + i] = (tid << 16) | i;
+    if (tid < E) {
+      for (int i = 0; i < nbig; ++i) tiles[bpos + i] = (tid << 16) | i;
+      if (nsmall) tiles[nbig_tot + spos] = (tid << 16) | nbig;
+    }
   }
   return off;
 }
@@ -791,17 +799,21 @@ __device__ void plan_wave(const int* cnt, int* run, int E, int32_t* __restrict__
   const int lane = threadIdx.x & 63;
   const int pe = (E + 63) >> 6;
   int c[PE];
-  int cs = 0, as = 0, ts = 0;
+  int cs = 0, as = 0, bs = 0, ss = 0;
+  auto n_small = [&](int cc) { const int rem = cc % BM; return (rem > 0 && rem <= BM / 2) ? 1 : 0; };
 #pragma unroll
   for (int q = 0; q < PE; ++q) {
     const int e = lane * pe + q;
     c[q] = (q < pe && e < E) ? cnt[e] : 0;
     cs += c[q];
     as += c[q] > 0 ? 1 : 0;
-    ts += (c[q] + BM - 1) / BM;
+    ss += n_small(c[q]);
+    bs += (c[q] + BM - 1) / BM - n_small(c[q]);
   }
-  const int ci = wave_incl_scan(cs, lane), ai = wave_incl_scan(as, lane), ti = wave_incl_scan(ts, lane);
-  int off = ci - cs, apos = ai - as, tpos = ti - ts;
+  const int ci = wave_incl_scan(cs, lane), ai = wave_incl_scan(as, lane);
+  const int bi = wave_incl_scan(bs, lane), si = wave_incl_scan(ss, lane);
+  const int nbig_tot = __builtin_amdgcn_readlane(bi, 63);
+  int off = ci - cs, apos = ai - as, bpos = bi - bs, spos = nbig_tot + si - ss;
 #pragma unroll
   for (int q = 0; q < PE; ++q) {
     const int e = lane * pe + q;
@@ -812,16 +824,18 @@ __device__ void plan_wave(const int* cnt, int* run, int E, int32_t* __restrict__
         *reinterpret_cast<int4*>(desc + 4 * apos) = make_int4(e, off, c[q], 0);
         ++apos;
       }
-      const int nt = (c[q] + BM - 1) / BM;
-      for (int i = 0; i < nt; ++i) tiles[tpos + i] = (e << 16) | i;
-      tpos += nt;
+      const int sm = n_small(c[q]);
+      const int nb = (c[q] + BM - 1) / BM - sm;
+      for (int i = 0; i < nb; ++i) tiles[bpos + i] = (e << 16) | i;
+      bpos += nb;
+      if (sm) tiles[spos++] = (e << 16) | nb;
       off += c[q];
     }
   }
   if (lane == 63) {
     offsets[E] = ci;
     counters[0] = ai;
-    counters[1] = ti;
+    counters[1] = bi + si;
   }
 }
 
@@ -918,7 +932,8 @@ __device__ void moe_sort_body(ExpertOf expert_of, int M, int topk, int E,
 __global__ __launch_bounds__(kSortThreads) void k_moe_sort(
     const int64_t* __restrict__ idx_in, int M, int topk, int E, int32_t* __restrict__ sorted_pos,
     int32_t* __restrict__ offsets, int32_t* __restrict__ desc, int32_t* __restrict__ counters,
-    int32_t* __restrict__ tiles, int BM) {
+    int32_t* __restrict__ tiles, int BM, int32_t* __restrict__ queues) {
+  if (queues != nullptr && threadIdx.x < kPrefillQueueInts) queues[threadIdx.x] = 0;
   moe_sort_body([&](int row) -> int64_t { return idx_in[row]; }, M, topk, E, sorted_pos, offsets,
                 desc, counters, tiles, BM);
 }
@@ -1113,11 +1128,12 @@ __global__ __launch_bounds__(kSortThreads) void k_sort_hist(const int64_t* __res
 __global__ __launch_bounds__(kSortThreads) void k_sort_scatter(
     const int64_t* __restrict__ idx, int M, int topk, int E, const int32_t* __restrict__ blockcnt,
     int32_t* __restrict__ sorted_pos, int32_t* __restrict__ offsets, int32_t* __restrict__ desc,
-    int32_t* __restrict__ counters, int32_t* __restrict__ tiles, int BM) {
+    int32_t* __restrict__ counters, int32_t* __restrict__ tiles, int BM, int32_t* __restrict__ queues) {
   __shared__ int base[kMaxExperts];
   __shared__ int wcnt[kSortWaves][kMaxExperts];
   __shared__ int wsum[kSortWaves];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (queues != nullptr && blockIdx.x == 0 && tid < kPrefillQueueInts) queues[tid] = 0;
   const int b = blockIdx.x, nb = gridDim.x;
   // this thread's entry, loaded first so its latency overlaps the counts'
   const int total = M * topk;
@@ -1176,20 +1192,20 @@ int sort_blocks(int64_t rows) { return (int)((rows + kSortThreads - 1) / kSortTh
 
 hipError_t launch_sort_multi(const int64_t* idx, int M, int topk, int E, int32_t* sorted_pos,
                              int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
-                             int32_t* blockcnt, int BM, hipStream_t s) {
+                             int32_t* blockcnt, int BM, hipStream_t s, int32_t* queues) {
   const int nb = sort_blocks((int64_t)M * topk);
   if (nb <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_sort_hist, dim3(nb), dim3(kSortThreads), 0, s, idx, M, topk, E, blockcnt);
   hipLaunchKernelGGL(k_sort_scatter, dim3(nb), dim3(kSortThreads), 0, s, idx, M, topk, E, blockcnt,
-                     sorted_pos, offsets, desc, counters, tiles, BM);
+                     sorted_pos, offsets, desc, counters, tiles, BM, queues);
   return hipGetLastError();
 }
 
 hipError_t launch_sort(const int64_t* idx, int M, int topk, int E, int32_t* sorted_pos,
                        int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
-                       int BM, hipStream_t s) {
+                       int BM, hipStream_t s, int32_t* queues) {
   hipLaunchKernelGGL(k_moe_sort, dim3(1), dim3(kSortThreads), 0, s, idx, M, topk, E, sorted_pos,
-                     offsets, desc, counters, tiles, BM);
+                     offsets, desc, counters, tiles, BM, queues);
   return hipGetLastError();
 }
 

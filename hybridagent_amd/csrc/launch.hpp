@@ -13,6 +13,10 @@ constexpr int kMaxTopK = 32;
 // m-tile (token rows) and n-tile (weight rows) of the prefill grouped GEMM
 constexpr int kPrefillBM = 128;
 constexpr int kPfBN = 128;
+// m-tile of the exact-form prefill GEMM (kernels_prefill_x.hip)
+constexpr int kPrefillXBM = 256;
+// prefill work-queue counters in the MoE workspace: gate_up [0, 16), down [16, 32)
+constexpr int kPrefillQueueInts = 32;
 
 // Arguments of the decode-shaped (few rows per weight matrix) MFMA kernel.
 struct DecodeArgs {
@@ -59,9 +63,14 @@ struct PrefillArgs {
   // (chunk 4 kb + s of the tile stored at 4 s + kb); ldc = the tile stride
   // of the correction tables, which are [tile][segment row]
   int lda, ldo, ldc;
-  // bias form only: the work queues of this launch, 9 ints (one counter
-  // per XCD, then the count of workgroups that have left), zero at launch
+  // the work queues of this launch, 9 ints (one counter per XCD, then the
+  // count of workgroups that have left), zero at launch
   int32_t* queues;
+  // exact-form kernel: bytes of act (its buffer bound), log2 G and the
+  // routed rows (entries of sorted_pos)
+  int64_t act_bytes;
+  int gshift;
+  int rows_total;
 };
 
 enum DecodeMode { kModeDense = 0, kModeGateUp = 1, kModeDown = 2 };
@@ -89,15 +98,17 @@ hipError_t launch_add_rms_norm(const uint16_t* h, const uint16_t* delta, const u
                                hipStream_t s);
 hipError_t launch_combine(const uint16_t* dn, const int64_t* idx, const float* w, uint16_t* out,
                           int M, int topk, int E, int H, hipStream_t s);
+// The expert sort; with `queues` (nullable) it also zeroes the
+// kPrefillQueueInts prefill work-queue counters there.
 hipError_t launch_sort(const int64_t* idx, int M, int topk, int E, int32_t* sorted_pos,
                        int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
-                       int BM, hipStream_t s);
+                       int BM, hipStream_t s, int32_t* queues = nullptr);
 // the sort over several workgroups (large batches); blockcnt holds
 // sort_blocks(M * topk) * E ints
 int sort_blocks(int64_t rows);
 hipError_t launch_sort_multi(const int64_t* idx, int M, int topk, int E, int32_t* sorted_pos,
                              int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
-                             int32_t* blockcnt, int BM, hipStream_t s);
+                             int32_t* blockcnt, int BM, hipStream_t s, int32_t* queues = nullptr);
 hipError_t launch_router_norm(const uint16_t* h, const uint16_t* scale, float scalar_root,
                               float eps, uint16_t* r, int M, int H, hipStream_t s);
 hipError_t launch_router_logits(const uint16_t* r, const uint16_t* proj, float* partial, int M,
@@ -160,13 +171,16 @@ hipError_t launch_prefill(int mode, PrefillArgs a, int max_mtiles, hipStream_t s
 // ([K / 128][ldc]); K a multiple of 128
 // It also zeroes `queues` (kPrefillQueueInts ints: the gate_up and down
 // kernels' work queues).
-constexpr int kPrefillQueueInts = 32;
 hipError_t launch_prefill_prep(const uint16_t* x, uint16_t* xb, float* crx, int M, int K, int ldx,
                                const int32_t* sorted_pos, const int32_t* rows_total, int topk,
                                float* crs, int ldc, int32_t* queues, hipStream_t s);
 // the bias-form prefill kernels stage each item's scales in LDS: they take
 // an even number of scale groups per row, at most 24
 bool prefill_bias_supported(int ng);
+// the exact-form prefill GEMM (kernels_prefill_x.hip): H and I multiples of
+// 64, G a power of two >= 32; items of up to kPrefillXBM rows
+bool prefill_x_supported(int64_t H, int64_t I, int64_t G);
+hipError_t launch_prefill_x(int mode, PrefillArgs a, int max_mtiles, hipStream_t s);
 hipError_t launch_prefill_bias(int mode, PrefillArgs a, int max_mtiles, hipStream_t s);
 int prefill_grid_size(const void* kern, int threads, size_t lds, int max_items);
 
