@@ -28,27 +28,29 @@
 //      row, the aligned 16 bytes of its scales that hold this stage's
 //      group(s) (an aligned pair of bf16).
 // A ring of three stages keeps two in flight while one is multiplied, and
-// runs on across items: a workgroup's next item's first two stages load
-// during the current item's last two, and its epilogue runs while they
-// land.  Each
+// runs on across items: a workgroup issues its next item's first two stages
+// before the current item's epilogue, which runs while they land.  Each
 // lane dequantises the four packed words of its weight row that its four
 // MFMA steps need exactly as the reference does -- bf16_RNE(q * s),
 // q = u - 8 -- in registers; one B fragment feeds the MB MFMAs of its step.
 // The lane layout of an MFMA step: lane l holds row (col) l % 32 and the
 // 8 k of chunk 4 (l / 32) + s of the stage, for A and B alike.
 //
-// Epilogue: accumulators -> bf16 -> wavefront-private LDS rows (a region of
-// their own, apart from the ring) -> 16-byte stores; gate_up pairs each gate
-// column with its up column there and applies gelu_tanh(gate) * up with the
-// reference's bf16 rounding points.
+// The MFMAs compute D[weight row][activation row] (dequantised weights as
+// the A operand), so each lane ends with four consecutive output columns of
+// one activation row per register quad: the epilogue stores 8 bytes per
+// lane straight from registers; gate_up finds each gate column's up column
+// in the same lane and applies gelu_tanh(gate) * up with the reference's
+// bf16 rounding points.
 //
 // While direct LDS loads are in flight the kernel issues no other vector
 // memory load: row indices (gate_up: the next item's gathered token rows;
 // down: the current item's output rows) come into an LDS table by a direct
-// load of their own, one per stage (unused ones land in the junk block).
-// (A direct LDS load and an ordinary load issued after it need not
-// complete in that order, so a vmcnt wait counted for one could pass while
-// the other is outstanding.)
+// load of their own with the item's second-to-last stage.  (A direct LDS
+// load and an ordinary load issued after it need not complete in that
+// order, so a vmcnt wait counted for one could pass while the other is
+// outstanding.)  Each wavefront issues only the loads it needs; a stage's
+// wait counts the loads that wavefront issued after it.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -63,27 +65,42 @@ constexpr int kPxBN = 32 * kPxWaves;         // 256 weight rows per item
 constexpr int kPxKT = 64;                    // k per stage
 constexpr int kPxStages = 3;
 // LDS: the ring of stages, each A [256 rows][128 B] | B words [256 tile
-// rows][32 B] | scale chunks [256 tile rows][16 B]; then 1 KiB that unused
-// loads land in; the row-index table (512 ints from a 16-byte-aligned
-// start: sorted_pos[s & ~3 ..] for a segment starting at s); the epilogue
-// rows, 32 rows x 32 bf16 per wavefront
+// rows][32 B] | scale chunks [256 tile rows][16 B]; the row-index table
+// (512 ints from a 16-byte-aligned start: sorted_pos[s & ~3 ..] for a
+// segment starting at s); down's epilogue rows
 constexpr int kPxBOff = kPxBM * kPxKT * 2;
 constexpr int kPxSOff = kPxBOff + kPxBN * kPxKT / 2;
 constexpr int kPxStageBytes = kPxSOff + kPxBN * 16;
-constexpr int kPxJunk = kPxStages * kPxStageBytes;
-constexpr int kPxTable = kPxJunk + 1024;  // 512 row indices
+constexpr int kPxTable = kPxStages * kPxStageBytes;  // 512 row indices
+// down's epilogue rows: 32 rows x 32 bf16 per wavefront, rows 80 bytes
+// apart (the 8-byte writes of 32 rows spread over the banks)
 constexpr int kPxEpiOff = kPxTable + 2048;
-constexpr int kPxEpiBytes = 32 * 64;
+constexpr int kPxEpiPitch = 80;
+constexpr int kPxEpiBytes = 32 * kPxEpiPitch;
 constexpr int kPxLds = kPxEpiOff + kPxWaves * kPxEpiBytes;
-// direct A loads per wavefront and stage (tiles of fewer rows send the
-// unused ones to the junk block, so every stage counts the same loads),
-// then one B-word, one scale-pair and one row-index load
+// at most four direct A loads per wavefront and stage (fewer for tiles of
+// fewer rows), then one B-word load and one scale-chunk load (wavefronts
+// 0..3)
 constexpr int kPxNA = 4;
-constexpr int kPxLoads = kPxNA + 3;
+
 
 // s_waitcnt immediate for vmcnt <= n with expcnt and lgkmcnt not waited for
 // (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
 constexpr int px_vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// s_waitcnt vmcnt(n) for a wavefront-uniform n <= 7
+__device__ __forceinline__ void px_wait_vm(int n) {
+  switch (n) {
+    case 1: __builtin_amdgcn_s_waitcnt(px_vm_wait(1)); break;
+    case 2: __builtin_amdgcn_s_waitcnt(px_vm_wait(2)); break;
+    case 3: __builtin_amdgcn_s_waitcnt(px_vm_wait(3)); break;
+    case 4: __builtin_amdgcn_s_waitcnt(px_vm_wait(4)); break;
+    case 5: __builtin_amdgcn_s_waitcnt(px_vm_wait(5)); break;
+    case 6: __builtin_amdgcn_s_waitcnt(px_vm_wait(6)); break;
+    case 7: __builtin_amdgcn_s_waitcnt(px_vm_wait(7)); break;
+    default: __builtin_amdgcn_s_waitcnt(px_vm_wait(0)); break;
+  }
+}
 
 // Workgroup barrier for LDS data only: each wavefront waits for its own LDS
 // operations, then meets the others.  (__syncthreads() would also wait for
@@ -150,12 +167,13 @@ __device__ __forceinline__ PxItem px_item_info(const PrefillArgs& a, int xcd, in
   return it;
 }
 
-// A lane's load sources for one item (and the destinations, which are
-// wavefront-uniform).
+// A lane's load sources for one item; na = the wavefront's A loads per
+// stage, n = all its loads per stage (both wavefront-uniform).
 struct PxLoads {
   __amdgpu_buffer_rsrc_t wsrc, ssrc;
-  int avoff[kPxNA], adst[kPxNA];
-  int bvoff, svoff, sdst;
+  int avoff[kPxNA];
+  int bvoff, svoff;
+  int na, n;
 };
 
 // weight row of tile row tr of n-tile nt (gate_up: wavefront w's tile rows
@@ -183,17 +201,19 @@ __device__ __forceinline__ PxLoads px_loads(const PrefillArgs& a, const PxItem& 
   // row 8 j + l / 8 into LDS slot l % 8, i.e. chunk (l % 8) ^ ((row / 2) % 8)
   // of the row (rows past the segment repeat its last row).
   const int* table = reinterpret_cast<const int*>(smem + kPxTable);
+  L.na = 0;
 #pragma unroll
   for (int i = 0; i < kPxNA; ++i) {
     const int j = wave + 8 * i;
     const bool real = j < 4 * it.mb;
+    L.na += real ? 1 : 0;
     const int r = 8 * j + (lane >> 3);
     const int rr = min(r, it.nrows - 1);
     const int64_t src = MODE == kModeGateUp ? (real ? table[(it.seg0 & 3) + rr] : 0) / a.topk : it.seg0 + rr;
     const int chunk = (lane & 7) ^ ((r >> 1) & 7);
     L.avoff[i] = real ? (int)(src * a.lda * 2) + 16 * chunk : 0;
-    L.adst[i] = real ? j * 1024 : kPxJunk;
   }
+  L.n = L.na + 1 + (wave < 4 ? 1 : 0);
   // B words: instruction `wave` brings tile rows 32 wave .. + 31, lane l row
   // 32 wave + l / 2, bytes 16 (l % 2) of the stage's 32
   const int K2 = a.K >> 1;  // packed bytes per weight row
@@ -202,50 +222,58 @@ __device__ __forceinline__ PxLoads px_loads(const PrefillArgs& a, const PxItem& 
   L.bvoff = px_weight_row<MODE>(a, it.nt, 32 * wave + (lane >> 1)) * K2 + 16 * (lane & 1);
   // scale chunks: waves 0..3 bring tile rows 64 wave + l, the aligned 16
   // bytes holding the stage's scale pair (the stage adds 2 x the pair's
-  // group index, the lane rounds down to 16 bytes); waves 4..7 load one
-  // unused block.  The descriptor starts at the expert's scales rounded
-  // down to 16 bytes; svoff carries the difference.
+  // group index, the lane rounds down to 16 bytes).  The descriptor starts
+  // at the expert's scales rounded down to 16 bytes; svoff carries the
+  // difference.
   const uintptr_t sbase = reinterpret_cast<uintptr_t>(a.ws + (int64_t)it.e * a.N * a.ng);
   L.ssrc = make_rsrc(reinterpret_cast<const void*>(sbase & ~uintptr_t(15)), (uint32_t)a.N * a.ng * 2u + 16u);
   const bool sreal = wave < 4;
   L.svoff = sreal ? (int)(sbase & 15) + px_weight_row<MODE>(a, it.nt, 64 * wave + lane) * a.ng * 2 : 0;
-  L.sdst = sreal ? kPxSOff + 1024 * wave : kPxJunk;
   return L;
 }
 
-// The kPxLoads direct loads of stage kt of an item into ring slot `slot`;
-// with tseg >= 0 the last ones of wavefronts 0 and 1 bring the row indices
-// sorted_pos[tseg & ~3 ..] (512 entries; past the routed rows they read as
-// zero, readers clamp to the segment) into the LDS table, otherwise they
-// land in the junk block.
+// Part `part` (0..3, issued before MFMA step `part`) of the direct loads of
+// stage kt of an item into ring slot `slot`, L.n loads in all: part p brings
+// A load p (if this wavefront has one), part 0 also the B words, part 1 the
+// scale chunks.
 __device__ __forceinline__ void px_issue(const PrefillArgs& a, const PxLoads& L, unsigned char* smem, int kt,
-                                         int slot, int tseg) {
-  const int lane = threadIdx.x & 63;
+                                         int slot, int part) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   unsigned char* st = smem + slot * kPxStageBytes;
-#pragma unroll
-  for (int i = 0; i < kPxNA; ++i)
-    px_dma16(make_rsrc(a.act, (uint32_t)a.act_bytes), L.avoff[i], kt * (kPxKT * 2),
-             L.adst[i] == kPxJunk ? smem + kPxJunk : st + L.adst[i]);
-  px_dma16(L.wsrc, L.bvoff, kt * (kPxKT / 2), st + kPxBOff + wave * 1024);
-  const int gpair = ((kt * kPxKT) >> a.gshift) & ~1;
-  px_dma16(L.ssrc, (L.svoff + 2 * gpair) & ~15, 0, L.sdst == kPxJunk ? smem + kPxJunk : st + L.sdst);
-  {
-    const bool treal = tseg >= 0 && wave < 2;
-    const __amdgpu_buffer_rsrc_t tsrc = make_rsrc(a.sorted_pos, (uint32_t)a.rows_total * 4u);
-    px_dma16(tsrc, treal ? 4 * ((tseg & ~3) + 256 * wave + 4 * lane) : 0, 0,
-             treal ? smem + kPxTable + 1024 * wave : smem + kPxJunk);
+  if (part < L.na)
+    px_dma16(make_rsrc(a.act, (uint32_t)a.act_bytes), L.avoff[part], kt * (kPxKT * 2),
+             st + (wave + 8 * part) * 1024);
+  if (part == 0) px_dma16(L.wsrc, L.bvoff, kt * (kPxKT / 2), st + kPxBOff + wave * 1024);
+  if (part == 1 && wave < 4) {
+    const int gpair = ((kt * kPxKT) >> a.gshift) & ~1;
+    px_dma16(L.ssrc, (L.svoff + 2 * gpair) & ~15, 0, st + kPxSOff + 1024 * wave);
   }
 }
 
+__device__ __forceinline__ void px_issue_all(const PrefillArgs& a, const PxLoads& L, unsigned char* smem, int kt,
+                                             int slot) {
+#pragma unroll
+  for (int p = 0; p < 4; ++p) px_issue(a, L, smem, kt, slot, p);
+}
+
+// One direct load per wavefront: the row indices sorted_pos[tseg & ~3 ..]
+// (512 entries; past the routed rows they read as zero, readers clamp to the
+// segment) into the LDS table; wavefronts w and w + 2 bring the same part.
+__device__ __forceinline__ void px_issue_table(const PrefillArgs& a, unsigned char* smem, int tseg) {
+  const int lane = threadIdx.x & 63;
+  const int half = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 1;
+  px_dma16(make_rsrc(a.sorted_pos, (uint32_t)a.rows_total * 4u), 4 * ((tseg & ~3) + 256 * half + 4 * lane), 0,
+           smem + kPxTable + 1024 * half);
+}
+
 // Multiply one item.  On entry its stages 0 and 1 are issued into slots p0
-// and p0 + 1; with `first` stage 0 has not been waited for.  Its last two
-// iterations (peeled, so the next item's load sources are live only there)
-// issue the next item's stages 0 and 1 (or, when there is none, its own
-// last stage again, unused), so on return those are in flight.
+// and p0 + 1 (this wavefront's n_inflight loads each; gate_up: the LDS table
+// holds the item's rows).  After its last stage it issues the next item's
+// stages 0 and 1 (when has_next) and returns their per-stage load count;
+// the epilogue runs while they land.
 template <int MODE, int MB>
-__device__ __forceinline__ void px_run(const PrefillArgs& a, unsigned char* smem, const PxItem& it,
-                                       const PxItem& nx, bool has_next, int p0, bool first) {
+__device__ __forceinline__ int px_run(const PrefillArgs& a, unsigned char* smem, const PxItem& it,
+                                      const PxItem& nx, bool has_next, int p0, int n_inflight) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nkt = a.K / kPxKT;
@@ -286,19 +314,23 @@ __device__ __forceinline__ void px_run(const PrefillArgs& a, unsigned char* smem
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) af[mb] = *reinterpret_cast<const u32x4_t*>(st + mb * 4096 + aoff[s]);
   };
+  // D[weight row][activation row]: the dequantised weights are the MFMA's A
+  // operand, the activation rows its B operand
   auto mfmas = [&](const u32x4_t* af, u32x4_t bf) {
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) acc[mb] = mfma32x(af[mb], bf, acc[mb]);
+    for (int mb = 0; mb < MB; ++mb) acc[mb] = mfma32x(bf, af[mb], acc[mb]);
   };
   auto stage_ptr = [&](int sl) -> const unsigned char* { return smem + sl * kPxStageBytes; };
-  auto wait_and_sync = [&]() {
+  // the loads issued after the awaited stage: those of the stage issued in
+  // this iteration (n of them)
+  auto wait_and_sync = [&](int n) {
     __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(px_vm_wait(kPxLoads));
+    px_wait_vm(n);
     __builtin_amdgcn_sched_barrier(0);
     px_barrier();
   };
 
-  if (first) wait_and_sync();  // stage 0 landed (stage 1 may still be loading)
+  wait_and_sync(n_inflight);  // stage 0 landed (stage 1 may still be loading)
   // Software pipeline: each A fragment register is reloaded with the next
   // step's fragment right after the MFMA that reads it, and the next step's
   // B fragment is dequantised while the current step's MFMAs run.  Stage
@@ -317,8 +349,7 @@ __device__ __forceinline__ void px_run(const PrefillArgs& a, unsigned char* smem
   int slot2 = p0 + 2 >= kPxStages ? p0 + 2 - kPxStages : p0 + 2;
   // one k stage: refill the slot stage t - 1 used (issue(slot2)), multiply
   // stage t, wait for stage t + 1 and meet the other wavefronts
-  auto iter = [&](int t, auto issue) {
-    issue(slot2);
+  auto iter = [&](int t, int n, auto issue) {
     const int nslot = slot == kPxStages - 1 ? 0 : slot + 1;
     if (work) {
       const unsigned char* st = stage_ptr(slot);
@@ -327,22 +358,24 @@ __device__ __forceinline__ void px_run(const PrefillArgs& a, unsigned char* smem
       u32x4_t bf = dequant_word(wv[0], sc, m8);
 #pragma unroll
       for (int s2 = 0; s2 < 3; ++s2) {
+        issue(slot2, s2);
         const u32x4_t bfn = dequant_word(wv[s2 + 1], sc, m8);
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
-          acc[mb] = mfma32x(af[mb], bf, acc[mb]);
+          acc[mb] = mfma32x(bf, af[mb], acc[mb]);
           af[mb] = *reinterpret_cast<const u32x4_t*>(st + mb * 4096 + aoff[s2 + 1]);
         }
         bf = bfn;
       }
-      wait_and_sync();  // stage t + 1 landed (stage t + 2 may still be loading)
+      issue(slot2, 3);
+      wait_and_sync(n);  // stage t + 1 landed (stage t + 2 may still be loading)
       if (t + 1 < nkt) {
         const unsigned char* sn = stage_ptr(nslot);
         bw = *reinterpret_cast<const u32x4_t*>(sn + boff);
         const uint32_t sp = *reinterpret_cast<const uint32_t*>(sn + soff_of(t + 1));
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
-          acc[mb] = mfma32x(af[mb], bf, acc[mb]);
+          acc[mb] = mfma32x(bf, af[mb], acc[mb]);
           af[mb] = *reinterpret_cast<const u32x4_t*>(sn + mb * 4096 + aoff[0]);
         }
         sc = scale_of(t + 1, sp);
@@ -350,102 +383,95 @@ __device__ __forceinline__ void px_run(const PrefillArgs& a, unsigned char* smem
         mfmas(af, bf);
       }
     } else {
-      wait_and_sync();
+#pragma unroll
+      for (int p = 0; p < 4; ++p) issue(slot2, p);
+      wait_and_sync(n);
     }
     slot = nslot;
     slot2 = slot2 == kPxStages - 1 ? 0 : slot2 + 1;
   };
-  // the row-index table: gate_up loads the next item's rows with stage
-  // nkt - 2 (issued in iteration nkt - 4, landed before iteration nkt - 2
-  // builds the next item's load sources); down loads its own output rows with
-  // stage 3 (iteration 1: every wavefront is past the previous epilogue)
-  auto table_seg = [&](int t) -> int {
-    if (MODE == kModeGateUp) return (t == nkt - 4 && has_next) ? nx.seg0 : -1;
-    return t == 1 ? seg0 : -1;
-  };
   {
     const PxLoads lc = px_loads<MODE>(a, it, smem);
-    for (int t = 0; t + 2 < nkt; ++t) iter(t, [&](int sl) { px_issue(a, lc, smem, t + 2, sl, table_seg(t)); });
-    if (!has_next) {
-      iter(nkt - 2, [&](int sl) { px_issue(a, lc, smem, nkt - 1, sl, -1); });
-      iter(nkt - 1, [&](int sl) { px_issue(a, lc, smem, nkt - 1, sl, -1); });
-    }
+    for (int t = 0; t + 2 < nkt; ++t) iter(t, lc.n, [&](int sl, int p) { px_issue(a, lc, smem, t + 2, sl, p); });
   }
+  // the last two stages issue no stage loads; the second-to-last brings the
+  // row-index table (gate_up: the next item's rows, for its load sources;
+  // down: this item's output rows, for its epilogue)
+  const int tseg = MODE == kModeGateUp ? (has_next ? nx.seg0 : seg0) : seg0;
+  iter(nkt - 2, 1, [&](int, int p) {
+    if (p == 0) px_issue_table(a, smem, tseg);
+  });
+  iter(nkt - 1, 0, [&](int, int) {});
+  // every wavefront is past the last barrier: the next item's first two
+  // stages go into the slots of this item's stages nkt - 3 and nkt - 2
+  int n_next = 0;
   if (has_next) {
     const PxLoads ln = px_loads<MODE>(a, nx, smem);
-    iter(nkt - 2, [&](int sl) { px_issue(a, ln, smem, 0, sl, -1); });
-    iter(nkt - 1, [&](int sl) { px_issue(a, ln, smem, 1, sl, -1); });
+    const int q0 = (p0 + nkt) % kPxStages;
+    px_issue_all(a, ln, smem, 0, q0);
+    px_issue_all(a, ln, smem, 1, q0 == kPxStages - 1 ? 0 : q0 + 1);
+    n_next = ln.n;
   }
-  if (!work) return;
+  if (!work) return n_next;
 
-  // ---- epilogue, in passes of 32 rows (one m-block).  Lane l holds
-  // column c of block mb at rows 32 mb + 8 (q / 4) + 4 h + q % 4
-  // (q = 0..15).  Each wavefront writes its rows x 32 columns as bf16 into
-  // its own 64-byte LDS rows, then reads 16 bytes per lane back for the
-  // global stores (it reads only what it wrote: no barrier).  The region is
-  // not part of the ring, so the next item's stages land meanwhile.
-  constexpr int HB = 1;  // m-blocks per pass
-  constexpr int PR = 32 * HB;          // rows per pass
-  uint16_t* ob = reinterpret_cast<uint16_t*>(smem + kPxEpiOff + wave * kPxEpiBytes);
+  // ---- epilogue.  Lane l holds, for activation row 32 mb + c of block mb,
+  // the wavefront's weight rows 8 J + 4 h + i in acc[mb][4 J + i] (J, i =
+  // 0..3): four consecutive output columns per J.  gate_up stores them as 8
+  // bytes from registers: weight rows 0..15 are the gate rows and 16..31
+  // their up rows, so acc[mb][q] (gate) pairs with acc[mb][q + 8] (up).
 #pragma unroll
-  for (int p = 0; p < MB / HB; ++p) {
+  for (int mb = 0; mb < MB && MODE == kModeGateUp; ++mb) {
+    const int grow = 32 * mb + c;
+    if (grow >= nrows) continue;
+    {
+      uint16_t* orow = a.out + (int64_t)(seg0 + grow) * a.ldo + 128 * nt + 16 * wave + 4 * h;
 #pragma unroll
-    for (int mb = 0; mb < HB; ++mb)
+      for (int J = 0; J < 2; ++J) {
+        float hv[4];
 #pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        const int row = 32 * mb + 8 * (q >> 2) + 4 * h + (q & 3);
-        ob[row * 32 + c] = f32_to_bf16_bits(acc[p * HB + mb][q]);
-      }
-    if (MODE == kModeGateUp) {
-      // row r, half hp: gate columns 8 hp .. 8 hp + 7 (bytes 16 hp) and
-      // their up columns (bytes 32 + 16 hp) -> 8 intermediate values
-#pragma unroll
-      for (int itr = 0; itr < PR * 2 / 64; ++itr) {
-        const int idx = lane + 64 * itr;
-        const int row = idx >> 1, hp = idx & 1;
-        const u32x4_t gv = *reinterpret_cast<const u32x4_t*>(ob + row * 32 + 8 * hp);
-        const u32x4_t uv = *reinterpret_cast<const u32x4_t*>(ob + row * 32 + 16 + 8 * hp);
-        const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
-        uint32_t hw[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float g0 = bf16_bits_to_f32(gw[q] & 0xFFFFu), g1 = bf16_bits_to_f32(gw[q] >> 16);
-          const float u0 = bf16_bits_to_f32(uw[q] & 0xFFFFu), u1 = bf16_bits_to_f32(uw[q] >> 16);
-          hw[q] = pack_bf16x2(round_bf16(gelu_tanh_f32(g0)) * u0, round_bf16(gelu_tanh_f32(g1)) * u1);
+        for (int i = 0; i < 4; ++i) {
+          const float g = round_bf16(acc[mb][4 * J + i]);
+          const float u = round_bf16(acc[mb][4 * J + i + 8]);
+          hv[i] = round_bf16(gelu_tanh_f32(g)) * u;
         }
-        const int grow = PR * p + row;
-        if (grow < nrows)
-          st16(a.out + (int64_t)(seg0 + grow) * a.ldo + 128 * nt + 16 * wave + 8 * hp,
-               u32x4_t{hw[0], hw[1], hw[2], hw[3]});
+        *reinterpret_cast<uint2*>(orow + 8 * J) = make_uint2(pack_bf16x2(hv[0], hv[1]), pack_bf16x2(hv[2], hv[3]));
       }
-    } else {
-      // output rows: dn row sorted_pos[seg0 + row], from the LDS table
-      const int* table = reinterpret_cast<const int*>(smem + kPxTable);
+    }
+  }
+  if (MODE == kModeDown) {
+    // dn rows are long (N columns, rows scattered by sorted_pos): the
+    // wavefront's 32 columns of each row go out as 16-byte stores, through
+    // LDS one m-block at a time (it reads only what it wrote: no barrier)
+    const int* table = reinterpret_cast<const int*>(smem + kPxTable);
+    unsigned char* ob = smem + kPxEpiOff + wave * kPxEpiBytes;
 #pragma unroll
-      for (int itr = 0; itr < PR * 4 / 64; ++itr) {
+    for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+      for (int J = 0; J < 4; ++J)
+        *reinterpret_cast<uint2*>(ob + c * kPxEpiPitch + 2 * (8 * J + 4 * h)) =
+            make_uint2(pack_bf16x2(acc[mb][4 * J], acc[mb][4 * J + 1]), pack_bf16x2(acc[mb][4 * J + 2], acc[mb][4 * J + 3]));
+#pragma unroll
+      for (int itr = 0; itr < 2; ++itr) {
         const int idx = lane + 64 * itr;
         const int row = idx >> 2, q4 = idx & 3;
-        const int grow = PR * p + row;
+        const int grow = 32 * mb + row;
         if (grow < nrows) {
-          const u32x4_t v = *reinterpret_cast<const u32x4_t*>(ob + row * 32 + 8 * q4);
+          const u32x4_t v = *reinterpret_cast<const u32x4_t*>(ob + row * kPxEpiPitch + 16 * q4);
           st16(a.out + (int64_t)table[(seg0 & 3) + grow] * a.N + kPxBN * nt + 32 * wave + 8 * q4, v);
         }
       }
     }
   }
+  return n_next;
 }
 
 template <int MODE>
-__device__ __forceinline__ void px_dispatch(const PrefillArgs& a, unsigned char* smem, const PxItem& it,
-                                            const PxItem& nx, bool has_next, int p0, bool first) {
-  if (it.mb == 8)
-    px_run<MODE, 8>(a, smem, it, nx, has_next, p0, first);
-  else if (it.mb == 4)
-    px_run<MODE, 4>(a, smem, it, nx, has_next, p0, first);
-  else if (it.mb == 2)
-    px_run<MODE, 2>(a, smem, it, nx, has_next, p0, first);
-  else
-    px_run<MODE, 1>(a, smem, it, nx, has_next, p0, first);
+__device__ __forceinline__ int px_dispatch(const PrefillArgs& a, unsigned char* smem, const PxItem& it,
+                                           const PxItem& nx, bool has_next, int p0, int n_inflight) {
+  if (it.mb == 8) return px_run<MODE, 8>(a, smem, it, nx, has_next, p0, n_inflight);
+  if (it.mb == 4) return px_run<MODE, 4>(a, smem, it, nx, has_next, p0, n_inflight);
+  if (it.mb == 2) return px_run<MODE, 2>(a, smem, it, nx, has_next, p0, n_inflight);
+  return px_run<MODE, 1>(a, smem, it, nx, has_next, p0, n_inflight);
 }
 
 // Persistent grid, one workgroup per CU; workgroup b of XCD x = b % 8 takes
@@ -476,23 +502,23 @@ void k_prefill_x(PrefillArgs a) {
     __builtin_amdgcn_s_waitcnt(px_vm_wait(0));
     px_barrier();
   }
+  int n_inflight;
   {
     const PxLoads lc = px_loads<MODE>(a, cur, smem);
-    px_issue(a, lc, smem, 0, 0, -1);
-    px_issue(a, lc, smem, 1, 1, -1);
+    px_issue_all(a, lc, smem, 0, 0);
+    px_issue_all(a, lc, smem, 1, 1);
+    n_inflight = lc.n;
   }
   int p0 = 0;
-  bool first = true;
   for (;;) {
     const int nitem = item + step;
     const bool has_next = nitem < it_end;
     const PxItem nxt = has_next ? px_item_info(a, xcd, nitem) : cur;
-    px_dispatch<MODE>(a, smem, cur, nxt, has_next, p0, first);
+    n_inflight = px_dispatch<MODE>(a, smem, cur, nxt, has_next, p0, n_inflight);
     if (!has_next) break;
     item = nitem;
     cur = nxt;
     p0 = (p0 + nkt) % kPxStages;
-    first = false;
   }
   // the loads issued past the last stage land before the workgroup leaves
   __builtin_amdgcn_s_waitcnt(px_vm_wait(0));
@@ -500,11 +526,11 @@ void k_prefill_x(PrefillArgs a) {
 
 size_t prefill_x_lds_bytes() { return (size_t)kPxLds; }
 
-// H and I multiples of the 64-wide stage, at least four stages; G a power of two >= 32 whose
+// H and I multiples of the 64-wide stage, at least three stages; G a power of two >= 32 whose
 // group counts per row are even for both matrices (a stage's scale pair is
 // one aligned dword)
 bool prefill_x_supported(int64_t H, int64_t I, int64_t G) {
-  if (H % kPxKT != 0 || I % kPxKT != 0 || H < 4 * kPxKT || I < 4 * kPxKT || G < 32 || (G & (G - 1)) != 0)
+  if (H % kPxKT != 0 || I % kPxKT != 0 || H < 3 * kPxKT || I < 3 * kPxKT || G < 32 || (G & (G - 1)) != 0)
     return false;
   const int64_t ng_h = (H + G - 1) / G, ng_i = (I + G - 1) / G;
   return ng_h % 2 == 0 && ng_i % 2 == 0;
