@@ -202,7 +202,7 @@ def dense_sweep(dev, steps, warmup):
 def prefill(dev, steps, warmup, n_layers, g: int = G, stages: bool = True):
     """the whole layer (router + sort + gate_up + down + combine) at
     M = 4096 with Zipf routing; with ``stages`` also the gate_up stage alone
-    (prefill prep + the grouped gate_up GEMM, the dominant kernel)."""
+    (the grouped gate_up GEMM, the dominant kernel)."""
     layers = [Layer(seed=9000 + 17 * i, dev=dev, zipf=True, g=g) for i in range(n_layers)]
     x = synth.zipf_activations(PREFILL_M, H, seed=9999, device=dev)
     _, idx = layers[0].route(x)
@@ -255,13 +255,13 @@ def counter_summary(path, key):
 
 def roofline_prefill(pre):
     """The prefill's dominant kernel against the bf16 MFMA peak: the gate_up
-    stage (k_prefill_prep + k_prefill_cr_gather + k_prefill_bias<gateup>; the
-    GEMM is all but a few us of it), algorithmic flops 2 * 4096 * 8 * 2816 *
-    1408 per launch over its HIP-event time."""
+    stage (one launch of k_prefill_x<gateup>, the exact-form grouped GEMM),
+    algorithmic flops 2 * 4096 * 8 * 2816 * 1408 per launch over its HIP-event
+    time."""
     st = pre["gate_up_stage"]
     return {
         "bound": "mfma",
-        "kernel": "k_prefill_bias<gateup> (moe_gate_up stage, prep included)",
+        "kernel": "k_prefill_x<gateup> (moe_gate_up stage)",
         "M": PREFILL_M,
         "achieved": round(st["tflops"], 2),
         "peak": PEAK_BF16_TFLOPS,
