@@ -77,7 +77,9 @@ constexpr int kPxTable = kPxStages * kPxStageBytes;  // 512 row indices
 constexpr int kPxEpiOff = kPxTable + 2048;
 constexpr int kPxEpiPitch = 80;
 constexpr int kPxEpiBytes = 32 * kPxEpiPitch;
-constexpr int kPxLds = kPxEpiOff + kPxWaves * kPxEpiBytes;
+// the item index a workgroup takes from its XCD's queue (one int)
+constexpr int kPxQSlot = kPxEpiOff + kPxWaves * kPxEpiBytes;
+constexpr int kPxLds = kPxQSlot + 16;
 // at most four direct A loads per wavefront and stage (fewer for tiles of
 // fewer rows), then one B-word load and one scale-chunk load (wavefronts
 // 0..3)
@@ -271,11 +273,22 @@ __device__ __forceinline__ void px_issue_table(const PrefillArgs& a, unsigned ch
 // holds the item's rows).  After its last stage it issues the next item's
 // stages 0 and 1 (when has_next) and returns their per-stage load count;
 // the epilogue runs while they land.
-template <int MODE, int MB>
+// SPLIT (gate_up's last n-tile when I % 128 == 64: only wavefronts 0..3
+// have columns): wavefront w multiplies the weight rows of wavefront w % 4
+// with m-blocks MB (w / 4) .. + MB - 1 of the item's 2 MB, so all eight
+// wavefronts share the work instead of four idling.
+// With fetch_q (non-null) wavefront 0 takes an index from that queue
+// counter during the last stage (no stage load is issued after it, so the
+// stage's vmcnt(0) wait covers it) and leaves it in LDS at kPxQSlot.
+template <int MODE, int MB, bool SPLIT = false>
 __device__ __forceinline__ int px_run(const PrefillArgs& a, unsigned char* smem, const PxItem& it,
-                                      const PxItem& nx, bool has_next, int p0, int n_inflight) {
+                                      const PxItem& nx, bool has_next, int p0, int n_inflight,
+                                      int* fetch_q) {
+  static_assert(!SPLIT || MODE == kModeGateUp, "only gate_up has half n-tiles");
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wg = SPLIT ? (wave & 3) : wave;      // weight rows 32 wg .. of the tile
+  const int mo = SPLIT ? (wave >> 2) * MB : 0;   // first m-block
   const int nkt = a.K / kPxKT;
   const int h = lane >> 5;  // which half of the step's 16 k this lane holds
   const int c = lane & 31;  // row (A) / column (B) inside a 32-block
@@ -287,17 +300,17 @@ __device__ __forceinline__ int px_run(const PrefillArgs& a, unsigned char* smem,
   // tile row 32 wave + c
   int aoff[4];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) aoff[s] = c * 128 + 16 * ((4 * h + s) ^ ((c >> 1) & 7));
-  const int boff = kPxBOff + (32 * wave + c) * 32 + 16 * h;
+  for (int s = 0; s < 4; ++s) aoff[s] = mo * 4096 + c * 128 + 16 * ((4 * h + s) ^ ((c >> 1) & 7));
+  const int boff = kPxBOff + (32 * wg + c) * 32 + 16 * h;
   // the scale chunk of tile row 32 wave + c; the pair sits at byte
   // (2 (row ng + pair group)) % 16 of it
-  const int soff = kPxSOff + (32 * wave + c) * 16;
+  const int soff = kPxSOff + (32 * wg + c) * 16;
   const int srow2 = (int)(reinterpret_cast<uintptr_t>(a.ws + (int64_t)it.e * a.N * a.ng) & 15) +
-                    px_weight_row<MODE>(a, nt, 32 * wave + c) * a.ng * 2;
+                    px_weight_row<MODE>(a, nt, 32 * wg + c) * a.ng * 2;
   auto soff_of = [&](int t) -> int { return soff + ((srow2 + 2 * (((t * kPxKT) >> gshift) & ~1)) & 15); };
   // wavefronts whose columns lie past the matrix (gate_up's last n-tile
   // when I % 128 == 64) do no MFMA work and store nothing
-  const bool work = MODE == kModeGateUp ? 128 * nt + 16 * wave < a.I : kPxBN * nt + 32 * wave < a.N;
+  const bool work = SPLIT || (MODE == kModeGateUp ? 128 * nt + 16 * wave < a.I : kPxBN * nt + 32 * wave < a.N);
 
   f32x16_t acc[MB];
 #pragma unroll
@@ -323,14 +336,18 @@ __device__ __forceinline__ int px_run(const PrefillArgs& a, unsigned char* smem,
   auto stage_ptr = [&](int sl) -> const unsigned char* { return smem + sl * kPxStageBytes; };
   // the loads issued after the awaited stage: those of the stage issued in
   // this iteration (n of them)
-  auto wait_and_sync = [&](int n) {
+  auto no_hook = [] {};
+  // hook: runs after the wait, before the barrier (its LDS writes are seen
+  // by every wavefront after it)
+  auto wait_and_sync = [&](int n, auto hook) {
     __builtin_amdgcn_sched_barrier(0);
     px_wait_vm(n);
     __builtin_amdgcn_sched_barrier(0);
+    hook();
     px_barrier();
   };
 
-  wait_and_sync(n_inflight);  // stage 0 landed (stage 1 may still be loading)
+  wait_and_sync(n_inflight, no_hook);  // stage 0 landed (stage 1 may still be loading)
   // Software pipeline: each A fragment register is reloaded with the next
   // step's fragment right after the MFMA that reads it, and the next step's
   // B fragment is dequantised while the current step's MFMAs run.  Stage
@@ -349,7 +366,7 @@ __device__ __forceinline__ int px_run(const PrefillArgs& a, unsigned char* smem,
   int slot2 = p0 + 2 >= kPxStages ? p0 + 2 - kPxStages : p0 + 2;
   // one k stage: refill the slot stage t - 1 used (issue(slot2)), multiply
   // stage t, wait for stage t + 1 and meet the other wavefronts
-  auto iter = [&](int t, int n, auto issue) {
+  auto iter = [&](int t, int n, auto issue, auto hook) {
     const int nslot = slot == kPxStages - 1 ? 0 : slot + 1;
     if (work) {
       const unsigned char* st = stage_ptr(slot);
@@ -368,7 +385,7 @@ __device__ __forceinline__ int px_run(const PrefillArgs& a, unsigned char* smem,
         bf = bfn;
       }
       issue(slot2, 3);
-      wait_and_sync(n);  // stage t + 1 landed (stage t + 2 may still be loading)
+      wait_and_sync(n, hook);  // stage t + 1 landed (stage t + 2 may still be loading)
       if (t + 1 < nkt) {
         const unsigned char* sn = stage_ptr(nslot);
         bw = *reinterpret_cast<const u32x4_t*>(sn + boff);
@@ -385,14 +402,15 @@ __device__ __forceinline__ int px_run(const PrefillArgs& a, unsigned char* smem,
     } else {
 #pragma unroll
       for (int p = 0; p < 4; ++p) issue(slot2, p);
-      wait_and_sync(n);
+      wait_and_sync(n, hook);
     }
     slot = nslot;
     slot2 = slot2 == kPxStages - 1 ? 0 : slot2 + 1;
   };
   {
     const PxLoads lc = px_loads<MODE>(a, it, smem);
-    for (int t = 0; t + 2 < nkt; ++t) iter(t, lc.n, [&](int sl, int p) { px_issue(a, lc, smem, t + 2, sl, p); });
+    for (int t = 0; t + 2 < nkt; ++t)
+      iter(t, lc.n, [&](int sl, int p) { px_issue(a, lc, smem, t + 2, sl, p); }, no_hook);
   }
   // the last two stages issue no stage loads; the second-to-last brings the
   // row-index table (gate_up: the next item's rows, for its load sources;
@@ -400,8 +418,16 @@ __device__ __forceinline__ int px_run(const PrefillArgs& a, unsigned char* smem,
   const int tseg = MODE == kModeGateUp ? (has_next ? nx.seg0 : seg0) : seg0;
   iter(nkt - 2, 1, [&](int, int p) {
     if (p == 0) px_issue_table(a, smem, tseg);
-  });
-  iter(nkt - 1, 0, [&](int, int) {});
+  }, no_hook);
+  const bool fetch = fetch_q != nullptr && wave == 0;  // wavefront-uniform
+  int fv = 0;
+  iter(nkt - 1, 0,
+       [&](int, int p) {
+         if (p == 0 && fetch && lane == 0) fv = __hip_atomic_fetch_add(fetch_q, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+       },
+       [&] {
+         if (fetch && lane == 0) *reinterpret_cast<int*>(smem + kPxQSlot) = fv;
+       });
   // every wavefront is past the last barrier: the next item's first two
   // stages go into the slots of this item's stages nkt - 3 and nkt - 2
   int n_next = 0;
@@ -421,10 +447,10 @@ __device__ __forceinline__ int px_run(const PrefillArgs& a, unsigned char* smem,
   // their up rows, so acc[mb][q] (gate) pairs with acc[mb][q + 8] (up).
 #pragma unroll
   for (int mb = 0; mb < MB && MODE == kModeGateUp; ++mb) {
-    const int grow = 32 * mb + c;
+    const int grow = 32 * (mo + mb) + c;
     if (grow >= nrows) continue;
     {
-      uint16_t* orow = a.out + (int64_t)(seg0 + grow) * a.ldo + 128 * nt + 16 * wave + 4 * h;
+      uint16_t* orow = a.out + (int64_t)(seg0 + grow) * a.ldo + 128 * nt + 16 * wg + 4 * h;
 #pragma unroll
       for (int J = 0; J < 2; ++J) {
         float hv[4];
@@ -467,19 +493,36 @@ __device__ __forceinline__ int px_run(const PrefillArgs& a, unsigned char* smem,
 
 template <int MODE>
 __device__ __forceinline__ int px_dispatch(const PrefillArgs& a, unsigned char* smem, const PxItem& it,
-                                           const PxItem& nx, bool has_next, int p0, int n_inflight) {
-  if (it.mb == 8) return px_run<MODE, 8>(a, smem, it, nx, has_next, p0, n_inflight);
-  if (it.mb == 4) return px_run<MODE, 4>(a, smem, it, nx, has_next, p0, n_inflight);
-  if (it.mb == 2) return px_run<MODE, 2>(a, smem, it, nx, has_next, p0, n_inflight);
-  return px_run<MODE, 1>(a, smem, it, nx, has_next, p0, n_inflight);
+                                           const PxItem& nx, bool has_next, int p0, int n_inflight,
+                                           int* fetch_q) {
+  if constexpr (MODE == kModeGateUp) {
+    if (a.I - 128 * it.nt == 64 && it.mb >= 2) {
+      // half n-tile: eight wavefronts on four wavefronts' columns
+      if (it.mb == 8) return px_run<MODE, 4, true>(a, smem, it, nx, has_next, p0, n_inflight, fetch_q);
+      if (it.mb == 4) return px_run<MODE, 2, true>(a, smem, it, nx, has_next, p0, n_inflight, fetch_q);
+      return px_run<MODE, 1, true>(a, smem, it, nx, has_next, p0, n_inflight, fetch_q);
+    }
+  }
+  if (it.mb == 8) return px_run<MODE, 8>(a, smem, it, nx, has_next, p0, n_inflight, fetch_q);
+  if (it.mb == 4) return px_run<MODE, 4>(a, smem, it, nx, has_next, p0, n_inflight, fetch_q);
+  if (it.mb == 2) return px_run<MODE, 2>(a, smem, it, nx, has_next, p0, n_inflight, fetch_q);
+  return px_run<MODE, 1>(a, smem, it, nx, has_next, p0, n_inflight, fetch_q);
 }
 
-// Persistent grid, one workgroup per CU; workgroup b of XCD x = b % 8 takes
-// that XCD's local items b / 8, b / 8 + P, b / 8 + 2 P, ... (P = workgroups
-// per XCD).  Local item i is n-tile i % n_nt of the XCD's m-tile i / n_nt,
-// global m-tile x + 8 (i / n_nt): the large items come first, the small ones
-// fill in at the end, and the items of an m-tile run side by side on the
-// XCD's workgroups.
+// Persistent grid, one workgroup per CU.  Local item i of XCD x is n-tile
+// i % n_nt of the XCD's m-tile i / n_nt, global m-tile x + 8 (i / n_nt); the
+// tile list runs from large tiles to small, so the list is large items
+// first.  Workgroup b of XCD x = b % 8 takes local items b / 8 and
+// b / 8 + P (P = workgroups per XCD), then the items that XCD's queue
+// counter hands out, 2 P, 2 P + 1, ... in the order the workgroups ask:
+// each asks during the last stage of the item before its next one, so the
+// index is known one item ahead (the next item's rows and first stages are
+// loaded during the current one).  Work then goes to whichever workgroup
+// is free first: item costs vary (segment tails, the half n-tile) and a
+// fixed deal leaves some workgroups with markedly more.  queues[x] counts
+// XCD x's handed-out items, queues[8] the workgroups that have left; the
+// expert sort zeroes them and the last workgroup to leave resets them.
+// Without queues the deal is fixed: items b / 8 + r P.
 template <int MODE>
 __global__ __launch_bounds__(kPxThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_prefill_x(PrefillArgs a) {
@@ -488,9 +531,23 @@ void k_prefill_x(PrefillArgs a) {
   const int xcd = blockIdx.x & 7;
   const int n_local = ntiles > xcd ? (ntiles - xcd + 7) >> 3 : 0;  // this XCD's m-tiles
   const int it_end = n_local * a.n_nt;
-  const int step = gridDim.x >> 3;
+  const int P = gridDim.x >> 3;
+  int* const queue = a.queues != nullptr ? a.queues + xcd : nullptr;
+  // the last workgroup to leave resets the counters for the next launch
+  // (every other one has taken its last index before counting itself out)
+  auto leave = [&] {
+    if (a.queues == nullptr || threadIdx.x != 0) return;
+    const int d = __hip_atomic_fetch_add(a.queues + 8, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (d == (int)gridDim.x - 1) {
+#pragma unroll
+      for (int x = 0; x < 9; ++x) __hip_atomic_store(a.queues + x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  };
   int item = blockIdx.x >> 3;
-  if (item >= it_end) return;
+  if (item >= it_end) {
+    leave();
+    return;
+  }
   const int nkt = a.K / kPxKT;
   PxItem cur = px_item_info(a, xcd, item);
   if (MODE == kModeGateUp) {
@@ -510,18 +567,22 @@ void k_prefill_x(PrefillArgs a) {
     n_inflight = lc.n;
   }
   int p0 = 0;
+  int nitem = item + P;
   for (;;) {
-    const int nitem = item + step;
     const bool has_next = nitem < it_end;
     const PxItem nxt = has_next ? px_item_info(a, xcd, nitem) : cur;
-    n_inflight = px_dispatch<MODE>(a, smem, cur, nxt, has_next, p0, n_inflight);
+    // with a next item, take the index of the one after it during this item
+    n_inflight = px_dispatch<MODE>(a, smem, cur, nxt, has_next, p0, n_inflight, has_next ? queue : nullptr);
     if (!has_next) break;
     item = nitem;
+    nitem = queue != nullptr ? 2 * P + __builtin_amdgcn_readfirstlane(*reinterpret_cast<volatile int*>(smem + kPxQSlot))
+                             : item + P;
     cur = nxt;
     p0 = (p0 + nkt) % kPxStages;
   }
   // the loads issued past the last stage land before the workgroup leaves
   __builtin_amdgcn_s_waitcnt(px_vm_wait(0));
+  leave();
 }
 
 size_t prefill_x_lds_bytes() { return (size_t)kPxLds; }
