@@ -570,6 +570,61 @@ int moe_combine(const int64_t* topk_idx, const float* topk_w, uint16_t* out, int
                                       (int)H, static_cast<hipStream_t>(stream)));
 }
 
+}  // extern "C"
+
+namespace {
+
+// Routed rows up to which the one-call forwards fuse down and combine: the
+// fused launch measured faster up to 32 rows (decode layer M = 1 / 2 / 4 at
+// top-8: 32.6 -> 30.0, 37.9 -> 35.0, 44.2 -> 43.0 us) and slower at 64 (M = 8:
+// 59.2 -> 60.6 us), where the down streamer's 512 workgroups stream the
+// weights faster than the fused kernel's 176.
+constexpr int64_t kFuseDownCombineRows = 32;
+
+// The down projection and the weighted combine of the fused forwards: at
+// decode sizes with few routed rows in one launch (k_down_combine, the same
+// result bit for bit), otherwise moe_down then moe_combine.
+int down_and_combine(const int32_t* dn_packed, const uint16_t* dn_scale, const int64_t* topk_idx,
+                     const float* topk_w, uint16_t* out, int64_t M, int64_t top_k, int64_t E,
+                     int64_t H, int64_t I, int64_t group_size, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  if (use_prefill(M, H, I) || M * top_k > kFuseDownCombineRows || !down_combine_supported(M, top_k, I)) {
+    int st = moe_down(dn_packed, dn_scale, M, top_k, E, H, I, group_size, workspace,
+                      workspace_bytes, stream);
+    if (st == W4A16_OK)
+      st = moe_combine(topk_idx, topk_w, out, M, top_k, E, H, I, workspace, workspace_bytes,
+                       stream);
+    return st;
+  }
+  MoeLayout L{};
+  int st = moe_check(M, top_k, E, H, I, group_size, workspace, workspace_bytes, &L);
+  if (st != W4A16_OK || M == 0) return st;
+  if (!dn_packed || !dn_scale || !topk_idx || !topk_w || !out) return W4A16_ERR_NULL;
+  if (!aligned16(dn_packed) || !aligned16(out)) return W4A16_ERR_ALIGN;
+  DownCombineArgs a{};
+  a.act = L.inter;
+  a.wp = dn_packed;
+  a.ws = dn_scale;
+  a.sorted_pos = L.sorted_pos;
+  a.desc = L.desc;
+  a.n_active = L.counters;
+  a.topk_idx = topk_idx;
+  a.topk_w = topk_w;
+  a.out = out;
+  a.M = (int)M;
+  a.topk = (int)top_k;
+  a.E = (int)E;
+  a.N = (int)H;
+  a.K = (int)I;
+  a.G = (int)group_size;
+  a.ng = (int)((I + group_size - 1) / group_size);
+  return launch_status(launch_down_combine(group_size % 128 == 0, a, static_cast<hipStream_t>(stream)));
+}
+
+}  // namespace
+
+extern "C" {
+
 int moe_forward(const uint16_t* hidden, const int64_t* topk_idx, const float* topk_w,
                 const int32_t* gu_packed, const uint16_t* gu_scale, const int32_t* dn_packed,
                 const uint16_t* dn_scale, uint16_t* out, int64_t M, int64_t top_k, int64_t E,
@@ -587,11 +642,8 @@ int moe_forward(const uint16_t* hidden, const int64_t* topk_idx, const float* to
     st = moe_gate_up(hidden, gu_packed, gu_scale, M, top_k, E, H, I, group_size, workspace,
                      workspace_bytes, stream);
   if (st == W4A16_OK)
-    st = moe_down(dn_packed, dn_scale, M, top_k, E, H, I, group_size, workspace,
-                  workspace_bytes, stream);
-  if (st == W4A16_OK)
-    st = moe_combine(topk_idx, topk_w, out, M, top_k, E, H, I, workspace, workspace_bytes,
-                     stream);
+    st = down_and_combine(dn_packed, dn_scale, topk_idx, topk_w, out, M, top_k, E, H, I,
+                          group_size, workspace, workspace_bytes, stream);
   return st;
 }
 
@@ -862,10 +914,8 @@ int moe_layer_forward(const uint16_t* router_in, const uint16_t* router_scale, f
   st = moe_gate_up(hidden, gu_packed, gu_scale, M, top_k, E, H, I, group_size, workspace,
                    moe_bytes, stream);
   if (st == W4A16_OK)
-    st = moe_down(dn_packed, dn_scale, M, top_k, E, H, I, group_size, workspace, moe_bytes,
-                  stream);
-  if (st == W4A16_OK)
-    st = moe_combine(topk_idx, topk_w, out, M, top_k, E, H, I, workspace, moe_bytes, stream);
+    st = down_and_combine(dn_packed, dn_scale, topk_idx, topk_w, out, M, top_k, E, H, I,
+                          group_size, workspace, moe_bytes, stream);
   return st;
 }
 

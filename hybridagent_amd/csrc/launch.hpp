@@ -75,6 +75,22 @@ struct PrefillArgs {
 
 enum DecodeMode { kModeDense = 0, kModeGateUp = 1, kModeDown = 2 };
 
+// Arguments of the fused down projection + weighted combine for decode
+// sizes (kernels_down_combine.hip).
+constexpr int kDownCombineMaxRows = 64;
+struct DownCombineArgs {
+  const uint16_t* act;        // intermediate rows [M*k, K] in segment order
+  const int32_t* wp;          // packed down weights [E, N, K/8]
+  const uint16_t* ws;         // bf16 scales [E, N, ng]
+  const int32_t* sorted_pos;  // [M*k] rows t*k+j in segment order
+  const int32_t* desc;        // [E][4] (expert, segment start, rows, 0) per active slot
+  const int32_t* n_active;    // [1]
+  const int64_t* topk_idx;    // [M, k]
+  const float* topk_w;        // [M, k]
+  uint16_t* out;              // [M, N]
+  int M, topk, E, N, K, G, ng;
+};
+
 // Arguments of the BF16 experts' grouped GEMMs (kernels_bf16_experts.hip).
 struct Bf16ExpertArgs {
   const uint16_t* act;        // gate_up: hidden [M, K]; down: inter [M*k, K] in segment order
@@ -98,6 +114,10 @@ hipError_t launch_add_rms_norm(const uint16_t* h, const uint16_t* delta, const u
                                hipStream_t s);
 hipError_t launch_combine(const uint16_t* dn, const int64_t* idx, const float* w, uint16_t* out,
                           int M, int topk, int E, int H, hipStream_t s);
+// down + combine in one launch: M <= 16, M * topk <= kDownCombineMaxRows,
+// K <= 768 and a multiple of 32; bias_form as for the decode streamer
+bool down_combine_supported(int64_t M, int64_t topk, int64_t K);
+hipError_t launch_down_combine(bool bias_form, DownCombineArgs a, hipStream_t s);
 // The expert sort; with `queues` (nullable) it also zeroes the
 // kPrefillQueueInts prefill work-queue counters there.
 hipError_t launch_sort(const int64_t* idx, int M, int topk, int E, int32_t* sorted_pos,

@@ -1,0 +1,116 @@
+"""GPU: the fused down projection + weighted combine (k_down_combine, used by
+the one-call forwards at decode sizes with at most 32 routed rows) against
+the separate down streamer + k_combine (the stage API) -- bit for bit -- and
+against the numpy oracle (quantization.py:122-129)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from hybridagent_amd import _lib, synth
+
+pytestmark = pytest.mark.gpu
+
+E, H, I = 128, 2816, 704
+
+
+def _bits(t):
+    return t.detach().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.fixture(scope="module")
+def dev():
+    assert _lib.available(), "libw4a16moe.so must be built"
+    return torch.device("cuda:0")
+
+
+@pytest.fixture(scope="module", params=[128, 32])
+def weights(request, dev):
+    G = request.param
+    w = synth.moe_weights(E, H, I, G, seed=4100 + G)
+    return G, w, [getattr(w, k).to(dev) for k in ("gate_up_packed", "gate_up_scale", "down_packed", "down_scale")]
+
+
+def _routing(M, k, seed, dev, invalid=False):
+    g = torch.Generator().manual_seed(seed)
+    idx = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(M)])
+    w = torch.rand(M, k, generator=g) + 0.05
+    w = w / w.sum(1, keepdim=True)
+    if invalid and M > 1:
+        idx[0, k - 1] = -1   # slots without an expert contribute nothing
+        idx[M - 1, 0] = E
+    return idx.to(dev), w.float().to(dev)
+
+
+def _stages(x, idx, w, G, gpu):
+    M, k = idx.shape
+    st = _lib.MoEStages(M, k, E, H, I, G, x.device)
+    st.plan(x, idx)
+    st.gate_up(x, gpu[0], gpu[1])
+    st.down(gpu[2], gpu[3])
+    return st.combine(idx, w).clone()
+
+
+# (8, 8): 64 rows, past the fused range -- the separate path, equal too
+@pytest.mark.parametrize("M,k", [(1, 8), (2, 8), (4, 8), (3, 5), (8, 4), (16, 2), (3, 1), (8, 8)])
+def test_fused_equals_stages(dev, weights, M, k):
+    G, _, gpu = weights
+    print(f"down+combine fused vs stages G={G} M={M} k={k}", flush=True)
+    x = synth.activations(M, H, seed=4200 + M).to(dev)
+    idx, w = _routing(M, k, 4300 + M + 17 * k, dev)
+    y = _lib.moe_forward(x, idx, w, *gpu, group_size=G)
+    ref = _stages(x, idx, w, G, gpu)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(y), _bits(ref)), f"G={G} M={M} k={k}: fused down+combine differs"
+
+
+def test_fused_invalid_slots(dev, weights):
+    G, _, gpu = weights
+    M, k = 4, 8
+    x = synth.activations(M, H, seed=4400).to(dev)
+    idx, w = _routing(M, k, 4401, dev, invalid=True)
+    y = _lib.moe_forward(x, idx, w, *gpu, group_size=G)
+    ref = _stages(x, idx, w, G, gpu)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(y), _bits(ref))
+
+
+@pytest.mark.parametrize("M", [1, 4])
+def test_fused_against_oracle(dev, weights, M):
+    G, wts, gpu = weights
+    k = 8
+    x = synth.activations(M, H, seed=4500 + M).to(dev)
+    idx, w = _routing(M, k, 4501 + M, dev)
+    y = _lib.moe_forward(x, idx, w, *gpu, group_size=G)
+    torch.cuda.synchronize()
+    bits = lambda t: t.view(torch.int16).numpy().view(np.uint16)
+    ref = oracle.moe_forward(x.float().cpu().numpy(), idx.cpu().numpy(), w.cpu().numpy(),
+                             wts.gate_up_packed.numpy(), bits(wts.gate_up_scale), wts.down_packed.numpy(),
+                             bits(wts.down_scale), G)
+    assert oracle.max_abs_rel(y.float().cpu().numpy(), ref) <= 1e-2
+
+
+def test_fused_graph_replay(dev, weights):
+    """Captured in a HIP graph and replayed, with eager work in between, every
+    replay equals the eager result."""
+    G, _, gpu = weights
+    M, k = 4, 8
+    x = synth.activations(M, H, seed=4600).to(dev)
+    idx, w = _routing(M, k, 4601, dev)
+    eager = _lib.moe_forward(x, idx, w, *gpu, group_size=G).clone()
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        _lib.moe_forward(x, idx, w, *gpu, group_size=G)
+    torch.cuda.current_stream(dev).wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = _lib.moe_forward(x, idx, w, *gpu, group_size=G)
+    x2 = synth.activations(M, H, seed=4602).to(dev)
+    for r in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(_bits(out), _bits(eager)), f"replay {r}"
+        _lib.moe_forward(x2, idx, w, *gpu, group_size=G)  # eager work between replays
+        torch.cuda.synchronize()
