@@ -53,6 +53,7 @@ __global__ __launch_bounds__(kDcThreads) void k_down_combine(DownCombineArgs a) 
   float* __restrict__ prod = csum + kDcTiles * R;                                // [R][16]
   int* __restrict__ slot_pos = reinterpret_cast<int*>(prod + R * kDcCols);       // [threads]: t*k+j of segment row s
   float* __restrict__ wts = reinterpret_cast<float*>(slot_pos + kDcThreads);      // [threads]: bf16(w[t, j]) at t*k+j
+  int* __restrict__ has_e = reinterpret_cast<int*>(wts + kDcThreads);            // [threads]: slot t*k+j has an expert
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -99,6 +100,7 @@ __global__ __launch_bounds__(kDcThreads) void k_down_combine(DownCombineArgs a) 
   }
   const int spos = a.sorted_pos[min(tid, R - 1)];
   const float wrt = a.topk_w[min(tid, R - 1)];
+  const int64_t ex = a.topk_idx[min(tid, R - 1)];
   // (scales kept 32 bits wide: packing two 16-bit loads into one register
   // would wait for both where the loop carries them)
   u32x4_t bw0[kDcTiles], bw1[kDcTiles];
@@ -108,6 +110,7 @@ __global__ __launch_bounds__(kDcThreads) void k_down_combine(DownCombineArgs a) 
   __builtin_amdgcn_sched_barrier(0);
   slot_pos[tid] = spos;  // entries past R are not read
   wts[tid] = round_bf16(wrt);
+  has_e[tid] = ex >= 0 && ex < a.E;
   if (has) {
     float half[2] = {0.f, 0.f};
 #pragma unroll
@@ -191,8 +194,8 @@ __global__ __launch_bounds__(kDcThreads) void k_down_combine(DownCombineArgs a) 
     if (n0 + c >= a.N) continue;
     float y = 0.f;
     for (int jj = 0; jj < a.topk; ++jj) {
-      const int64_t ex = a.topk_idx[(int64_t)t * a.topk + jj];
-      if (ex >= 0 && ex < a.E) y += prod[(t * a.topk + jj) * kDcCols + c];
+      const int r = t * a.topk + jj;
+      if (has_e[r]) y += prod[r * kDcCols + c];
     }
     a.out[(int64_t)t * a.N + n0 + c] = f32_to_bf16_bits(y);
   }
@@ -200,7 +203,7 @@ __global__ __launch_bounds__(kDcThreads) void k_down_combine(DownCombineArgs a) 
 
 size_t down_combine_lds(int rows) {
   return (size_t)16 * kDcTiles * rows * 16 + (size_t)kDcTiles * rows * 4 + (size_t)rows * kDcCols * 4 +
-         (size_t)kDcThreads * 8;
+         (size_t)kDcThreads * 12;
 }
 
 // every expert's rows fit one 16-row MFMA tile (an expert gets each token
