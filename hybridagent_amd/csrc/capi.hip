@@ -109,7 +109,7 @@ MoeLayout moe_layout(void* ws, int64_t M, int64_t k, int64_t E, int64_t H, int64
   MoeLayout L;
   L.offsets = c.take<int32_t>(E + 1);
   L.desc = c.take<int32_t>(4 * E);
-  L.counters = c.take<int32_t>(3);
+  L.counters = c.take<int32_t>(2);
   L.queues = c.take<int32_t>(kPrefillQueueInts);
   L.sorted_pos = c.take<int32_t>(M * k);
   L.tiles = c.take<int32_t>(M * k / kPrefillBM + E + 1);
@@ -289,7 +289,7 @@ int moe_topk_from_logits(const uint16_t* logits, const uint16_t* per_expert_scal
 
 size_t moe_sort_workspace_bytes(int64_t M, int64_t top_k, int64_t E) {
   if (M <= 0 || top_k <= 0 || E <= 0) return 0;
-  return round256(size_t(E) * 16) + round256(12) + round256(size_t(M * top_k / kPrefillBM + E + 1) * 4) +
+  return round256(size_t(E) * 16) + round256(8) + round256(size_t(M * top_k / kPrefillBM + E + 1) * 4) +
          round256(size_t(sort_blocks(M * top_k)) * E * 4);
 }
 
@@ -305,7 +305,7 @@ int moe_sort_permute(const int64_t* topk_idx, int64_t M, int64_t top_k, int64_t 
   if (workspace == nullptr || workspace_bytes < need) return W4A16_ERR_WORKSPACE;
   Carve c(workspace);
   int32_t* desc = c.take<int32_t>(4 * E);
-  int32_t* counters = c.take<int32_t>(3);
+  int32_t* counters = c.take<int32_t>(2);
   int32_t* tiles = c.take<int32_t>(M * top_k / kPrefillBM + E + 1);
   int32_t* blockcnt = c.take<int32_t>(size_t(sort_blocks(M * top_k)) * E);
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -452,8 +452,7 @@ int moe_gate_up(const uint16_t* hidden, const int32_t* gu_packed, const uint16_t
     p.ng = (int)((H + group_size - 1) / group_size);
     p.gshift = log2_int(group_size);
     p.rows_total = (int)(M * top_k);
-    p.n_nt = (int)((I + 127) / 128);   // 128 intermediate columns per item
-    p.n_nt2 = (int)((I + 255) / 256);  // tails: 256 per item
+    p.n_nt = (int)((I + 127) / 128);  // 128 intermediate columns per item
     p.queues = L.queues;
     return launch_status(launch_prefill_x(kModeGateUp, p, max_mtiles(M, top_k, E, kPrefillXBM), s));
   }
@@ -521,8 +520,7 @@ int moe_down(const int32_t* dn_packed, const uint16_t* dn_scale, int64_t M, int6
     p.ng = (int)((I + group_size - 1) / group_size);
     p.gshift = log2_int(group_size);
     p.rows_total = (int)(M * top_k);
-    p.n_nt = (int)((H + 255) / 256);   // 256 output columns per item
-    p.n_nt2 = (int)((H + 511) / 512);  // tails: 512 per item
+    p.n_nt = (int)((H + 255) / 256);  // 256 output columns per item
     p.queues = L.queues + kPrefillQueueInts / 2;
     return launch_status(launch_prefill_x(kModeDown, p, max_mtiles(M, top_k, E, kPrefillXBM), s));
   }

@@ -71,11 +71,6 @@ constexpr int kPxStages = 3;
 constexpr int kPxBOff = kPxBM * kPxKT * 2;
 constexpr int kPxSOff = kPxBOff + kPxBN * kPxKT / 2;
 constexpr int kPxStageBytes = kPxSOff + kPxBN * 16;
-// wide items (tail m-tiles of at most 128 rows, 512 weight rows): A takes at
-// most 16 KB, then B words [512 rows][32 B] and scale chunks [512][16 B]
-constexpr int kPxBOff2 = 16384;
-constexpr int kPxSOff2 = kPxBOff2 + 2 * kPxBN * kPxKT / 2;
-static_assert(kPxSOff2 + 2 * kPxBN * 16 <= kPxStageBytes, "a wide stage fits a ring slot");
 constexpr int kPxTable = kPxStages * kPxStageBytes;  // 512 row indices
 // down's epilogue rows: 32 rows x 32 bf16 per wavefront, rows 80 bytes
 // apart (the 8-byte writes of 32 rows spread over the banks)
@@ -157,31 +152,15 @@ __device__ __forceinline__ f32x16_t mfma32x(u32x4_t a, u32x4_t b, f32x16_t c) {
 }  // namespace
 
 
-// One work item: (m-tile, n-tile) and what that fixes.  Large m-tiles
-// (more than 128 rows) have n-tiles of 256 weight rows; the tails (at most
-// 128 rows) wide ones of 512 (ng = 2: each wavefront two 32-row groups),
-// so a tail's per-stage fixed costs (barrier, waits, load latencies) serve
-// twice the dequantisation and MFMA work.
+// One work item: (m-tile, n-tile) and what that fixes.
 struct PxItem {
-  int nt, e, seg0, nrows, mb, ng;
+  int nt, e, seg0, nrows, mb;
 };
 
-// Local item i of an XCD with nbx large m-tiles: i < nbx n_nt is n-tile
-// i % n_nt of large m-tile i / n_nt, after that the tails' wide n-tiles.
-__device__ __forceinline__ PxItem px_item_info(const PrefillArgs& a, int xcd, int nbx, int item) {
+__device__ __forceinline__ PxItem px_item_info(const PrefillArgs& a, int xcd, int item) {
   PxItem it;
-  int lm;
-  if (item < nbx * a.n_nt) {
-    lm = item / a.n_nt;
-    it.nt = item - lm * a.n_nt;
-    it.ng = 1;
-  } else {
-    const int j = item - nbx * a.n_nt;
-    const int q = j / a.n_nt2;
-    lm = nbx + q;
-    it.nt = j - q * a.n_nt2;
-    it.ng = 2;
-  }
+  const int lm = item / a.n_nt;
+  it.nt = item - lm * a.n_nt;
   const int tile = ld_uniform(a.tiles, xcd + 8 * lm);
   it.e = tile >> 16;
   it.seg0 = ld_uniform(a.offsets, it.e) + (tile & 0xFFFF) * kPxBM;
@@ -195,23 +174,22 @@ __device__ __forceinline__ PxItem px_item_info(const PrefillArgs& a, int xcd, in
 struct PxLoads {
   __amdgpu_buffer_rsrc_t wsrc, ssrc;
   int avoff[kPxNA];
-  int bvoff[2], svoff;
-  int na, n, ng;
-  bool sreal;
+  int bvoff, svoff;
+  int na, n;
 };
 
-// weight row of tile row tr of n-tile nt of 256 ng rows (gate_up: group g's
-// tile rows 32 g .. 32 g + 31 are gate rows 128 ng nt + 16 g .. + 15, then
-// the matching up rows; rows past the matrix repeat its last row, their
-// results are dropped)
+// weight row of tile row tr of n-tile nt (gate_up: wavefront w's tile rows
+// 32 w .. 32 w + 31 are gate rows 128 nt + 16 w .. + 15, then the matching
+// up rows; rows past the matrix repeat its last row, their results are
+// dropped)
 template <int MODE>
-__device__ __forceinline__ int px_weight_row(const PrefillArgs& a, int nt, int tr, int ng = 1) {
+__device__ __forceinline__ int px_weight_row(const PrefillArgs& a, int nt, int tr) {
   if (MODE == kModeGateUp) {
-    const int g = tr >> 5, cc = tr & 31;
-    const int col = min(128 * ng * nt + 16 * g + (cc & 15), a.I - 1);
+    const int w = tr >> 5, cc = tr & 31;
+    const int col = min(128 * nt + 16 * w + (cc & 15), a.I - 1);
     return cc < 16 ? col : a.I + col;
   }
-  return min(kPxBN * ng * nt + tr, a.N - 1);
+  return min(kPxBN * nt + tr, a.N - 1);
 }
 
 // gate_up reads the item's gathered rows from the LDS table, which must
@@ -237,32 +215,29 @@ __device__ __forceinline__ PxLoads px_loads(const PrefillArgs& a, const PxItem& 
     const int chunk = (lane & 7) ^ ((r >> 1) & 7);
     L.avoff[i] = real ? (int)(src * a.lda * 2) + 16 * chunk : 0;
   }
-  L.ng = it.ng;
-  L.sreal = it.ng == 2 || wave < 4;
-  L.n = L.na + it.ng + (L.sreal ? 1 : 0);
-  // B words: instruction b of wavefront w brings tile rows 32 (w + 8 b) ..
-  // + 31, lane l row 32 (w + 8 b) + l / 2, bytes 16 (l % 2) of the stage's 32
+  L.n = L.na + 1 + (wave < 4 ? 1 : 0);
+  // B words: instruction `wave` brings tile rows 32 wave .. + 31, lane l row
+  // 32 wave + l / 2, bytes 16 (l % 2) of the stage's 32
   const int K2 = a.K >> 1;  // packed bytes per weight row
   L.wsrc = make_rsrc(reinterpret_cast<const uint32_t*>(a.wp) + (int64_t)it.e * a.N * (a.K >> 3),
                      (uint32_t)a.N * K2);
-#pragma unroll
-  for (int b = 0; b < 2; ++b)
-    L.bvoff[b] = px_weight_row<MODE>(a, it.nt, 32 * (wave + 8 * b) + (lane >> 1), it.ng) * K2 + 16 * (lane & 1);
-  // scale chunks: 64 tile rows per instruction (waves 0..3, or all eight for
-  // wide items), lane l row 64 wave + l: the aligned 16 bytes holding the
-  // stage's scale pair (the stage adds 2 x the pair's group index, the lane
-  // rounds down to 16 bytes).  The descriptor starts at the expert's scales
-  // rounded down to 16 bytes; svoff carries the difference.
+  L.bvoff = px_weight_row<MODE>(a, it.nt, 32 * wave + (lane >> 1)) * K2 + 16 * (lane & 1);
+  // scale chunks: waves 0..3 bring tile rows 64 wave + l, the aligned 16
+  // bytes holding the stage's scale pair (the stage adds 2 x the pair's
+  // group index, the lane rounds down to 16 bytes).  The descriptor starts
+  // at the expert's scales rounded down to 16 bytes; svoff carries the
+  // difference.
   const uintptr_t sbase = reinterpret_cast<uintptr_t>(a.ws + (int64_t)it.e * a.N * a.ng);
   L.ssrc = make_rsrc(reinterpret_cast<const void*>(sbase & ~uintptr_t(15)), (uint32_t)a.N * a.ng * 2u + 16u);
-  L.svoff = L.sreal ? (int)(sbase & 15) + px_weight_row<MODE>(a, it.nt, 64 * wave + lane, it.ng) * a.ng * 2 : 0;
+  const bool sreal = wave < 4;
+  L.svoff = sreal ? (int)(sbase & 15) + px_weight_row<MODE>(a, it.nt, 64 * wave + lane) * a.ng * 2 : 0;
   return L;
 }
 
 // Part `part` (0..3, issued before MFMA step `part`) of the direct loads of
 // stage kt of an item into ring slot `slot`, L.n loads in all: part p brings
-// A load p (if this wavefront has one), part 0 also the B words (part 2 the
-// second group's for wide items), part 1 the scale chunks.
+// A load p (if this wavefront has one), part 0 also the B words, part 1 the
+// scale chunks.
 __device__ __forceinline__ void px_issue(const PrefillArgs& a, const PxLoads& L, unsigned char* smem, int kt,
                                          int slot, int part) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -270,12 +245,10 @@ __device__ __forceinline__ void px_issue(const PrefillArgs& a, const PxLoads& L,
   if (part < L.na)
     px_dma16(make_rsrc(a.act, (uint32_t)a.act_bytes), L.avoff[part], kt * (kPxKT * 2),
              st + (wave + 8 * part) * 1024);
-  const int boff = L.ng == 2 ? kPxBOff2 : kPxBOff;
-  if (part == 0) px_dma16(L.wsrc, L.bvoff[0], kt * (kPxKT / 2), st + boff + wave * 1024);
-  if (part == 2 && L.ng == 2) px_dma16(L.wsrc, L.bvoff[1], kt * (kPxKT / 2), st + boff + (wave + 8) * 1024);
-  if (part == 1 && L.sreal) {
+  if (part == 0) px_dma16(L.wsrc, L.bvoff, kt * (kPxKT / 2), st + kPxBOff + wave * 1024);
+  if (part == 1 && wave < 4) {
     const int gpair = ((kt * kPxKT) >> a.gshift) & ~1;
-    px_dma16(L.ssrc, (L.svoff + 2 * gpair) & ~15, 0, st + (L.ng == 2 ? kPxSOff2 : kPxSOff) + 1024 * wave);
+    px_dma16(L.ssrc, (L.svoff + 2 * gpair) & ~15, 0, st + kPxSOff + 1024 * wave);
   }
 }
 
@@ -300,21 +273,18 @@ __device__ __forceinline__ void px_issue_table(const PrefillArgs& a, unsigned ch
 // holds the item's rows).  After its last stage it issues the next item's
 // stages 0 and 1 (when has_next) and returns their per-stage load count;
 // the epilogue runs while they land.
-// With fetch_q (non-null) wavefront 0 takes an index from that queue
-// counter during the last stage (no stage load is issued after it, so the
-// stage's vmcnt(0) wait covers it) and leaves it in LDS at kPxQSlot.
 // SPLIT (gate_up's last n-tile when I % 128 == 64: only wavefronts 0..3
 // have columns): wavefront w multiplies the weight rows of wavefront w % 4
 // with m-blocks MB (w / 4) .. + MB - 1 of the item's 2 MB, so all eight
 // wavefronts share the work instead of four idling.
-// NG = 2 (wide items): each wavefront multiplies two 32-row weight groups,
-// tile rows 32 wave and 32 (wave + 8).
-template <int MODE, int MB, bool SPLIT = false, int NG = 1>
+// With fetch_q (non-null) wavefront 0 takes an index from that queue
+// counter during the last stage (no stage load is issued after it, so the
+// stage's vmcnt(0) wait covers it) and leaves it in LDS at kPxQSlot.
+template <int MODE, int MB, bool SPLIT = false>
 __device__ __forceinline__ int px_run(const PrefillArgs& a, unsigned char* smem, const PxItem& it,
                                       const PxItem& nx, bool has_next, int p0, int n_inflight,
                                       int* fetch_q) {
   static_assert(!SPLIT || MODE == kModeGateUp, "only gate_up has half n-tiles");
-  static_assert(!SPLIT || NG == 1, "the half n-tile is a 256-row one");
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wg = SPLIT ? (wave & 3) : wave;      // weight rows 32 wg .. of the tile
@@ -331,35 +301,22 @@ __device__ __forceinline__ int px_run(const PrefillArgs& a, unsigned char* smem,
   int aoff[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) aoff[s] = mo * 4096 + c * 128 + 16 * ((4 * h + s) ^ ((c >> 1) & 7));
-  int boff[NG], soff[NG], srow2[NG];
-  bool wk[NG];
-#pragma unroll
-  for (int g = 0; g < NG; ++g) {
-    const int tr = 32 * (wg + 8 * g) + c;  // tile row of this lane's B fragment
-    boff[g] = (NG == 2 ? kPxBOff2 : kPxBOff) + tr * 32 + 16 * h;
-    // the scale chunk of tile row tr; the pair sits at byte
-    // (2 (row ng + pair group)) % 16 of it
-    soff[g] = (NG == 2 ? kPxSOff2 : kPxSOff) + tr * 16;
-    srow2[g] = (int)(reinterpret_cast<uintptr_t>(a.ws + (int64_t)it.e * a.N * a.ng) & 15) +
-               px_weight_row<MODE>(a, nt, tr, NG) * a.ng * 2;
-    // groups whose columns lie past the matrix (gate_up's last n-tile when
-    // I % 128 == 64, the last wide n-tiles) store nothing
-    const int gw = wave + 8 * g;
-    wk[g] = SPLIT || (MODE == kModeGateUp ? 128 * NG * nt + 16 * gw < a.I : kPxBN * NG * nt + 32 * gw < a.N);
-  }
-  auto soff_of = [&](int g, int t) -> int {
-    return soff[g] + ((srow2[g] + 2 * (((t * kPxKT) >> gshift) & ~1)) & 15);
-  };
-  // a wavefront without columns does no MFMA work
-  const bool work = wk[0];
+  const int boff = kPxBOff + (32 * wg + c) * 32 + 16 * h;
+  // the scale chunk of tile row 32 wave + c; the pair sits at byte
+  // (2 (row ng + pair group)) % 16 of it
+  const int soff = kPxSOff + (32 * wg + c) * 16;
+  const int srow2 = (int)(reinterpret_cast<uintptr_t>(a.ws + (int64_t)it.e * a.N * a.ng) & 15) +
+                    px_weight_row<MODE>(a, nt, 32 * wg + c) * a.ng * 2;
+  auto soff_of = [&](int t) -> int { return soff + ((srow2 + 2 * (((t * kPxKT) >> gshift) & ~1)) & 15); };
+  // wavefronts whose columns lie past the matrix (gate_up's last n-tile
+  // when I % 128 == 64) do no MFMA work and store nothing
+  const bool work = SPLIT || (MODE == kModeGateUp ? 128 * nt + 16 * wave < a.I : kPxBN * nt + 32 * wave < a.N);
 
-  f32x16_t acc[NG][MB];
+  f32x16_t acc[MB];
 #pragma unroll
-  for (int g = 0; g < NG; ++g)
+  for (int i = 0; i < MB; ++i)
 #pragma unroll
-    for (int i = 0; i < MB; ++i)
-#pragma unroll
-      for (int q = 0; q < 16; ++q) acc[g][i][q] = 0.f;
+    for (int q = 0; q < 16; ++q) acc[i][q] = 0.f;
 
   auto scale_of = [&](int t, uint32_t sp) -> float {
     const int g = (t * kPxKT + 32 * h) >> gshift;
@@ -372,11 +329,9 @@ __device__ __forceinline__ int px_run(const PrefillArgs& a, unsigned char* smem,
   };
   // D[weight row][activation row]: the dequantised weights are the MFMA's A
   // operand, the activation rows its B operand
-  auto mfmas = [&](const u32x4_t* af, const u32x4_t* bf) {
+  auto mfmas = [&](const u32x4_t* af, u32x4_t bf) {
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int g = 0; g < NG; ++g) acc[g][mb] = mfma32x(bf[g], af[mb], acc[g][mb]);
+    for (int mb = 0; mb < MB; ++mb) acc[mb] = mfma32x(bf, af[mb], acc[mb]);
   };
   auto stage_ptr = [&](int sl) -> const unsigned char* { return smem + sl * kPxStageBytes; };
   // the loads issued after the awaited stage: those of the stage issued in
@@ -400,20 +355,12 @@ __device__ __forceinline__ int px_run(const PrefillArgs& a, unsigned char* smem,
   // the stage, so after it each MFMA of that step is followed by the read
   // of stage t + 1's first fragment for the same block.
   u32x4_t af[MB];
-  u32x4_t bw[NG];
-  float sc[NG];
-#pragma unroll
-  for (int g = 0; g < NG; ++g) {
-    bw[g] = u32x4_t{0u, 0u, 0u, 0u};
-    sc[g] = 0.f;
-  }
+  u32x4_t bw = {0u, 0u, 0u, 0u};
+  float sc = 0.f;
   if (work) {
     read_a(stage_ptr(p0), 0, af);
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-      bw[g] = *reinterpret_cast<const u32x4_t*>(stage_ptr(p0) + boff[g]);
-      sc[g] = scale_of(0, *reinterpret_cast<const uint32_t*>(stage_ptr(p0) + soff_of(g, 0)));
-    }
+    bw = *reinterpret_cast<const u32x4_t*>(stage_ptr(p0) + boff);
+    sc = scale_of(0, *reinterpret_cast<const uint32_t*>(stage_ptr(p0) + soff_of(0)));
   }
   int slot = p0;
   int slot2 = p0 + 2 >= kPxStages ? p0 + 2 - kPxStages : p0 + 2;
@@ -423,51 +370,32 @@ __device__ __forceinline__ int px_run(const PrefillArgs& a, unsigned char* smem,
     const int nslot = slot == kPxStages - 1 ? 0 : slot + 1;
     if (work) {
       const unsigned char* st = stage_ptr(slot);
-      float m8[NG];
-      uint32_t wv[NG][4];
-      u32x4_t bf[NG];
-#pragma unroll
-      for (int g = 0; g < NG; ++g) {
-        m8[g] = -8.0f * sc[g];
-        wv[g][0] = bw[g].x;
-        wv[g][1] = bw[g].y;
-        wv[g][2] = bw[g].z;
-        wv[g][3] = bw[g].w;
-        bf[g] = dequant_word(wv[g][0], sc[g], m8[g]);
-      }
+      const float m8 = -8.0f * sc;
+      const uint32_t wv[4] = {bw.x, bw.y, bw.z, bw.w};
+      u32x4_t bf = dequant_word(wv[0], sc, m8);
 #pragma unroll
       for (int s2 = 0; s2 < 3; ++s2) {
         issue(slot2, s2);
-        u32x4_t bfn[NG];
-#pragma unroll
-        for (int g = 0; g < NG; ++g) bfn[g] = dequant_word(wv[g][s2 + 1], sc[g], m8[g]);
+        const u32x4_t bfn = dequant_word(wv[s2 + 1], sc, m8);
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
-#pragma unroll
-          for (int g = 0; g < NG; ++g) acc[g][mb] = mfma32x(bf[g], af[mb], acc[g][mb]);
+          acc[mb] = mfma32x(bf, af[mb], acc[mb]);
           af[mb] = *reinterpret_cast<const u32x4_t*>(st + mb * 4096 + aoff[s2 + 1]);
         }
-#pragma unroll
-        for (int g = 0; g < NG; ++g) bf[g] = bfn[g];
+        bf = bfn;
       }
       issue(slot2, 3);
       wait_and_sync(n, hook);  // stage t + 1 landed (stage t + 2 may still be loading)
       if (t + 1 < nkt) {
         const unsigned char* sn = stage_ptr(nslot);
-        uint32_t sp[NG];
-#pragma unroll
-        for (int g = 0; g < NG; ++g) {
-          bw[g] = *reinterpret_cast<const u32x4_t*>(sn + boff[g]);
-          sp[g] = *reinterpret_cast<const uint32_t*>(sn + soff_of(g, t + 1));
-        }
+        bw = *reinterpret_cast<const u32x4_t*>(sn + boff);
+        const uint32_t sp = *reinterpret_cast<const uint32_t*>(sn + soff_of(t + 1));
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
-#pragma unroll
-          for (int g = 0; g < NG; ++g) acc[g][mb] = mfma32x(bf[g], af[mb], acc[g][mb]);
+          acc[mb] = mfma32x(bf, af[mb], acc[mb]);
           af[mb] = *reinterpret_cast<const u32x4_t*>(sn + mb * 4096 + aoff[0]);
         }
-#pragma unroll
-        for (int g = 0; g < NG; ++g) sc[g] = scale_of(t + 1, sp[g]);
+        sc = scale_of(t + 1, sp);
       } else {
         mfmas(af, bf);
       }
@@ -513,26 +441,24 @@ __device__ __forceinline__ int px_run(const PrefillArgs& a, unsigned char* smem,
   if (!work) return n_next;
 
   // ---- epilogue.  Lane l holds, for activation row 32 mb + c of block mb,
-  // group g's weight rows 8 J + 4 h + i in acc[g][mb][4 J + i] (J, i =
+  // the wavefront's weight rows 8 J + 4 h + i in acc[mb][4 J + i] (J, i =
   // 0..3): four consecutive output columns per J.  gate_up stores them as 8
   // bytes from registers: weight rows 0..15 are the gate rows and 16..31
-  // their up rows, so acc[g][mb][q] (gate) pairs with acc[g][mb][q + 8] (up).
+  // their up rows, so acc[mb][q] (gate) pairs with acc[mb][q + 8] (up).
 #pragma unroll
-  for (int g = 0; g < NG && MODE == kModeGateUp; ++g) {
-    if (!wk[g]) continue;
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const int grow = 32 * (mo + mb) + c;
-      if (grow >= nrows) continue;
-      uint16_t* orow = a.out + (int64_t)(seg0 + grow) * a.ldo + 128 * NG * nt + 16 * (wg + 8 * g) + 4 * h;
+  for (int mb = 0; mb < MB && MODE == kModeGateUp; ++mb) {
+    const int grow = 32 * (mo + mb) + c;
+    if (grow >= nrows) continue;
+    {
+      uint16_t* orow = a.out + (int64_t)(seg0 + grow) * a.ldo + 128 * nt + 16 * wg + 4 * h;
 #pragma unroll
       for (int J = 0; J < 2; ++J) {
         float hv[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float gv = round_bf16(acc[g][mb][4 * J + i]);
-          const float u = round_bf16(acc[g][mb][4 * J + i + 8]);
-          hv[i] = round_bf16(gelu_tanh_f32(gv)) * u;
+          const float g = round_bf16(acc[mb][4 * J + i]);
+          const float u = round_bf16(acc[mb][4 * J + i + 8]);
+          hv[i] = round_bf16(gelu_tanh_f32(g)) * u;
         }
         *reinterpret_cast<uint2*>(orow + 8 * J) = make_uint2(pack_bf16x2(hv[0], hv[1]), pack_bf16x2(hv[2], hv[3]));
       }
@@ -545,24 +471,19 @@ __device__ __forceinline__ int px_run(const PrefillArgs& a, unsigned char* smem,
     const int* table = reinterpret_cast<const int*>(smem + kPxTable);
     unsigned char* ob = smem + kPxEpiOff + wave * kPxEpiBytes;
 #pragma unroll
-    for (int g = 0; g < NG; ++g) {
-      if (!wk[g]) continue;
+    for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
+      for (int J = 0; J < 4; ++J)
+        *reinterpret_cast<uint2*>(ob + c * kPxEpiPitch + 2 * (8 * J + 4 * h)) =
+            make_uint2(pack_bf16x2(acc[mb][4 * J], acc[mb][4 * J + 1]), pack_bf16x2(acc[mb][4 * J + 2], acc[mb][4 * J + 3]));
 #pragma unroll
-        for (int J = 0; J < 4; ++J)
-          *reinterpret_cast<uint2*>(ob + c * kPxEpiPitch + 2 * (8 * J + 4 * h)) =
-              make_uint2(pack_bf16x2(acc[g][mb][4 * J], acc[g][mb][4 * J + 1]),
-                         pack_bf16x2(acc[g][mb][4 * J + 2], acc[g][mb][4 * J + 3]));
-#pragma unroll
-        for (int itr = 0; itr < 2; ++itr) {
-          const int idx = lane + 64 * itr;
-          const int row = idx >> 2, q4 = idx & 3;
-          const int grow = 32 * mb + row;
-          if (grow < nrows) {
-            const u32x4_t v = *reinterpret_cast<const u32x4_t*>(ob + row * kPxEpiPitch + 16 * q4);
-            st16(a.out + (int64_t)table[(seg0 & 3) + grow] * a.N + kPxBN * NG * nt + 32 * (wave + 8 * g) + 8 * q4, v);
-          }
+      for (int itr = 0; itr < 2; ++itr) {
+        const int idx = lane + 64 * itr;
+        const int row = idx >> 2, q4 = idx & 3;
+        const int grow = 32 * mb + row;
+        if (grow < nrows) {
+          const u32x4_t v = *reinterpret_cast<const u32x4_t*>(ob + row * kPxEpiPitch + 16 * q4);
+          st16(a.out + (int64_t)table[(seg0 & 3) + grow] * a.N + kPxBN * nt + 32 * wave + 8 * q4, v);
         }
       }
     }
@@ -574,49 +495,42 @@ template <int MODE>
 __device__ __forceinline__ int px_dispatch(const PrefillArgs& a, unsigned char* smem, const PxItem& it,
                                            const PxItem& nx, bool has_next, int p0, int n_inflight,
                                            int* fetch_q) {
-#define W4A16_PX(MB_, SPLIT_, NG_) \
-  return px_run<MODE, MB_, SPLIT_, NG_>(a, smem, it, nx, has_next, p0, n_inflight, fetch_q)
-  if (it.ng == 2) {
-    // wide items: the tails (at most 128 rows)
-    if (it.mb == 4) W4A16_PX(4, false, 2);
-    if (it.mb == 2) W4A16_PX(2, false, 2);
-    W4A16_PX(1, false, 2);
-  }
   if constexpr (MODE == kModeGateUp) {
-    // half n-tile: eight wavefronts on four wavefronts' columns
-    if (a.I - 128 * it.nt == 64) W4A16_PX(4, true, 1);
+    if (a.I - 128 * it.nt == 64 && it.mb >= 2) {
+      // half n-tile: eight wavefronts on four wavefronts' columns
+      if (it.mb == 8) return px_run<MODE, 4, true>(a, smem, it, nx, has_next, p0, n_inflight, fetch_q);
+      if (it.mb == 4) return px_run<MODE, 2, true>(a, smem, it, nx, has_next, p0, n_inflight, fetch_q);
+      return px_run<MODE, 1, true>(a, smem, it, nx, has_next, p0, n_inflight, fetch_q);
+    }
   }
-  W4A16_PX(8, false, 1);
-#undef W4A16_PX
+  if (it.mb == 8) return px_run<MODE, 8>(a, smem, it, nx, has_next, p0, n_inflight, fetch_q);
+  if (it.mb == 4) return px_run<MODE, 4>(a, smem, it, nx, has_next, p0, n_inflight, fetch_q);
+  if (it.mb == 2) return px_run<MODE, 2>(a, smem, it, nx, has_next, p0, n_inflight, fetch_q);
+  return px_run<MODE, 1>(a, smem, it, nx, has_next, p0, n_inflight, fetch_q);
 }
 
-// Persistent grid, one workgroup per CU.  XCD x owns global m-tiles x,
-// x + 8, ...; its local items are the n-tiles of its large m-tiles, then the
-// wide n-tiles of its tails (px_item_info): the tile list runs from large
-// tiles to small, so the item list is large items first.  Workgroup b of
-// XCD x = b % 8 takes local items b / 8 and b / 8 + P (P = workgroups per
-// XCD), then the items that XCD's queue counter hands out, 2 P, 2 P + 1,
-// ... in the order the workgroups ask: each asks during the last stage of
-// the item before its next one, so the index is known one item ahead (the
-// next item's rows and first stages are loaded during the current one).
-// Work then goes to whichever workgroup is free first: item costs vary
-// (segment tails, the half n-tile) and a fixed deal leaves some workgroups
-// with markedly more.  (Deciding three stages before an item's end instead,
-// with a full wait at that stage, measured no faster and spilled registers.)
-// queues[x] counts XCD x's handed-out items, queues[8] the workgroups that
-// have left; the expert sort zeroes them and the last workgroup to leave
-// resets them.
+// Persistent grid, one workgroup per CU.  Local item i of XCD x is n-tile
+// i % n_nt of the XCD's m-tile i / n_nt, global m-tile x + 8 (i / n_nt); the
+// tile list runs from large tiles to small, so the list is large items
+// first.  Workgroup b of XCD x = b % 8 takes local items b / 8 and
+// b / 8 + P (P = workgroups per XCD), then the items that XCD's queue
+// counter hands out, 2 P, 2 P + 1, ... in the order the workgroups ask:
+// each asks during the last stage of the item before its next one, so the
+// index is known one item ahead (the next item's rows and first stages are
+// loaded during the current one).  Work then goes to whichever workgroup
+// is free first: item costs vary (segment tails, the half n-tile) and a
+// fixed deal leaves some workgroups with markedly more.  queues[x] counts
+// XCD x's handed-out items, queues[8] the workgroups that have left; the
+// expert sort zeroes them and the last workgroup to leave resets them.
 // Without queues the deal is fixed: items b / 8 + r P.
 template <int MODE>
 __global__ __launch_bounds__(kPxThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_prefill_x(PrefillArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int ntiles = ld_uniform(a.counters, 1);
-  const int nbig = ld_uniform(a.counters, 2);
   const int xcd = blockIdx.x & 7;
   const int n_local = ntiles > xcd ? (ntiles - xcd + 7) >> 3 : 0;  // this XCD's m-tiles
-  const int nbx = nbig > xcd ? (nbig - xcd + 7) >> 3 : 0;          // ... of them large
-  const int it_end = nbx * a.n_nt + (n_local - nbx) * a.n_nt2;
+  const int it_end = n_local * a.n_nt;
   const int P = gridDim.x >> 3;
   int* const queue = a.queues != nullptr ? a.queues + xcd : nullptr;
   // the last workgroup to leave resets the counters for the next launch
@@ -635,7 +549,7 @@ void k_prefill_x(PrefillArgs a) {
     return;
   }
   const int nkt = a.K / kPxKT;
-  PxItem cur = px_item_info(a, xcd, nbx, item);
+  PxItem cur = px_item_info(a, xcd, item);
   if (MODE == kModeGateUp) {
     // the first item's gathered rows into the table (nothing else in flight)
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -656,7 +570,7 @@ void k_prefill_x(PrefillArgs a) {
   int nitem = item + P;
   for (;;) {
     const bool has_next = nitem < it_end;
-    const PxItem nxt = has_next ? px_item_info(a, xcd, nbx, nitem) : cur;
+    const PxItem nxt = has_next ? px_item_info(a, xcd, nitem) : cur;
     // with a next item, take the index of the one after it during this item
     n_inflight = px_dispatch<MODE>(a, smem, cur, nxt, has_next, p0, n_inflight, has_next ? queue : nullptr);
     if (!has_next) break;

@@ -722,8 +722,7 @@ hipError_t launch_router_topk(const float* partial, int ksplit, const uint16_t* 
 // expert sort: one workgroup of 1024 threads
 //   desc[4*u .. 4*u+3] = (expert, segment start, segment rows, 0) for the u-th
 //     active expert in ascending expert order
-//   counters[0] = number of active experts, counters[1] = number of prefill
-//     tiles, counters[2] = how many of them have more than BM / 2 rows
+//   counters[0] = number of active experts, counters[1] = number of prefill tiles
 //   tiles[i] = (expert << 16) | m_tile for the i-th (expert, m-tile) pair:
 //     first every tile of more than BM / 2 rows (expert order), then the
 //     segment tails of at most BM / 2 rows (expert order), so work queues
@@ -775,7 +774,6 @@ __device__ int write_plan(int c, int E, int32_t* __restrict__ offsets, int32_t* 
       offsets[E] = tot;
       counters[0] = nact;
       counters[1] = nbig_tot + nsmall_tot;
-      counters[2] = nbig_tot;
     }
     if (tid < E && c > 0) {
       const int4 d = make_int4(tid, off, c, 0);
@@ -838,7 +836,6 @@ __device__ void plan_wave(const int* cnt, int* run, int E, int32_t* __restrict__
     offsets[E] = ci;
     counters[0] = ai;
     counters[1] = bi + si;
-    counters[2] = nbig_tot;
   }
 }
 

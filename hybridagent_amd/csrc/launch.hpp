@@ -49,10 +49,9 @@ struct PrefillArgs {
   const int32_t* sorted_pos;  // [M*k] rows t*k+j in expert-segment order
   const int32_t* offsets;     // [E+1] segment starts
   const int32_t* tiles;       // m-tiles (expert << 16 | tile index in the segment)
-  const int32_t* counters;    // [1] = number of m-tiles, [2] = those of more than 128 rows
+  const int32_t* counters;    // [1] = number of m-tiles
   int N, K, G, ng, topk, I;
   int n_nt;                   // n-tiles per m-tile
-  int n_nt2;                  // exact-form kernel: wide n-tiles per tail m-tile (ceil(n_nt / 2))
   // bias form only: 136 * activation sums per (128-wide k tile, segment
   // row), [ncr][ldc] -- gate_up: of the routed token rows; down: of the
   // intermediate rows, written by the gate_up epilogue into cr_out
