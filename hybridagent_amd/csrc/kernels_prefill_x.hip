@@ -7,10 +7,11 @@
 //
 // Work item = (m-tile of up to 256 rows of one expert's segment, n-tile of
 // 256 weight rows; gate_up: 128 gate rows + the matching 128 up rows).  A
-// persistent grid of one 512-thread workgroup per CU: XCD x (workgroups are
-// dealt to the 8 XCDs in turn) owns m-tiles x, x + 8, ... of the tile list
-// (which lists the large tiles first) with all their n-tiles, and its
-// workgroups take its items in turn.  Each of the eight wavefronts owns 32
+// persistent grid of one 512-thread workgroup per CU takes the items from a
+// work queue (the tile list lists the large tiles first): for down, XCD x
+// (workgroups are dealt to the 8 XCDs in turn) owns m-tiles x, x + 8, ...
+// with all their n-tiles and a queue of its own; gate_up has one queue for
+// the chip.  Each of the eight wavefronts owns 32
 // weight rows (gate_up: 16 gate + their 16 up rows) for all the item's
 // rows: MB m-blocks of v_mfma_f32_32x32x16_bf16 accumulators (MB = 8 for
 // 256 rows; 4, 2, 1 for segment tails of up to 128, 64, 32 rows).
@@ -157,11 +158,12 @@ struct PxItem {
   int nt, e, seg0, nrows, mb;
 };
 
-__device__ __forceinline__ PxItem px_item_info(const PrefillArgs& a, int xcd, int item) {
+// Item `item` of a queue whose m-tiles are tile list entries x0, x0 + xs, ...
+__device__ __forceinline__ PxItem px_item_info(const PrefillArgs& a, int x0, int xs, int item) {
   PxItem it;
   const int lm = item / a.n_nt;
   it.nt = item - lm * a.n_nt;
-  const int tile = ld_uniform(a.tiles, xcd + 8 * lm);
+  const int tile = ld_uniform(a.tiles, x0 + xs * lm);
   it.e = tile >> 16;
   it.seg0 = ld_uniform(a.offsets, it.e) + (tile & 0xFFFF) * kPxBM;
   it.nrows = min(kPxBM, ld_uniform(a.offsets, it.e + 1) - it.seg0);
@@ -509,30 +511,35 @@ __device__ __forceinline__ int px_dispatch(const PrefillArgs& a, unsigned char* 
   return px_run<MODE, 1>(a, smem, it, nx, has_next, p0, n_inflight, fetch_q);
 }
 
-// Persistent grid, one workgroup per CU.  Local item i of XCD x is n-tile
-// i % n_nt of the XCD's m-tile i / n_nt, global m-tile x + 8 (i / n_nt); the
-// tile list runs from large tiles to small, so the list is large items
-// first.  Workgroup b of XCD x = b % 8 takes local items b / 8 and
-// b / 8 + P (P = workgroups per XCD), then the items that XCD's queue
-// counter hands out, 2 P, 2 P + 1, ... in the order the workgroups ask:
-// each asks during the last stage of the item before its next one, so the
+// Persistent grid, one workgroup per CU.  down: local item i of XCD x is
+// n-tile i % n_nt of the XCD's m-tile i / n_nt, tile list entry x + 8 (i /
+// n_nt), so an m-tile's activation rows are read into one L2 for its 11
+// n-tiles; workgroup b of XCD x = b % 8 takes local items b / 8 and b / 8 +
+// P (P = workgroups per XCD), then the items that XCD's queue counter
+// (queues[x]) hands out, 2 P, 2 P + 1, ...  gate_up: item i is n-tile i %
+// n_nt of tile list entry i / n_nt, workgroup b takes items b and b + P (P
+// = all workgroups), then those of the one queue (queues[0]): its items
+// differ more in cost (segment tails, the half n-tile) and the XCDs in
+// speed, and the whole chip draining one queue ends them closer together
+// than the rows kept in one L2 save.  The list runs from large tiles to
+// small, so large items go first.  Workgroups ask in the order they get
+// there, during the last stage of the item before their next one, so the
 // index is known one item ahead (the next item's rows and first stages are
-// loaded during the current one).  Work then goes to whichever workgroup
-// is free first: item costs vary (segment tails, the half n-tile) and a
-// fixed deal leaves some workgroups with markedly more.  queues[x] counts
-// XCD x's handed-out items, queues[8] the workgroups that have left; the
-// expert sort zeroes them and the last workgroup to leave resets them.
-// Without queues the deal is fixed: items b / 8 + r P.
+// loaded during the current one).  queues[8] counts the workgroups that
+// have left; the expert sort zeroes the counters and the last workgroup to
+// leave resets them.  Without queues the deal is fixed: items b + r P.
 template <int MODE>
 __global__ __launch_bounds__(kPxThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void k_prefill_x(PrefillArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int ntiles = ld_uniform(a.counters, 1);
-  const int xcd = blockIdx.x & 7;
-  const int n_local = ntiles > xcd ? (ntiles - xcd + 7) >> 3 : 0;  // this XCD's m-tiles
+  constexpr bool kChip = MODE == kModeGateUp;  // one queue for the chip
+  const int x0 = kChip ? 0 : (int)(blockIdx.x & 7);
+  const int xs = kChip ? 1 : 8;
+  const int n_local = kChip ? ntiles : (ntiles > x0 ? (ntiles - x0 + 7) >> 3 : 0);  // the queue's m-tiles
   const int it_end = n_local * a.n_nt;
-  const int P = gridDim.x >> 3;
-  int* const queue = a.queues != nullptr ? a.queues + xcd : nullptr;
+  const int P = kChip ? (int)gridDim.x : (int)(gridDim.x >> 3);
+  int* const queue = a.queues != nullptr ? a.queues + x0 : nullptr;
   // the last workgroup to leave resets the counters for the next launch
   // (every other one has taken its last index before counting itself out)
   auto leave = [&] {
@@ -543,13 +550,13 @@ void k_prefill_x(PrefillArgs a) {
       for (int x = 0; x < 9; ++x) __hip_atomic_store(a.queues + x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   };
-  int item = blockIdx.x >> 3;
+  int item = kChip ? (int)blockIdx.x : (int)(blockIdx.x >> 3);
   if (item >= it_end) {
     leave();
     return;
   }
   const int nkt = a.K / kPxKT;
-  PxItem cur = px_item_info(a, xcd, item);
+  PxItem cur = px_item_info(a, x0, xs, item);
   if (MODE == kModeGateUp) {
     // the first item's gathered rows into the table (nothing else in flight)
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -570,7 +577,7 @@ void k_prefill_x(PrefillArgs a) {
   int nitem = item + P;
   for (;;) {
     const bool has_next = nitem < it_end;
-    const PxItem nxt = has_next ? px_item_info(a, xcd, nitem) : cur;
+    const PxItem nxt = has_next ? px_item_info(a, x0, xs, nitem) : cur;
     // with a next item, take the index of the one after it during this item
     n_inflight = px_dispatch<MODE>(a, smem, cur, nxt, has_next, p0, n_inflight, has_next ? queue : nullptr);
     if (!has_next) break;
