@@ -59,6 +59,13 @@ SIGNATURES = {
                                              _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "moe_layer_forward": (ctypes.c_int, [_VP, _VP, _F32, _VP, _VP, _F32, _VP, _VP, _VP, _VP, _VP, _VP,
                                          _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
+    "w4a16_tiled_gate_up_bytes": (_SZ, [_I64, _I64, _I64]),
+    "w4a16_tile_gate_up": (ctypes.c_int, [_VP, _I64, _I64, _I64, _VP, _SZ, _VP]),
+    "moe_gate_up_tiled": (ctypes.c_int, [_VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ,
+                                         _VP]),
+    "moe_layer_forward_tiled": (ctypes.c_int, [_VP, _VP, _F32, _VP, _VP, _F32, _VP, _VP, _VP, _VP, _VP, _VP,
+                                               _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ,
+                                               _VP]),
 }
 
 _lib = None
@@ -366,12 +373,33 @@ def moe_forward(hidden_states: torch.Tensor, top_k_index: torch.Tensor, top_k_we
     return out.reshape(*hidden_states.shape[:-1], H)
 
 
+def tile_gate_up(gu_packed: torch.Tensor) -> torch.Tensor | None:
+    """The tiled copy of gate_up_packed [E, 2I, H/8] that the decode gate_up streamer
+    reads contiguously (a load-time re-layout beside quantization.py:325-430; the
+    original stays as it is), or None where the streamer has no tiled form."""
+    dev = _require_gpu(gu_packed)
+    gu_packed = _i32(gu_packed, "gate_up_packed")
+    E, two_i, h8 = gu_packed.shape
+    lib = load()
+    nbytes = lib.w4a16_tiled_gate_up_bytes(E, h8 * 8, two_i // 2)
+    if nbytes == 0:
+        return None
+    tiled = torch.empty(nbytes // 4, dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        _check(lib.w4a16_tile_gate_up(_ptr(gu_packed), E, h8 * 8, two_i // 2, _ptr(tiled), nbytes, _stream(dev)),
+               "w4a16_tile_gate_up")
+    return tiled
+
+
 def moe_layer_forward(router_in: torch.Tensor, router_scale: torch.Tensor, scalar_root: float,
                       proj_w: torch.Tensor, per_expert_scale: torch.Tensor, eps: float, top_k: int,
                       hidden_states: torch.Tensor, gu_packed: torch.Tensor, gu_scale: torch.Tensor,
-                      dn_packed: torch.Tensor, dn_scale: torch.Tensor, group_size: int | None = None):
+                      dn_packed: torch.Tensor, dn_scale: torch.Tensor, group_size: int | None = None,
+                      gu_tiled: torch.Tensor | None = None):
     """Router (backends.py:111-117) on ``router_in`` + experts (quantization.py:88-129) on
-    ``hidden_states`` in one call -> (out [T, H] bf16, top_k_weights fp32, top_k_index int64)."""
+    ``hidden_states`` in one call -> (out [T, H] bf16, top_k_weights fp32, top_k_index int64).
+    ``gu_tiled`` (from tile_gate_up) lets the decode gate_up streamer read contiguous tiles;
+    the output is bit-identical."""
     dev = _require_gpu(router_in, router_scale, proj_w, per_expert_scale, hidden_states, gu_packed,
                        gu_scale, dn_packed, dn_scale)
     H = hidden_states.shape[-1]
@@ -398,12 +426,23 @@ def moe_layer_forward(router_in: torch.Tensor, router_scale: torch.Tensor, scala
     lib = load()
     ws = _workspace(lib.moe_layer_workspace_bytes(max(M, 1), top_k, E, H, I), dev)
     with torch.cuda.device(dev):
-        _check(lib.moe_layer_forward(_ptr(r2), _ptr(router_scale), float(scalar_root), _ptr(proj_w),
-                                     _ptr(per_expert_scale), float(eps), _ptr(x), _ptr(gu_packed),
-                                     _ptr(gu_scale), _ptr(dn_packed), _ptr(dn_scale), _ptr(out), _ptr(idx),
-                                     _ptr(w), M, top_k, E, H, I, G, _ptr(ws),
-                                     0 if ws is None else ws.numel(), _stream(dev)),
-               "moe_layer_forward")
+        if gu_tiled is None:
+            _check(lib.moe_layer_forward(_ptr(r2), _ptr(router_scale), float(scalar_root), _ptr(proj_w),
+                                         _ptr(per_expert_scale), float(eps), _ptr(x), _ptr(gu_packed),
+                                         _ptr(gu_scale), _ptr(dn_packed), _ptr(dn_scale), _ptr(out), _ptr(idx),
+                                         _ptr(w), M, top_k, E, H, I, G, _ptr(ws),
+                                         0 if ws is None else ws.numel(), _stream(dev)),
+                   "moe_layer_forward")
+        else:
+            gu_tiled = _i32(gu_tiled, "gate_up tiled copy")
+            if gu_tiled.device != dev or gu_tiled.numel() * 4 < lib.w4a16_tiled_gate_up_bytes(E, H, I):
+                raise ValueError("gate_up tiled copy does not match the expert weights")
+            _check(lib.moe_layer_forward_tiled(_ptr(r2), _ptr(router_scale), float(scalar_root), _ptr(proj_w),
+                                               _ptr(per_expert_scale), float(eps), _ptr(x), _ptr(gu_packed),
+                                               _ptr(gu_tiled), _ptr(gu_scale), _ptr(dn_packed), _ptr(dn_scale),
+                                               _ptr(out), _ptr(idx), _ptr(w), M, top_k, E, H, I, G, _ptr(ws),
+                                               0 if ws is None else ws.numel(), _stream(dev)),
+                   "moe_layer_forward_tiled")
     return out.reshape(*hidden_states.shape[:-1], H), w, idx
 
 
@@ -520,10 +559,16 @@ class MoEStages:
         _check(self.lib.moe_plan(_ptr(hidden), _ptr(top_k_index), *self._dims(), self.G, _ptr(self.ws),
                                  self.ws.numel(), s), "moe_plan")
 
-    def gate_up(self, hidden: torch.Tensor, gu_packed: torch.Tensor, gu_scale: torch.Tensor) -> None:
+    def gate_up(self, hidden: torch.Tensor, gu_packed: torch.Tensor, gu_scale: torch.Tensor,
+                gu_tiled: torch.Tensor | None = None) -> None:
         s = _stream(self.device)
-        _check(self.lib.moe_gate_up(_ptr(hidden), _ptr(gu_packed), _ptr(gu_scale), *self._dims(), self.G,
-                                    _ptr(self.ws), self.ws.numel(), s), "moe_gate_up")
+        if gu_tiled is None:
+            _check(self.lib.moe_gate_up(_ptr(hidden), _ptr(gu_packed), _ptr(gu_scale), *self._dims(), self.G,
+                                        _ptr(self.ws), self.ws.numel(), s), "moe_gate_up")
+        else:
+            _check(self.lib.moe_gate_up_tiled(_ptr(hidden), _ptr(gu_packed), _ptr(gu_tiled), _ptr(gu_scale),
+                                              *self._dims(), self.G, _ptr(self.ws), self.ws.numel(), s),
+                   "moe_gate_up_tiled")
 
     def down(self, dn_packed: torch.Tensor, dn_scale: torch.Tensor) -> None:
         s = _stream(self.device)

@@ -428,9 +428,14 @@ int moe_plan(const uint16_t* hidden, const int64_t* topk_idx, int64_t M, int64_t
   return launch_status(e);
 }
 
-int moe_gate_up(const uint16_t* hidden, const int32_t* gu_packed, const uint16_t* gu_scale,
-                int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t group_size,
-                void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+// gate_up on either weight layout: gu_tiled (the tiled copy, nullable) serves
+// the decode streamer where it applies, gu_packed everything else
+int gate_up_impl(const uint16_t* hidden, const int32_t* gu_packed, const uint16_t* gu_scale,
+                 const int32_t* gu_tiled, int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I,
+                 int64_t group_size, void* workspace, size_t workspace_bytes, void* stream) {
   MoeLayout L{};
   int st = moe_check(M, top_k, E, H, I, group_size, workspace, workspace_bytes, &L);
   if (st != W4A16_OK || M == 0) return st;
@@ -495,7 +500,45 @@ int moe_gate_up(const uint16_t* hidden, const int32_t* gu_packed, const uint16_t
   a.N = (int)(2 * I);
   a.K = (int)H;
   a.ng = (int)((H + group_size - 1) / group_size);
+  if (gu_tiled != nullptr && group_size == 128 && (a.ng % 2) == 0 && tiled_gate_up_bytes_per_expert(H, I) > 0) {
+    if (!aligned16(gu_tiled)) return W4A16_ERR_ALIGN;
+    a.wp = gu_tiled;
+    return launch_status(launch_decode_gate_up_tiled(a, max_slots, s));
+  }
   return launch_status(launch_decode(kModeGateUp, group_size % 128 == 0, a, max_slots, s));
+}
+}  // namespace
+
+extern "C" {
+
+int moe_gate_up(const uint16_t* hidden, const int32_t* gu_packed, const uint16_t* gu_scale,
+                int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t group_size,
+                void* workspace, size_t workspace_bytes, void* stream) {
+  return gate_up_impl(hidden, gu_packed, gu_scale, nullptr, M, top_k, E, H, I, group_size, workspace,
+                      workspace_bytes, stream);
+}
+
+int moe_gate_up_tiled(const uint16_t* hidden, const int32_t* gu_packed, const int32_t* gu_tiled,
+                      const uint16_t* gu_scale, int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I,
+                      int64_t group_size, void* workspace, size_t workspace_bytes, void* stream) {
+  return gate_up_impl(hidden, gu_packed, gu_scale, gu_tiled, M, top_k, E, H, I, group_size, workspace,
+                      workspace_bytes, stream);
+}
+
+size_t w4a16_tiled_gate_up_bytes(int64_t E, int64_t H, int64_t I) {
+  if (E <= 0 || E > kMaxExperts) return 0;
+  return (size_t)E * tiled_gate_up_bytes_per_expert(H, I);
+}
+
+int w4a16_tile_gate_up(const int32_t* gu_packed, int64_t E, int64_t H, int64_t I, int32_t* tiled,
+                       size_t tiled_bytes, void* stream) {
+  const size_t need = w4a16_tiled_gate_up_bytes(E, H, I);
+  if (need == 0) return W4A16_ERR_SHAPE;
+  if (!gu_packed || !tiled) return W4A16_ERR_NULL;
+  if (!aligned16(gu_packed) || !aligned16(tiled)) return W4A16_ERR_ALIGN;
+  if (tiled_bytes < need) return W4A16_ERR_WORKSPACE;
+  return launch_status(launch_tile_gate_up(gu_packed, (int)E, (int)H, (int)I, tiled,
+                                           static_cast<hipStream_t>(stream)));
 }
 
 int moe_down(const int32_t* dn_packed, const uint16_t* dn_scale, int64_t M, int64_t top_k,
@@ -867,13 +910,13 @@ size_t moe_layer_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t H,
   return moe_layout(nullptr, M, top_k, E, H, I).bytes + moe_router_workspace_bytes(M, H, E);
 }
 
-int moe_layer_forward(const uint16_t* router_in, const uint16_t* router_scale, float scalar_root,
-                      const uint16_t* proj_w, const uint16_t* per_expert_scale, float eps,
-                      const uint16_t* hidden, const int32_t* gu_packed, const uint16_t* gu_scale,
-                      const int32_t* dn_packed, const uint16_t* dn_scale, uint16_t* out,
-                      int64_t* topk_idx, float* topk_w, int64_t M, int64_t top_k, int64_t E,
-                      int64_t H, int64_t I, int64_t group_size, void* workspace,
-                      size_t workspace_bytes, void* stream) {
+static int layer_forward_impl(const uint16_t* router_in, const uint16_t* router_scale, float scalar_root,
+                              const uint16_t* proj_w, const uint16_t* per_expert_scale, float eps,
+                              const uint16_t* hidden, const int32_t* gu_packed, const int32_t* gu_tiled,
+                              const uint16_t* gu_scale, const int32_t* dn_packed, const uint16_t* dn_scale,
+                              uint16_t* out, int64_t* topk_idx, float* topk_w, int64_t M, int64_t top_k,
+                              int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
+                              size_t workspace_bytes, void* stream) {
   if (M < 0 || M > (1 << 24) || top_k > E) return W4A16_ERR_SHAPE;
   if (M == 0) {
     MoeLayout dummy{};
@@ -911,12 +954,36 @@ int moe_layer_forward(const uint16_t* router_in, const uint16_t* router_scale, f
     st = moe_plan(hidden, topk_idx, M, top_k, E, H, I, group_size, workspace, moe_bytes, stream);
     if (st != W4A16_OK) return st;
   }
-  st = moe_gate_up(hidden, gu_packed, gu_scale, M, top_k, E, H, I, group_size, workspace,
-                   moe_bytes, stream);
+  st = gate_up_impl(hidden, gu_packed, gu_scale, gu_tiled, M, top_k, E, H, I, group_size, workspace,
+                    moe_bytes, stream);
   if (st == W4A16_OK)
     st = down_and_combine(dn_packed, dn_scale, topk_idx, topk_w, out, M, top_k, E, H, I,
                           group_size, workspace, moe_bytes, stream);
   return st;
+}
+
+int moe_layer_forward(const uint16_t* router_in, const uint16_t* router_scale, float scalar_root,
+                      const uint16_t* proj_w, const uint16_t* per_expert_scale, float eps,
+                      const uint16_t* hidden, const int32_t* gu_packed, const uint16_t* gu_scale,
+                      const int32_t* dn_packed, const uint16_t* dn_scale, uint16_t* out,
+                      int64_t* topk_idx, float* topk_w, int64_t M, int64_t top_k, int64_t E,
+                      int64_t H, int64_t I, int64_t group_size, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+  return layer_forward_impl(router_in, router_scale, scalar_root, proj_w, per_expert_scale, eps, hidden,
+                            gu_packed, nullptr, gu_scale, dn_packed, dn_scale, out, topk_idx, topk_w, M,
+                            top_k, E, H, I, group_size, workspace, workspace_bytes, stream);
+}
+
+int moe_layer_forward_tiled(const uint16_t* router_in, const uint16_t* router_scale, float scalar_root,
+                            const uint16_t* proj_w, const uint16_t* per_expert_scale, float eps,
+                            const uint16_t* hidden, const int32_t* gu_packed, const int32_t* gu_tiled,
+                            const uint16_t* gu_scale, const int32_t* dn_packed, const uint16_t* dn_scale,
+                            uint16_t* out, int64_t* topk_idx, float* topk_w, int64_t M, int64_t top_k,
+                            int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  return layer_forward_impl(router_in, router_scale, scalar_root, proj_w, per_expert_scale, eps, hidden,
+                            gu_packed, gu_tiled, gu_scale, dn_packed, dn_scale, out, topk_idx, topk_w, M,
+                            top_k, E, H, I, group_size, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

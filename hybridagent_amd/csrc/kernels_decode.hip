@@ -125,7 +125,10 @@ __device__ __forceinline__ int frag_slot(int b, int rb, int j) {
 
 // WIDE (group size 128, an even number of groups per row): the scales of one
 // item's TPW tiles are consecutive bf16 values, fetched with one load.
-template <int MODE, bool BIAS, int TPW, int KSPLIT, bool LONGK, bool WIDE>
+// TILED (gate_up, bias form, K split): the weights come in the tiled layout
+// written by k_tile_gate_up, where each wavefront's tile of an item is one
+// contiguous KiB (lane l's 16 bytes at 16 l) instead of 16 rows x 64 bytes.
+template <int MODE, bool BIAS, int TPW, int KSPLIT, bool LONGK, bool WIDE, bool TILED = false>
 __global__ __launch_bounds__(stream_threads(KSPLIT)) __attribute__((amdgpu_waves_per_eu(TPW >= 4 ? 2 : 4, 8)))
 void k_decode(DecodeArgs a) {
   constexpr int kStreamThreads = stream_threads(KSPLIT);
@@ -138,6 +141,7 @@ void k_decode(DecodeArgs a) {
   float* __restrict__ csum = reinterpret_cast<float*>(smem_raw + (size_t)ntiles * 16 * a.rb * 16);
   static_assert(KSPLIT == 1 || KSPLIT == 4, "the split-K epilogue gives wavefront ks output row ks");
   static_assert(!WIDE || (BIAS && !LONGK), "wide scale loads serve the bias form");
+  static_assert(!TILED || (MODE == kModeGateUp && BIAS && KSPLIT == 4 && !LONGK), "tiled gate_up layout");
   // split-K partials, double-buffered so one barrier per item suffices
   __shared__ f32x4_t red[2][KSPLIT > 1 ? NWAVES : 1][64];
   __shared__ int tok[16];
@@ -223,8 +227,10 @@ void k_decode(DecodeArgs a) {
   // lane carries one byte offset per item.  Rows past the matrix read as
   // zero; chunks past the row end read the next row, harmless because their
   // activation operand is zero.
+  // tiled: an expert is n_ct items of NWAVES x TPW KiB tiles
+  const int64_t wstride = TILED ? (int64_t)a.n_ct * NWAVES * TPW * 256 : (int64_t)a.N * K8;
   const __amdgpu_buffer_rsrc_t wsrc =
-      make_rsrc(reinterpret_cast<const uint32_t*>(a.wp) + (int64_t)e * a.N * K8, (uint32_t)a.N * K8 * 4u);
+      make_rsrc(reinterpret_cast<const uint32_t*>(a.wp) + (int64_t)e * wstride, (uint32_t)wstride * 4u);
   const __amdgpu_buffer_rsrc_t ssrc = make_rsrc(a.ws + (int64_t)e * a.N * a.ng, (uint32_t)a.N * a.ng * 2u);
   struct Off {
     int woff, srow;
@@ -232,6 +238,7 @@ void k_decode(DecodeArgs a) {
   auto off_of = [&](int ct) -> Off {
     bool ok;
     const int wrow = weight_row(ct, &ok);
+    if (TILED) return Off{(ct * NWAVES + wave) * (TPW * 1024) + 16 * lane, wrow * a.ng};
     return Off{wrow * K8 * 4 + 16 * kb, wrow * a.ng};
   };
   auto scale_off = [&](const Off& o, int t) -> int {
@@ -274,7 +281,8 @@ void k_decode(DecodeArgs a) {
     if (WIDE) load_scales_wide(r, o);
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
-      bw[r][i] = buf_ld16(wsrc, o.woff + 64 * tb, 64 * i);
+      bw[r][i] = TILED ? buf_ld16(wsrc, tb + i < ntiles ? o.woff : 16 * lane, tb + i < ntiles ? 1024 * i : 0)
+                       : buf_ld16(wsrc, o.woff + 64 * tb, 64 * i);
       if (!WIDE) sc[r][i] = buf_ld_u16(ssrc, scale_off(o, tb + i));
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -431,7 +439,10 @@ void k_decode(DecodeArgs a) {
         bv[3] = unpack_exact<false>(bw[r][i].w, sci);
       }
       if (REFILL) {
-        bw[r][i] = buf_ld16(wsrc, nx.woff + 64 * tb, 64 * i);
+        // tiled: tiles past K read the expert's first KiB (cached; their
+        // scale is zero)
+        bw[r][i] = TILED ? buf_ld16(wsrc, t_ok ? nx.woff : 16 * lane, t_ok ? 1024 * i : 0)
+                         : buf_ld16(wsrc, nx.woff + 64 * tb, 64 * i);
         if (!WIDE) sc[r][i] = buf_ld_u16(ssrc, scale_off(nx, tc));
       }
       if (BIAS) {
@@ -624,9 +635,9 @@ static size_t stream_lds(const DecodeArgs& a) {
   return (size_t)ntiles * 16 * a.rb * 16 + (size_t)ntiles * 16 * 4;
 }
 
-template <int MODE, bool BIAS, int TPW, int KSPLIT, bool LONGK, bool WIDE = false>
+template <int MODE, bool BIAS, int TPW, int KSPLIT, bool LONGK, bool WIDE = false, bool TILED = false>
 static hipError_t launch_stream(DecodeArgs a, int max_slots, hipStream_t s) {
-  auto kern = k_decode<MODE, BIAS, TPW, KSPLIT, LONGK, WIDE>;
+  auto kern = k_decode<MODE, BIAS, TPW, KSPLIT, LONGK, WIDE, TILED>;
   // the workgroups that fit on the chip at once, at least one per possible
   // expert slot and at most one per item; the kernel spreads them over the
   // experts that turn out active (dense: the row groups)
@@ -690,6 +701,93 @@ hipError_t launch_decode(int mode, bool bias_form, DecodeArgs a, int max_slots, 
                      : launch_decode_mode<kModeGateUp, false>(a, max_slots, s);
   return bias_form ? launch_decode_mode<kModeDown, true>(a, max_slots, s)
                    : launch_decode_mode<kModeDown, false>(a, max_slots, s);
+}
+
+// ---------------------------------------------------------------------------
+// Tiled gate_up weights (a load-time copy for the decode streamer).  The
+// streamer's K-split shape (TPW k tiles per wavefront, 4 wavefronts per K
+// range, 4 column groups of 8 intermediate columns) reads, per item and
+// wavefront, TPW tiles of 16 weight rows x 64 bytes.  The tiled copy puts
+// each such tile in one contiguous KiB, in the order the streamer reads
+// them:
+//   byte ((((e * n_ct + ct) * 16 + w) * TPW + i) * 64 + l) * 16 .. + 15
+//     = packed row r of expert e, bytes 64 (ks TPW + i) + 16 (l / 16) .. + 15
+//   with w = 4 cg + ks, j = l % 16, colblk = 4 ct + cg,
+//   r = 8 colblk + j % 8 (+ I for j >= 8: the matching up row);
+// pieces past the row's K / 2 bytes or of column blocks past I are zero.
+// Supported where the streamer takes that shape: gate_up with K = H whose
+// decode shape is the K split without the long-K loop, I a multiple of 8.
+// ---------------------------------------------------------------------------
+bool tiled_gate_up_shape(int64_t H, int64_t I, int* tpw, int* n_ct) {
+  if (H <= 0 || I <= 0 || H % 32 != 0 || I % 8 != 0) return false;
+  const DecodeShape sh = decode_shape((int)H);
+  const int ntiles = (int)(((H >> 5) + 3) >> 2);
+  if (sh.ksplit != 4 || ntiles > 24) return false;
+  *tpw = sh.tpw;
+  *n_ct = (int)((I / 8 + 3) / 4);
+  return true;
+}
+
+size_t tiled_gate_up_bytes_per_expert(int64_t H, int64_t I) {
+  int tpw = 0, n_ct = 0;
+  if (!tiled_gate_up_shape(H, I, &tpw, &n_ct)) return 0;
+  return (size_t)n_ct * 16 * tpw * 1024;
+}
+
+// one thread per 16-byte piece of the tiled copy
+__global__ __launch_bounds__(256) void k_tile_gate_up(const uint32_t* __restrict__ packed,
+                                                      uint32_t* __restrict__ tiled, int I, int K,
+                                                      int tpw, int n_ct, int64_t pieces) {
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (p >= pieces) return;
+  const int l = (int)(p & 63);
+  int64_t q = p >> 6;
+  const int i = (int)(q % tpw);
+  q /= tpw;
+  const int w = (int)(q & 15);
+  q >>= 4;
+  const int ct = (int)(q % n_ct);
+  const int64_t e = q / n_ct;
+  const int cg = w >> 2, ks = w & 3;
+  const int j = l & 15, kb = l >> 4;
+  const int colblk = 4 * ct + cg;
+  const int row = 8 * colblk + (j & 7) + (j >= 8 ? I : 0);
+  const int rowbytes = K / 2;
+  const int byte = 64 * (ks * tpw + i) + 16 * kb;
+  u32x4_t v = {0u, 0u, 0u, 0u};
+  if (8 * colblk + 8 <= I && byte + 16 <= rowbytes)
+    v = *reinterpret_cast<const u32x4_t*>(packed + ((e * 2 * I + row) * (int64_t)rowbytes + byte) / 4);
+  *reinterpret_cast<u32x4_t*>(tiled + p * 4) = v;
+}
+
+hipError_t launch_tile_gate_up(const int32_t* packed, int E, int H, int I, int32_t* tiled, hipStream_t s) {
+  int tpw = 0, n_ct = 0;
+  if (!tiled_gate_up_shape(H, I, &tpw, &n_ct)) return hipErrorInvalidValue;
+  const int64_t pieces = (int64_t)E * n_ct * 16 * tpw * 64;
+  if (pieces == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_tile_gate_up, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, s,
+                     reinterpret_cast<const uint32_t*>(packed), reinterpret_cast<uint32_t*>(tiled), I, H,
+                     tpw, n_ct, pieces);
+  return hipGetLastError();
+}
+
+// The gate_up streamer on tiled weights (a.wp = the tiled copy): bias form
+// with one scale load per item (group size 128, an even group count).
+hipError_t launch_decode_gate_up_tiled(DecodeArgs a, int max_slots, hipStream_t s) {
+  if (max_slots <= 0) return hipSuccess;
+  if ((int64_t)a.M * a.topk * a.I * 2 >= (int64_t)0x7FFFFFF0) return hipErrorInvalidValue;
+  int tpw = 0, n_ct = 0;
+  if (!tiled_gate_up_shape(a.K, a.I, &tpw, &n_ct) || a.G != 128 || (a.ng % 2) != 0)
+    return hipErrorInvalidValue;
+  const int cg = stream_threads(4) / 64 / 4;
+  a.n_ct = (a.I / 8 + cg - 1) / cg;
+  a.rb = stage_rows(a.K, 4);
+  int rows_cap = 1;
+  while (rows_cap < a.rows_hint && rows_cap < 16) rows_cap <<= 1;
+  if (a.rb > rows_cap) a.rb = rows_cap;
+  if (tpw == 2) return launch_stream<kModeGateUp, true, 2, 4, false, true, true>(a, max_slots, s);
+  if (tpw == 4) return launch_stream<kModeGateUp, true, 4, 4, false, true, true>(a, max_slots, s);
+  return launch_stream<kModeGateUp, true, 6, 4, false, true, true>(a, max_slots, s);
 }
 
 // ---------------------------------------------------------------------------

@@ -1,0 +1,136 @@
+"""GPU: the tiled gate_up copy (w4a16_tile_gate_up) and the decode gate_up
+streamer reading it.  The copy is checked piece by piece against a numpy
+restatement of its documented layout; the layer and stage outputs on the
+tiled copy are compared bit for bit with the untiled path (same operands, same
+fold order), at decode sizes where it is used and at sizes where it is not."""
+import numpy as np
+import pytest
+import torch
+
+from hybridagent_amd import _lib, synth
+
+pytestmark = pytest.mark.gpu
+
+E, H, I, K_TOP = 128, 2816, 704, 8
+
+
+@pytest.fixture(scope="module")
+def dev():
+    assert _lib.available(), "libw4a16moe.so must be built"
+    return torch.device("cuda:0")
+
+
+def _tiled_reference(packed: np.ndarray, I: int, H: int, tpw: int) -> np.ndarray:
+    """The tiled layout restated from its definition: piece (e, ct, w, i, l) =
+    16 bytes of packed row r at byte 64 (ks tpw + i) + 16 (l / 16), w = 4 cg + ks,
+    colblk = 4 ct + cg, r = 8 colblk + (l % 16) % 8 (+ I for l % 16 >= 8);
+    zero past the row or for column blocks past I."""
+    Ex = packed.shape[0]
+    rowbytes = H // 2
+    rows = packed.view(np.uint8).reshape(Ex, 2 * I, rowbytes)
+    n_ct = (I // 8 + 3) // 4
+    out = np.zeros((Ex, n_ct, 16, tpw, 64, 16), np.uint8)
+    for ct in range(n_ct):
+        for w in range(16):
+            cg, ks = w >> 2, w & 3
+            colblk = 4 * ct + cg
+            if 8 * colblk + 8 > I:
+                continue
+            for i in range(tpw):
+                for l in range(64):
+                    j, kb = l & 15, l >> 4
+                    r = 8 * colblk + (j & 7) + (I if j >= 8 else 0)
+                    b = 64 * (ks * tpw + i) + 16 * kb
+                    if b + 16 <= rowbytes:
+                        out[:, ct, w, i, l] = rows[:, r, b:b + 16]
+    return out.reshape(-1)
+
+
+def test_tile_layout(dev):
+    Ex = 3
+    wts = synth.moe_weights(Ex, H, I, 128, seed=7100)
+    tiled = _lib.tile_gate_up(wts.gate_up_packed.to(dev))
+    assert tiled is not None
+    got = tiled.cpu().numpy().view(np.uint8)
+    ref = _tiled_reference(wts.gate_up_packed.numpy(), I, H, tpw=6)
+    assert got.shape == ref.shape
+    assert np.array_equal(got, ref)
+
+
+def test_tile_unsupported_shape(dev):
+    wts = synth.moe_weights(4, 256, 64, 128, seed=7101)
+    assert _lib.tile_gate_up(wts.gate_up_packed.to(dev)) is None
+
+
+@pytest.fixture(scope="module", params=[128, 32])
+def layer(request, dev):
+    G = request.param
+    w = synth.moe_weights(E, H, I, G, seed=7200 + G)
+    gpu = [getattr(w, k).to(dev) for k in ("gate_up_packed", "gate_up_scale", "down_packed", "down_scale")]
+    rw = synth.router_weights(E, H, seed=7300)
+    r = (rw.scale.to(dev), rw.scalar_root, rw.proj.to(dev), rw.per_expert_scale.to(dev), 1e-6, K_TOP)
+    return G, gpu, r, _lib.tile_gate_up(gpu[0])
+
+
+def _bits(t):
+    return t.detach().cpu().view(torch.int16).numpy()
+
+
+# decode sizes (the tiled streamer at G = 128; G = 32 keeps the packed path)
+# and a prefill size (packed path)
+@pytest.mark.parametrize("M", [1, 8, 32, 64, 300])
+def test_layer_tiled_equals_untiled(dev, layer, M):
+    G, gpu, r, tiled = layer
+    print(f"tiled layer G={G} M={M}", flush=True)
+    x = synth.activations(M, H, seed=7400 + M).to(dev)
+    y0, w0, i0 = _lib.moe_layer_forward(x, r[0], r[1], r[2], r[3], r[4], r[5], x, gpu[0], gpu[1], gpu[2], gpu[3])
+    y1, w1, i1 = _lib.moe_layer_forward(x, r[0], r[1], r[2], r[3], r[4], r[5], x, gpu[0], gpu[1], gpu[2], gpu[3],
+                                        gu_tiled=tiled)
+    torch.cuda.synchronize()
+    assert torch.equal(i0, i1) and torch.equal(w0, w1)
+    assert np.array_equal(_bits(y0), _bits(y1)), f"G={G} M={M}: tiled layer output differs"
+
+
+@pytest.mark.parametrize("M", [4, 64])
+def test_stage_gate_up_tiled(dev, layer, M):
+    """The stage API: gate_up on the tiled copy, then down and combine, equals
+    the untiled stages bit for bit."""
+    G, gpu, r, tiled = layer
+    x = synth.activations(M, H, seed=7500 + M).to(dev)
+    w, idx = _lib.router_topk(x, *r)
+    outs = []
+    for t in (None, tiled):
+        st = _lib.MoEStages(M, K_TOP, E, H, I, G, dev)
+        st.plan(x, idx)
+        st.gate_up(x, gpu[0], gpu[1], gu_tiled=t)
+        st.down(gpu[2], gpu[3])
+        outs.append(st.combine(idx, w).clone())
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(outs[0]), _bits(outs[1]))
+
+
+def test_layer_tiled_graph_replay(dev, layer):
+    """Captured in a HIP graph and replayed with eager work in between: every
+    replay equals the eager result."""
+    G, gpu, r, tiled = layer
+    M = 32
+    x = synth.activations(M, H, seed=7600).to(dev)
+    fwd = lambda xx: _lib.moe_layer_forward(xx, r[0], r[1], r[2], r[3], r[4], r[5], xx, gpu[0], gpu[1], gpu[2],
+                                            gpu[3], gu_tiled=tiled)
+    eager = fwd(x)[0].clone()
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        fwd(x)
+    torch.cuda.current_stream(dev).wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = fwd(x)[0]
+    x2 = synth.activations(M, H, seed=7601).to(dev)
+    for rep in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(_bits(out), _bits(eager)), f"replay {rep}"
+        fwd(x2)
+        torch.cuda.synchronize()
