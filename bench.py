@@ -96,8 +96,11 @@ class Layer:
         self.rw = (synth.zipf_router_weights(E, H, seed=seed, device=dev) if zipf
                    else synth.router_weights(E, H, seed=seed, device=dev))
         self.ew = synth.moe_weights(E, H, I, g, seed=seed + 1000, device=dev)
-        # the load-time tiled copy the decode gate_up streamer reads (group size 128)
+        # load-time tiled copies: the decode gate_up streamer's (group size 128;
+        # the decode layers) and the prefill GEMMs' (the Zipf prefill layers)
         self.gu_tiled = _lib.tile_gate_up(self.ew.gate_up_packed) if g == 128 and not zipf else None
+        self.gu_ptiled = _lib.tile_prefill(self.ew.gate_up_packed, "gate_up") if zipf else None
+        self.dn_ptiled = _lib.tile_prefill(self.ew.down_packed, "down") if zipf else None
 
     def route(self, x):
         rw = self.rw
@@ -109,7 +112,8 @@ class Layer:
         out, _, _ = _lib.moe_layer_forward(x, rw.scale, rw.scalar_root, rw.proj, rw.per_expert_scale,
                                            rw.eps, TOPK, x, ew.gate_up_packed, ew.gate_up_scale,
                                            ew.down_packed, ew.down_scale, group_size=self.g,
-                                           gu_tiled=self.gu_tiled)
+                                           gu_tiled=self.gu_tiled, gu_ptiled=self.gu_ptiled,
+                                           dn_ptiled=self.dn_ptiled)
         return out
 
 
@@ -229,7 +233,7 @@ def prefill(dev, steps, warmup, n_layers, g: int = G, stages: bool = True):
 
         def run():
             for ly, st in zip(layers, sts):
-                st.gate_up(x, ly.ew.gate_up_packed, ly.ew.gate_up_scale)
+                st.gate_up(x, ly.ew.gate_up_packed, ly.ew.gate_up_scale, gu_ptiled=ly.gu_ptiled)
 
         tg = time_graph(run, len(layers), steps, warmup)
         gflop = 2.0 * PREFILL_M * TOPK * H * 2 * I
@@ -264,7 +268,7 @@ def roofline_prefill(pre):
     st = pre["gate_up_stage"]
     return {
         "bound": "mfma",
-        "kernel": "k_prefill_x<gateup> (moe_gate_up stage)",
+        "kernel": "k_prefill_x<gateup> on the tiled weights (moe_gate_up_tiled stage)",
         "M": PREFILL_M,
         "achieved": round(st["tflops"], 2),
         "peak": PEAK_BF16_TFLOPS,

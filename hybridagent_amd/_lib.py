@@ -61,11 +61,14 @@ SIGNATURES = {
                                          _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "w4a16_tiled_gate_up_bytes": (_SZ, [_I64, _I64, _I64]),
     "w4a16_tile_gate_up": (ctypes.c_int, [_VP, _I64, _I64, _I64, _VP, _SZ, _VP]),
-    "moe_gate_up_tiled": (ctypes.c_int, [_VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ,
+    "w4a16_tiled_prefill_bytes": (_SZ, [ctypes.c_int, _I64, _I64, _I64]),
+    "w4a16_tile_prefill": (ctypes.c_int, [ctypes.c_int, _VP, _I64, _I64, _I64, _VP, _SZ, _VP]),
+    "moe_gate_up_tiled": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ,
                                          _VP]),
+    "moe_down_tiled": (ctypes.c_int, [_VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "moe_layer_forward_tiled": (ctypes.c_int, [_VP, _VP, _F32, _VP, _VP, _F32, _VP, _VP, _VP, _VP, _VP, _VP,
-                                               _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ,
-                                               _VP]),
+                                               _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP,
+                                               _SZ, _VP]),
 }
 
 _lib = None
@@ -391,15 +394,52 @@ def tile_gate_up(gu_packed: torch.Tensor) -> torch.Tensor | None:
     return tiled
 
 
+def tile_prefill(packed: torch.Tensor, which: str) -> torch.Tensor | None:
+    """The exact-form prefill GEMM's tiled copy of gate_up_packed [E, 2I, H/8]
+    (``which="gate_up"``) or down_packed [E, H, I/8] (``which="down"``): each item's
+    k stage one contiguous 8 KiB block (a load-time re-layout beside
+    quantization.py:325-430; the original stays as it is), or None where that
+    kernel does not serve the shape."""
+    dev = _require_gpu(packed)
+    packed = _i32(packed, f"{which}_packed")
+    E, n, k8 = packed.shape
+    if which == "gate_up":
+        w, H, I = 0, k8 * 8, n // 2
+    elif which == "down":
+        w, H, I = 1, n, k8 * 8
+    else:
+        raise ValueError("which must be 'gate_up' or 'down'")
+    lib = load()
+    nbytes = lib.w4a16_tiled_prefill_bytes(w, E, H, I)
+    if nbytes == 0:
+        return None
+    tiled = torch.empty(nbytes // 4, dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        _check(lib.w4a16_tile_prefill(w, _ptr(packed), E, H, I, _ptr(tiled), nbytes, _stream(dev)),
+               "w4a16_tile_prefill")
+    return tiled
+
+
+def _tiled_arg(t: torch.Tensor | None, name: str, nbytes: int, dev) -> torch.Tensor | None:
+    if t is None:
+        return None
+    t = _i32(t, name)
+    if t.device != dev or t.numel() * 4 < nbytes:
+        raise ValueError(f"{name} does not match the expert weights")
+    return t
+
+
 def moe_layer_forward(router_in: torch.Tensor, router_scale: torch.Tensor, scalar_root: float,
                       proj_w: torch.Tensor, per_expert_scale: torch.Tensor, eps: float, top_k: int,
                       hidden_states: torch.Tensor, gu_packed: torch.Tensor, gu_scale: torch.Tensor,
                       dn_packed: torch.Tensor, dn_scale: torch.Tensor, group_size: int | None = None,
-                      gu_tiled: torch.Tensor | None = None):
+                      gu_tiled: torch.Tensor | None = None, gu_ptiled: torch.Tensor | None = None,
+                      dn_ptiled: torch.Tensor | None = None):
     """Router (backends.py:111-117) on ``router_in`` + experts (quantization.py:88-129) on
     ``hidden_states`` in one call -> (out [T, H] bf16, top_k_weights fp32, top_k_index int64).
-    ``gu_tiled`` (from tile_gate_up) lets the decode gate_up streamer read contiguous tiles;
-    the output is bit-identical."""
+    ``gu_tiled`` (from tile_gate_up) and ``gu_ptiled`` / ``dn_ptiled`` (from tile_prefill) let
+    the decode gate_up streamer and the prefill GEMMs read contiguous tiles; the output is
+    bit-identical."""
     dev = _require_gpu(router_in, router_scale, proj_w, per_expert_scale, hidden_states, gu_packed,
                        gu_scale, dn_packed, dn_scale)
     H = hidden_states.shape[-1]
@@ -426,7 +466,7 @@ def moe_layer_forward(router_in: torch.Tensor, router_scale: torch.Tensor, scala
     lib = load()
     ws = _workspace(lib.moe_layer_workspace_bytes(max(M, 1), top_k, E, H, I), dev)
     with torch.cuda.device(dev):
-        if gu_tiled is None:
+        if gu_tiled is None and gu_ptiled is None and dn_ptiled is None:
             _check(lib.moe_layer_forward(_ptr(r2), _ptr(router_scale), float(scalar_root), _ptr(proj_w),
                                          _ptr(per_expert_scale), float(eps), _ptr(x), _ptr(gu_packed),
                                          _ptr(gu_scale), _ptr(dn_packed), _ptr(dn_scale), _ptr(out), _ptr(idx),
@@ -434,12 +474,14 @@ def moe_layer_forward(router_in: torch.Tensor, router_scale: torch.Tensor, scala
                                          0 if ws is None else ws.numel(), _stream(dev)),
                    "moe_layer_forward")
         else:
-            gu_tiled = _i32(gu_tiled, "gate_up tiled copy")
-            if gu_tiled.device != dev or gu_tiled.numel() * 4 < lib.w4a16_tiled_gate_up_bytes(E, H, I):
-                raise ValueError("gate_up tiled copy does not match the expert weights")
+            gu_tiled = _tiled_arg(gu_tiled, "gate_up tiled copy", lib.w4a16_tiled_gate_up_bytes(E, H, I), dev)
+            gu_ptiled = _tiled_arg(gu_ptiled, "gate_up prefill tiled copy",
+                                   lib.w4a16_tiled_prefill_bytes(0, E, H, I), dev)
+            dn_ptiled = _tiled_arg(dn_ptiled, "down prefill tiled copy", lib.w4a16_tiled_prefill_bytes(1, E, H, I), dev)
             _check(lib.moe_layer_forward_tiled(_ptr(r2), _ptr(router_scale), float(scalar_root), _ptr(proj_w),
                                                _ptr(per_expert_scale), float(eps), _ptr(x), _ptr(gu_packed),
-                                               _ptr(gu_tiled), _ptr(gu_scale), _ptr(dn_packed), _ptr(dn_scale),
+                                               _ptr(gu_tiled), _ptr(gu_ptiled), _ptr(gu_scale), _ptr(dn_packed),
+                                               _ptr(dn_ptiled), _ptr(dn_scale),
                                                _ptr(out), _ptr(idx), _ptr(w), M, top_k, E, H, I, G, _ptr(ws),
                                                0 if ws is None else ws.numel(), _stream(dev)),
                    "moe_layer_forward_tiled")
@@ -560,18 +602,22 @@ class MoEStages:
                                  self.ws.numel(), s), "moe_plan")
 
     def gate_up(self, hidden: torch.Tensor, gu_packed: torch.Tensor, gu_scale: torch.Tensor,
-                gu_tiled: torch.Tensor | None = None) -> None:
+                gu_tiled: torch.Tensor | None = None, gu_ptiled: torch.Tensor | None = None) -> None:
         s = _stream(self.device)
-        if gu_tiled is None:
+        if gu_tiled is None and gu_ptiled is None:
             _check(self.lib.moe_gate_up(_ptr(hidden), _ptr(gu_packed), _ptr(gu_scale), *self._dims(), self.G,
                                         _ptr(self.ws), self.ws.numel(), s), "moe_gate_up")
         else:
-            _check(self.lib.moe_gate_up_tiled(_ptr(hidden), _ptr(gu_packed), _ptr(gu_tiled), _ptr(gu_scale),
-                                              *self._dims(), self.G, _ptr(self.ws), self.ws.numel(), s),
-                   "moe_gate_up_tiled")
+            _check(self.lib.moe_gate_up_tiled(_ptr(hidden), _ptr(gu_packed), _ptr(gu_tiled), _ptr(gu_ptiled),
+                                              _ptr(gu_scale), *self._dims(), self.G, _ptr(self.ws),
+                                              self.ws.numel(), s), "moe_gate_up_tiled")
 
-    def down(self, dn_packed: torch.Tensor, dn_scale: torch.Tensor) -> None:
+    def down(self, dn_packed: torch.Tensor, dn_scale: torch.Tensor, dn_ptiled: torch.Tensor | None = None) -> None:
         s = _stream(self.device)
+        if dn_ptiled is not None:
+            _check(self.lib.moe_down_tiled(_ptr(dn_packed), _ptr(dn_ptiled), _ptr(dn_scale), *self._dims(), self.G,
+                                           _ptr(self.ws), self.ws.numel(), s), "moe_down_tiled")
+            return
         _check(self.lib.moe_down(_ptr(dn_packed), _ptr(dn_scale), *self._dims(), self.G, _ptr(self.ws),
                                  self.ws.numel(), s), "moe_down")
 

@@ -434,7 +434,7 @@ namespace {
 // gate_up on either weight layout: gu_tiled (the tiled copy, nullable) serves
 // the decode streamer where it applies, gu_packed everything else
 int gate_up_impl(const uint16_t* hidden, const int32_t* gu_packed, const uint16_t* gu_scale,
-                 const int32_t* gu_tiled, int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I,
+                 const int32_t* gu_tiled, const int32_t* gu_ptiled, int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I,
                  int64_t group_size, void* workspace, size_t workspace_bytes, void* stream) {
   MoeLayout L{};
   int st = moe_check(M, top_k, E, H, I, group_size, workspace, workspace_bytes, &L);
@@ -459,6 +459,10 @@ int gate_up_impl(const uint16_t* hidden, const int32_t* gu_packed, const uint16_
     p.rows_total = (int)(M * top_k);
     p.n_nt = (int)((I + 127) / 128);  // 128 intermediate columns per item
     p.queues = L.queues;
+    if (gu_ptiled != nullptr) {
+      if (!aligned16(gu_ptiled)) return W4A16_ERR_ALIGN;
+      p.wt = gu_ptiled;
+    }
     return launch_status(launch_prefill_x(kModeGateUp, p, max_mtiles(M, top_k, E, kPrefillXBM), s));
   }
   if (use_prefill(M, H, I)) {
@@ -514,20 +518,37 @@ extern "C" {
 int moe_gate_up(const uint16_t* hidden, const int32_t* gu_packed, const uint16_t* gu_scale,
                 int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t group_size,
                 void* workspace, size_t workspace_bytes, void* stream) {
-  return gate_up_impl(hidden, gu_packed, gu_scale, nullptr, M, top_k, E, H, I, group_size, workspace,
+  return gate_up_impl(hidden, gu_packed, gu_scale, nullptr, nullptr, M, top_k, E, H, I, group_size, workspace,
                       workspace_bytes, stream);
 }
 
 int moe_gate_up_tiled(const uint16_t* hidden, const int32_t* gu_packed, const int32_t* gu_tiled,
-                      const uint16_t* gu_scale, int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I,
-                      int64_t group_size, void* workspace, size_t workspace_bytes, void* stream) {
-  return gate_up_impl(hidden, gu_packed, gu_scale, gu_tiled, M, top_k, E, H, I, group_size, workspace,
+                      const int32_t* gu_ptiled, const uint16_t* gu_scale, int64_t M, int64_t top_k, int64_t E,
+                      int64_t H, int64_t I, int64_t group_size, void* workspace, size_t workspace_bytes,
+                      void* stream) {
+  return gate_up_impl(hidden, gu_packed, gu_scale, gu_tiled, gu_ptiled, M, top_k, E, H, I, group_size, workspace,
                       workspace_bytes, stream);
 }
 
 size_t w4a16_tiled_gate_up_bytes(int64_t E, int64_t H, int64_t I) {
   if (E <= 0 || E > kMaxExperts) return 0;
   return (size_t)E * tiled_gate_up_bytes_per_expert(H, I);
+}
+
+size_t w4a16_tiled_prefill_bytes(int which, int64_t E, int64_t H, int64_t I) {
+  if (E <= 0 || E > kMaxExperts || (which != 0 && which != 1)) return 0;
+  return (size_t)E * prefill_tiled_bytes_per_expert(which == 0 ? kModeGateUp : kModeDown, H, I);
+}
+
+int w4a16_tile_prefill(int which, const int32_t* packed, int64_t E, int64_t H, int64_t I, int32_t* tiled,
+                       size_t tiled_bytes, void* stream) {
+  const size_t need = w4a16_tiled_prefill_bytes(which, E, H, I);
+  if (need == 0) return W4A16_ERR_SHAPE;
+  if (!packed || !tiled) return W4A16_ERR_NULL;
+  if (!aligned16(packed) || !aligned16(tiled)) return W4A16_ERR_ALIGN;
+  if (tiled_bytes < need) return W4A16_ERR_WORKSPACE;
+  return launch_status(launch_tile_prefill(which == 0 ? kModeGateUp : kModeDown, packed, (int)E, (int)H, (int)I,
+                                           tiled, static_cast<hipStream_t>(stream)));
 }
 
 int w4a16_tile_gate_up(const int32_t* gu_packed, int64_t E, int64_t H, int64_t I, int32_t* tiled,
@@ -541,9 +562,9 @@ int w4a16_tile_gate_up(const int32_t* gu_packed, int64_t E, int64_t H, int64_t I
                                            static_cast<hipStream_t>(stream)));
 }
 
-int moe_down(const int32_t* dn_packed, const uint16_t* dn_scale, int64_t M, int64_t top_k,
-             int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
-             size_t workspace_bytes, void* stream) {
+static int down_impl(const int32_t* dn_packed, const int32_t* dn_ptiled, const uint16_t* dn_scale, int64_t M,
+                     int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
+                     size_t workspace_bytes, void* stream) {
   MoeLayout L{};
   int st = moe_check(M, top_k, E, H, I, group_size, workspace, workspace_bytes, &L);
   if (st != W4A16_OK || M == 0) return st;
@@ -565,6 +586,10 @@ int moe_down(const int32_t* dn_packed, const uint16_t* dn_scale, int64_t M, int6
     p.rows_total = (int)(M * top_k);
     p.n_nt = (int)((H + 255) / 256);  // 256 output columns per item
     p.queues = L.queues + kPrefillQueueInts / 2;
+    if (dn_ptiled != nullptr) {
+      if (!aligned16(dn_ptiled)) return W4A16_ERR_ALIGN;
+      p.wt = dn_ptiled;
+    }
     return launch_status(launch_prefill_x(kModeDown, p, max_mtiles(M, top_k, E, kPrefillXBM), s));
   }
   if (use_prefill(M, H, I)) {
@@ -601,6 +626,20 @@ int moe_down(const int32_t* dn_packed, const uint16_t* dn_scale, int64_t M, int6
   return launch_status(launch_decode(kModeDown, group_size % 128 == 0, a, max_slots, s));
 }
 
+int moe_down(const int32_t* dn_packed, const uint16_t* dn_scale, int64_t M, int64_t top_k,
+             int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
+             size_t workspace_bytes, void* stream) {
+  return down_impl(dn_packed, nullptr, dn_scale, M, top_k, E, H, I, group_size, workspace, workspace_bytes,
+                   stream);
+}
+
+int moe_down_tiled(const int32_t* dn_packed, const int32_t* dn_ptiled, const uint16_t* dn_scale, int64_t M,
+                   int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+  return down_impl(dn_packed, dn_ptiled, dn_scale, M, top_k, E, H, I, group_size, workspace, workspace_bytes,
+                   stream);
+}
+
 int moe_combine(const int64_t* topk_idx, const float* topk_w, uint16_t* out, int64_t M,
                 int64_t top_k, int64_t E, int64_t H, int64_t I, void* workspace,
                 size_t workspace_bytes, void* stream) {
@@ -630,10 +669,10 @@ constexpr int64_t kFuseDownCombineRows = 32;
 int down_and_combine(const int32_t* dn_packed, const uint16_t* dn_scale, const int64_t* topk_idx,
                      const float* topk_w, uint16_t* out, int64_t M, int64_t top_k, int64_t E,
                      int64_t H, int64_t I, int64_t group_size, void* workspace,
-                     size_t workspace_bytes, void* stream) {
+                     size_t workspace_bytes, void* stream, const int32_t* dn_ptiled = nullptr) {
   if (use_prefill(M, H, I) || M * top_k > kFuseDownCombineRows || !down_combine_supported(M, top_k, I)) {
-    int st = moe_down(dn_packed, dn_scale, M, top_k, E, H, I, group_size, workspace,
-                      workspace_bytes, stream);
+    int st = down_impl(dn_packed, dn_ptiled, dn_scale, M, top_k, E, H, I, group_size, workspace,
+                       workspace_bytes, stream);
     if (st == W4A16_OK)
       st = moe_combine(topk_idx, topk_w, out, M, top_k, E, H, I, workspace, workspace_bytes,
                        stream);
@@ -913,7 +952,8 @@ size_t moe_layer_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t H,
 static int layer_forward_impl(const uint16_t* router_in, const uint16_t* router_scale, float scalar_root,
                               const uint16_t* proj_w, const uint16_t* per_expert_scale, float eps,
                               const uint16_t* hidden, const int32_t* gu_packed, const int32_t* gu_tiled,
-                              const uint16_t* gu_scale, const int32_t* dn_packed, const uint16_t* dn_scale,
+                              const int32_t* gu_ptiled, const uint16_t* gu_scale, const int32_t* dn_packed,
+                              const int32_t* dn_ptiled, const uint16_t* dn_scale,
                               uint16_t* out, int64_t* topk_idx, float* topk_w, int64_t M, int64_t top_k,
                               int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
                               size_t workspace_bytes, void* stream) {
@@ -954,11 +994,11 @@ static int layer_forward_impl(const uint16_t* router_in, const uint16_t* router_
     st = moe_plan(hidden, topk_idx, M, top_k, E, H, I, group_size, workspace, moe_bytes, stream);
     if (st != W4A16_OK) return st;
   }
-  st = gate_up_impl(hidden, gu_packed, gu_scale, gu_tiled, M, top_k, E, H, I, group_size, workspace,
+  st = gate_up_impl(hidden, gu_packed, gu_scale, gu_tiled, gu_ptiled, M, top_k, E, H, I, group_size, workspace,
                     moe_bytes, stream);
   if (st == W4A16_OK)
     st = down_and_combine(dn_packed, dn_scale, topk_idx, topk_w, out, M, top_k, E, H, I,
-                          group_size, workspace, moe_bytes, stream);
+                          group_size, workspace, moe_bytes, stream, dn_ptiled);
   return st;
 }
 
@@ -970,19 +1010,22 @@ int moe_layer_forward(const uint16_t* router_in, const uint16_t* router_scale, f
                       int64_t H, int64_t I, int64_t group_size, void* workspace,
                       size_t workspace_bytes, void* stream) {
   return layer_forward_impl(router_in, router_scale, scalar_root, proj_w, per_expert_scale, eps, hidden,
-                            gu_packed, nullptr, gu_scale, dn_packed, dn_scale, out, topk_idx, topk_w, M,
+                            gu_packed, nullptr, nullptr, gu_scale, dn_packed, nullptr, dn_scale, out, topk_idx,
+                            topk_w, M,
                             top_k, E, H, I, group_size, workspace, workspace_bytes, stream);
 }
 
 int moe_layer_forward_tiled(const uint16_t* router_in, const uint16_t* router_scale, float scalar_root,
                             const uint16_t* proj_w, const uint16_t* per_expert_scale, float eps,
                             const uint16_t* hidden, const int32_t* gu_packed, const int32_t* gu_tiled,
-                            const uint16_t* gu_scale, const int32_t* dn_packed, const uint16_t* dn_scale,
+                            const int32_t* gu_ptiled, const uint16_t* gu_scale, const int32_t* dn_packed,
+                            const int32_t* dn_ptiled, const uint16_t* dn_scale,
                             uint16_t* out, int64_t* topk_idx, float* topk_w, int64_t M, int64_t top_k,
                             int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
                             size_t workspace_bytes, void* stream) {
   return layer_forward_impl(router_in, router_scale, scalar_root, proj_w, per_expert_scale, eps, hidden,
-                            gu_packed, gu_tiled, gu_scale, dn_packed, dn_scale, out, topk_idx, topk_w, M,
+                            gu_packed, gu_tiled, gu_ptiled, gu_scale, dn_packed, dn_ptiled, dn_scale, out,
+                            topk_idx, topk_w, M,
                             top_k, E, H, I, group_size, workspace, workspace_bytes, stream);
 }
 

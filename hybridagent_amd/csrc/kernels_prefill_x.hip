@@ -176,7 +176,7 @@ __device__ __forceinline__ PxItem px_item_info(const PrefillArgs& a, int x0, int
 struct PxLoads {
   __amdgpu_buffer_rsrc_t wsrc, ssrc;
   int avoff[kPxNA];
-  int bvoff, svoff;
+  int bvoff, bstride, svoff;
   int na, n;
 };
 
@@ -221,9 +221,20 @@ __device__ __forceinline__ PxLoads px_loads(const PrefillArgs& a, const PxItem& 
   // B words: instruction `wave` brings tile rows 32 wave .. + 31, lane l row
   // 32 wave + l / 2, bytes 16 (l % 2) of the stage's 32
   const int K2 = a.K >> 1;  // packed bytes per weight row
-  L.wsrc = make_rsrc(reinterpret_cast<const uint32_t*>(a.wp) + (int64_t)it.e * a.N * (a.K >> 3),
-                     (uint32_t)a.N * K2);
-  L.bvoff = px_weight_row<MODE>(a, it.nt, 32 * wave + (lane >> 1)) * K2 + 16 * (lane & 1);
+  if (a.wt != nullptr) {
+    // tiled copy: the item's stage kt is the 8 KiB block (nt, kt) of the
+    // expert, tile rows in order, so instruction `wave` reads one KiB
+    const int nkt = a.K / kPxKT;
+    const int64_t per_e = (int64_t)a.n_nt * nkt * 2048;  // int32 words
+    L.wsrc = make_rsrc(reinterpret_cast<const uint32_t*>(a.wt) + (int64_t)it.e * per_e, (uint32_t)(per_e * 4));
+    L.bvoff = it.nt * nkt * 8192 + wave * 1024 + 16 * lane;
+    L.bstride = 8192;
+  } else {
+    L.wsrc = make_rsrc(reinterpret_cast<const uint32_t*>(a.wp) + (int64_t)it.e * a.N * (a.K >> 3),
+                       (uint32_t)a.N * K2);
+    L.bvoff = px_weight_row<MODE>(a, it.nt, 32 * wave + (lane >> 1)) * K2 + 16 * (lane & 1);
+    L.bstride = kPxKT / 2;
+  }
   // scale chunks: waves 0..3 bring tile rows 64 wave + l, the aligned 16
   // bytes holding the stage's scale pair (the stage adds 2 x the pair's
   // group index, the lane rounds down to 16 bytes).  The descriptor starts
@@ -247,7 +258,7 @@ __device__ __forceinline__ void px_issue(const PrefillArgs& a, const PxLoads& L,
   if (part < L.na)
     px_dma16(make_rsrc(a.act, (uint32_t)a.act_bytes), L.avoff[part], kt * (kPxKT * 2),
              st + (wave + 8 * part) * 1024);
-  if (part == 0) px_dma16(L.wsrc, L.bvoff, kt * (kPxKT / 2), st + kPxBOff + wave * 1024);
+  if (part == 0) px_dma16(L.wsrc, L.bvoff, kt * L.bstride, st + kPxBOff + wave * 1024);
   if (part == 1 && wave < 4) {
     const int gpair = ((kt * kPxKT) >> a.gshift) & ~1;
     px_dma16(L.ssrc, (L.svoff + 2 * gpair) & ~15, 0, st + kPxSOff + 1024 * wave);
@@ -590,6 +601,55 @@ void k_prefill_x(PrefillArgs a) {
   // the loads issued past the last stage land before the workgroup leaves
   __builtin_amdgcn_s_waitcnt(px_vm_wait(0));
   leave();
+}
+
+// The tiled weight copy: piece (e, nt, kt, tr, h) = 16 bytes of weight row
+// px_weight_row(nt, tr) at byte 32 kt + 16 h, so stage kt of n-tile nt is
+// 8 KiB in the order the kernel's B loads fill LDS (tile row tr at 32 tr).
+template <int MODE>
+__global__ __launch_bounds__(256) void k_tile_prefill(const uint32_t* __restrict__ packed,
+                                                      uint32_t* __restrict__ tiled, PrefillArgs a,
+                                                      int64_t pieces) {
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (p >= pieces) return;
+  const int nkt = a.K / kPxKT;
+  const int h = (int)(p & 1);
+  const int tr = (int)((p >> 1) & 255);
+  int64_t q = p >> 9;
+  const int kt = (int)(q % nkt);
+  q /= nkt;
+  const int nt = (int)(q % a.n_nt);
+  const int64_t e = q / a.n_nt;
+  const int row = px_weight_row<MODE>(a, nt, tr);
+  const int64_t src = (e * a.N + row) * (int64_t)(a.K / 2) + 32 * kt + 16 * h;
+  *reinterpret_cast<u32x4_t*>(tiled + p * 4) = *reinterpret_cast<const u32x4_t*>(packed + src / 4);
+}
+
+size_t prefill_tiled_bytes_per_expert(int mode, int64_t H, int64_t I) {
+  if (H % kPxKT != 0 || I % kPxKT != 0 || H < 3 * kPxKT || I < 3 * kPxKT) return 0;
+  const int64_t K = mode == kModeGateUp ? H : I;
+  const int64_t n_nt = mode == kModeGateUp ? (I + 127) / 128 : (H + 255) / 256;
+  return (size_t)(n_nt * (K / kPxKT) * 8192);
+}
+
+hipError_t launch_tile_prefill(int mode, const int32_t* packed, int E, int H, int I, int32_t* tiled,
+                               hipStream_t s) {
+  if (prefill_tiled_bytes_per_expert(mode, H, I) == 0) return hipErrorInvalidValue;
+  PrefillArgs a{};
+  a.I = I;
+  a.N = mode == kModeGateUp ? 2 * I : H;
+  a.K = mode == kModeGateUp ? H : I;
+  a.n_nt = mode == kModeGateUp ? (I + 127) / 128 : (H + 255) / 256;
+  const int64_t pieces = (int64_t)E * a.n_nt * (a.K / kPxKT) * 512;
+  if (pieces == 0) return hipSuccess;
+  const dim3 grid((unsigned)((pieces + 255) / 256));
+  const uint32_t* src = reinterpret_cast<const uint32_t*>(packed);
+  uint32_t* dst = reinterpret_cast<uint32_t*>(tiled);
+  if (mode == kModeGateUp)
+    hipLaunchKernelGGL(k_tile_prefill<kModeGateUp>, grid, dim3(256), 0, s, src, dst, a, pieces);
+  else
+    hipLaunchKernelGGL(k_tile_prefill<kModeDown>, grid, dim3(256), 0, s, src, dst, a, pieces);
+  return hipGetLastError();
 }
 
 size_t prefill_x_lds_bytes() { return (size_t)kPxLds; }

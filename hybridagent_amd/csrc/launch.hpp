@@ -71,6 +71,9 @@ struct PrefillArgs {
   int64_t act_bytes;
   int gshift;
   int rows_total;
+  // exact-form kernel, nullable: the weights' tiled copy (k_tile_prefill):
+  // [E][n_nt][K/64][256 tile rows][32 B], each item's stage one 8 KiB block
+  const int32_t* wt;
 };
 
 enum DecodeMode { kModeDense = 0, kModeGateUp = 1, kModeDown = 2 };
@@ -209,6 +212,12 @@ bool prefill_bias_supported(int ng);
 // 64, G a power of two >= 32; items of up to kPrefillXBM rows
 bool prefill_x_supported(int64_t H, int64_t I, int64_t G);
 hipError_t launch_prefill_x(int mode, PrefillArgs a, int max_mtiles, hipStream_t s);
+// the exact-form prefill kernel's tiled weight copy: bytes per expert of
+// the gate_up (mode kModeGateUp, N = 2I, K = H) or down (N = H, K = I)
+// weights, 0 where the kernel does not serve (H, I); and the copy
+size_t prefill_tiled_bytes_per_expert(int mode, int64_t H, int64_t I);
+hipError_t launch_tile_prefill(int mode, const int32_t* packed, int E, int H, int I, int32_t* tiled,
+                               hipStream_t s);
 hipError_t launch_prefill_bias(int mode, PrefillArgs a, int max_mtiles, hipStream_t s);
 int prefill_grid_size(const void* kern, int threads, size_t lds, int max_items);
 

@@ -230,3 +230,19 @@ def test_tiled_gate_up_host_side(lib):
     assert lib.w4a16_tile_gate_up(NULL, 2, 2816, 704, fake, need, NULL) == 1
     assert lib.w4a16_tile_gate_up(fake, 2, 2816, 704, ctypes.c_void_p(4100), need, NULL) == 4
     assert lib.w4a16_tile_gate_up(fake, 2, 2816, 704, fake, need - 16, NULL) == 5
+
+
+def test_tiled_prefill_host_side(lib):
+    """Size of the prefill GEMMs' tiled copies and the validation that returns
+    before any launch."""
+    # gate_up: 6 n-tiles x 44 k stages x 8 KiB per expert; down: 11 x 11 x 8 KiB
+    assert lib.w4a16_tiled_prefill_bytes(0, 128, 2816, 704) == 128 * 6 * 44 * 8192
+    assert lib.w4a16_tiled_prefill_bytes(1, 128, 2816, 704) == 128 * 11 * 11 * 8192
+    assert lib.w4a16_tiled_prefill_bytes(2, 128, 2816, 704) == 0       # no such matrix
+    assert lib.w4a16_tiled_prefill_bytes(0, 128, 2816, 700) == 0       # I not a multiple of 64
+    fake = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    need = lib.w4a16_tiled_prefill_bytes(1, 2, 2816, 704)
+    assert lib.w4a16_tile_prefill(0, fake, 2, 2816, 700, fake, 1 << 30, NULL) == 2
+    assert lib.w4a16_tile_prefill(1, NULL, 2, 2816, 704, fake, need, NULL) == 1
+    assert lib.w4a16_tile_prefill(1, fake, 2, 2816, 704, ctypes.c_void_p(4100), need, NULL) == 4
+    assert lib.w4a16_tile_prefill(1, fake, 2, 2816, 704, fake, need - 16, NULL) == 5

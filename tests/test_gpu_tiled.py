@@ -1,8 +1,9 @@
-"""GPU: the tiled gate_up copy (w4a16_tile_gate_up) and the decode gate_up
-streamer reading it.  The copy is checked piece by piece against a numpy
+"""GPU: the tiled weight copies -- the decode gate_up streamer's
+(w4a16_tile_gate_up) and the prefill GEMMs' (w4a16_tile_prefill) -- and the
+kernels reading them.  Each copy is checked piece by piece against a numpy
 restatement of its documented layout; the layer and stage outputs on the
-tiled copy are compared bit for bit with the untiled path (same operands, same
-fold order), at decode sizes where it is used and at sizes where it is not."""
+tiled copies are compared bit for bit with the untiled path (same operands,
+same fold order), at sizes where each copy is used and where it is not."""
 import numpy as np
 import pytest
 import torch
@@ -57,6 +58,38 @@ def test_tile_layout(dev):
     assert np.array_equal(got, ref)
 
 
+def _prefill_rows(which: str, nt: int, tr: np.ndarray, I: int, N: int) -> np.ndarray:
+    """Weight row of tile row tr of n-tile nt (gate_up: 32-row groups of 16 gate
+    rows then their 16 up rows, 128 gate columns per n-tile; down: 256 rows per
+    n-tile; rows past the matrix repeat its last row)."""
+    if which == "gate_up":
+        g, cc = tr >> 5, tr & 31
+        col = np.minimum(128 * nt + 16 * g + (cc & 15), I - 1)
+        return np.where(cc < 16, col, I + col)
+    return np.minimum(256 * nt + tr, N - 1)
+
+
+@pytest.mark.parametrize("which", ["gate_up", "down"])
+def test_tile_prefill_layout(dev, which):
+    Ex = 2
+    wts = synth.moe_weights(Ex, H, I, 128, seed=7150)
+    packed = (wts.gate_up_packed if which == "gate_up" else wts.down_packed).numpy()
+    tiled = _lib.tile_prefill(torch.from_numpy(packed).to(dev), which)
+    assert tiled is not None
+    N, K = (2 * I, H) if which == "gate_up" else (H, I)
+    n_nt = (I + 127) // 128 if which == "gate_up" else (H + 255) // 256
+    nkt = K // 64
+    rows = packed.view(np.uint8).reshape(Ex, N, K // 2)
+    ref = np.empty((Ex, n_nt, nkt, 256, 32), np.uint8)
+    tr = np.arange(256)
+    for nt in range(n_nt):
+        r = _prefill_rows(which, nt, tr, I, N)
+        for kt in range(nkt):
+            ref[:, nt, kt] = rows[:, r, 32 * kt:32 * kt + 32]
+    got = tiled.cpu().numpy().view(np.uint8)
+    assert np.array_equal(got, ref.reshape(-1))
+
+
 def test_tile_unsupported_shape(dev):
     wts = synth.moe_weights(4, 256, 64, 128, seed=7101)
     assert _lib.tile_gate_up(wts.gate_up_packed.to(dev)) is None
@@ -69,7 +102,7 @@ def layer(request, dev):
     gpu = [getattr(w, k).to(dev) for k in ("gate_up_packed", "gate_up_scale", "down_packed", "down_scale")]
     rw = synth.router_weights(E, H, seed=7300)
     r = (rw.scale.to(dev), rw.scalar_root, rw.proj.to(dev), rw.per_expert_scale.to(dev), 1e-6, K_TOP)
-    return G, gpu, r, _lib.tile_gate_up(gpu[0])
+    return G, gpu, r, _lib.tile_gate_up(gpu[0]), _lib.tile_prefill(gpu[0], "gate_up"), _lib.tile_prefill(gpu[2], "down")
 
 
 def _bits(t):
@@ -77,46 +110,46 @@ def _bits(t):
 
 
 # decode sizes (the tiled streamer at G = 128; G = 32 keeps the packed path)
-# and a prefill size (packed path)
-@pytest.mark.parametrize("M", [1, 8, 32, 64, 300])
+# and prefill sizes (the prefill copies)
+@pytest.mark.parametrize("M", [1, 8, 32, 64, 300, 2048])
 def test_layer_tiled_equals_untiled(dev, layer, M):
-    G, gpu, r, tiled = layer
+    G, gpu, r, tiled, gpt, dpt = layer
     print(f"tiled layer G={G} M={M}", flush=True)
     x = synth.activations(M, H, seed=7400 + M).to(dev)
     y0, w0, i0 = _lib.moe_layer_forward(x, r[0], r[1], r[2], r[3], r[4], r[5], x, gpu[0], gpu[1], gpu[2], gpu[3])
     y1, w1, i1 = _lib.moe_layer_forward(x, r[0], r[1], r[2], r[3], r[4], r[5], x, gpu[0], gpu[1], gpu[2], gpu[3],
-                                        gu_tiled=tiled)
+                                        gu_tiled=tiled, gu_ptiled=gpt, dn_ptiled=dpt)
     torch.cuda.synchronize()
     assert torch.equal(i0, i1) and torch.equal(w0, w1)
     assert np.array_equal(_bits(y0), _bits(y1)), f"G={G} M={M}: tiled layer output differs"
 
 
-@pytest.mark.parametrize("M", [4, 64])
+@pytest.mark.parametrize("M", [4, 64, 512])
 def test_stage_gate_up_tiled(dev, layer, M):
     """The stage API: gate_up on the tiled copy, then down and combine, equals
     the untiled stages bit for bit."""
-    G, gpu, r, tiled = layer
+    G, gpu, r, tiled, gpt, dpt = layer
     x = synth.activations(M, H, seed=7500 + M).to(dev)
     w, idx = _lib.router_topk(x, *r)
     outs = []
     for t in (None, tiled):
         st = _lib.MoEStages(M, K_TOP, E, H, I, G, dev)
         st.plan(x, idx)
-        st.gate_up(x, gpu[0], gpu[1], gu_tiled=t)
-        st.down(gpu[2], gpu[3])
+        st.gate_up(x, gpu[0], gpu[1], gu_tiled=t, gu_ptiled=None if t is None else gpt)
+        st.down(gpu[2], gpu[3], dn_ptiled=None if t is None else dpt)
         outs.append(st.combine(idx, w).clone())
     torch.cuda.synchronize()
     assert np.array_equal(_bits(outs[0]), _bits(outs[1]))
 
 
-def test_layer_tiled_graph_replay(dev, layer):
+@pytest.mark.parametrize("M", [32, 300])
+def test_layer_tiled_graph_replay(dev, layer, M):
     """Captured in a HIP graph and replayed with eager work in between: every
-    replay equals the eager result."""
-    G, gpu, r, tiled = layer
-    M = 32
+    replay equals the eager result (decode and prefill sizes)."""
+    G, gpu, r, tiled, gpt, dpt = layer
     x = synth.activations(M, H, seed=7600).to(dev)
     fwd = lambda xx: _lib.moe_layer_forward(xx, r[0], r[1], r[2], r[3], r[4], r[5], xx, gpu[0], gpu[1], gpu[2],
-                                            gpu[3], gu_tiled=tiled)
+                                            gpu[3], gu_tiled=tiled, gu_ptiled=gpt, dn_ptiled=dpt)
     eager = fwd(x)[0].clone()
     s = torch.cuda.Stream(dev)
     s.wait_stream(torch.cuda.current_stream(dev))
