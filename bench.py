@@ -96,9 +96,10 @@ class Layer:
         self.rw = (synth.zipf_router_weights(E, H, seed=seed, device=dev) if zipf
                    else synth.router_weights(E, H, seed=seed, device=dev))
         self.ew = synth.moe_weights(E, H, I, g, seed=seed + 1000, device=dev)
-        # load-time tiled copies: the decode gate_up streamer's (group size 128;
-        # the decode layers) and the prefill GEMMs' (the Zipf prefill layers)
+        # load-time tiled copies: the decode streamers' (group size 128; the
+        # decode layers) and the prefill GEMMs' (the Zipf prefill layers)
         self.gu_tiled = _lib.tile_gate_up(self.ew.gate_up_packed) if g == 128 and not zipf else None
+        self.dn_tiled = _lib.tile_down(self.ew.down_packed) if g == 128 and not zipf else None
         self.gu_ptiled = _lib.tile_prefill(self.ew.gate_up_packed, "gate_up") if zipf else None
         self.dn_ptiled = _lib.tile_prefill(self.ew.down_packed, "down") if zipf else None
 
@@ -113,7 +114,7 @@ class Layer:
                                            rw.eps, TOPK, x, ew.gate_up_packed, ew.gate_up_scale,
                                            ew.down_packed, ew.down_scale, group_size=self.g,
                                            gu_tiled=self.gu_tiled, gu_ptiled=self.gu_ptiled,
-                                           dn_ptiled=self.dn_ptiled)
+                                           dn_tiled=self.dn_tiled, dn_ptiled=self.dn_ptiled)
         return out
 
 

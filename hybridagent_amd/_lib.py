@@ -61,14 +61,16 @@ SIGNATURES = {
                                          _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "w4a16_tiled_gate_up_bytes": (_SZ, [_I64, _I64, _I64]),
     "w4a16_tile_gate_up": (ctypes.c_int, [_VP, _I64, _I64, _I64, _VP, _SZ, _VP]),
+    "w4a16_tiled_down_bytes": (_SZ, [_I64, _I64, _I64]),
+    "w4a16_tile_down": (ctypes.c_int, [_VP, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "w4a16_tiled_prefill_bytes": (_SZ, [ctypes.c_int, _I64, _I64, _I64]),
     "w4a16_tile_prefill": (ctypes.c_int, [ctypes.c_int, _VP, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "moe_gate_up_tiled": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ,
                                          _VP]),
-    "moe_down_tiled": (ctypes.c_int, [_VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
+    "moe_down_tiled": (ctypes.c_int, [_VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "moe_layer_forward_tiled": (ctypes.c_int, [_VP, _VP, _F32, _VP, _VP, _F32, _VP, _VP, _VP, _VP, _VP, _VP,
-                                               _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP,
-                                               _SZ, _VP]),
+                                               _VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64,
+                                               _VP, _SZ, _VP]),
 }
 
 _lib = None
@@ -394,6 +396,24 @@ def tile_gate_up(gu_packed: torch.Tensor) -> torch.Tensor | None:
     return tiled
 
 
+def tile_down(dn_packed: torch.Tensor) -> torch.Tensor | None:
+    """The tiled copy of down_packed [E, H, I/8] that the decode down streamer reads
+    contiguously (a load-time re-layout beside quantization.py:325-430; the original
+    stays as it is), or None where the streamer has no tiled form."""
+    dev = _require_gpu(dn_packed)
+    dn_packed = _i32(dn_packed, "down_packed")
+    E, H, i8 = dn_packed.shape
+    lib = load()
+    nbytes = lib.w4a16_tiled_down_bytes(E, H, i8 * 8)
+    if nbytes == 0:
+        return None
+    tiled = torch.empty(nbytes // 4, dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        _check(lib.w4a16_tile_down(_ptr(dn_packed), E, H, i8 * 8, _ptr(tiled), nbytes, _stream(dev)),
+               "w4a16_tile_down")
+    return tiled
+
+
 def tile_prefill(packed: torch.Tensor, which: str) -> torch.Tensor | None:
     """The exact-form prefill GEMM's tiled copy of gate_up_packed [E, 2I, H/8]
     (``which="gate_up"``) or down_packed [E, H, I/8] (``which="down"``): each item's
@@ -434,12 +454,12 @@ def moe_layer_forward(router_in: torch.Tensor, router_scale: torch.Tensor, scala
                       hidden_states: torch.Tensor, gu_packed: torch.Tensor, gu_scale: torch.Tensor,
                       dn_packed: torch.Tensor, dn_scale: torch.Tensor, group_size: int | None = None,
                       gu_tiled: torch.Tensor | None = None, gu_ptiled: torch.Tensor | None = None,
-                      dn_ptiled: torch.Tensor | None = None):
+                      dn_tiled: torch.Tensor | None = None, dn_ptiled: torch.Tensor | None = None):
     """Router (backends.py:111-117) on ``router_in`` + experts (quantization.py:88-129) on
     ``hidden_states`` in one call -> (out [T, H] bf16, top_k_weights fp32, top_k_index int64).
-    ``gu_tiled`` (from tile_gate_up) and ``gu_ptiled`` / ``dn_ptiled`` (from tile_prefill) let
-    the decode gate_up streamer and the prefill GEMMs read contiguous tiles; the output is
-    bit-identical."""
+    ``gu_tiled`` / ``dn_tiled`` (from tile_gate_up / tile_down) and ``gu_ptiled`` /
+    ``dn_ptiled`` (from tile_prefill) let the decode streamers and the prefill GEMMs read
+    contiguous tiles; the output is bit-identical."""
     dev = _require_gpu(router_in, router_scale, proj_w, per_expert_scale, hidden_states, gu_packed,
                        gu_scale, dn_packed, dn_scale)
     H = hidden_states.shape[-1]
@@ -466,7 +486,7 @@ def moe_layer_forward(router_in: torch.Tensor, router_scale: torch.Tensor, scala
     lib = load()
     ws = _workspace(lib.moe_layer_workspace_bytes(max(M, 1), top_k, E, H, I), dev)
     with torch.cuda.device(dev):
-        if gu_tiled is None and gu_ptiled is None and dn_ptiled is None:
+        if gu_tiled is None and gu_ptiled is None and dn_tiled is None and dn_ptiled is None:
             _check(lib.moe_layer_forward(_ptr(r2), _ptr(router_scale), float(scalar_root), _ptr(proj_w),
                                          _ptr(per_expert_scale), float(eps), _ptr(x), _ptr(gu_packed),
                                          _ptr(gu_scale), _ptr(dn_packed), _ptr(dn_scale), _ptr(out), _ptr(idx),
@@ -477,11 +497,12 @@ def moe_layer_forward(router_in: torch.Tensor, router_scale: torch.Tensor, scala
             gu_tiled = _tiled_arg(gu_tiled, "gate_up tiled copy", lib.w4a16_tiled_gate_up_bytes(E, H, I), dev)
             gu_ptiled = _tiled_arg(gu_ptiled, "gate_up prefill tiled copy",
                                    lib.w4a16_tiled_prefill_bytes(0, E, H, I), dev)
+            dn_tiled = _tiled_arg(dn_tiled, "down tiled copy", lib.w4a16_tiled_down_bytes(E, H, I), dev)
             dn_ptiled = _tiled_arg(dn_ptiled, "down prefill tiled copy", lib.w4a16_tiled_prefill_bytes(1, E, H, I), dev)
             _check(lib.moe_layer_forward_tiled(_ptr(r2), _ptr(router_scale), float(scalar_root), _ptr(proj_w),
                                                _ptr(per_expert_scale), float(eps), _ptr(x), _ptr(gu_packed),
                                                _ptr(gu_tiled), _ptr(gu_ptiled), _ptr(gu_scale), _ptr(dn_packed),
-                                               _ptr(dn_ptiled), _ptr(dn_scale),
+                                               _ptr(dn_tiled), _ptr(dn_ptiled), _ptr(dn_scale),
                                                _ptr(out), _ptr(idx), _ptr(w), M, top_k, E, H, I, G, _ptr(ws),
                                                0 if ws is None else ws.numel(), _stream(dev)),
                    "moe_layer_forward_tiled")
@@ -612,11 +633,13 @@ class MoEStages:
                                               _ptr(gu_scale), *self._dims(), self.G, _ptr(self.ws),
                                               self.ws.numel(), s), "moe_gate_up_tiled")
 
-    def down(self, dn_packed: torch.Tensor, dn_scale: torch.Tensor, dn_ptiled: torch.Tensor | None = None) -> None:
+    def down(self, dn_packed: torch.Tensor, dn_scale: torch.Tensor, dn_ptiled: torch.Tensor | None = None,
+             dn_tiled: torch.Tensor | None = None) -> None:
         s = _stream(self.device)
-        if dn_ptiled is not None:
-            _check(self.lib.moe_down_tiled(_ptr(dn_packed), _ptr(dn_ptiled), _ptr(dn_scale), *self._dims(), self.G,
-                                           _ptr(self.ws), self.ws.numel(), s), "moe_down_tiled")
+        if dn_ptiled is not None or dn_tiled is not None:
+            _check(self.lib.moe_down_tiled(_ptr(dn_packed), _ptr(dn_tiled), _ptr(dn_ptiled), _ptr(dn_scale),
+                                           *self._dims(), self.G, _ptr(self.ws), self.ws.numel(), s),
+                   "moe_down_tiled")
             return
         _check(self.lib.moe_down(_ptr(dn_packed), _ptr(dn_scale), *self._dims(), self.G, _ptr(self.ws),
                                  self.ws.numel(), s), "moe_down")

@@ -504,10 +504,11 @@ int gate_up_impl(const uint16_t* hidden, const int32_t* gu_packed, const uint16_
   a.N = (int)(2 * I);
   a.K = (int)H;
   a.ng = (int)((H + group_size - 1) / group_size);
-  if (gu_tiled != nullptr && group_size == 128 && (a.ng % 2) == 0 && tiled_gate_up_bytes_per_expert(H, I) > 0) {
+  if (gu_tiled != nullptr && group_size == 128 && (a.ng % 2) == 0 &&
+      tiled_decode_bytes_per_expert(kModeGateUp, H, I) > 0) {
     if (!aligned16(gu_tiled)) return W4A16_ERR_ALIGN;
     a.wp = gu_tiled;
-    return launch_status(launch_decode_gate_up_tiled(a, max_slots, s));
+    return launch_status(launch_decode_tiled(kModeGateUp, a, max_slots, s));
   }
   return launch_status(launch_decode(kModeGateUp, group_size % 128 == 0, a, max_slots, s));
 }
@@ -532,7 +533,7 @@ int moe_gate_up_tiled(const uint16_t* hidden, const int32_t* gu_packed, const in
 
 size_t w4a16_tiled_gate_up_bytes(int64_t E, int64_t H, int64_t I) {
   if (E <= 0 || E > kMaxExperts) return 0;
-  return (size_t)E * tiled_gate_up_bytes_per_expert(H, I);
+  return (size_t)E * tiled_decode_bytes_per_expert(kModeGateUp, H, I);
 }
 
 size_t w4a16_tiled_prefill_bytes(int which, int64_t E, int64_t H, int64_t I) {
@@ -558,11 +559,28 @@ int w4a16_tile_gate_up(const int32_t* gu_packed, int64_t E, int64_t H, int64_t I
   if (!gu_packed || !tiled) return W4A16_ERR_NULL;
   if (!aligned16(gu_packed) || !aligned16(tiled)) return W4A16_ERR_ALIGN;
   if (tiled_bytes < need) return W4A16_ERR_WORKSPACE;
-  return launch_status(launch_tile_gate_up(gu_packed, (int)E, (int)H, (int)I, tiled,
-                                           static_cast<hipStream_t>(stream)));
+  return launch_status(launch_tile_decode(kModeGateUp, gu_packed, (int)E, (int)H, (int)I, tiled,
+                                          static_cast<hipStream_t>(stream)));
 }
 
-static int down_impl(const int32_t* dn_packed, const int32_t* dn_ptiled, const uint16_t* dn_scale, int64_t M,
+size_t w4a16_tiled_down_bytes(int64_t E, int64_t H, int64_t I) {
+  if (E <= 0 || E > kMaxExperts) return 0;
+  return (size_t)E * tiled_decode_bytes_per_expert(kModeDown, H, I);
+}
+
+int w4a16_tile_down(const int32_t* dn_packed, int64_t E, int64_t H, int64_t I, int32_t* tiled, size_t tiled_bytes,
+                    void* stream) {
+  const size_t need = w4a16_tiled_down_bytes(E, H, I);
+  if (need == 0) return W4A16_ERR_SHAPE;
+  if (!dn_packed || !tiled) return W4A16_ERR_NULL;
+  if (!aligned16(dn_packed) || !aligned16(tiled)) return W4A16_ERR_ALIGN;
+  if (tiled_bytes < need) return W4A16_ERR_WORKSPACE;
+  return launch_status(launch_tile_decode(kModeDown, dn_packed, (int)E, (int)H, (int)I, tiled,
+                                          static_cast<hipStream_t>(stream)));
+}
+
+static int down_impl(const int32_t* dn_packed, const int32_t* dn_tiled, const int32_t* dn_ptiled,
+                     const uint16_t* dn_scale, int64_t M,
                      int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
                      size_t workspace_bytes, void* stream) {
   MoeLayout L{};
@@ -623,21 +641,27 @@ static int down_impl(const int32_t* dn_packed, const int32_t* dn_ptiled, const u
   a.N = (int)H;
   a.K = (int)I;
   a.ng = (int)((I + group_size - 1) / group_size);
+  if (dn_tiled != nullptr && group_size == 128 && (a.ng % 2) == 0 &&
+      tiled_decode_bytes_per_expert(kModeDown, H, I) > 0) {
+    if (!aligned16(dn_tiled)) return W4A16_ERR_ALIGN;
+    a.wp = dn_tiled;
+    return launch_status(launch_decode_tiled(kModeDown, a, max_slots, s));
+  }
   return launch_status(launch_decode(kModeDown, group_size % 128 == 0, a, max_slots, s));
 }
 
 int moe_down(const int32_t* dn_packed, const uint16_t* dn_scale, int64_t M, int64_t top_k,
              int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
              size_t workspace_bytes, void* stream) {
-  return down_impl(dn_packed, nullptr, dn_scale, M, top_k, E, H, I, group_size, workspace, workspace_bytes,
-                   stream);
+  return down_impl(dn_packed, nullptr, nullptr, dn_scale, M, top_k, E, H, I, group_size, workspace,
+                   workspace_bytes, stream);
 }
 
-int moe_down_tiled(const int32_t* dn_packed, const int32_t* dn_ptiled, const uint16_t* dn_scale, int64_t M,
-                   int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
-                   size_t workspace_bytes, void* stream) {
-  return down_impl(dn_packed, dn_ptiled, dn_scale, M, top_k, E, H, I, group_size, workspace, workspace_bytes,
-                   stream);
+int moe_down_tiled(const int32_t* dn_packed, const int32_t* dn_tiled, const int32_t* dn_ptiled,
+                   const uint16_t* dn_scale, int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I,
+                   int64_t group_size, void* workspace, size_t workspace_bytes, void* stream) {
+  return down_impl(dn_packed, dn_tiled, dn_ptiled, dn_scale, M, top_k, E, H, I, group_size, workspace,
+                   workspace_bytes, stream);
 }
 
 int moe_combine(const int64_t* topk_idx, const float* topk_w, uint16_t* out, int64_t M,
@@ -669,9 +693,10 @@ constexpr int64_t kFuseDownCombineRows = 32;
 int down_and_combine(const int32_t* dn_packed, const uint16_t* dn_scale, const int64_t* topk_idx,
                      const float* topk_w, uint16_t* out, int64_t M, int64_t top_k, int64_t E,
                      int64_t H, int64_t I, int64_t group_size, void* workspace,
-                     size_t workspace_bytes, void* stream, const int32_t* dn_ptiled = nullptr) {
+                     size_t workspace_bytes, void* stream, const int32_t* dn_tiled = nullptr,
+                     const int32_t* dn_ptiled = nullptr) {
   if (use_prefill(M, H, I) || M * top_k > kFuseDownCombineRows || !down_combine_supported(M, top_k, I)) {
-    int st = down_impl(dn_packed, dn_ptiled, dn_scale, M, top_k, E, H, I, group_size, workspace,
+    int st = down_impl(dn_packed, dn_tiled, dn_ptiled, dn_scale, M, top_k, E, H, I, group_size, workspace,
                        workspace_bytes, stream);
     if (st == W4A16_OK)
       st = moe_combine(topk_idx, topk_w, out, M, top_k, E, H, I, workspace, workspace_bytes,
@@ -953,7 +978,7 @@ static int layer_forward_impl(const uint16_t* router_in, const uint16_t* router_
                               const uint16_t* proj_w, const uint16_t* per_expert_scale, float eps,
                               const uint16_t* hidden, const int32_t* gu_packed, const int32_t* gu_tiled,
                               const int32_t* gu_ptiled, const uint16_t* gu_scale, const int32_t* dn_packed,
-                              const int32_t* dn_ptiled, const uint16_t* dn_scale,
+                              const int32_t* dn_tiled, const int32_t* dn_ptiled, const uint16_t* dn_scale,
                               uint16_t* out, int64_t* topk_idx, float* topk_w, int64_t M, int64_t top_k,
                               int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
                               size_t workspace_bytes, void* stream) {
@@ -998,7 +1023,7 @@ static int layer_forward_impl(const uint16_t* router_in, const uint16_t* router_
                     moe_bytes, stream);
   if (st == W4A16_OK)
     st = down_and_combine(dn_packed, dn_scale, topk_idx, topk_w, out, M, top_k, E, H, I,
-                          group_size, workspace, moe_bytes, stream, dn_ptiled);
+                          group_size, workspace, moe_bytes, stream, dn_tiled, dn_ptiled);
   return st;
 }
 
@@ -1010,7 +1035,7 @@ int moe_layer_forward(const uint16_t* router_in, const uint16_t* router_scale, f
                       int64_t H, int64_t I, int64_t group_size, void* workspace,
                       size_t workspace_bytes, void* stream) {
   return layer_forward_impl(router_in, router_scale, scalar_root, proj_w, per_expert_scale, eps, hidden,
-                            gu_packed, nullptr, nullptr, gu_scale, dn_packed, nullptr, dn_scale, out, topk_idx,
+                            gu_packed, nullptr, nullptr, gu_scale, dn_packed, nullptr, nullptr, dn_scale, out, topk_idx,
                             topk_w, M,
                             top_k, E, H, I, group_size, workspace, workspace_bytes, stream);
 }
@@ -1019,12 +1044,12 @@ int moe_layer_forward_tiled(const uint16_t* router_in, const uint16_t* router_sc
                             const uint16_t* proj_w, const uint16_t* per_expert_scale, float eps,
                             const uint16_t* hidden, const int32_t* gu_packed, const int32_t* gu_tiled,
                             const int32_t* gu_ptiled, const uint16_t* gu_scale, const int32_t* dn_packed,
-                            const int32_t* dn_ptiled, const uint16_t* dn_scale,
+                            const int32_t* dn_tiled, const int32_t* dn_ptiled, const uint16_t* dn_scale,
                             uint16_t* out, int64_t* topk_idx, float* topk_w, int64_t M, int64_t top_k,
                             int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
                             size_t workspace_bytes, void* stream) {
   return layer_forward_impl(router_in, router_scale, scalar_root, proj_w, per_expert_scale, eps, hidden,
-                            gu_packed, gu_tiled, gu_ptiled, gu_scale, dn_packed, dn_ptiled, dn_scale, out,
+                            gu_packed, gu_tiled, gu_ptiled, gu_scale, dn_packed, dn_tiled, dn_ptiled, dn_scale, out,
                             topk_idx, topk_w, M,
                             top_k, E, H, I, group_size, workspace, workspace_bytes, stream);
 }

@@ -125,9 +125,9 @@ __device__ __forceinline__ int frag_slot(int b, int rb, int j) {
 
 // WIDE (group size 128, an even number of groups per row): the scales of one
 // item's TPW tiles are consecutive bf16 values, fetched with one load.
-// TILED (gate_up, bias form, K split): the weights come in the tiled layout
-// written by k_tile_gate_up, where each wavefront's tile of an item is one
-// contiguous KiB (lane l's 16 bytes at 16 l) instead of 16 rows x 64 bytes.
+// TILED (MoE, bias form): the weights come in the tiled layout written by
+// k_tile_decode, where each wavefront's tile of an item is one contiguous
+// KiB (lane l's 16 bytes at 16 l) instead of 16 rows x 64 bytes.
 template <int MODE, bool BIAS, int TPW, int KSPLIT, bool LONGK, bool WIDE, bool TILED = false>
 __global__ __launch_bounds__(stream_threads(KSPLIT)) __attribute__((amdgpu_waves_per_eu(TPW >= 4 ? 2 : 4, 8)))
 void k_decode(DecodeArgs a) {
@@ -141,7 +141,7 @@ void k_decode(DecodeArgs a) {
   float* __restrict__ csum = reinterpret_cast<float*>(smem_raw + (size_t)ntiles * 16 * a.rb * 16);
   static_assert(KSPLIT == 1 || KSPLIT == 4, "the split-K epilogue gives wavefront ks output row ks");
   static_assert(!WIDE || (BIAS && !LONGK), "wide scale loads serve the bias form");
-  static_assert(!TILED || (MODE == kModeGateUp && BIAS && KSPLIT == 4 && !LONGK), "tiled gate_up layout");
+  static_assert(!TILED || (BIAS && !LONGK && MODE != kModeDense), "tiled expert layout");
   // split-K partials, double-buffered so one barrier per item suffices
   __shared__ f32x4_t red[2][KSPLIT > 1 ? NWAVES : 1][64];
   __shared__ int tok[16];
@@ -704,90 +704,131 @@ hipError_t launch_decode(int mode, bool bias_form, DecodeArgs a, int max_slots, 
 }
 
 // ---------------------------------------------------------------------------
-// Tiled gate_up weights (a load-time copy for the decode streamer).  The
-// streamer's K-split shape (TPW k tiles per wavefront, 4 wavefronts per K
-// range, 4 column groups of 8 intermediate columns) reads, per item and
-// wavefront, TPW tiles of 16 weight rows x 64 bytes.  The tiled copy puts
-// each such tile in one contiguous KiB, in the order the streamer reads
-// them:
-//   byte ((((e * n_ct + ct) * 16 + w) * TPW + i) * 64 + l) * 16 .. + 15
+// Tiled expert weights (a load-time copy for the decode streamer).  The
+// streamer reads, per item and wavefront, TPW tiles of 16 weight rows x 64
+// bytes.  The tiled copy puts each such tile in one contiguous KiB, in the
+// order the streamer reads them:
+//   byte ((((e * n_ct + ct) * NW + w) * TPW + i) * 64 + l) * 16 .. + 15
 //     = packed row r of expert e, bytes 64 (ks TPW + i) + 16 (l / 16) .. + 15
-//   with w = 4 cg + ks, j = l % 16, colblk = 4 ct + cg,
-//   r = 8 colblk + j % 8 (+ I for j >= 8: the matching up row);
-// pieces past the row's K / 2 bytes or of column blocks past I are zero.
-// Supported where the streamer takes that shape: gate_up with K = H whose
-// decode shape is the K split without the long-K loop, I a multiple of 8.
+//   with NW wavefronts per workgroup, w = KS cg + ks (KS wavefronts per K
+//   range), j = l % 16, colblk = 4 ct + cg and
+//     gate_up: r = 8 colblk + j % 8 (+ I for j >= 8: the matching up row),
+//     down:    r = 16 colblk + j;
+// pieces past the row's K / 2 bytes or of rows past the matrix are zero.
+// Supported where the streamer's shape for that K has no long-K loop (and,
+// for gate_up, I is a multiple of 8).
 // ---------------------------------------------------------------------------
-bool tiled_gate_up_shape(int64_t H, int64_t I, int* tpw, int* n_ct) {
-  if (H <= 0 || I <= 0 || H % 32 != 0 || I % 8 != 0) return false;
-  const DecodeShape sh = decode_shape((int)H);
-  const int ntiles = (int)(((H >> 5) + 3) >> 2);
-  if (sh.ksplit != 4 || ntiles > 24) return false;
-  *tpw = sh.tpw;
-  *n_ct = (int)((I / 8 + 3) / 4);
+struct TiledShape {
+  int tpw, ksplit, nwaves, n_ct;
+};
+
+static bool tiled_shape(int mode, int64_t H, int64_t I, TiledShape* t) {
+  if (H <= 0 || I <= 0 || H % 32 != 0 || I % 32 != 0) return false;
+  const int64_t K = mode == kModeGateUp ? H : I;
+  const DecodeShape sh = decode_shape((int)K);
+  const int ntiles = (int)(((K >> 5) + 3) >> 2);
+  if (ntiles > 24) return false;
+  t->tpw = sh.tpw;
+  t->ksplit = sh.ksplit;
+  t->nwaves = stream_threads(sh.ksplit) / 64;
+  const int cg = t->nwaves / sh.ksplit;
+  const int64_t ncolblk = mode == kModeGateUp ? I / 8 : (H + 15) / 16;
+  t->n_ct = (int)((ncolblk + cg - 1) / cg);
   return true;
 }
 
-size_t tiled_gate_up_bytes_per_expert(int64_t H, int64_t I) {
-  int tpw = 0, n_ct = 0;
-  if (!tiled_gate_up_shape(H, I, &tpw, &n_ct)) return 0;
-  return (size_t)n_ct * 16 * tpw * 1024;
+size_t tiled_decode_bytes_per_expert(int mode, int64_t H, int64_t I) {
+  TiledShape t;
+  if (!tiled_shape(mode, H, I, &t)) return 0;
+  return (size_t)t.n_ct * t.nwaves * t.tpw * 1024;
 }
 
 // one thread per 16-byte piece of the tiled copy
-__global__ __launch_bounds__(256) void k_tile_gate_up(const uint32_t* __restrict__ packed,
-                                                      uint32_t* __restrict__ tiled, int I, int K,
-                                                      int tpw, int n_ct, int64_t pieces) {
+template <int MODE>
+__global__ __launch_bounds__(256) void k_tile_decode(const uint32_t* __restrict__ packed,
+                                                     uint32_t* __restrict__ tiled, int N, int K, int I,
+                                                     TiledShape t, int64_t pieces) {
   const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (p >= pieces) return;
   const int l = (int)(p & 63);
   int64_t q = p >> 6;
-  const int i = (int)(q % tpw);
-  q /= tpw;
-  const int w = (int)(q & 15);
-  q >>= 4;
-  const int ct = (int)(q % n_ct);
-  const int64_t e = q / n_ct;
-  const int cg = w >> 2, ks = w & 3;
+  const int i = (int)(q % t.tpw);
+  q /= t.tpw;
+  const int w = (int)(q % t.nwaves);
+  q /= t.nwaves;
+  const int ct = (int)(q % t.n_ct);
+  const int64_t e = q / t.n_ct;
+  const int cg = w / t.ksplit, ks = w - cg * t.ksplit;
   const int j = l & 15, kb = l >> 4;
-  const int colblk = 4 * ct + cg;
-  const int row = 8 * colblk + (j & 7) + (j >= 8 ? I : 0);
+  const int colblk = (t.nwaves / t.ksplit) * ct + cg;
+  int row;
+  bool ok;
+  if (MODE == kModeGateUp) {
+    row = 8 * colblk + (j & 7) + (j >= 8 ? I : 0);
+    ok = 8 * colblk + 8 <= I;
+  } else {
+    row = 16 * colblk + j;
+    ok = row < N;
+  }
   const int rowbytes = K / 2;
-  const int byte = 64 * (ks * tpw + i) + 16 * kb;
+  const int byte = 64 * (ks * t.tpw + i) + 16 * kb;
   u32x4_t v = {0u, 0u, 0u, 0u};
-  if (8 * colblk + 8 <= I && byte + 16 <= rowbytes)
-    v = *reinterpret_cast<const u32x4_t*>(packed + ((e * 2 * I + row) * (int64_t)rowbytes + byte) / 4);
+  if (ok && byte + 16 <= rowbytes)
+    v = *reinterpret_cast<const u32x4_t*>(packed + ((e * N + row) * (int64_t)rowbytes + byte) / 4);
   *reinterpret_cast<u32x4_t*>(tiled + p * 4) = v;
 }
 
-hipError_t launch_tile_gate_up(const int32_t* packed, int E, int H, int I, int32_t* tiled, hipStream_t s) {
-  int tpw = 0, n_ct = 0;
-  if (!tiled_gate_up_shape(H, I, &tpw, &n_ct)) return hipErrorInvalidValue;
-  const int64_t pieces = (int64_t)E * n_ct * 16 * tpw * 64;
+hipError_t launch_tile_decode(int mode, const int32_t* packed, int E, int H, int I, int32_t* tiled,
+                              hipStream_t s) {
+  TiledShape t;
+  if (!tiled_shape(mode, H, I, &t)) return hipErrorInvalidValue;
+  const int64_t pieces = (int64_t)E * t.n_ct * t.nwaves * t.tpw * 64;
   if (pieces == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_tile_gate_up, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, s,
-                     reinterpret_cast<const uint32_t*>(packed), reinterpret_cast<uint32_t*>(tiled), I, H,
-                     tpw, n_ct, pieces);
+  const dim3 grid((unsigned)((pieces + 255) / 256));
+  const uint32_t* src = reinterpret_cast<const uint32_t*>(packed);
+  uint32_t* dst = reinterpret_cast<uint32_t*>(tiled);
+  if (mode == kModeGateUp)
+    hipLaunchKernelGGL(k_tile_decode<kModeGateUp>, grid, dim3(256), 0, s, src, dst, 2 * I, H, I, t, pieces);
+  else
+    hipLaunchKernelGGL(k_tile_decode<kModeDown>, grid, dim3(256), 0, s, src, dst, H, I, I, t, pieces);
   return hipGetLastError();
 }
 
-// The gate_up streamer on tiled weights (a.wp = the tiled copy): bias form
+// The MoE streamers on tiled weights (a.wp = the tiled copy): bias form
 // with one scale load per item (group size 128, an even group count).
-hipError_t launch_decode_gate_up_tiled(DecodeArgs a, int max_slots, hipStream_t s) {
+hipError_t launch_decode_tiled(int mode, DecodeArgs a, int max_slots, hipStream_t s) {
   if (max_slots <= 0) return hipSuccess;
-  if ((int64_t)a.M * a.topk * a.I * 2 >= (int64_t)0x7FFFFFF0) return hipErrorInvalidValue;
-  int tpw = 0, n_ct = 0;
-  if (!tiled_gate_up_shape(a.K, a.I, &tpw, &n_ct) || a.G != 128 || (a.ng % 2) != 0)
+  if (mode != kModeGateUp && mode != kModeDown) return hipErrorInvalidValue;
+  if ((int64_t)a.M * a.topk * (mode == kModeGateUp ? a.I : a.N) * 2 >= (int64_t)0x7FFFFFF0)
     return hipErrorInvalidValue;
-  const int cg = stream_threads(4) / 64 / 4;
-  a.n_ct = (a.I / 8 + cg - 1) / cg;
-  a.rb = stage_rows(a.K, 4);
+  TiledShape t;
+  const int64_t H = mode == kModeGateUp ? a.K : a.N;
+  if (!tiled_shape(mode, H, a.I, &t) || a.G != 128 || (a.ng % 2) != 0) return hipErrorInvalidValue;
+  a.n_ct = t.n_ct;
+  a.rb = stage_rows(a.K, t.ksplit);
   int rows_cap = 1;
   while (rows_cap < a.rows_hint && rows_cap < 16) rows_cap <<= 1;
   if (a.rb > rows_cap) a.rb = rows_cap;
-  if (tpw == 2) return launch_stream<kModeGateUp, true, 2, 4, false, true, true>(a, max_slots, s);
-  if (tpw == 4) return launch_stream<kModeGateUp, true, 4, 4, false, true, true>(a, max_slots, s);
-  return launch_stream<kModeGateUp, true, 6, 4, false, true, true>(a, max_slots, s);
+#define W4A16_DEC_T(M_, T_, K_) return launch_stream<M_, true, T_, K_, false, true, true>(a, max_slots, s)
+  if (mode == kModeGateUp) {
+    if (t.ksplit == 4) {
+      if (t.tpw == 2) W4A16_DEC_T(kModeGateUp, 2, 4);
+      if (t.tpw == 4) W4A16_DEC_T(kModeGateUp, 4, 4);
+      W4A16_DEC_T(kModeGateUp, 6, 4);
+    }
+    if (t.tpw == 2) W4A16_DEC_T(kModeGateUp, 2, 1);
+    if (t.tpw == 4) W4A16_DEC_T(kModeGateUp, 4, 1);
+    W4A16_DEC_T(kModeGateUp, 6, 1);
+  }
+  if (t.ksplit == 4) {
+    if (t.tpw == 2) W4A16_DEC_T(kModeDown, 2, 4);
+    if (t.tpw == 4) W4A16_DEC_T(kModeDown, 4, 4);
+    W4A16_DEC_T(kModeDown, 6, 4);
+  }
+  if (t.tpw == 2) W4A16_DEC_T(kModeDown, 2, 1);
+  if (t.tpw == 4) W4A16_DEC_T(kModeDown, 4, 1);
+  W4A16_DEC_T(kModeDown, 6, 1);
+#undef W4A16_DEC_T
 }
 
 // ---------------------------------------------------------------------------

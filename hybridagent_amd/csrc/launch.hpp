@@ -111,14 +111,13 @@ hipError_t launch_dequant(const int32_t* packed, const uint16_t* scale, uint16_t
 hipError_t launch_bias_order(const uint16_t* x, uint16_t* xp, int64_t rows, int K, hipStream_t s);
 // max_slots: upper bound of active experts (1 for dense)
 hipError_t launch_decode(int mode, bool bias_form, DecodeArgs a, int max_slots, hipStream_t s);
-// Tiled gate_up weights for the decode streamer (kernels_decode.hip): the
-// streamer shape that reads them (false: not supported for H, I), bytes per
-// expert of the tiled copy (0: not supported), the copy, and the gate_up
-// streamer reading it (group size 128).
-bool tiled_gate_up_shape(int64_t H, int64_t I, int* tpw, int* n_ct);
-size_t tiled_gate_up_bytes_per_expert(int64_t H, int64_t I);
-hipError_t launch_tile_gate_up(const int32_t* packed, int E, int H, int I, int32_t* tiled, hipStream_t s);
-hipError_t launch_decode_gate_up_tiled(DecodeArgs a, int max_slots, hipStream_t s);
+// Tiled expert weights for the decode streamers (kernels_decode.hip): bytes
+// per expert of the tiled copy of the gate_up (mode kModeGateUp) or down
+// weights (0: no tiled form for H, I), the copy, and the streamer reading it
+// (group size 128).
+size_t tiled_decode_bytes_per_expert(int mode, int64_t H, int64_t I);
+hipError_t launch_tile_decode(int mode, const int32_t* packed, int E, int H, int I, int32_t* tiled, hipStream_t s);
+hipError_t launch_decode_tiled(int mode, DecodeArgs a, int max_slots, hipStream_t s);
 // x = bf16(h + delta) -> h_out (delta may be null), y = bf16(rms_norm(x) * w)
 hipError_t launch_add_rms_norm(const uint16_t* h, const uint16_t* delta, const uint16_t* w,
                                uint16_t* h_out, uint16_t* y, int64_t M, int H, float eps,

@@ -218,8 +218,10 @@ W4A16_API int moe_layer_forward(const uint16_t* router_in, const uint16_t* route
  * are left as they are and still serve every path).
  *   w4a16_tiled_gate_up_bytes  bytes of the decode gate_up streamer's copy
  *                              of gate_up_packed, 0 where the streamer has
- *                              no tiled form for (H, I);
+ *                              no tiled form for (H, I) (its long-K loop);
  *   w4a16_tile_gate_up         writes it;
+ *   w4a16_tiled_down_bytes,    the same for the decode down streamer and
+ *   w4a16_tile_down            down_packed;
  *   w4a16_tiled_prefill_bytes  bytes of the prefill GEMM's copy of
  *                              gate_up_packed (which = 0) or down_packed
  *                              (which = 1), 0 where that kernel does not
@@ -229,7 +231,8 @@ W4A16_API int moe_layer_forward(const uint16_t* router_in, const uint16_t* route
  *                              group size 128) and gu_ptiled (the exact-form
  *                              prefill GEMM) where they apply and are not
  *                              NULL, gu_packed elsewhere;
- *   moe_down_tiled             moe_down reading dn_ptiled likewise;
+ *   moe_down_tiled             moe_down reading dn_tiled (decode sizes,
+ *                              group size 128) and dn_ptiled likewise;
  *   moe_layer_forward_tiled    moe_layer_forward (backends.py:111-122)
  *                              through the two above.
  * The copy functions return W4A16_ERR_SHAPE when the bytes are 0 and
@@ -238,6 +241,9 @@ W4A16_API int moe_layer_forward(const uint16_t* router_in, const uint16_t* route
 W4A16_API size_t w4a16_tiled_gate_up_bytes(int64_t E, int64_t H, int64_t I);
 W4A16_API int w4a16_tile_gate_up(const int32_t* gu_packed, int64_t E, int64_t H, int64_t I, int32_t* tiled,
                                  size_t tiled_bytes, void* stream);
+W4A16_API size_t w4a16_tiled_down_bytes(int64_t E, int64_t H, int64_t I);
+W4A16_API int w4a16_tile_down(const int32_t* dn_packed, int64_t E, int64_t H, int64_t I, int32_t* tiled,
+                              size_t tiled_bytes, void* stream);
 W4A16_API size_t w4a16_tiled_prefill_bytes(int which, int64_t E, int64_t H, int64_t I);
 W4A16_API int w4a16_tile_prefill(int which, const int32_t* packed, int64_t E, int64_t H, int64_t I,
                                  int32_t* tiled, size_t tiled_bytes, void* stream);
@@ -245,16 +251,18 @@ W4A16_API int moe_gate_up_tiled(const uint16_t* hidden, const int32_t* gu_packed
                                 const int32_t* gu_ptiled, const uint16_t* gu_scale, int64_t M, int64_t top_k,
                                 int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
                                 size_t workspace_bytes, void* stream);
-W4A16_API int moe_down_tiled(const int32_t* dn_packed, const int32_t* dn_ptiled, const uint16_t* dn_scale,
-                             int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t group_size,
-                             void* workspace, size_t workspace_bytes, void* stream);
+W4A16_API int moe_down_tiled(const int32_t* dn_packed, const int32_t* dn_tiled, const int32_t* dn_ptiled,
+                             const uint16_t* dn_scale, int64_t M, int64_t top_k, int64_t E, int64_t H,
+                             int64_t I, int64_t group_size, void* workspace, size_t workspace_bytes,
+                             void* stream);
 W4A16_API int moe_layer_forward_tiled(const uint16_t* router_in, const uint16_t* router_scale,
                                       float scalar_root, const uint16_t* proj_w,
                                       const uint16_t* per_expert_scale, float eps, const uint16_t* hidden,
                                       const int32_t* gu_packed, const int32_t* gu_tiled,
                                       const int32_t* gu_ptiled, const uint16_t* gu_scale,
-                                      const int32_t* dn_packed, const int32_t* dn_ptiled,
-                                      const uint16_t* dn_scale, uint16_t* out, int64_t* topk_idx,
+                                      const int32_t* dn_packed, const int32_t* dn_tiled,
+                                      const int32_t* dn_ptiled, const uint16_t* dn_scale, uint16_t* out,
+                                      int64_t* topk_idx,
                                       float* topk_w, int64_t M, int64_t top_k, int64_t E, int64_t H,
                                       int64_t I, int64_t group_size, void* workspace,
                                       size_t workspace_bytes, void* stream);

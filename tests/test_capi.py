@@ -219,14 +219,17 @@ def test_tiled_gate_up_host_side(lib):
     # Gemma shape: 22 column-tile items of 16 wavefronts x 6 KiB tiles per expert
     assert lib.w4a16_tiled_gate_up_bytes(128, 2816, 704) == 128 * 22 * 16 * 6 * 1024
     assert lib.w4a16_tiled_gate_up_bytes(1, 2816, 704) == 22 * 16 * 6 * 1024
-    # shapes the streamer runs without its K split (short K) or with the
-    # long-K loop have no tiled form; E out of range neither
-    assert lib.w4a16_tiled_gate_up_bytes(8, 256, 64) == 0
-    assert lib.w4a16_tiled_gate_up_bytes(8, 8192, 704) == 0
+    # shapes the streamer runs with its long-K loop have no tiled form; E out
+    # of range neither
+    assert lib.w4a16_tiled_gate_up_bytes(8, 8192, 704) == 0              # long-K loop
+    assert lib.w4a16_tiled_gate_up_bytes(8, 2816, 700) == 0              # I not a multiple of 32
+    # down: 44 items of 4 wavefronts x 6 KiB tiles per expert
+    assert lib.w4a16_tiled_down_bytes(128, 2816, 704) == 128 * 44 * 4 * 6 * 1024
+    assert lib.w4a16_tile_down(None, 2, 2816, 704, ctypes.c_void_p(4096), 1 << 30, None) == 1
     assert lib.w4a16_tiled_gate_up_bytes(0, 2816, 704) == 0
     fake = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
     need = lib.w4a16_tiled_gate_up_bytes(2, 2816, 704)
-    assert lib.w4a16_tile_gate_up(fake, 8, 256, 64, fake, 1 << 30, NULL) == 2
+    assert lib.w4a16_tile_gate_up(fake, 8, 8192, 704, fake, 1 << 30, NULL) == 2
     assert lib.w4a16_tile_gate_up(NULL, 2, 2816, 704, fake, need, NULL) == 1
     assert lib.w4a16_tile_gate_up(fake, 2, 2816, 704, ctypes.c_void_p(4100), need, NULL) == 4
     assert lib.w4a16_tile_gate_up(fake, 2, 2816, 704, fake, need - 16, NULL) == 5

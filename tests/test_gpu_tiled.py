@@ -90,8 +90,31 @@ def test_tile_prefill_layout(dev, which):
     assert np.array_equal(got, ref.reshape(-1))
 
 
+def test_tile_down_layout(dev):
+    """The decode down copy: 4 wavefronts (no K split), 6 k tiles each, column
+    block 4 ct + w of 16 rows; piece (e, ct, w, i, l) = row 16 colblk + l % 16
+    at byte 64 i + 16 (l / 16), zero past the 352-byte row."""
+    Ex = 2
+    wts = synth.moe_weights(Ex, H, I, 128, seed=7160)
+    tiled = _lib.tile_down(wts.down_packed.to(dev))
+    assert tiled is not None
+    rowbytes = I // 2
+    rows = wts.down_packed.numpy().view(np.uint8).reshape(Ex, H, rowbytes)
+    n_ct, tpw = (H // 16 + 3) // 4, 6
+    ref = np.zeros((Ex, n_ct, 4, tpw, 64, 16), np.uint8)
+    for ct in range(n_ct):
+        for w in range(4):
+            for i in range(tpw):
+                for l in range(64):
+                    r, b = 16 * (4 * ct + w) + (l & 15), 64 * i + 16 * (l >> 4)
+                    if r < H and b + 16 <= rowbytes:
+                        ref[:, ct, w, i, l] = rows[:, r, b:b + 16]
+    assert np.array_equal(tiled.cpu().numpy().view(np.uint8), ref.reshape(-1))
+
+
 def test_tile_unsupported_shape(dev):
-    wts = synth.moe_weights(4, 256, 64, 128, seed=7101)
+    # K = 8192 takes the streamer's long-K loop: no tiled form
+    wts = synth.moe_weights(2, 8192, 64, 128, seed=7101)
     assert _lib.tile_gate_up(wts.gate_up_packed.to(dev)) is None
 
 
@@ -102,7 +125,9 @@ def layer(request, dev):
     gpu = [getattr(w, k).to(dev) for k in ("gate_up_packed", "gate_up_scale", "down_packed", "down_scale")]
     rw = synth.router_weights(E, H, seed=7300)
     r = (rw.scale.to(dev), rw.scalar_root, rw.proj.to(dev), rw.per_expert_scale.to(dev), 1e-6, K_TOP)
-    return G, gpu, r, _lib.tile_gate_up(gpu[0]), _lib.tile_prefill(gpu[0], "gate_up"), _lib.tile_prefill(gpu[2], "down")
+    tiles = (_lib.tile_gate_up(gpu[0]), _lib.tile_prefill(gpu[0], "gate_up"), _lib.tile_down(gpu[2]),
+             _lib.tile_prefill(gpu[2], "down"))
+    return (G, gpu, r) + tiles
 
 
 def _bits(t):
@@ -113,12 +138,12 @@ def _bits(t):
 # and prefill sizes (the prefill copies)
 @pytest.mark.parametrize("M", [1, 8, 32, 64, 300, 2048])
 def test_layer_tiled_equals_untiled(dev, layer, M):
-    G, gpu, r, tiled, gpt, dpt = layer
+    G, gpu, r, tiled, gpt, dt, dpt = layer
     print(f"tiled layer G={G} M={M}", flush=True)
     x = synth.activations(M, H, seed=7400 + M).to(dev)
     y0, w0, i0 = _lib.moe_layer_forward(x, r[0], r[1], r[2], r[3], r[4], r[5], x, gpu[0], gpu[1], gpu[2], gpu[3])
     y1, w1, i1 = _lib.moe_layer_forward(x, r[0], r[1], r[2], r[3], r[4], r[5], x, gpu[0], gpu[1], gpu[2], gpu[3],
-                                        gu_tiled=tiled, gu_ptiled=gpt, dn_ptiled=dpt)
+                                        gu_tiled=tiled, gu_ptiled=gpt, dn_tiled=dt, dn_ptiled=dpt)
     torch.cuda.synchronize()
     assert torch.equal(i0, i1) and torch.equal(w0, w1)
     assert np.array_equal(_bits(y0), _bits(y1)), f"G={G} M={M}: tiled layer output differs"
@@ -128,7 +153,7 @@ def test_layer_tiled_equals_untiled(dev, layer, M):
 def test_stage_gate_up_tiled(dev, layer, M):
     """The stage API: gate_up on the tiled copy, then down and combine, equals
     the untiled stages bit for bit."""
-    G, gpu, r, tiled, gpt, dpt = layer
+    G, gpu, r, tiled, gpt, dt, dpt = layer
     x = synth.activations(M, H, seed=7500 + M).to(dev)
     w, idx = _lib.router_topk(x, *r)
     outs = []
@@ -136,7 +161,7 @@ def test_stage_gate_up_tiled(dev, layer, M):
         st = _lib.MoEStages(M, K_TOP, E, H, I, G, dev)
         st.plan(x, idx)
         st.gate_up(x, gpu[0], gpu[1], gu_tiled=t, gu_ptiled=None if t is None else gpt)
-        st.down(gpu[2], gpu[3], dn_ptiled=None if t is None else dpt)
+        st.down(gpu[2], gpu[3], dn_ptiled=None if t is None else dpt, dn_tiled=None if t is None else dt)
         outs.append(st.combine(idx, w).clone())
     torch.cuda.synchronize()
     assert np.array_equal(_bits(outs[0]), _bits(outs[1]))
@@ -146,10 +171,10 @@ def test_stage_gate_up_tiled(dev, layer, M):
 def test_layer_tiled_graph_replay(dev, layer, M):
     """Captured in a HIP graph and replayed with eager work in between: every
     replay equals the eager result (decode and prefill sizes)."""
-    G, gpu, r, tiled, gpt, dpt = layer
+    G, gpu, r, tiled, gpt, dt, dpt = layer
     x = synth.activations(M, H, seed=7600).to(dev)
     fwd = lambda xx: _lib.moe_layer_forward(xx, r[0], r[1], r[2], r[3], r[4], r[5], xx, gpu[0], gpu[1], gpu[2],
-                                            gpu[3], gu_tiled=tiled, gu_ptiled=gpt, dn_ptiled=dpt)
+                                            gpu[3], gu_tiled=tiled, gu_ptiled=gpt, dn_tiled=dt, dn_ptiled=dpt)
     eager = fwd(x)[0].clone()
     s = torch.cuda.Stream(dev)
     s.wait_stream(torch.cuda.current_stream(dev))
