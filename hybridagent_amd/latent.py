@@ -29,11 +29,13 @@ class _Layer:
     router: synth.RouterWeights
     experts: synth.MoEWeights
     pre_norm: torch.Tensor  # RMSNorm weight of the MoE input (bf16 [H])
+    gu_tiled: torch.Tensor | None = None  # the decode streamers' tiled weight copies
+    dn_tiled: torch.Tensor | None = None
 
 
 class LatentStack:
     def __init__(self, n_layers: int, E: int, H: int, I: int, top_k: int, group_size: int, seed: int,
-                 device, eps: float = 1e-6):
+                 device, eps: float = 1e-6, tiled: bool = True):
         self.H, self.top_k, self.G, self.eps = H, top_k, group_size, eps
         dev = torch.device(device)
         g = torch.Generator(device=dev).manual_seed(seed)
@@ -42,7 +44,10 @@ class LatentStack:
             rw = synth.router_weights(E, H, seed=seed + 31 * i, device=dev)
             ew = synth.moe_weights(E, H, I, group_size, seed=seed + 31 * i + 7, device=dev)
             pre = (1.0 + 0.05 * torch.randn(H, generator=g, device=dev)).to(torch.bfloat16)
-            self.layers.append(_Layer(rw, ew, pre))
+            ly = _Layer(rw, ew, pre)
+            if tiled and group_size == 128 and dev.type == "cuda":
+                ly.gu_tiled, ly.dn_tiled = _lib.tile_gate_up(ew.gate_up_packed), _lib.tile_down(ew.down_packed)
+            self.layers.append(ly)
         std = 1.0 / math.sqrt(H)
         mk = lambda *s, sc=1.0: (sc * torch.randn(*s, generator=g, device=dev)).to(torch.bfloat16)
         self.hl = {
@@ -68,7 +73,8 @@ class LatentStack:
         rw, ew = ly.router, ly.experts
         out, w, idx = _lib.moe_layer_forward(h, rw.scale, rw.scalar_root, rw.proj, rw.per_expert_scale,
                                              rw.eps, self.top_k, xin, ew.gate_up_packed, ew.gate_up_scale,
-                                             ew.down_packed, ew.down_scale, group_size=self.G)
+                                             ew.down_packed, ew.down_scale, group_size=self.G,
+                                             gu_tiled=ly.gu_tiled, dn_tiled=ly.dn_tiled)
         return out, idx, w
 
     def layer(self, h: torch.Tensor, i: int):
