@@ -67,6 +67,8 @@ SIGNATURES = {
     "w4a16_tile_prefill": (ctypes.c_int, [ctypes.c_int, _VP, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "moe_gate_up_tiled": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ,
                                          _VP]),
+    "moe_forward_tiled": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64,
+                                         _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "moe_down_tiled": (ctypes.c_int, [_VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "moe_layer_forward_tiled": (ctypes.c_int, [_VP, _VP, _F32, _VP, _VP, _F32, _VP, _VP, _VP, _VP, _VP, _VP,
                                                _VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64,
@@ -343,8 +345,12 @@ def sort_permute(top_k_index: torch.Tensor, num_experts: int):
 
 def moe_forward(hidden_states: torch.Tensor, top_k_index: torch.Tensor, top_k_weights: torch.Tensor,
                 gu_packed: torch.Tensor, gu_scale: torch.Tensor, dn_packed: torch.Tensor,
-                dn_scale: torch.Tensor, group_size: int | None = None) -> torch.Tensor:
-    """W4A16 MoE layer output [T, H] bf16  (quantization.py:88-129)."""
+                dn_scale: torch.Tensor, group_size: int | None = None, *, gu_tiled: torch.Tensor | None = None,
+                gu_ptiled: torch.Tensor | None = None, dn_tiled: torch.Tensor | None = None,
+                dn_ptiled: torch.Tensor | None = None) -> torch.Tensor:
+    """W4A16 MoE layer output [T, H] bf16  (quantization.py:88-129).  The tiled weight
+    copies (tile_gate_up, tile_down, tile_prefill; each optional) serve the kernels that
+    read them; the output is bit-identical."""
     dev = _require_gpu(hidden_states, top_k_index, top_k_weights, gu_packed, gu_scale, dn_packed, dn_scale)
     H = hidden_states.shape[-1]
     x = _bf16(hidden_states, "hidden_states").reshape(-1, H)
@@ -371,10 +377,22 @@ def moe_forward(hidden_states: torch.Tensor, top_k_index: torch.Tensor, top_k_we
     lib = load()
     ws = _workspace(lib.moe_workspace_bytes(max(M, 1), k, E, H, I), dev)
     with torch.cuda.device(dev):
-        _check(lib.moe_forward(_ptr(x), _ptr(idx), _ptr(w), _ptr(gu_packed), _ptr(gu_scale), _ptr(dn_packed),
-                               _ptr(dn_scale), _ptr(out), M, k, E, H, I, G, _ptr(ws),
-                               0 if ws is None else ws.numel(), _stream(dev)),
-               "moe_forward")
+        if gu_tiled is None and gu_ptiled is None and dn_tiled is None and dn_ptiled is None:
+            _check(lib.moe_forward(_ptr(x), _ptr(idx), _ptr(w), _ptr(gu_packed), _ptr(gu_scale), _ptr(dn_packed),
+                                   _ptr(dn_scale), _ptr(out), M, k, E, H, I, G, _ptr(ws),
+                                   0 if ws is None else ws.numel(), _stream(dev)),
+                   "moe_forward")
+        else:
+            gu_tiled = _tiled_arg(gu_tiled, "gate_up tiled copy", lib.w4a16_tiled_gate_up_bytes(E, H, I), dev)
+            gu_ptiled = _tiled_arg(gu_ptiled, "gate_up prefill tiled copy",
+                                   lib.w4a16_tiled_prefill_bytes(0, E, H, I), dev)
+            dn_tiled = _tiled_arg(dn_tiled, "down tiled copy", lib.w4a16_tiled_down_bytes(E, H, I), dev)
+            dn_ptiled = _tiled_arg(dn_ptiled, "down prefill tiled copy", lib.w4a16_tiled_prefill_bytes(1, E, H, I), dev)
+            _check(lib.moe_forward_tiled(_ptr(x), _ptr(idx), _ptr(w), _ptr(gu_packed), _ptr(gu_tiled),
+                                         _ptr(gu_ptiled), _ptr(gu_scale), _ptr(dn_packed), _ptr(dn_tiled),
+                                         _ptr(dn_ptiled), _ptr(dn_scale), _ptr(out), M, k, E, H, I, G, _ptr(ws),
+                                         0 if ws is None else ws.numel(), _stream(dev)),
+                   "moe_forward_tiled")
     return out.reshape(*hidden_states.shape[:-1], H)
 
 

@@ -754,6 +754,29 @@ int moe_forward(const uint16_t* hidden, const int64_t* topk_idx, const float* to
   return st;
 }
 
+int moe_forward_tiled(const uint16_t* hidden, const int64_t* topk_idx, const float* topk_w,
+                      const int32_t* gu_packed, const int32_t* gu_tiled, const int32_t* gu_ptiled,
+                      const uint16_t* gu_scale, const int32_t* dn_packed, const int32_t* dn_tiled,
+                      const int32_t* dn_ptiled, const uint16_t* dn_scale, uint16_t* out, int64_t M,
+                      int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+  MoeLayout L{};
+  int st = moe_check(M, top_k, E, H, I, group_size, workspace, workspace_bytes, &L);
+  if (st != W4A16_OK || M == 0) return st;
+  if (!hidden || !topk_idx || !topk_w || !gu_packed || !gu_scale || !dn_packed || !dn_scale ||
+      !out)
+    return W4A16_ERR_NULL;
+  st = moe_plan(hidden, topk_idx, M, top_k, E, H, I, group_size, workspace, workspace_bytes,
+                stream);
+  if (st == W4A16_OK)
+    st = gate_up_impl(hidden, gu_packed, gu_scale, gu_tiled, gu_ptiled, M, top_k, E, H, I, group_size,
+                      workspace, workspace_bytes, stream);
+  if (st == W4A16_OK)
+    st = down_and_combine(dn_packed, dn_scale, topk_idx, topk_w, out, M, top_k, E, H, I,
+                          group_size, workspace, workspace_bytes, stream, dn_tiled, dn_ptiled);
+  return st;
+}
+
 }  // extern "C"
 
 namespace {

@@ -148,9 +148,33 @@ class Gemma4TextExperts4Bit(nn.Module):
         top_k_weights: torch.Tensor,
     ) -> torch.Tensor:
         """[T, H] bf16 -> [T, H] bf16 (quantization.py:225-240); GPU only, zero-sync."""
+        tiles = getattr(self, "_tiles", None)
+        if tiles:
+            return _lib.moe_forward(hidden_states, top_k_index, top_k_weights, self.gate_up_packed,
+                                    self.gate_up_scale, self.down_packed, self.down_scale, self.group_size,
+                                    **tiles)
         return fused_triton_4bit_moe_forward(
             hidden_states, top_k_index, top_k_weights,
             self.gate_up_packed, self.gate_up_scale, self.down_packed, self.down_scale)
+
+    def tile_weights(self) -> None:
+        """Build the kernels' tiled copies of the loaded expert weights (opt-in; no
+        counterpart in the reference): the decode streamers read them as contiguous KiBs
+        and the prefill GEMMs as 8 KiB blocks, with bit-identical results.  They take
+        about as much memory again as the experts; the buffers and the state dict are
+        unchanged.  Call after the weights are loaded, on their device; reloading or
+        moving the weights needs another call (``untile_weights`` drops them)."""
+        gu, dn = self.gate_up_packed, self.down_packed
+        self._tiles = {
+            "gu_tiled": _lib.tile_gate_up(gu) if self.group_size == 128 else None,
+            "dn_tiled": _lib.tile_down(dn) if self.group_size == 128 else None,
+            "gu_ptiled": _lib.tile_prefill(gu, "gate_up"),
+            "dn_ptiled": _lib.tile_prefill(dn, "down"),
+        }
+
+    def untile_weights(self) -> None:
+        """Drop the tiled copies made by ``tile_weights``."""
+        self._tiles = None
 
 
 def is_pack_quantized_dir(model_dir: Path) -> bool:

@@ -233,6 +233,8 @@ W4A16_API int moe_layer_forward(const uint16_t* router_in, const uint16_t* route
  *                              NULL, gu_packed elsewhere;
  *   moe_down_tiled             moe_down reading dn_tiled (decode sizes,
  *                              group size 128) and dn_ptiled likewise;
+ *   moe_forward_tiled          moe_forward (fused_triton_4bit_moe_forward,
+ *                              quantization.py:88-129) through the two above;
  *   moe_layer_forward_tiled    moe_layer_forward (backends.py:111-122)
  *                              through the two above.
  * The copy functions return W4A16_ERR_SHAPE when the bytes are 0 and
@@ -255,6 +257,12 @@ W4A16_API int moe_down_tiled(const int32_t* dn_packed, const int32_t* dn_tiled, 
                              const uint16_t* dn_scale, int64_t M, int64_t top_k, int64_t E, int64_t H,
                              int64_t I, int64_t group_size, void* workspace, size_t workspace_bytes,
                              void* stream);
+W4A16_API int moe_forward_tiled(const uint16_t* hidden, const int64_t* topk_idx, const float* topk_w,
+                                const int32_t* gu_packed, const int32_t* gu_tiled, const int32_t* gu_ptiled,
+                                const uint16_t* gu_scale, const int32_t* dn_packed, const int32_t* dn_tiled,
+                                const int32_t* dn_ptiled, const uint16_t* dn_scale, uint16_t* out, int64_t M,
+                                int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t group_size,
+                                void* workspace, size_t workspace_bytes, void* stream);
 W4A16_API int moe_layer_forward_tiled(const uint16_t* router_in, const uint16_t* router_scale,
                                       float scalar_root, const uint16_t* proj_w,
                                       const uint16_t* per_expert_scale, float eps, const uint16_t* hidden,

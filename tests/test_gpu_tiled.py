@@ -192,3 +192,50 @@ def test_layer_tiled_graph_replay(dev, layer, M):
         assert np.array_equal(_bits(out), _bits(eager)), f"replay {rep}"
         fwd(x2)
         torch.cuda.synchronize()
+
+
+def _route(M, seed, dev):
+    g = torch.Generator().manual_seed(seed)
+    idx = torch.stack([torch.randperm(E, generator=g)[:K_TOP] for _ in range(M)])
+    w = torch.rand(M, K_TOP, generator=g) + 0.05
+    return idx.to(dev), (w / w.sum(1, keepdim=True)).float().to(dev)
+
+
+@pytest.mark.parametrize("M", [1, 8, 64, 2048])
+def test_moe_forward_tiled(dev, layer, M):
+    """The one-call experts forward (fused_triton_4bit_moe_forward) on all four
+    copies equals the packed path bit for bit."""
+    G, gpu, r, tiled, gpt, dt, dpt = layer
+    x = synth.activations(M, H, seed=7700 + M).to(dev)
+    idx, w = _route(M, 7701 + M, dev)
+    y0 = _lib.moe_forward(x, idx, w, *gpu)
+    y1 = _lib.moe_forward(x, idx, w, *gpu, gu_tiled=tiled, gu_ptiled=gpt, dn_tiled=dt, dn_ptiled=dpt)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(y0), _bits(y1)), f"G={G} M={M}"
+
+
+def test_module_tile_weights(dev):
+    """Gemma4TextExperts4Bit.tile_weights: forward with the copies equals forward
+    without them; the state dict is unchanged."""
+    import types
+    from hybridagent_amd import quantization as q
+    cfg = types.SimpleNamespace(
+        num_experts=E, hidden_size=H, moe_intermediate_size=I, hidden_activation="gelu_pytorch_tanh",
+        quantization_config={"quant_method": "compressed-tensors", "format": "pack-quantized",
+                             "config_groups": {"group_0": {"weights": {"num_bits": 4, "group_size": 128}}}})
+    mod = q.Gemma4TextExperts4Bit(cfg)
+    wts = synth.moe_weights(E, H, I, 128, seed=7800)
+    for name in ("gate_up_packed", "gate_up_scale", "down_packed", "down_scale"):
+        getattr(mod, name).copy_(getattr(wts, name))
+    mod = mod.to(dev)
+    keys = sorted(mod.state_dict())
+    for M in (1, 64, 512):
+        x = synth.activations(M, H, seed=7801 + M).to(dev)
+        idx, w = _route(M, 7802 + M, dev)
+        mod.untile_weights()
+        y0 = mod(x, idx, w)
+        mod.tile_weights()
+        y1 = mod(x, idx, w)
+        torch.cuda.synchronize()
+        assert np.array_equal(_bits(y0), _bits(y1)), f"M={M}"
+    assert sorted(mod.state_dict()) == keys
