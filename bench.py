@@ -479,7 +479,8 @@ class FfnLayer:
                          layer_scalar=torch.ones(1, dtype=torch.bfloat16, device=dev), eps=1e-6, top_k=TOPK)
 
     def forward(self, residual, attn_out):
-        return _lib.ffn_block(residual, attn_out, **self.args, group_size=G)
+        return _lib.ffn_block(residual, attn_out, **self.args, group_size=G, gu_tiled=self.moe.gu_tiled,
+                              dn_tiled=self.moe.dn_tiled)
 
 
 def ffn_leg(dev, steps, warmup, n_layers):

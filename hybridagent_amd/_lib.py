@@ -70,6 +70,10 @@ SIGNATURES = {
     "moe_forward_tiled": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64,
                                          _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "moe_down_tiled": (ctypes.c_int, [_VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
+    "moe_ffn_block_forward_tiled": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _F32, _VP, _VP,
+                                                   _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
+                                                   _F32, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _VP,
+                                                   _SZ, _VP]),
     "moe_layer_forward_tiled": (ctypes.c_int, [_VP, _VP, _F32, _VP, _VP, _F32, _VP, _VP, _VP, _VP, _VP, _VP,
                                                _VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64,
                                                _VP, _SZ, _VP]),
@@ -562,9 +566,13 @@ def ffn_block(residual: torch.Tensor, attn_out: torch.Tensor, post_attn_ln_w: to
               pre_ff_ln2_w: torch.Tensor, gu_packed: torch.Tensor, gu_scale: torch.Tensor,
               dn_packed: torch.Tensor, dn_scale: torch.Tensor, post_ff_ln2_w: torch.Tensor,
               post_ff_ln_w: torch.Tensor, layer_scalar: torch.Tensor, eps: float, top_k: int,
-              group_size: int | None = None) -> torch.Tensor:
+              group_size: int | None = None, *, gu_tiled: torch.Tensor | None = None,
+              gu_ptiled: torch.Tensor | None = None, dn_tiled: torch.Tensor | None = None,
+              dn_ptiled: torch.Tensor | None = None) -> torch.Tensor:
     """The post-attention FFN block ``_ffn_moe_4bit_step`` (backends.py:77-126), same
-    arguments in the same order: residual / attn_out [..., H] bf16 -> [..., H] bf16."""
+    arguments in the same order: residual / attn_out [..., H] bf16 -> [..., H] bf16.
+    The experts' tiled weight copies (tile_gate_up, tile_down, tile_prefill; each
+    optional) serve the kernels that read them, with bit-identical output."""
     dense = (post_attn_ln_w, pre_ff_ln_w, mlp_gate_w, mlp_up_w, mlp_down_w, post_ff_ln1_w, router_scale,
              router_proj_w, router_per_expert_scale, pre_ff_ln2_w, post_ff_ln2_w, post_ff_ln_w)
     dev = _require_gpu(residual, attn_out, *dense, gu_packed, gu_scale, dn_packed, dn_scale, layer_scalar)
@@ -605,13 +613,28 @@ def ffn_block(residual: torch.Tensor, attn_out: torch.Tensor, post_attn_ln_w: to
     lib = load()
     ws = _workspace(lib.moe_ffn_block_workspace_bytes(max(M, 1), top_k, E, H, I, Im), dev)
     with torch.cuda.device(dev):
-        _check(lib.moe_ffn_block_forward(
-            _ptr(res), _ptr(att), _ptr(post_attn_ln_w), _ptr(pre_ff_ln_w), _ptr(mlp_gate_w), _ptr(mlp_up_w),
-            _ptr(mlp_down_w), _ptr(post_ff_ln1_w), _ptr(router_scale), float(router_scalar_root),
-            _ptr(router_proj_w), _ptr(router_per_expert_scale), _ptr(pre_ff_ln2_w), _ptr(gu_packed),
-            _ptr(gu_scale), _ptr(dn_packed), _ptr(dn_scale), _ptr(post_ff_ln2_w), _ptr(post_ff_ln_w), _ptr(ls),
-            float(eps), _ptr(out), M, int(top_k), E, H, I, Im, G, _ptr(ws), 0 if ws is None else ws.numel(),
-            _stream(dev)), "moe_ffn_block_forward")
+        if gu_tiled is None and gu_ptiled is None and dn_tiled is None and dn_ptiled is None:
+            _check(lib.moe_ffn_block_forward(
+                _ptr(res), _ptr(att), _ptr(post_attn_ln_w), _ptr(pre_ff_ln_w), _ptr(mlp_gate_w), _ptr(mlp_up_w),
+                _ptr(mlp_down_w), _ptr(post_ff_ln1_w), _ptr(router_scale), float(router_scalar_root),
+                _ptr(router_proj_w), _ptr(router_per_expert_scale), _ptr(pre_ff_ln2_w), _ptr(gu_packed),
+                _ptr(gu_scale), _ptr(dn_packed), _ptr(dn_scale), _ptr(post_ff_ln2_w), _ptr(post_ff_ln_w), _ptr(ls),
+                float(eps), _ptr(out), M, int(top_k), E, H, I, Im, G, _ptr(ws), 0 if ws is None else ws.numel(),
+                _stream(dev)), "moe_ffn_block_forward")
+        else:
+            gu_tiled = _tiled_arg(gu_tiled, "gate_up tiled copy", lib.w4a16_tiled_gate_up_bytes(E, H, I), dev)
+            gu_ptiled = _tiled_arg(gu_ptiled, "gate_up prefill tiled copy",
+                                   lib.w4a16_tiled_prefill_bytes(0, E, H, I), dev)
+            dn_tiled = _tiled_arg(dn_tiled, "down tiled copy", lib.w4a16_tiled_down_bytes(E, H, I), dev)
+            dn_ptiled = _tiled_arg(dn_ptiled, "down prefill tiled copy", lib.w4a16_tiled_prefill_bytes(1, E, H, I), dev)
+            _check(lib.moe_ffn_block_forward_tiled(
+                _ptr(res), _ptr(att), _ptr(post_attn_ln_w), _ptr(pre_ff_ln_w), _ptr(mlp_gate_w), _ptr(mlp_up_w),
+                _ptr(mlp_down_w), _ptr(post_ff_ln1_w), _ptr(router_scale), float(router_scalar_root),
+                _ptr(router_proj_w), _ptr(router_per_expert_scale), _ptr(pre_ff_ln2_w), _ptr(gu_packed),
+                _ptr(gu_tiled), _ptr(gu_ptiled), _ptr(gu_scale), _ptr(dn_packed), _ptr(dn_tiled), _ptr(dn_ptiled),
+                _ptr(dn_scale), _ptr(post_ff_ln2_w), _ptr(post_ff_ln_w), _ptr(ls), float(eps), _ptr(out), M,
+                int(top_k), E, H, I, Im, G, _ptr(ws), 0 if ws is None else ws.numel(), _stream(dev)),
+                "moe_ffn_block_forward_tiled")
     return out.reshape(residual.shape)
 
 

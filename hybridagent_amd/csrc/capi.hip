@@ -824,7 +824,7 @@ size_t moe_ffn_block_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_
   return ffn_layout(nullptr, M, top_k, E, H, I, Im).bytes;
 }
 
-int moe_ffn_block_forward(const uint16_t* residual, const uint16_t* attn_out,
+static int ffn_block_impl(const uint16_t* residual, const uint16_t* attn_out,
                           const uint16_t* post_attn_ln_w, const uint16_t* pre_ff_ln_w,
                           const uint16_t* mlp_gate_w, const uint16_t* mlp_up_w,
                           const uint16_t* mlp_down_w, const uint16_t* post_ff_ln1_w,
@@ -836,7 +836,8 @@ int moe_ffn_block_forward(const uint16_t* residual, const uint16_t* attn_out,
                           const uint16_t* post_ff_ln_w, const uint16_t* layer_scalar, float eps,
                           uint16_t* out, int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I,
                           int64_t Im, int64_t group_size, void* workspace, size_t workspace_bytes,
-                          void* stream) {
+                          void* stream, const int32_t* gu_tiled, const int32_t* gu_ptiled,
+                          const int32_t* dn_tiled, const int32_t* dn_ptiled) {
   // row kernels: H <= 8192, one workgroup per row; shared-MLP linears:
   // K % 32 == 0 and ceil(M / 64) <= 65535 row tiles
   if (M < 0 || M > kMaxHybridLinkRows || top_k <= 0 || top_k > E || H <= 0 || H % 32 != 0 || H > 8192 ||
@@ -870,12 +871,53 @@ int moe_ffn_block_forward(const uint16_t* residual, const uint16_t* attn_out,
     e = launch_linear_bf16(kLinPlain, L.inter, mlp_down_w, nullptr, nullptr, nullptr, L.h_mlp, M, (int)H,
                            (int)Im, s);
   if (e != hipSuccess) return W4A16_ERR_LAUNCH;
-  st = moe_layer_forward(L.res, router_scale, router_scalar_root, router_proj_w, router_per_expert_scale,
-                         eps, L.h2_in, gu_packed, gu_scale, dn_packed, dn_scale, L.moe, L.idx, L.w, M,
-                         top_k, E, H, I, group_size, L.moe_ws, L.moe_bytes, stream);
+  st = moe_layer_forward_tiled(L.res, router_scale, router_scalar_root, router_proj_w, router_per_expert_scale,
+                               eps, L.h2_in, gu_packed, gu_tiled, gu_ptiled, gu_scale, dn_packed, dn_tiled,
+                               dn_ptiled, dn_scale, L.moe, L.idx, L.w, M, top_k, E, H, I, group_size, L.moe_ws,
+                               L.moe_bytes, stream);
   if (st != W4A16_OK) return st;
   return launch_status(launch_ffn_post(L.h_mlp, L.moe, L.res, post_ff_ln1_w, post_ff_ln2_w, post_ff_ln_w,
                                        layer_scalar, out, M, (int)H, eps, s));
+}
+
+int moe_ffn_block_forward(const uint16_t* residual, const uint16_t* attn_out,
+                          const uint16_t* post_attn_ln_w, const uint16_t* pre_ff_ln_w,
+                          const uint16_t* mlp_gate_w, const uint16_t* mlp_up_w,
+                          const uint16_t* mlp_down_w, const uint16_t* post_ff_ln1_w,
+                          const uint16_t* router_scale, float router_scalar_root,
+                          const uint16_t* router_proj_w, const uint16_t* router_per_expert_scale,
+                          const uint16_t* pre_ff_ln2_w, const int32_t* gu_packed,
+                          const uint16_t* gu_scale, const int32_t* dn_packed,
+                          const uint16_t* dn_scale, const uint16_t* post_ff_ln2_w,
+                          const uint16_t* post_ff_ln_w, const uint16_t* layer_scalar, float eps,
+                          uint16_t* out, int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I,
+                          int64_t Im, int64_t group_size, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  return ffn_block_impl(residual, attn_out, post_attn_ln_w, pre_ff_ln_w, mlp_gate_w, mlp_up_w, mlp_down_w,
+                        post_ff_ln1_w, router_scale, router_scalar_root, router_proj_w, router_per_expert_scale,
+                        pre_ff_ln2_w, gu_packed, gu_scale, dn_packed, dn_scale, post_ff_ln2_w, post_ff_ln_w,
+                        layer_scalar, eps, out, M, top_k, E, H, I, Im, group_size, workspace, workspace_bytes,
+                        stream, nullptr, nullptr, nullptr, nullptr);
+}
+
+int moe_ffn_block_forward_tiled(const uint16_t* residual, const uint16_t* attn_out,
+                                const uint16_t* post_attn_ln_w, const uint16_t* pre_ff_ln_w,
+                                const uint16_t* mlp_gate_w, const uint16_t* mlp_up_w,
+                                const uint16_t* mlp_down_w, const uint16_t* post_ff_ln1_w,
+                                const uint16_t* router_scale, float router_scalar_root,
+                                const uint16_t* router_proj_w, const uint16_t* router_per_expert_scale,
+                                const uint16_t* pre_ff_ln2_w, const int32_t* gu_packed, const int32_t* gu_tiled,
+                                const int32_t* gu_ptiled, const uint16_t* gu_scale, const int32_t* dn_packed,
+                                const int32_t* dn_tiled, const int32_t* dn_ptiled, const uint16_t* dn_scale,
+                                const uint16_t* post_ff_ln2_w, const uint16_t* post_ff_ln_w,
+                                const uint16_t* layer_scalar, float eps, uint16_t* out, int64_t M, int64_t top_k,
+                                int64_t E, int64_t H, int64_t I, int64_t Im, int64_t group_size, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  return ffn_block_impl(residual, attn_out, post_attn_ln_w, pre_ff_ln_w, mlp_gate_w, mlp_up_w, mlp_down_w,
+                        post_ff_ln1_w, router_scale, router_scalar_root, router_proj_w, router_per_expert_scale,
+                        pre_ff_ln2_w, gu_packed, gu_scale, dn_packed, dn_scale, post_ff_ln2_w, post_ff_ln_w,
+                        layer_scalar, eps, out, M, top_k, E, H, I, Im, group_size, workspace, workspace_bytes,
+                        stream, gu_tiled, gu_ptiled, dn_tiled, dn_ptiled);
 }
 
 size_t moe_bf16_experts_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I) {

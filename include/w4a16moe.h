@@ -236,7 +236,9 @@ W4A16_API int moe_layer_forward(const uint16_t* router_in, const uint16_t* route
  *   moe_forward_tiled          moe_forward (fused_triton_4bit_moe_forward,
  *                              quantization.py:88-129) through the two above;
  *   moe_layer_forward_tiled    moe_layer_forward (backends.py:111-122)
- *                              through the two above.
+ *                              through the two above;
+ *   moe_ffn_block_forward_tiled moe_ffn_block_forward (backends.py:77-126)
+ *                              with its experts through them.
  * The copy functions return W4A16_ERR_SHAPE when the bytes are 0 and
  * W4A16_ERR_WORKSPACE when tiled_bytes is short; the forwards give output
  * bit-identical to the untiled calls.                                      */
@@ -263,6 +265,16 @@ W4A16_API int moe_forward_tiled(const uint16_t* hidden, const int64_t* topk_idx,
                                 const int32_t* dn_ptiled, const uint16_t* dn_scale, uint16_t* out, int64_t M,
                                 int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t group_size,
                                 void* workspace, size_t workspace_bytes, void* stream);
+W4A16_API int moe_ffn_block_forward_tiled(
+    const uint16_t* residual, const uint16_t* attn_out, const uint16_t* post_attn_ln_w, const uint16_t* pre_ff_ln_w,
+    const uint16_t* mlp_gate_w, const uint16_t* mlp_up_w, const uint16_t* mlp_down_w, const uint16_t* post_ff_ln1_w,
+    const uint16_t* router_scale, float router_scalar_root, const uint16_t* router_proj_w,
+    const uint16_t* router_per_expert_scale, const uint16_t* pre_ff_ln2_w, const int32_t* gu_packed,
+    const int32_t* gu_tiled, const int32_t* gu_ptiled, const uint16_t* gu_scale, const int32_t* dn_packed,
+    const int32_t* dn_tiled, const int32_t* dn_ptiled, const uint16_t* dn_scale, const uint16_t* post_ff_ln2_w,
+    const uint16_t* post_ff_ln_w, const uint16_t* layer_scalar, float eps, uint16_t* out, int64_t M, int64_t top_k,
+    int64_t E, int64_t H, int64_t I, int64_t Im, int64_t group_size, void* workspace, size_t workspace_bytes,
+    void* stream);
 W4A16_API int moe_layer_forward_tiled(const uint16_t* router_in, const uint16_t* router_scale,
                                       float scalar_root, const uint16_t* proj_w,
                                       const uint16_t* per_expert_scale, float eps, const uint16_t* hidden,

@@ -239,3 +239,25 @@ def test_module_tile_weights(dev):
         torch.cuda.synchronize()
         assert np.array_equal(_bits(y0), _bits(y1)), f"M={M}"
     assert sorted(mod.state_dict()) == keys
+
+
+@pytest.mark.parametrize("M", [1, 32, 300])
+def test_ffn_block_tiled(dev, layer, M):
+    """The FFN block on the experts' tiled copies equals the packed path bit for
+    bit (the block's other weights random, the experts from the layer fixture)."""
+    G, gpu, r, tiled, gpt, dt, dpt = layer
+    Im = 2112
+    g = torch.Generator(device=dev).manual_seed(7900 + M)
+    nrm = lambda: (1 + 0.1 * torch.randn(H, generator=g, device=dev)).to(torch.bfloat16)
+    lin = lambda o, i: (torch.randn(o, i, generator=g, device=dev) / i ** 0.5).to(torch.bfloat16)
+    args = dict(post_attn_ln_w=nrm(), pre_ff_ln_w=nrm(), mlp_gate_w=lin(Im, H), mlp_up_w=lin(Im, H),
+                mlp_down_w=lin(H, Im), post_ff_ln1_w=nrm(), router_scale=r[0], router_scalar_root=r[1],
+                router_proj_w=r[2], router_per_expert_scale=r[3], pre_ff_ln2_w=nrm(), gu_packed=gpu[0],
+                gu_scale=gpu[1], dn_packed=gpu[2], dn_scale=gpu[3], post_ff_ln2_w=nrm(), post_ff_ln_w=nrm(),
+                layer_scalar=torch.ones(1, dtype=torch.bfloat16, device=dev), eps=1e-6, top_k=K_TOP)
+    res = synth.activations(M, H, seed=7901 + M).to(dev)
+    att = synth.activations(M, H, seed=7902 + M).to(dev)
+    y0 = _lib.ffn_block(res, att, **args, group_size=G)
+    y1 = _lib.ffn_block(res, att, **args, group_size=G, gu_tiled=tiled, gu_ptiled=gpt, dn_tiled=dt, dn_ptiled=dpt)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(y0), _bits(y1)), f"G={G} M={M}"
