@@ -161,7 +161,7 @@ class Gemma4TextExperts4Bit(nn.Module):
         """Build the kernels' tiled copies of the loaded expert weights (opt-in; no
         counterpart in the reference): the decode streamers read them as contiguous KiBs
         and the prefill GEMMs as 8 KiB blocks, with bit-identical results.  They take
-        about as much memory again as the experts; the buffers and the state dict are
+        about twice the experts' memory; the buffers and the state dict are
         unchanged.  Call after the weights are loaded, on their device; reloading or
         moving the weights needs another call (``untile_weights`` drops them)."""
         gu, dn = self.gate_up_packed, self.down_packed
