@@ -91,30 +91,30 @@ def expert_bytes(g: int) -> int:
 class Layer:
     """One MoE layer's device-resident weights (router + experts)."""
 
-    def __init__(self, seed: int, dev, zipf: bool = False, g: int = G):
+    def __init__(self, seed: int, dev, zipf: bool = False, g: int = G, tiled: bool = True):
         self.g = g
         self.rw = (synth.zipf_router_weights(E, H, seed=seed, device=dev) if zipf
                    else synth.router_weights(E, H, seed=seed, device=dev))
         self.ew = synth.moe_weights(E, H, I, g, seed=seed + 1000, device=dev)
-        # load-time tiled copies: the decode streamers' (group size 128; the
-        # decode layers) and the prefill GEMMs' (the Zipf prefill layers)
-        self.gu_tiled = _lib.tile_gate_up(self.ew.gate_up_packed) if g == 128 and not zipf else None
-        self.dn_tiled = _lib.tile_down(self.ew.down_packed) if g == 128 and not zipf else None
-        self.gu_ptiled = _lib.tile_prefill(self.ew.gate_up_packed, "gate_up") if zipf else None
-        self.dn_ptiled = _lib.tile_prefill(self.ew.down_packed, "down") if zipf else None
+        # load-time tiled copies: the decode streamers' (the decode layers) and
+        # the prefill GEMMs' (the Zipf prefill layers); with ``tiled=False`` the
+        # kernels read the packed checkpoint layout (the drop-in default)
+        ew = self.ew
+        self.tiles = _lib.tile_experts(ew.gate_up_packed, ew.gate_up_scale, ew.down_packed, ew.down_scale, g,
+                                       decode=not zipf, prefill=zipf) if tiled else None
 
     def route(self, x):
         rw = self.rw
         return _lib.router_topk(x, rw.scale, rw.scalar_root, rw.proj, rw.per_expert_scale, rw.eps, TOPK)
 
-    def forward(self, x):
-        """Router + experts (the MoE half of backends.py:111-122) through one C-ABI call."""
+    def forward(self, x, tiled: bool = True):
+        """Router + experts (the MoE half of backends.py:111-122) through one C-ABI call;
+        ``tiled=False`` reads the packed checkpoint layout."""
         rw, ew = self.rw, self.ew
         out, _, _ = _lib.moe_layer_forward(x, rw.scale, rw.scalar_root, rw.proj, rw.per_expert_scale,
                                            rw.eps, TOPK, x, ew.gate_up_packed, ew.gate_up_scale,
                                            ew.down_packed, ew.down_scale, group_size=self.g,
-                                           gu_tiled=self.gu_tiled, gu_ptiled=self.gu_ptiled,
-                                           dn_tiled=self.dn_tiled, dn_ptiled=self.dn_ptiled)
+                                           tiles=self.tiles if tiled else None)
         return out
 
 
@@ -144,7 +144,7 @@ def time_graph(fn, calls_per_replay: int, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) * 1e-3 / (replays * calls_per_replay)
 
 
-def decode_sweep(layers, dev, steps, warmup, ms=DECODE_MS):
+def decode_sweep(layers, dev, steps, warmup, ms=DECODE_MS, tiled: bool = True):
     out = {}
     g = layers[0].g
     for M in ms:
@@ -154,12 +154,13 @@ def decode_sweep(layers, dev, steps, warmup, ms=DECODE_MS):
             _, idx = ly.route(x)
             uniq.append(int(torch.unique(idx).numel()))
         U = sum(uniq) / len(uniq)
-        t = time_graph(lambda: [ly.forward(x) for ly in layers], len(layers), steps, warmup)
+        t = time_graph(lambda: [ly.forward(x, tiled) for ly in layers], len(layers), steps, warmup)
         nbytes = U * expert_bytes(g) + ROUTER_BYTES + 2 * M * H * 2
         out[M] = {"us": t * 1e6, "unique_experts": U, "bytes": nbytes, "gbps": nbytes / t / 1e9,
                   "frac_hbm": nbytes / t / 1e9 / PEAK_HBM_GBS,
                   "distinct_bytes_per_replay": len(layers) * U * expert_bytes(g)}
-        log(f"decode G={g} M={M}: {t*1e6:.1f} us/layer, U={U:.1f}, {out[M]['gbps']:.0f} GB/s")
+        log(f"decode G={g} M={M}{'' if tiled else ' (packed layout)'}: {t*1e6:.1f} us/layer, U={U:.1f}, "
+            f"{out[M]['gbps']:.0f} GB/s")
     return out
 
 
@@ -177,7 +178,7 @@ def gateup_kernel(layers, dev, M, steps, warmup):
 
     def run():
         for ly, st in zip(layers, stages):
-            st.gate_up(x, ly.ew.gate_up_packed, ly.ew.gate_up_scale, gu_tiled=ly.gu_tiled)
+            st.gate_up(x, ly.ew.gate_up_packed, ly.ew.gate_up_scale, tiles=ly.tiles)
 
     t = time_graph(run, len(layers), steps, warmup)
     U = sum(uniq) / len(uniq)
@@ -234,7 +235,7 @@ def prefill(dev, steps, warmup, n_layers, g: int = G, stages: bool = True):
 
         def run():
             for ly, st in zip(layers, sts):
-                st.gate_up(x, ly.ew.gate_up_packed, ly.ew.gate_up_scale, gu_ptiled=ly.gu_ptiled)
+                st.gate_up(x, ly.ew.gate_up_packed, ly.ew.gate_up_scale, tiles=ly.tiles)
 
         tg = time_graph(run, len(layers), steps, warmup)
         gflop = 2.0 * PREFILL_M * TOPK * H * 2 * I
@@ -479,8 +480,7 @@ class FfnLayer:
                          layer_scalar=torch.ones(1, dtype=torch.bfloat16, device=dev), eps=1e-6, top_k=TOPK)
 
     def forward(self, residual, attn_out):
-        return _lib.ffn_block(residual, attn_out, **self.args, group_size=G, gu_tiled=self.moe.gu_tiled,
-                              dn_tiled=self.moe.dn_tiled)
+        return _lib.ffn_block(residual, attn_out, **self.args, group_size=G, tiles=self.moe.tiles)
 
 
 def ffn_leg(dev, steps, warmup, n_layers):
@@ -721,6 +721,9 @@ def main(argv=None):
         print(json.dumps({"roofline": roofline(kern)}), flush=True)
         return 0
     dec = decode_sweep(layers, dev, args.steps, args.warmup)
+    # the same layers on the packed checkpoint layout (no tiled copies): what a
+    # caller gets without tile_weights()
+    dec_packed = decode_sweep(layers, dev, args.steps, args.warmup, tiled=False)
     kern = gateup_kernel(layers, dev, max(DECODE_MS), args.steps, args.warmup)
     log(f"gate_up kernel M={kern['M']}: {kern['us']:.1f} us, {kern['gbps']:.0f} GB/s")
     del layers
@@ -761,11 +764,18 @@ def main(argv=None):
                         "uniform routing (BASELINE configs[2]); prefill M=4096 Zipf(1.1) routing (configs[3])",
             "hidden": H, "experts": E, "top_k": TOPK, "intermediate": I, "group_size": G,
             "layers_rotated": args.layers, "timing": "HIP graph replay, HIP events",
+            "weights": "decode legs read load-time tiled copies of the experts (+1x expert HBM, "
+                       "Gemma4TextExperts4Bit.tile_weights / load_pack_quantized_backbone(tile=True)); "
+                       "decode_packed is the same sweep on the packed checkpoint layout",
         },
         "roofline": roofline(kern),
         "roofline_prefill": None if pre is None else _rounded(roofline_prefill(pre)),
         "decode": {str(M): {k: (round(v, 4) if isinstance(v, float) else v) for k, v in d.items()}
                    for M, d in dec.items()},
+        "decode_packed": {"value": round(sum(d["bytes"] for d in dec_packed.values()) /
+                                         (sum(d["us"] for d in dec_packed.values()) * 1e-6) / 1e9, 2),
+                          **{str(M): {k: (round(v, 4) if isinstance(v, float) else v) for k, v in d.items()}
+                             for M, d in dec_packed.items()}},
         "prefill": None if pre is None else {k: (round(v, 4) if isinstance(v, float) else v)
                                              for k, v in pre.items()},
         "latent": None if lat is None else {k: (round(v, 4) if isinstance(v, float) else v)

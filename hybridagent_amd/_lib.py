@@ -12,6 +12,10 @@ from __future__ import annotations
 
 import ctypes
 import os
+import threading
+import warnings
+import weakref
+from dataclasses import dataclass
 from pathlib import Path
 
 import torch
@@ -22,8 +26,23 @@ W4A16_OK = 0
 _STATUS_EXC = {1: ValueError, 2: ValueError, 3: ValueError, 4: ValueError, 5: ValueError,
                6: RuntimeError}
 
+# kinds of tiled weight copies (enum w4a16_tiled_kind)
+TILED_GATE_UP_DECODE, TILED_DOWN_DECODE, TILED_GATE_UP_PREFILL, TILED_DOWN_PREFILL = 0, 1, 2, 3
+
+
+class TiledExpertsC(ctypes.Structure):
+    """struct w4a16_tiled_experts: the tiled copies of one expert stack and its shape."""
+    _fields_ = [("E", ctypes.c_int64), ("H", ctypes.c_int64), ("I", ctypes.c_int64),
+                ("group_size", ctypes.c_int64),
+                ("gu_decode", ctypes.c_void_p), ("gu_decode_bytes", ctypes.c_size_t),
+                ("dn_decode", ctypes.c_void_p), ("dn_decode_bytes", ctypes.c_size_t),
+                ("gu_prefill", ctypes.c_void_p), ("gu_prefill_bytes", ctypes.c_size_t),
+                ("dn_prefill", ctypes.c_void_p), ("dn_prefill_bytes", ctypes.c_size_t)]
+
+
 # name -> (restype, argtypes); the exact set declared in include/w4a16moe.h
 _VP, _I64, _SZ, _F32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_size_t, ctypes.c_float
+_TP = ctypes.POINTER(TiledExpertsC)
 SIGNATURES = {
     "w4a16moe_version": (ctypes.c_int, []),
     "w4a16moe_status_string": (ctypes.c_char_p, [ctypes.c_int]),
@@ -59,24 +78,19 @@ SIGNATURES = {
                                              _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "moe_layer_forward": (ctypes.c_int, [_VP, _VP, _F32, _VP, _VP, _F32, _VP, _VP, _VP, _VP, _VP, _VP,
                                          _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
-    "w4a16_tiled_gate_up_bytes": (_SZ, [_I64, _I64, _I64]),
-    "w4a16_tile_gate_up": (ctypes.c_int, [_VP, _I64, _I64, _I64, _VP, _SZ, _VP]),
-    "w4a16_tiled_down_bytes": (_SZ, [_I64, _I64, _I64]),
-    "w4a16_tile_down": (ctypes.c_int, [_VP, _I64, _I64, _I64, _VP, _SZ, _VP]),
-    "w4a16_tiled_prefill_bytes": (_SZ, [ctypes.c_int, _I64, _I64, _I64]),
-    "w4a16_tile_prefill": (ctypes.c_int, [ctypes.c_int, _VP, _I64, _I64, _I64, _VP, _SZ, _VP]),
-    "moe_gate_up_tiled": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ,
-                                         _VP]),
-    "moe_forward_tiled": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64,
-                                         _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
-    "moe_down_tiled": (ctypes.c_int, [_VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
+    "w4a16_tiled_bytes": (_SZ, [ctypes.c_int, _I64, _I64, _I64, _I64]),
+    "w4a16_tile": (ctypes.c_int, [ctypes.c_int, _VP, _VP, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
+    "moe_gate_up_tiled": (ctypes.c_int, [_VP, _VP, _VP, _TP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
+    "moe_down_tiled": (ctypes.c_int, [_VP, _VP, _TP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
+    "moe_forward_tiled": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _TP, _VP, _I64, _I64, _I64, _I64, _I64,
+                                         _I64, _VP, _SZ, _VP]),
+    "moe_layer_forward_tiled": (ctypes.c_int, [_VP, _VP, _F32, _VP, _VP, _F32, _VP, _VP, _VP, _VP, _VP, _TP,
+                                               _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
     "moe_ffn_block_forward_tiled": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _F32, _VP, _VP,
-                                                   _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
-                                                   _F32, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _VP,
-                                                   _SZ, _VP]),
-    "moe_layer_forward_tiled": (ctypes.c_int, [_VP, _VP, _F32, _VP, _VP, _F32, _VP, _VP, _VP, _VP, _VP, _VP,
-                                               _VP, _VP, _VP, _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64,
-                                               _VP, _SZ, _VP]),
+                                                   _VP, _VP, _VP, _VP, _VP, _TP, _VP, _VP, _VP, _F32, _VP, _I64,
+                                                   _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
+    "moe_ffn_block_routing_offsets": (ctypes.c_int, [_I64, _I64, _I64, _I64, _I64, _I64,
+                                                     ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)]),
 }
 
 _lib = None
@@ -349,12 +363,10 @@ def sort_permute(top_k_index: torch.Tensor, num_experts: int):
 
 def moe_forward(hidden_states: torch.Tensor, top_k_index: torch.Tensor, top_k_weights: torch.Tensor,
                 gu_packed: torch.Tensor, gu_scale: torch.Tensor, dn_packed: torch.Tensor,
-                dn_scale: torch.Tensor, group_size: int | None = None, *, gu_tiled: torch.Tensor | None = None,
-                gu_ptiled: torch.Tensor | None = None, dn_tiled: torch.Tensor | None = None,
-                dn_ptiled: torch.Tensor | None = None) -> torch.Tensor:
-    """W4A16 MoE layer output [T, H] bf16  (quantization.py:88-129).  The tiled weight
-    copies (tile_gate_up, tile_down, tile_prefill; each optional) serve the kernels that
-    read them; the output is bit-identical."""
+                dn_scale: torch.Tensor, group_size: int | None = None, *, tiles="auto") -> torch.Tensor:
+    """W4A16 MoE layer output [T, H] bf16  (quantization.py:88-129).  ``tiles``: the
+    stack's tiled weight copies (a TiledWeights), None for none, or "auto" for the
+    ones registered for these tensors (register_tiles)."""
     dev = _require_gpu(hidden_states, top_k_index, top_k_weights, gu_packed, gu_scale, dn_packed, dn_scale)
     H = hidden_states.shape[-1]
     x = _bf16(hidden_states, "hidden_states").reshape(-1, H)
@@ -365,123 +377,204 @@ def moe_forward(hidden_states: torch.Tensor, top_k_index: torch.Tensor, top_k_we
     dn_packed = _i32(dn_packed, "down_packed")
     gu_scale = _bf16(gu_scale, "gate_up_scale")
     dn_scale = _bf16(dn_scale, "down_scale")
-    E, two_i, h8 = gu_packed.shape
-    I = two_i // 2
-    if h8 * 8 != H or dn_packed.shape != (E, H, I // 8) or two_i % 2:
-        raise ValueError(f"expert weight shapes {tuple(gu_packed.shape)} / {tuple(dn_packed.shape)} "
-                         f"do not match hidden size {H}")
-    G = group_size or infer_group_size(H, gu_scale.shape[-1])
-    if gu_scale.shape != (E, two_i, -(-H // G)) or dn_scale.shape != (E, H, -(-I // G)):
-        raise ValueError(f"scale shapes {tuple(gu_scale.shape)} / {tuple(dn_scale.shape)} "
-                         f"do not match group size {G}")
+    if gu_packed.shape[-1] * 8 != H:
+        raise ValueError(f"expert weight shape {tuple(gu_packed.shape)} does not match hidden size {H}")
+    E, H, I, G = _expert_shape(gu_packed, gu_scale, dn_packed, dn_scale, group_size)
     if w.shape != idx.shape:
         raise ValueError("top_k_weights and top_k_index shapes differ")
     M, k = idx.shape
     out = torch.empty((M, H), dtype=torch.bfloat16, device=dev)
     lib = load()
     ws = _workspace(lib.moe_workspace_bytes(max(M, 1), k, E, H, I), dev)
+    st = _resolve_tiles(tiles, gu_packed, gu_scale, dn_packed, dn_scale, E, H, I, G)
     with torch.cuda.device(dev):
-        if gu_tiled is None and gu_ptiled is None and dn_tiled is None and dn_ptiled is None:
+        if st is None:
             _check(lib.moe_forward(_ptr(x), _ptr(idx), _ptr(w), _ptr(gu_packed), _ptr(gu_scale), _ptr(dn_packed),
                                    _ptr(dn_scale), _ptr(out), M, k, E, H, I, G, _ptr(ws),
                                    0 if ws is None else ws.numel(), _stream(dev)),
                    "moe_forward")
         else:
-            gu_tiled = _tiled_arg(gu_tiled, "gate_up tiled copy", lib.w4a16_tiled_gate_up_bytes(E, H, I), dev)
-            gu_ptiled = _tiled_arg(gu_ptiled, "gate_up prefill tiled copy",
-                                   lib.w4a16_tiled_prefill_bytes(0, E, H, I), dev)
-            dn_tiled = _tiled_arg(dn_tiled, "down tiled copy", lib.w4a16_tiled_down_bytes(E, H, I), dev)
-            dn_ptiled = _tiled_arg(dn_ptiled, "down prefill tiled copy", lib.w4a16_tiled_prefill_bytes(1, E, H, I), dev)
-            _check(lib.moe_forward_tiled(_ptr(x), _ptr(idx), _ptr(w), _ptr(gu_packed), _ptr(gu_tiled),
-                                         _ptr(gu_ptiled), _ptr(gu_scale), _ptr(dn_packed), _ptr(dn_tiled),
-                                         _ptr(dn_ptiled), _ptr(dn_scale), _ptr(out), M, k, E, H, I, G, _ptr(ws),
-                                         0 if ws is None else ws.numel(), _stream(dev)),
+            _check(lib.moe_forward_tiled(_ptr(x), _ptr(idx), _ptr(w), _ptr(gu_packed), _ptr(gu_scale),
+                                         _ptr(dn_packed), _ptr(dn_scale), ctypes.byref(st), _ptr(out), M, k, E, H,
+                                         I, G, _ptr(ws), 0 if ws is None else ws.numel(), _stream(dev)),
                    "moe_forward_tiled")
     return out.reshape(*hidden_states.shape[:-1], H)
 
 
-def tile_gate_up(gu_packed: torch.Tensor) -> torch.Tensor | None:
-    """The tiled copy of gate_up_packed [E, 2I, H/8] that the decode gate_up streamer
-    reads contiguously (a load-time re-layout beside quantization.py:325-430; the
-    original stays as it is), or None where the streamer has no tiled form."""
-    dev = _require_gpu(gu_packed)
-    gu_packed = _i32(gu_packed, "gate_up_packed")
+@dataclass
+class TiledWeights:
+    """Load-time tiled copies of one expert stack's packed weights (a re-layout
+    beside quantization.py:325-430; the packed tensors stay as they are): the
+    decode streamers' copies (group size 128, 32 or 64; at 32 and 64 they hold
+    the group scales too) and the prefill GEMM's.  Any of them may be None:
+    that kernel then reads the packed tensors."""
+    E: int
+    H: int
+    I: int
+    group_size: int
+    gu_decode: torch.Tensor | None = None
+    dn_decode: torch.Tensor | None = None
+    gu_prefill: torch.Tensor | None = None
+    dn_prefill: torch.Tensor | None = None
+
+    def struct(self) -> TiledExpertsC:
+        """The w4a16_tiled_experts the *_tiled entry points take."""
+        nb = lambda t: 0 if t is None else t.numel() * t.element_size()
+        return TiledExpertsC(self.E, self.H, self.I, self.group_size,
+                             _ptr(self.gu_decode), nb(self.gu_decode), _ptr(self.dn_decode), nb(self.dn_decode),
+                             _ptr(self.gu_prefill), nb(self.gu_prefill), _ptr(self.dn_prefill), nb(self.dn_prefill))
+
+    def nbytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in (self.gu_decode, self.dn_decode, self.gu_prefill,
+                                                          self.dn_prefill) if t is not None)
+
+
+def tiled_bytes(kind: int, E: int, H: int, I: int, group_size: int) -> int:
+    """Bytes of a tiled copy of ``kind`` (TILED_*) for the shape, 0 where none exists."""
+    return load().w4a16_tiled_bytes(kind, E, H, I, group_size)
+
+
+def _tile(kind: int, packed: torch.Tensor, scale: torch.Tensor | None, E: int, H: int, I: int, G: int):
+    nbytes = tiled_bytes(kind, E, H, I, G)
+    if nbytes == 0:
+        return None
+    dev = packed.device
+    tiled = torch.empty(nbytes // 4, dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        _check(load().w4a16_tile(kind, _ptr(packed), _ptr(scale), E, H, I, G, _ptr(tiled), nbytes, _stream(dev)),
+               "w4a16_tile")
+    return tiled
+
+
+def _expert_shape(gu_packed, gu_scale, dn_packed, dn_scale, group_size):
     E, two_i, h8 = gu_packed.shape
-    lib = load()
-    nbytes = lib.w4a16_tiled_gate_up_bytes(E, h8 * 8, two_i // 2)
-    if nbytes == 0:
+    H, I = h8 * 8, two_i // 2
+    if dn_packed.shape != (E, H, I // 8) or two_i % 2:
+        raise ValueError(f"expert weight shapes {tuple(gu_packed.shape)} / {tuple(dn_packed.shape)} do not match")
+    G = group_size or infer_group_size(H, gu_scale.shape[-1])
+    if gu_scale.shape != (E, two_i, -(-H // G)) or dn_scale.shape != (E, H, -(-I // G)):
+        raise ValueError(f"scale shapes {tuple(gu_scale.shape)} / {tuple(dn_scale.shape)} "
+                         f"do not match group size {G}")
+    return E, H, I, G
+
+
+def tile_experts(gu_packed: torch.Tensor, gu_scale: torch.Tensor, dn_packed: torch.Tensor,
+                 dn_scale: torch.Tensor, group_size: int | None = None, decode: bool = True,
+                 prefill: bool = True) -> TiledWeights:
+    """The tiled copies of an expert stack (gate_up_packed [E, 2I, H/8], down_packed
+    [E, H, I/8] and their scales): ``decode`` the decode streamers' (where they have
+    a tiled form for the group size), ``prefill`` the prefill GEMM's.  About one more
+    copy of the expert weights per kind asked for."""
+    dev = _require_gpu(gu_packed, gu_scale, dn_packed, dn_scale)
+    gu_packed, dn_packed = _i32(gu_packed, "gate_up_packed"), _i32(dn_packed, "down_packed")
+    gu_scale, dn_scale = _bf16(gu_scale, "gate_up_scale"), _bf16(dn_scale, "down_scale")
+    E, H, I, G = _expert_shape(gu_packed, gu_scale, dn_packed, dn_scale, group_size)
+    tw = TiledWeights(E, H, I, G)
+    if decode:
+        tw.gu_decode = _tile(TILED_GATE_UP_DECODE, gu_packed, gu_scale, E, H, I, G)
+        tw.dn_decode = _tile(TILED_DOWN_DECODE, dn_packed, dn_scale, E, H, I, G)
+    if prefill:
+        tw.gu_prefill = _tile(TILED_GATE_UP_PREFILL, gu_packed, None, E, H, I, G)
+        tw.dn_prefill = _tile(TILED_DOWN_PREFILL, dn_packed, None, E, H, I, G)
+    del dev
+    return tw
+
+
+# ------------------------------------------------------------ tiled-copy registry
+# The reference's entry points pass only the packed tensors (the 7 arguments of
+# fused_triton_4bit_moe_forward / hybrid_agent::fused_4bit_moe, quantization.py:88-96,
+# backends.py:48-60, and the 22 of _ffn_moe_4bit_step).  Copies registered for a
+# stack are found from those tensors: keyed by the packed gate_up buffer's address,
+# valid while all four tensors are the ones tiled (same addresses, shapes and
+# version counters -- an in-place reload through copy_ / load_state_dict bumps the
+# counter).  A stale entry is dropped and the call reads the packed tensors.
+_REGISTRY: dict[int, tuple] = {}
+_REGISTRY_LOCK = threading.Lock()
+
+
+def _version_of(t: torch.Tensor):
+    # inference-mode tensors keep no version counter (and cannot be changed in
+    # place outside inference mode)
+    try:
+        return t._version
+    except RuntimeError:
         return None
-    tiled = torch.empty(nbytes // 4, dtype=torch.int32, device=dev)
-    with torch.cuda.device(dev):
-        _check(lib.w4a16_tile_gate_up(_ptr(gu_packed), E, h8 * 8, two_i // 2, _ptr(tiled), nbytes, _stream(dev)),
-               "w4a16_tile_gate_up")
-    return tiled
 
 
-def tile_down(dn_packed: torch.Tensor) -> torch.Tensor | None:
-    """The tiled copy of down_packed [E, H, I/8] that the decode down streamer reads
-    contiguously (a load-time re-layout beside quantization.py:325-430; the original
-    stays as it is), or None where the streamer has no tiled form."""
-    dev = _require_gpu(dn_packed)
-    dn_packed = _i32(dn_packed, "down_packed")
-    E, H, i8 = dn_packed.shape
-    lib = load()
-    nbytes = lib.w4a16_tiled_down_bytes(E, H, i8 * 8)
-    if nbytes == 0:
+def _signature(*ts: torch.Tensor) -> tuple:
+    return tuple((t.data_ptr(), tuple(t.shape), _version_of(t)) for t in ts)
+
+
+def register_tiles(gu_packed: torch.Tensor, gu_scale: torch.Tensor, dn_packed: torch.Tensor,
+                   dn_scale: torch.Tensor, tiles: TiledWeights) -> None:
+    """Make ``tiles`` the copies every forward finds for this expert stack."""
+    key = gu_packed.data_ptr()
+    entry = (_signature(gu_packed, gu_scale, dn_packed, dn_scale), tiles)
+    with _REGISTRY_LOCK:
+        _REGISTRY[key] = entry
+    # the entry goes when the packed tensor does (its address may be reused)
+    weakref.finalize(gu_packed, _drop_if_same, key, entry)
+
+
+def _drop_if_same(key: int, entry) -> None:
+    with _REGISTRY_LOCK:
+        if _REGISTRY.get(key) is entry:
+            del _REGISTRY[key]
+
+
+def unregister_tiles(gu_packed: torch.Tensor) -> None:
+    with _REGISTRY_LOCK:
+        _REGISTRY.pop(gu_packed.data_ptr(), None)
+
+
+def lookup_tiles(gu_packed: torch.Tensor, gu_scale: torch.Tensor, dn_packed: torch.Tensor,
+                 dn_scale: torch.Tensor) -> TiledWeights | None:
+    """The registered copies of this expert stack, or None (none, or stale: then dropped)."""
+    if not _REGISTRY:
         return None
-    tiled = torch.empty(nbytes // 4, dtype=torch.int32, device=dev)
-    with torch.cuda.device(dev):
-        _check(lib.w4a16_tile_down(_ptr(dn_packed), E, H, i8 * 8, _ptr(tiled), nbytes, _stream(dev)),
-               "w4a16_tile_down")
-    return tiled
+    key = gu_packed.data_ptr()
+    with _REGISTRY_LOCK:
+        entry = _REGISTRY.get(key)
+        if entry is None:
+            return None
+        if entry[0] != _signature(gu_packed, gu_scale, dn_packed, dn_scale):
+            del _REGISTRY[key]
+            stale = True
+        else:
+            return entry[1]
+    if stale:
+        warnings.warn("the tiled copies of an expert stack were dropped: its weights changed after they were "
+                      "made (tile them again to use them); this call reads the packed weights", RuntimeWarning,
+                      stacklevel=3)
+    return None
 
 
-def tile_prefill(packed: torch.Tensor, which: str) -> torch.Tensor | None:
-    """The exact-form prefill GEMM's tiled copy of gate_up_packed [E, 2I, H/8]
-    (``which="gate_up"``) or down_packed [E, H, I/8] (``which="down"``): each item's
-    k stage one contiguous 8 KiB block (a load-time re-layout beside
-    quantization.py:325-430; the original stays as it is), or None where that
-    kernel does not serve the shape."""
-    dev = _require_gpu(packed)
-    packed = _i32(packed, f"{which}_packed")
-    E, n, k8 = packed.shape
-    if which == "gate_up":
-        w, H, I = 0, k8 * 8, n // 2
-    elif which == "down":
-        w, H, I = 1, n, k8 * 8
-    else:
-        raise ValueError("which must be 'gate_up' or 'down'")
-    lib = load()
-    nbytes = lib.w4a16_tiled_prefill_bytes(w, E, H, I)
-    if nbytes == 0:
+def _resolve_tiles(tiles, gu_packed, gu_scale, dn_packed, dn_scale, E, H, I, G):
+    """``tiles`` "auto": the registry's (if made for this call's shape and group
+    size); None: none; else the given TiledWeights, which must be for this shape
+    (the C ABI checks it again)."""
+    if isinstance(tiles, str):
+        if tiles != "auto":
+            raise ValueError("tiles must be 'auto', None or a TiledWeights")
+        tiles = lookup_tiles(gu_packed, gu_scale, dn_packed, dn_scale)
+        if tiles is not None and (tiles.E, tiles.H, tiles.I, tiles.group_size) != (E, H, I, G):
+            tiles = None
+    if tiles is None:
         return None
-    tiled = torch.empty(nbytes // 4, dtype=torch.int32, device=dev)
-    with torch.cuda.device(dev):
-        _check(lib.w4a16_tile_prefill(w, _ptr(packed), E, H, I, _ptr(tiled), nbytes, _stream(dev)),
-               "w4a16_tile_prefill")
-    return tiled
-
-
-def _tiled_arg(t: torch.Tensor | None, name: str, nbytes: int, dev) -> torch.Tensor | None:
-    if t is None:
-        return None
-    t = _i32(t, name)
-    if t.device != dev or t.numel() * 4 < nbytes:
-        raise ValueError(f"{name} does not match the expert weights")
-    return t
+    if (tiles.E, tiles.H, tiles.I, tiles.group_size) != (E, H, I, G):
+        raise ValueError(f"tiled copies are for (E, H, I, G) = {(tiles.E, tiles.H, tiles.I, tiles.group_size)}, "
+                         f"the call is {(E, H, I, G)}")
+    return tiles.struct()
 
 
 def moe_layer_forward(router_in: torch.Tensor, router_scale: torch.Tensor, scalar_root: float,
                       proj_w: torch.Tensor, per_expert_scale: torch.Tensor, eps: float, top_k: int,
                       hidden_states: torch.Tensor, gu_packed: torch.Tensor, gu_scale: torch.Tensor,
                       dn_packed: torch.Tensor, dn_scale: torch.Tensor, group_size: int | None = None,
-                      gu_tiled: torch.Tensor | None = None, gu_ptiled: torch.Tensor | None = None,
-                      dn_tiled: torch.Tensor | None = None, dn_ptiled: torch.Tensor | None = None):
+                      *, tiles="auto"):
     """Router (backends.py:111-117) on ``router_in`` + experts (quantization.py:88-129) on
     ``hidden_states`` in one call -> (out [T, H] bf16, top_k_weights fp32, top_k_index int64).
-    ``gu_tiled`` / ``dn_tiled`` (from tile_gate_up / tile_down) and ``gu_ptiled`` /
-    ``dn_ptiled`` (from tile_prefill) let the decode streamers and the prefill GEMMs read
-    contiguous tiles; the output is bit-identical."""
+    ``tiles`` as for moe_forward."""
     dev = _require_gpu(router_in, router_scale, proj_w, per_expert_scale, hidden_states, gu_packed,
                        gu_scale, dn_packed, dn_scale)
     H = hidden_states.shape[-1]
@@ -494,40 +587,27 @@ def moe_layer_forward(router_in: torch.Tensor, router_scale: torch.Tensor, scala
     per_expert_scale = _bf16(per_expert_scale, "per_expert_scale")
     gu_packed, dn_packed = _i32(gu_packed, "gate_up_packed"), _i32(dn_packed, "down_packed")
     gu_scale, dn_scale = _bf16(gu_scale, "gate_up_scale"), _bf16(dn_scale, "down_scale")
-    E, two_i, h8 = gu_packed.shape
-    I = two_i // 2
-    if h8 * 8 != H or dn_packed.shape != (E, H, I // 8) or proj_w.shape != (E, H):
-        raise ValueError("router / expert weight shapes do not match the hidden size")
-    G = group_size or infer_group_size(H, gu_scale.shape[-1])
-    if gu_scale.shape != (E, two_i, -(-H // G)) or dn_scale.shape != (E, H, -(-I // G)):
-        raise ValueError(f"scale shapes do not match group size {G}")
+    if gu_packed.shape[-1] * 8 != H:
+        raise ValueError("expert weight shapes do not match the hidden size")
+    E, H, I, G = _expert_shape(gu_packed, gu_scale, dn_packed, dn_scale, group_size)
+    if proj_w.shape != (E, H):
+        raise ValueError("router weight shape does not match the experts")
     M = x.shape[0]
     out = torch.empty((M, H), dtype=torch.bfloat16, device=dev)
     idx = torch.empty((M, top_k), dtype=torch.int64, device=dev)
     w = torch.empty((M, top_k), dtype=torch.float32, device=dev)
     lib = load()
     ws = _workspace(lib.moe_layer_workspace_bytes(max(M, 1), top_k, E, H, I), dev)
+    st = _resolve_tiles(tiles, gu_packed, gu_scale, dn_packed, dn_scale, E, H, I, G)
+    common = (_ptr(r2), _ptr(router_scale), float(scalar_root), _ptr(proj_w), _ptr(per_expert_scale), float(eps),
+              _ptr(x), _ptr(gu_packed), _ptr(gu_scale), _ptr(dn_packed), _ptr(dn_scale))
+    tail = (_ptr(out), _ptr(idx), _ptr(w), M, top_k, E, H, I, G, _ptr(ws), 0 if ws is None else ws.numel(),
+            _stream(dev))
     with torch.cuda.device(dev):
-        if gu_tiled is None and gu_ptiled is None and dn_tiled is None and dn_ptiled is None:
-            _check(lib.moe_layer_forward(_ptr(r2), _ptr(router_scale), float(scalar_root), _ptr(proj_w),
-                                         _ptr(per_expert_scale), float(eps), _ptr(x), _ptr(gu_packed),
-                                         _ptr(gu_scale), _ptr(dn_packed), _ptr(dn_scale), _ptr(out), _ptr(idx),
-                                         _ptr(w), M, top_k, E, H, I, G, _ptr(ws),
-                                         0 if ws is None else ws.numel(), _stream(dev)),
-                   "moe_layer_forward")
+        if st is None:
+            _check(lib.moe_layer_forward(*common, *tail), "moe_layer_forward")
         else:
-            gu_tiled = _tiled_arg(gu_tiled, "gate_up tiled copy", lib.w4a16_tiled_gate_up_bytes(E, H, I), dev)
-            gu_ptiled = _tiled_arg(gu_ptiled, "gate_up prefill tiled copy",
-                                   lib.w4a16_tiled_prefill_bytes(0, E, H, I), dev)
-            dn_tiled = _tiled_arg(dn_tiled, "down tiled copy", lib.w4a16_tiled_down_bytes(E, H, I), dev)
-            dn_ptiled = _tiled_arg(dn_ptiled, "down prefill tiled copy", lib.w4a16_tiled_prefill_bytes(1, E, H, I), dev)
-            _check(lib.moe_layer_forward_tiled(_ptr(r2), _ptr(router_scale), float(scalar_root), _ptr(proj_w),
-                                               _ptr(per_expert_scale), float(eps), _ptr(x), _ptr(gu_packed),
-                                               _ptr(gu_tiled), _ptr(gu_ptiled), _ptr(gu_scale), _ptr(dn_packed),
-                                               _ptr(dn_tiled), _ptr(dn_ptiled), _ptr(dn_scale),
-                                               _ptr(out), _ptr(idx), _ptr(w), M, top_k, E, H, I, G, _ptr(ws),
-                                               0 if ws is None else ws.numel(), _stream(dev)),
-                   "moe_layer_forward_tiled")
+            _check(lib.moe_layer_forward_tiled(*common, ctypes.byref(st), *tail), "moe_layer_forward_tiled")
     return out.reshape(*hidden_states.shape[:-1], H), w, idx
 
 
@@ -566,13 +646,11 @@ def ffn_block(residual: torch.Tensor, attn_out: torch.Tensor, post_attn_ln_w: to
               pre_ff_ln2_w: torch.Tensor, gu_packed: torch.Tensor, gu_scale: torch.Tensor,
               dn_packed: torch.Tensor, dn_scale: torch.Tensor, post_ff_ln2_w: torch.Tensor,
               post_ff_ln_w: torch.Tensor, layer_scalar: torch.Tensor, eps: float, top_k: int,
-              group_size: int | None = None, *, gu_tiled: torch.Tensor | None = None,
-              gu_ptiled: torch.Tensor | None = None, dn_tiled: torch.Tensor | None = None,
-              dn_ptiled: torch.Tensor | None = None) -> torch.Tensor:
+              group_size: int | None = None, *, tiles="auto", return_routing: bool = False):
     """The post-attention FFN block ``_ffn_moe_4bit_step`` (backends.py:77-126), same
     arguments in the same order: residual / attn_out [..., H] bf16 -> [..., H] bf16.
-    The experts' tiled weight copies (tile_gate_up, tile_down, tile_prefill; each
-    optional) serve the kernels that read them, with bit-identical output."""
+    ``tiles`` as for moe_forward.  With ``return_routing`` also the routing the block's
+    router step took: (out, top_k_index int64 [M, k], top_k_weights fp32 [M, k])."""
     dense = (post_attn_ln_w, pre_ff_ln_w, mlp_gate_w, mlp_up_w, mlp_down_w, post_ff_ln1_w, router_scale,
              router_proj_w, router_per_expert_scale, pre_ff_ln2_w, post_ff_ln2_w, post_ff_ln_w)
     dev = _require_gpu(residual, attn_out, *dense, gu_packed, gu_scale, dn_packed, dn_scale, layer_scalar)
@@ -601,41 +679,40 @@ def ffn_block(residual: torch.Tensor, attn_out: torch.Tensor, post_attn_ln_w: to
         raise ValueError("shared MLP weights must be gate/up [Im, H] and down [H, Im]")
     gu_packed, dn_packed = _i32(gu_packed, "gate_up_packed"), _i32(dn_packed, "down_packed")
     gu_scale, dn_scale = _bf16(gu_scale, "gate_up_scale"), _bf16(dn_scale, "down_scale")
-    E, two_i, h8 = gu_packed.shape
-    I = two_i // 2
-    if h8 * 8 != H or dn_packed.shape != (E, H, I // 8) or router_proj_w.shape != (E, H):
-        raise ValueError("router / expert weight shapes do not match the hidden size")
-    G = group_size or infer_group_size(H, gu_scale.shape[-1])
-    if gu_scale.shape != (E, two_i, -(-H // G)) or dn_scale.shape != (E, H, -(-I // G)):
-        raise ValueError(f"scale shapes do not match group size {G}")
+    if gu_packed.shape[-1] * 8 != H:
+        raise ValueError("expert weight shapes do not match the hidden size")
+    E, H, I, G = _expert_shape(gu_packed, gu_scale, dn_packed, dn_scale, group_size)
+    if router_proj_w.shape != (E, H):
+        raise ValueError("router weight shape does not match the experts")
     M = res.shape[0]
     out = torch.empty((M, H), dtype=torch.bfloat16, device=dev)
     lib = load()
     ws = _workspace(lib.moe_ffn_block_workspace_bytes(max(M, 1), top_k, E, H, I, Im), dev)
+    st = _resolve_tiles(tiles, gu_packed, gu_scale, dn_packed, dn_scale, E, H, I, G)
+    head = (_ptr(res), _ptr(att), _ptr(post_attn_ln_w), _ptr(pre_ff_ln_w), _ptr(mlp_gate_w), _ptr(mlp_up_w),
+            _ptr(mlp_down_w), _ptr(post_ff_ln1_w), _ptr(router_scale), float(router_scalar_root),
+            _ptr(router_proj_w), _ptr(router_per_expert_scale), _ptr(pre_ff_ln2_w), _ptr(gu_packed),
+            _ptr(gu_scale), _ptr(dn_packed), _ptr(dn_scale))
+    tail = (_ptr(post_ff_ln2_w), _ptr(post_ff_ln_w), _ptr(ls), float(eps), _ptr(out), M, int(top_k), E, H, I, Im,
+            G, _ptr(ws), 0 if ws is None else ws.numel(), _stream(dev))
     with torch.cuda.device(dev):
-        if gu_tiled is None and gu_ptiled is None and dn_tiled is None and dn_ptiled is None:
-            _check(lib.moe_ffn_block_forward(
-                _ptr(res), _ptr(att), _ptr(post_attn_ln_w), _ptr(pre_ff_ln_w), _ptr(mlp_gate_w), _ptr(mlp_up_w),
-                _ptr(mlp_down_w), _ptr(post_ff_ln1_w), _ptr(router_scale), float(router_scalar_root),
-                _ptr(router_proj_w), _ptr(router_per_expert_scale), _ptr(pre_ff_ln2_w), _ptr(gu_packed),
-                _ptr(gu_scale), _ptr(dn_packed), _ptr(dn_scale), _ptr(post_ff_ln2_w), _ptr(post_ff_ln_w), _ptr(ls),
-                float(eps), _ptr(out), M, int(top_k), E, H, I, Im, G, _ptr(ws), 0 if ws is None else ws.numel(),
-                _stream(dev)), "moe_ffn_block_forward")
+        if st is None:
+            _check(lib.moe_ffn_block_forward(*head, *tail), "moe_ffn_block_forward")
         else:
-            gu_tiled = _tiled_arg(gu_tiled, "gate_up tiled copy", lib.w4a16_tiled_gate_up_bytes(E, H, I), dev)
-            gu_ptiled = _tiled_arg(gu_ptiled, "gate_up prefill tiled copy",
-                                   lib.w4a16_tiled_prefill_bytes(0, E, H, I), dev)
-            dn_tiled = _tiled_arg(dn_tiled, "down tiled copy", lib.w4a16_tiled_down_bytes(E, H, I), dev)
-            dn_ptiled = _tiled_arg(dn_ptiled, "down prefill tiled copy", lib.w4a16_tiled_prefill_bytes(1, E, H, I), dev)
-            _check(lib.moe_ffn_block_forward_tiled(
-                _ptr(res), _ptr(att), _ptr(post_attn_ln_w), _ptr(pre_ff_ln_w), _ptr(mlp_gate_w), _ptr(mlp_up_w),
-                _ptr(mlp_down_w), _ptr(post_ff_ln1_w), _ptr(router_scale), float(router_scalar_root),
-                _ptr(router_proj_w), _ptr(router_per_expert_scale), _ptr(pre_ff_ln2_w), _ptr(gu_packed),
-                _ptr(gu_tiled), _ptr(gu_ptiled), _ptr(gu_scale), _ptr(dn_packed), _ptr(dn_tiled), _ptr(dn_ptiled),
-                _ptr(dn_scale), _ptr(post_ff_ln2_w), _ptr(post_ff_ln_w), _ptr(ls), float(eps), _ptr(out), M,
-                int(top_k), E, H, I, Im, G, _ptr(ws), 0 if ws is None else ws.numel(), _stream(dev)),
-                "moe_ffn_block_forward_tiled")
-    return out.reshape(residual.shape)
+            _check(lib.moe_ffn_block_forward_tiled(*head, ctypes.byref(st), *tail), "moe_ffn_block_forward_tiled")
+    out = out.reshape(residual.shape)
+    if not return_routing:
+        return out
+    if M == 0:
+        return out, torch.empty((0, top_k), dtype=torch.int64, device=dev), \
+            torch.empty((0, top_k), dtype=torch.float32, device=dev)
+    io, wo = ctypes.c_size_t(), ctypes.c_size_t()
+    _check(lib.moe_ffn_block_routing_offsets(M, top_k, E, H, I, Im, ctypes.byref(io), ctypes.byref(wo)),
+           "moe_ffn_block_routing_offsets")
+    n = M * top_k
+    idx = ws[io.value:io.value + 8 * n].view(torch.int64).reshape(M, top_k).clone()
+    w = ws[wo.value:wo.value + 4 * n].view(torch.float32).reshape(M, top_k).clone()
+    return out, idx, w
 
 
 class MoEStages:
@@ -664,26 +741,29 @@ class MoEStages:
                                  self.ws.numel(), s), "moe_plan")
 
     def gate_up(self, hidden: torch.Tensor, gu_packed: torch.Tensor, gu_scale: torch.Tensor,
-                gu_tiled: torch.Tensor | None = None, gu_ptiled: torch.Tensor | None = None) -> None:
+                tiles: TiledWeights | None = None) -> None:
+        """Grouped gate_up GEMM; ``tiles`` (the stack's TiledWeights) serve the kernels
+        that read them."""
         s = _stream(self.device)
-        if gu_tiled is None and gu_ptiled is None:
+        if tiles is None:
             _check(self.lib.moe_gate_up(_ptr(hidden), _ptr(gu_packed), _ptr(gu_scale), *self._dims(), self.G,
                                         _ptr(self.ws), self.ws.numel(), s), "moe_gate_up")
         else:
-            _check(self.lib.moe_gate_up_tiled(_ptr(hidden), _ptr(gu_packed), _ptr(gu_tiled), _ptr(gu_ptiled),
-                                              _ptr(gu_scale), *self._dims(), self.G, _ptr(self.ws),
-                                              self.ws.numel(), s), "moe_gate_up_tiled")
+            st = tiles.struct()
+            _check(self.lib.moe_gate_up_tiled(_ptr(hidden), _ptr(gu_packed), _ptr(gu_scale), ctypes.byref(st),
+                                              *self._dims(), self.G, _ptr(self.ws), self.ws.numel(), s),
+                   "moe_gate_up_tiled")
 
-    def down(self, dn_packed: torch.Tensor, dn_scale: torch.Tensor, dn_ptiled: torch.Tensor | None = None,
-             dn_tiled: torch.Tensor | None = None) -> None:
+    def down(self, dn_packed: torch.Tensor, dn_scale: torch.Tensor, tiles: TiledWeights | None = None) -> None:
+        """Grouped down GEMM; ``tiles`` serve the kernels that read them."""
         s = _stream(self.device)
-        if dn_ptiled is not None or dn_tiled is not None:
-            _check(self.lib.moe_down_tiled(_ptr(dn_packed), _ptr(dn_tiled), _ptr(dn_ptiled), _ptr(dn_scale),
-                                           *self._dims(), self.G, _ptr(self.ws), self.ws.numel(), s),
-                   "moe_down_tiled")
-            return
-        _check(self.lib.moe_down(_ptr(dn_packed), _ptr(dn_scale), *self._dims(), self.G, _ptr(self.ws),
-                                 self.ws.numel(), s), "moe_down")
+        if tiles is None:
+            _check(self.lib.moe_down(_ptr(dn_packed), _ptr(dn_scale), *self._dims(), self.G, _ptr(self.ws),
+                                     self.ws.numel(), s), "moe_down")
+        else:
+            st = tiles.struct()
+            _check(self.lib.moe_down_tiled(_ptr(dn_packed), _ptr(dn_scale), ctypes.byref(st), *self._dims(),
+                                           self.G, _ptr(self.ws), self.ws.numel(), s), "moe_down_tiled")
 
     def combine(self, top_k_index: torch.Tensor, top_k_weights: torch.Tensor) -> torch.Tensor:
         s = _stream(self.device)

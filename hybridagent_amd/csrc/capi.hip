@@ -89,20 +89,8 @@ struct MoeLayout {
   int32_t* blockcnt;
   uint16_t* inter;
   uint16_t* dn;
-  // bias-form prefill: hidden rows in bias order, their 128-wide k tile
-  // sums, and the intermediate rows' 128-column block sums
-  uint16_t* xb;
-  float* crx;
-  float* crs;
-  float* crh;
   size_t bytes;
 };
-
-// row strides of the bias-form prefill operands: whole 128-wide k tiles
-// plus 64 elements, so consecutive rows start an odd number of 128-byte
-// lines apart
-inline int64_t hidden_ld(int64_t H) { return (H + 127) / 128 * 128 + 64; }
-inline int64_t inter_ld(int64_t I) { return (I + 127) / 128 * 128 + 64; }
 
 MoeLayout moe_layout(void* ws, int64_t M, int64_t k, int64_t E, int64_t H, int64_t I) {
   Carve c(ws);
@@ -114,14 +102,65 @@ MoeLayout moe_layout(void* ws, int64_t M, int64_t k, int64_t E, int64_t H, int64
   L.sorted_pos = c.take<int32_t>(M * k);
   L.tiles = c.take<int32_t>(M * k / kPrefillBM + E + 1);
   L.blockcnt = c.take<int32_t>(size_t(sort_blocks(M * k)) * E);
-  L.inter = c.take<uint16_t>(M * k * std::max<int64_t>(I, inter_ld(I)));
+  L.inter = c.take<uint16_t>(M * k * I);
   L.dn = c.take<uint16_t>(M * k * H);
-  L.xb = c.take<uint16_t>(M * hidden_ld(H));
-  L.crx = c.take<float>(M * ((H + 127) / 128));
-  L.crs = c.take<float>(M * k * ((H + 127) / 128));
-  L.crh = c.take<float>(M * k * ((I + 127) / 128));
   L.bytes = c.used;
   return L;
+}
+
+// The tiled weight copies one call reads (NULL: that kernel reads the packed
+// tensors), resolved from the caller's w4a16_tiled_experts.
+struct Tiles {
+  const int32_t* gu_decode = nullptr;
+  const int32_t* dn_decode = nullptr;
+  const int32_t* gu_prefill = nullptr;
+  const int32_t* dn_prefill = nullptr;
+};
+
+// bytes of a tiled copy of `kind` for the shape, 0 where the kernel that
+// would read it has no tiled form there
+size_t tiled_need(int kind, int64_t E, int64_t H, int64_t I, int64_t G) {
+  if (E <= 0 || E > kMaxExperts || H <= 0 || I <= 0 || H % 32 != 0 || I % 32 != 0 || !valid_group(G))
+    return 0;
+  switch (kind) {
+    case W4A16_TILED_GATE_UP_DECODE:
+      return (size_t)E * tiled_decode_bytes_per_expert(kModeGateUp, H, I, G);
+    case W4A16_TILED_DOWN_DECODE:
+      return (size_t)E * tiled_decode_bytes_per_expert(kModeDown, H, I, G);
+    case W4A16_TILED_GATE_UP_PREFILL:
+      return (size_t)E * prefill_tiled_bytes_per_expert(kModeGateUp, H, I);
+    case W4A16_TILED_DOWN_PREFILL:
+      return (size_t)E * prefill_tiled_bytes_per_expert(kModeDown, H, I);
+    default:
+      return 0;
+  }
+}
+
+// Checks the copies against the call's shape: the tag must name the same
+// expert stack (E, H, I, group size), each copy given must exist for that
+// shape and hold its full size, 16-byte aligned.
+int resolve_tiles(const w4a16_tiled_experts* t, int64_t E, int64_t H, int64_t I, int64_t G, Tiles* out) {
+  *out = Tiles{};
+  if (t == nullptr) return W4A16_OK;
+  if (t->E != E || t->H != H || t->I != I || t->group_size != G) return W4A16_ERR_SHAPE;
+  const struct {
+    const int32_t* p;
+    size_t bytes;
+    int kind;
+    const int32_t** dst;
+  } copies[4] = {{t->gu_decode, t->gu_decode_bytes, W4A16_TILED_GATE_UP_DECODE, &out->gu_decode},
+                 {t->dn_decode, t->dn_decode_bytes, W4A16_TILED_DOWN_DECODE, &out->dn_decode},
+                 {t->gu_prefill, t->gu_prefill_bytes, W4A16_TILED_GATE_UP_PREFILL, &out->gu_prefill},
+                 {t->dn_prefill, t->dn_prefill_bytes, W4A16_TILED_DOWN_PREFILL, &out->dn_prefill}};
+  for (const auto& c : copies) {
+    if (c.p == nullptr) continue;
+    const size_t need = tiled_need(c.kind, E, H, I, G);
+    if (need == 0) return W4A16_ERR_SHAPE;
+    if (c.bytes < need) return W4A16_ERR_WORKSPACE;
+    if (!aligned16(c.p)) return W4A16_ERR_ALIGN;
+    *c.dst = c.p;
+  }
+  return W4A16_OK;
 }
 
 }  // namespace
@@ -223,7 +262,7 @@ int w4a16_linear(const uint16_t* x, const int32_t* w_packed, const uint16_t* w_s
   (void)workspace_bytes;
   if (K > kMaxStreamK) return W4A16_ERR_SHAPE;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool bias_form = group_size % 128 == 0;
+  const bool bias_form = kDecodeBiasForm && group_size % 128 == 0;
   DecodeArgs a{};
   a.act = x;
   a.wp = w_packed;
@@ -349,7 +388,8 @@ inline bool use_prefill(int64_t M, int64_t H, int64_t I) {
 }
 
 // the exact-form prefill GEMM serves group sizes that are powers of two
-// >= 32; the bias form and the older exact kernel the rest
+// >= 32 with an even group count per row; the fallback exact-form kernel the
+// rest (odd group counts, H or I below three 64-wide stages)
 inline bool x_prefill(int64_t M, int64_t H, int64_t I, int64_t G) {
   return use_prefill(M, H, I) && prefill_x_supported(H, I, G);
 }
@@ -357,12 +397,6 @@ inline bool x_prefill(int64_t M, int64_t H, int64_t I, int64_t G) {
 // m-tile of the prefill tile list the expert sort writes
 inline int plan_bm(int64_t M, int64_t H, int64_t I, int64_t G) {
   return x_prefill(M, H, I, G) ? kPrefillXBM : kPrefillBM;
-}
-
-// gate_up and down take the same form (the intermediate layout differs)
-inline bool bias_prefill(int64_t H, int64_t I, int64_t G) {
-  return G % 128 == 0 && prefill_bias_supported((int)((H + G - 1) / G)) &&
-         prefill_bias_supported((int)((I + G - 1) / G));
 }
 
 PrefillArgs prefill_args(const MoeLayout& L, int64_t M, int64_t top_k, int64_t I, int64_t G) {
@@ -400,7 +434,8 @@ DecodeArgs expert_args(const MoeLayout& L, int64_t M, int64_t top_k, int64_t I, 
   a.G = (int)G;
   a.I = (int)I;
   a.M = (int)M;
-  // an expert gets each token at most once: at most M rows
+  // rows staged per pass: an expert usually holds at most M rows (one per
+  // token); a token that routes several slots to one expert adds passes
   a.rows_hint = (int)(M < 16 ? M : 16);
   return a;
 }
@@ -431,11 +466,11 @@ int moe_plan(const uint16_t* hidden, const int64_t* topk_idx, int64_t M, int64_t
 }  // extern "C"
 
 namespace {
-// gate_up on either weight layout: gu_tiled (the tiled copy, nullable) serves
-// the decode streamer where it applies, gu_packed everything else
-int gate_up_impl(const uint16_t* hidden, const int32_t* gu_packed, const uint16_t* gu_scale,
-                 const int32_t* gu_tiled, const int32_t* gu_ptiled, int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I,
-                 int64_t group_size, void* workspace, size_t workspace_bytes, void* stream) {
+// gate_up on either weight layout: the tiled copies in t (checked by
+// resolve_tiles) serve the kernels that read them, gu_packed everything else
+int gate_up_impl(const uint16_t* hidden, const int32_t* gu_packed, const uint16_t* gu_scale, const Tiles& t,
+                 int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
+                 size_t workspace_bytes, void* stream) {
   MoeLayout L{};
   int st = moe_check(M, top_k, E, H, I, group_size, workspace, workspace_bytes, &L);
   if (st != W4A16_OK || M == 0) return st;
@@ -459,10 +494,7 @@ int gate_up_impl(const uint16_t* hidden, const int32_t* gu_packed, const uint16_
     p.rows_total = (int)(M * top_k);
     p.n_nt = (int)((I + 127) / 128);  // 128 intermediate columns per item
     p.queues = L.queues;
-    if (gu_ptiled != nullptr) {
-      if (!aligned16(gu_ptiled)) return W4A16_ERR_ALIGN;
-      p.wt = gu_ptiled;
-    }
+    p.wt = t.gu_prefill;
     return launch_status(launch_prefill_x(kModeGateUp, p, max_mtiles(M, top_k, E, kPrefillXBM), s));
   }
   if (use_prefill(M, H, I)) {
@@ -475,24 +507,6 @@ int gate_up_impl(const uint16_t* hidden, const int32_t* gu_packed, const uint16_
     p.K = (int)H;
     p.ng = (int)((H + group_size - 1) / group_size);
     p.n_nt = (int)(I / 64);
-    if (bias_prefill(H, I, group_size)) {
-      // bias form: hidden rows reordered once, with their k tile sums
-      hipError_t e = launch_prefill_prep(hidden, L.xb, L.crx, (int)M, (int)H, (int)hidden_ld(H),
-                                         L.sorted_pos, L.offsets + E, (int)top_k, L.crs,
-                                         (int)(M * top_k), L.queues, s);
-      if (e != hipSuccess) return launch_status(e);
-      p.act = L.xb;
-      p.lda = (int)hidden_ld(H);
-      p.ldo = (int)inter_ld(I);
-      p.ldc = (int)(M * top_k);
-      p.cr = L.crs;
-      p.ncr = (int)((H + 127) / 128);
-      p.cr_out = L.crh;
-      p.ncr_out = (int)((I + 127) / 128);
-      p.n_nt = (int)((I + 127) / 128);  // 128 intermediate columns per item
-      p.queues = L.queues;
-      return launch_status(launch_prefill_bias(kModeGateUp, p, max_mtiles(M, top_k, E), s));
-    }
     return launch_status(launch_prefill(kModeGateUp, p, max_mtiles(M, top_k, E), s));
   }
   const int max_slots = (int)(M * top_k < E ? M * top_k : E);
@@ -504,13 +518,11 @@ int gate_up_impl(const uint16_t* hidden, const int32_t* gu_packed, const uint16_
   a.N = (int)(2 * I);
   a.K = (int)H;
   a.ng = (int)((H + group_size - 1) / group_size);
-  if (gu_tiled != nullptr && group_size == 128 && (a.ng % 2) == 0 &&
-      tiled_decode_bytes_per_expert(kModeGateUp, H, I) > 0) {
-    if (!aligned16(gu_tiled)) return W4A16_ERR_ALIGN;
-    a.wp = gu_tiled;
+  if (t.gu_decode != nullptr) {
+    a.wp = t.gu_decode;
     return launch_status(launch_decode_tiled(kModeGateUp, a, max_slots, s));
   }
-  return launch_status(launch_decode(kModeGateUp, group_size % 128 == 0, a, max_slots, s));
+  return launch_status(launch_decode(kModeGateUp, kDecodeBiasForm && group_size % 128 == 0, a, max_slots, s));
 }
 }  // namespace
 
@@ -519,68 +531,46 @@ extern "C" {
 int moe_gate_up(const uint16_t* hidden, const int32_t* gu_packed, const uint16_t* gu_scale,
                 int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t group_size,
                 void* workspace, size_t workspace_bytes, void* stream) {
-  return gate_up_impl(hidden, gu_packed, gu_scale, nullptr, nullptr, M, top_k, E, H, I, group_size, workspace,
+  return gate_up_impl(hidden, gu_packed, gu_scale, Tiles{}, M, top_k, E, H, I, group_size, workspace,
                       workspace_bytes, stream);
 }
 
-int moe_gate_up_tiled(const uint16_t* hidden, const int32_t* gu_packed, const int32_t* gu_tiled,
-                      const int32_t* gu_ptiled, const uint16_t* gu_scale, int64_t M, int64_t top_k, int64_t E,
-                      int64_t H, int64_t I, int64_t group_size, void* workspace, size_t workspace_bytes,
-                      void* stream) {
-  return gate_up_impl(hidden, gu_packed, gu_scale, gu_tiled, gu_ptiled, M, top_k, E, H, I, group_size, workspace,
+int moe_gate_up_tiled(const uint16_t* hidden, const int32_t* gu_packed, const uint16_t* gu_scale,
+                      const w4a16_tiled_experts* tiled, int64_t M, int64_t top_k, int64_t E, int64_t H,
+                      int64_t I, int64_t group_size, void* workspace, size_t workspace_bytes, void* stream) {
+  Tiles t;
+  const int st = resolve_tiles(tiled, E, H, I, group_size, &t);
+  if (st != W4A16_OK) return st;
+  return gate_up_impl(hidden, gu_packed, gu_scale, t, M, top_k, E, H, I, group_size, workspace,
                       workspace_bytes, stream);
 }
 
-size_t w4a16_tiled_gate_up_bytes(int64_t E, int64_t H, int64_t I) {
-  if (E <= 0 || E > kMaxExperts) return 0;
-  return (size_t)E * tiled_decode_bytes_per_expert(kModeGateUp, H, I);
+size_t w4a16_tiled_bytes(int kind, int64_t E, int64_t H, int64_t I, int64_t group_size) {
+  return tiled_need(kind, E, H, I, group_size);
 }
 
-size_t w4a16_tiled_prefill_bytes(int which, int64_t E, int64_t H, int64_t I) {
-  if (E <= 0 || E > kMaxExperts || (which != 0 && which != 1)) return 0;
-  return (size_t)E * prefill_tiled_bytes_per_expert(which == 0 ? kModeGateUp : kModeDown, H, I);
-}
-
-int w4a16_tile_prefill(int which, const int32_t* packed, int64_t E, int64_t H, int64_t I, int32_t* tiled,
-                       size_t tiled_bytes, void* stream) {
-  const size_t need = w4a16_tiled_prefill_bytes(which, E, H, I);
+int w4a16_tile(int kind, const int32_t* packed, const uint16_t* scale, int64_t E, int64_t H, int64_t I,
+               int64_t group_size, int32_t* tiled, size_t tiled_bytes, void* stream) {
+  if (!valid_group(group_size)) return W4A16_ERR_GROUP;
+  const size_t need = tiled_need(kind, E, H, I, group_size);
   if (need == 0) return W4A16_ERR_SHAPE;
   if (!packed || !tiled) return W4A16_ERR_NULL;
   if (!aligned16(packed) || !aligned16(tiled)) return W4A16_ERR_ALIGN;
   if (tiled_bytes < need) return W4A16_ERR_WORKSPACE;
-  return launch_status(launch_tile_prefill(which == 0 ? kModeGateUp : kModeDown, packed, (int)E, (int)H, (int)I,
-                                           tiled, static_cast<hipStream_t>(stream)));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (kind) {
+    case W4A16_TILED_GATE_UP_DECODE:
+    case W4A16_TILED_DOWN_DECODE:
+      if (tiled_decode_needs_scale((int)group_size) && scale == nullptr) return W4A16_ERR_NULL;
+      return launch_status(launch_tile_decode(kind == W4A16_TILED_GATE_UP_DECODE ? kModeGateUp : kModeDown, packed,
+                                              scale, (int)E, (int)H, (int)I, (int)group_size, tiled, s));
+    default:
+      return launch_status(launch_tile_prefill(kind == W4A16_TILED_GATE_UP_PREFILL ? kModeGateUp : kModeDown,
+                                               packed, (int)E, (int)H, (int)I, tiled, s));
+  }
 }
 
-int w4a16_tile_gate_up(const int32_t* gu_packed, int64_t E, int64_t H, int64_t I, int32_t* tiled,
-                       size_t tiled_bytes, void* stream) {
-  const size_t need = w4a16_tiled_gate_up_bytes(E, H, I);
-  if (need == 0) return W4A16_ERR_SHAPE;
-  if (!gu_packed || !tiled) return W4A16_ERR_NULL;
-  if (!aligned16(gu_packed) || !aligned16(tiled)) return W4A16_ERR_ALIGN;
-  if (tiled_bytes < need) return W4A16_ERR_WORKSPACE;
-  return launch_status(launch_tile_decode(kModeGateUp, gu_packed, (int)E, (int)H, (int)I, tiled,
-                                          static_cast<hipStream_t>(stream)));
-}
-
-size_t w4a16_tiled_down_bytes(int64_t E, int64_t H, int64_t I) {
-  if (E <= 0 || E > kMaxExperts) return 0;
-  return (size_t)E * tiled_decode_bytes_per_expert(kModeDown, H, I);
-}
-
-int w4a16_tile_down(const int32_t* dn_packed, int64_t E, int64_t H, int64_t I, int32_t* tiled, size_t tiled_bytes,
-                    void* stream) {
-  const size_t need = w4a16_tiled_down_bytes(E, H, I);
-  if (need == 0) return W4A16_ERR_SHAPE;
-  if (!dn_packed || !tiled) return W4A16_ERR_NULL;
-  if (!aligned16(dn_packed) || !aligned16(tiled)) return W4A16_ERR_ALIGN;
-  if (tiled_bytes < need) return W4A16_ERR_WORKSPACE;
-  return launch_status(launch_tile_decode(kModeDown, dn_packed, (int)E, (int)H, (int)I, tiled,
-                                          static_cast<hipStream_t>(stream)));
-}
-
-static int down_impl(const int32_t* dn_packed, const int32_t* dn_tiled, const int32_t* dn_ptiled,
-                     const uint16_t* dn_scale, int64_t M,
+static int down_impl(const int32_t* dn_packed, const uint16_t* dn_scale, const Tiles& t, int64_t M,
                      int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
                      size_t workspace_bytes, void* stream) {
   MoeLayout L{};
@@ -604,10 +594,7 @@ static int down_impl(const int32_t* dn_packed, const int32_t* dn_tiled, const in
     p.rows_total = (int)(M * top_k);
     p.n_nt = (int)((H + 255) / 256);  // 256 output columns per item
     p.queues = L.queues + kPrefillQueueInts / 2;
-    if (dn_ptiled != nullptr) {
-      if (!aligned16(dn_ptiled)) return W4A16_ERR_ALIGN;
-      p.wt = dn_ptiled;
-    }
+    p.wt = t.dn_prefill;
     return launch_status(launch_prefill_x(kModeDown, p, max_mtiles(M, top_k, E, kPrefillXBM), s));
   }
   if (use_prefill(M, H, I)) {
@@ -620,16 +607,6 @@ static int down_impl(const int32_t* dn_packed, const int32_t* dn_tiled, const in
     p.K = (int)I;
     p.ng = (int)((I + group_size - 1) / group_size);
     p.n_nt = (int)(H / kPfBN);
-    if (bias_prefill(H, I, group_size)) {
-      // the gate_up epilogue wrote bias-ordered rows and their block sums
-      p.ldc = (int)(M * top_k);
-      p.cr = L.crh;
-      p.ncr = (int)((I + 127) / 128);
-      p.n_nt = (int)((H + 255) / 256);  // 256 output columns per item
-      p.queues = L.queues + kPrefillQueueInts / 2;
-      p.lda = (int)inter_ld(I);
-      return launch_status(launch_prefill_bias(kModeDown, p, max_mtiles(M, top_k, E), s));
-    }
     return launch_status(launch_prefill(kModeDown, p, max_mtiles(M, top_k, E), s));
   }
   const int max_slots = (int)(M * top_k < E ? M * top_k : E);
@@ -641,27 +618,27 @@ static int down_impl(const int32_t* dn_packed, const int32_t* dn_tiled, const in
   a.N = (int)H;
   a.K = (int)I;
   a.ng = (int)((I + group_size - 1) / group_size);
-  if (dn_tiled != nullptr && group_size == 128 && (a.ng % 2) == 0 &&
-      tiled_decode_bytes_per_expert(kModeDown, H, I) > 0) {
-    if (!aligned16(dn_tiled)) return W4A16_ERR_ALIGN;
-    a.wp = dn_tiled;
+  if (t.dn_decode != nullptr) {
+    a.wp = t.dn_decode;
     return launch_status(launch_decode_tiled(kModeDown, a, max_slots, s));
   }
-  return launch_status(launch_decode(kModeDown, group_size % 128 == 0, a, max_slots, s));
+  return launch_status(launch_decode(kModeDown, kDecodeBiasForm && group_size % 128 == 0, a, max_slots, s));
 }
 
 int moe_down(const int32_t* dn_packed, const uint16_t* dn_scale, int64_t M, int64_t top_k,
              int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
              size_t workspace_bytes, void* stream) {
-  return down_impl(dn_packed, nullptr, nullptr, dn_scale, M, top_k, E, H, I, group_size, workspace,
-                   workspace_bytes, stream);
+  return down_impl(dn_packed, dn_scale, Tiles{}, M, top_k, E, H, I, group_size, workspace, workspace_bytes,
+                   stream);
 }
 
-int moe_down_tiled(const int32_t* dn_packed, const int32_t* dn_tiled, const int32_t* dn_ptiled,
-                   const uint16_t* dn_scale, int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I,
-                   int64_t group_size, void* workspace, size_t workspace_bytes, void* stream) {
-  return down_impl(dn_packed, dn_tiled, dn_ptiled, dn_scale, M, top_k, E, H, I, group_size, workspace,
-                   workspace_bytes, stream);
+int moe_down_tiled(const int32_t* dn_packed, const uint16_t* dn_scale, const w4a16_tiled_experts* tiled, int64_t M,
+                   int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
+                   size_t workspace_bytes, void* stream) {
+  Tiles t;
+  const int st = resolve_tiles(tiled, E, H, I, group_size, &t);
+  if (st != W4A16_OK) return st;
+  return down_impl(dn_packed, dn_scale, t, M, top_k, E, H, I, group_size, workspace, workspace_bytes, stream);
 }
 
 int moe_combine(const int64_t* topk_idx, const float* topk_w, uint16_t* out, int64_t M,
@@ -693,11 +670,10 @@ constexpr int64_t kFuseDownCombineRows = 32;
 int down_and_combine(const int32_t* dn_packed, const uint16_t* dn_scale, const int64_t* topk_idx,
                      const float* topk_w, uint16_t* out, int64_t M, int64_t top_k, int64_t E,
                      int64_t H, int64_t I, int64_t group_size, void* workspace,
-                     size_t workspace_bytes, void* stream, const int32_t* dn_tiled = nullptr,
-                     const int32_t* dn_ptiled = nullptr) {
+                     size_t workspace_bytes, void* stream, const Tiles& t) {
   if (use_prefill(M, H, I) || M * top_k > kFuseDownCombineRows || !down_combine_supported(M, top_k, I)) {
-    int st = down_impl(dn_packed, dn_tiled, dn_ptiled, dn_scale, M, top_k, E, H, I, group_size, workspace,
-                       workspace_bytes, stream);
+    int st = down_impl(dn_packed, dn_scale, t, M, top_k, E, H, I, group_size, workspace, workspace_bytes,
+                       stream);
     if (st == W4A16_OK)
       st = moe_combine(topk_idx, topk_w, out, M, top_k, E, H, I, workspace, workspace_bytes,
                        stream);
@@ -725,56 +701,58 @@ int down_and_combine(const int32_t* dn_packed, const uint16_t* dn_scale, const i
   a.K = (int)I;
   a.G = (int)group_size;
   a.ng = (int)((I + group_size - 1) / group_size);
-  return launch_status(launch_down_combine(group_size % 128 == 0, a, static_cast<hipStream_t>(stream)));
+  // the down streamer's tiled copy serves the fused kernel too
+  if (t.dn_decode != nullptr &&
+      tiled_decode_down_geometry(H, I, group_size, &a.tpw, &a.block_bytes, &a.expert_bytes))
+    a.wt = t.dn_decode;
+  return launch_status(launch_down_combine(a, static_cast<hipStream_t>(stream)));
 }
 
 }  // namespace
 
 extern "C" {
 
+static int forward_impl(const uint16_t* hidden, const int64_t* topk_idx, const float* topk_w,
+                        const int32_t* gu_packed, const uint16_t* gu_scale, const int32_t* dn_packed,
+                        const uint16_t* dn_scale, const Tiles& t, uint16_t* out, int64_t M, int64_t top_k,
+                        int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  MoeLayout L{};
+  int st = moe_check(M, top_k, E, H, I, group_size, workspace, workspace_bytes, &L);
+  if (st != W4A16_OK || M == 0) return st;
+  if (!hidden || !topk_idx || !topk_w || !gu_packed || !gu_scale || !dn_packed || !dn_scale ||
+      !out)
+    return W4A16_ERR_NULL;
+  st = moe_plan(hidden, topk_idx, M, top_k, E, H, I, group_size, workspace, workspace_bytes,
+                stream);
+  if (st == W4A16_OK)
+    st = gate_up_impl(hidden, gu_packed, gu_scale, t, M, top_k, E, H, I, group_size, workspace,
+                      workspace_bytes, stream);
+  if (st == W4A16_OK)
+    st = down_and_combine(dn_packed, dn_scale, topk_idx, topk_w, out, M, top_k, E, H, I,
+                          group_size, workspace, workspace_bytes, stream, t);
+  return st;
+}
+
 int moe_forward(const uint16_t* hidden, const int64_t* topk_idx, const float* topk_w,
                 const int32_t* gu_packed, const uint16_t* gu_scale, const int32_t* dn_packed,
                 const uint16_t* dn_scale, uint16_t* out, int64_t M, int64_t top_k, int64_t E,
                 int64_t H, int64_t I, int64_t group_size, void* workspace,
                 size_t workspace_bytes, void* stream) {
-  MoeLayout L{};
-  int st = moe_check(M, top_k, E, H, I, group_size, workspace, workspace_bytes, &L);
-  if (st != W4A16_OK || M == 0) return st;
-  if (!hidden || !topk_idx || !topk_w || !gu_packed || !gu_scale || !dn_packed || !dn_scale ||
-      !out)
-    return W4A16_ERR_NULL;
-  st = moe_plan(hidden, topk_idx, M, top_k, E, H, I, group_size, workspace, workspace_bytes,
-                stream);
-  if (st == W4A16_OK)
-    st = moe_gate_up(hidden, gu_packed, gu_scale, M, top_k, E, H, I, group_size, workspace,
-                     workspace_bytes, stream);
-  if (st == W4A16_OK)
-    st = down_and_combine(dn_packed, dn_scale, topk_idx, topk_w, out, M, top_k, E, H, I,
-                          group_size, workspace, workspace_bytes, stream);
-  return st;
+  return forward_impl(hidden, topk_idx, topk_w, gu_packed, gu_scale, dn_packed, dn_scale, Tiles{}, out, M, top_k,
+                      E, H, I, group_size, workspace, workspace_bytes, stream);
 }
 
 int moe_forward_tiled(const uint16_t* hidden, const int64_t* topk_idx, const float* topk_w,
-                      const int32_t* gu_packed, const int32_t* gu_tiled, const int32_t* gu_ptiled,
-                      const uint16_t* gu_scale, const int32_t* dn_packed, const int32_t* dn_tiled,
-                      const int32_t* dn_ptiled, const uint16_t* dn_scale, uint16_t* out, int64_t M,
+                      const int32_t* gu_packed, const uint16_t* gu_scale, const int32_t* dn_packed,
+                      const uint16_t* dn_scale, const w4a16_tiled_experts* tiled, uint16_t* out, int64_t M,
                       int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
                       size_t workspace_bytes, void* stream) {
-  MoeLayout L{};
-  int st = moe_check(M, top_k, E, H, I, group_size, workspace, workspace_bytes, &L);
-  if (st != W4A16_OK || M == 0) return st;
-  if (!hidden || !topk_idx || !topk_w || !gu_packed || !gu_scale || !dn_packed || !dn_scale ||
-      !out)
-    return W4A16_ERR_NULL;
-  st = moe_plan(hidden, topk_idx, M, top_k, E, H, I, group_size, workspace, workspace_bytes,
-                stream);
-  if (st == W4A16_OK)
-    st = gate_up_impl(hidden, gu_packed, gu_scale, gu_tiled, gu_ptiled, M, top_k, E, H, I, group_size,
-                      workspace, workspace_bytes, stream);
-  if (st == W4A16_OK)
-    st = down_and_combine(dn_packed, dn_scale, topk_idx, topk_w, out, M, top_k, E, H, I,
-                          group_size, workspace, workspace_bytes, stream, dn_tiled, dn_ptiled);
-  return st;
+  Tiles t;
+  const int st = resolve_tiles(tiled, E, H, I, group_size, &t);
+  if (st != W4A16_OK) return st;
+  return forward_impl(hidden, topk_idx, topk_w, gu_packed, gu_scale, dn_packed, dn_scale, t, out, M, top_k, E, H,
+                      I, group_size, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"
@@ -792,6 +770,7 @@ struct FfnLayout {
   uint16_t* moe;    // experts' output
   int64_t* idx;
   float* w;
+  size_t idx_off, w_off;  // byte offsets of idx and w in the workspace
   void* moe_ws;
   size_t moe_bytes;
   size_t bytes;
@@ -806,7 +785,9 @@ FfnLayout ffn_layout(void* ws, int64_t M, int64_t k, int64_t E, int64_t H, int64
   L.inter = c.take<uint16_t>(M * Im);
   L.h_mlp = c.take<uint16_t>(M * H);
   L.moe = c.take<uint16_t>(M * H);
+  L.idx_off = c.used;
   L.idx = c.take<int64_t>(M * k);
+  L.w_off = c.used;
   L.w = c.take<float>(M * k);
   L.moe_bytes = moe_layer_workspace_bytes(M, k, E, H, I);
   L.moe_ws = c.take<unsigned char>(L.moe_bytes);
@@ -824,6 +805,14 @@ size_t moe_ffn_block_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_
   return ffn_layout(nullptr, M, top_k, E, H, I, Im).bytes;
 }
 
+static int layer_forward_impl(const uint16_t* router_in, const uint16_t* router_scale, float scalar_root,
+                              const uint16_t* proj_w, const uint16_t* per_expert_scale, float eps,
+                              const uint16_t* hidden, const int32_t* gu_packed, const uint16_t* gu_scale,
+                              const int32_t* dn_packed, const uint16_t* dn_scale, const Tiles& t,
+                              uint16_t* out, int64_t* topk_idx, float* topk_w, int64_t M, int64_t top_k,
+                              int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
 static int ffn_block_impl(const uint16_t* residual, const uint16_t* attn_out,
                           const uint16_t* post_attn_ln_w, const uint16_t* pre_ff_ln_w,
                           const uint16_t* mlp_gate_w, const uint16_t* mlp_up_w,
@@ -836,8 +825,7 @@ static int ffn_block_impl(const uint16_t* residual, const uint16_t* attn_out,
                           const uint16_t* post_ff_ln_w, const uint16_t* layer_scalar, float eps,
                           uint16_t* out, int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I,
                           int64_t Im, int64_t group_size, void* workspace, size_t workspace_bytes,
-                          void* stream, const int32_t* gu_tiled, const int32_t* gu_ptiled,
-                          const int32_t* dn_tiled, const int32_t* dn_ptiled) {
+                          void* stream, const Tiles& t) {
   // row kernels: H <= 8192, one workgroup per row; shared-MLP linears:
   // K % 32 == 0 and ceil(M / 64) <= 65535 row tiles
   if (M < 0 || M > kMaxHybridLinkRows || top_k <= 0 || top_k > E || H <= 0 || H % 32 != 0 || H > 8192 ||
@@ -871,9 +859,9 @@ static int ffn_block_impl(const uint16_t* residual, const uint16_t* attn_out,
     e = launch_linear_bf16(kLinPlain, L.inter, mlp_down_w, nullptr, nullptr, nullptr, L.h_mlp, M, (int)H,
                            (int)Im, s);
   if (e != hipSuccess) return W4A16_ERR_LAUNCH;
-  st = moe_layer_forward_tiled(L.res, router_scale, router_scalar_root, router_proj_w, router_per_expert_scale,
-                               eps, L.h2_in, gu_packed, gu_tiled, gu_ptiled, gu_scale, dn_packed, dn_tiled,
-                               dn_ptiled, dn_scale, L.moe, L.idx, L.w, M, top_k, E, H, I, group_size, L.moe_ws,
+  st = layer_forward_impl(L.res, router_scale, router_scalar_root, router_proj_w, router_per_expert_scale,
+                          eps, L.h2_in, gu_packed, gu_scale, dn_packed, dn_scale, t, L.moe, L.idx, L.w, M, top_k,
+                          E, H, I, group_size, L.moe_ws,
                                L.moe_bytes, stream);
   if (st != W4A16_OK) return st;
   return launch_status(launch_ffn_post(L.h_mlp, L.moe, L.res, post_ff_ln1_w, post_ff_ln2_w, post_ff_ln_w,
@@ -897,7 +885,7 @@ int moe_ffn_block_forward(const uint16_t* residual, const uint16_t* attn_out,
                         post_ff_ln1_w, router_scale, router_scalar_root, router_proj_w, router_per_expert_scale,
                         pre_ff_ln2_w, gu_packed, gu_scale, dn_packed, dn_scale, post_ff_ln2_w, post_ff_ln_w,
                         layer_scalar, eps, out, M, top_k, E, H, I, Im, group_size, workspace, workspace_bytes,
-                        stream, nullptr, nullptr, nullptr, nullptr);
+                        stream, Tiles{});
 }
 
 int moe_ffn_block_forward_tiled(const uint16_t* residual, const uint16_t* attn_out,
@@ -906,18 +894,30 @@ int moe_ffn_block_forward_tiled(const uint16_t* residual, const uint16_t* attn_o
                                 const uint16_t* mlp_down_w, const uint16_t* post_ff_ln1_w,
                                 const uint16_t* router_scale, float router_scalar_root,
                                 const uint16_t* router_proj_w, const uint16_t* router_per_expert_scale,
-                                const uint16_t* pre_ff_ln2_w, const int32_t* gu_packed, const int32_t* gu_tiled,
-                                const int32_t* gu_ptiled, const uint16_t* gu_scale, const int32_t* dn_packed,
-                                const int32_t* dn_tiled, const int32_t* dn_ptiled, const uint16_t* dn_scale,
-                                const uint16_t* post_ff_ln2_w, const uint16_t* post_ff_ln_w,
-                                const uint16_t* layer_scalar, float eps, uint16_t* out, int64_t M, int64_t top_k,
-                                int64_t E, int64_t H, int64_t I, int64_t Im, int64_t group_size, void* workspace,
-                                size_t workspace_bytes, void* stream) {
+                                const uint16_t* pre_ff_ln2_w, const int32_t* gu_packed, const uint16_t* gu_scale,
+                                const int32_t* dn_packed, const uint16_t* dn_scale,
+                                const w4a16_tiled_experts* tiled, const uint16_t* post_ff_ln2_w,
+                                const uint16_t* post_ff_ln_w, const uint16_t* layer_scalar, float eps, uint16_t* out,
+                                int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t Im,
+                                int64_t group_size, void* workspace, size_t workspace_bytes, void* stream) {
+  Tiles t;
+  const int st = resolve_tiles(tiled, E, H, I, group_size, &t);
+  if (st != W4A16_OK) return st;
   return ffn_block_impl(residual, attn_out, post_attn_ln_w, pre_ff_ln_w, mlp_gate_w, mlp_up_w, mlp_down_w,
                         post_ff_ln1_w, router_scale, router_scalar_root, router_proj_w, router_per_expert_scale,
                         pre_ff_ln2_w, gu_packed, gu_scale, dn_packed, dn_scale, post_ff_ln2_w, post_ff_ln_w,
                         layer_scalar, eps, out, M, top_k, E, H, I, Im, group_size, workspace, workspace_bytes,
-                        stream, gu_tiled, gu_ptiled, dn_tiled, dn_ptiled);
+                        stream, t);
+}
+
+int moe_ffn_block_routing_offsets(int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t Im,
+                                  size_t* idx_offset, size_t* w_offset) {
+  if (M <= 0 || top_k <= 0 || E <= 0 || H <= 0 || I <= 0 || Im <= 0) return W4A16_ERR_SHAPE;
+  if (!idx_offset || !w_offset) return W4A16_ERR_NULL;
+  const FfnLayout L = ffn_layout(nullptr, M, top_k, E, H, I, Im);
+  *idx_offset = L.idx_off;
+  *w_offset = L.w_off;
+  return W4A16_OK;
 }
 
 size_t moe_bf16_experts_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I) {
@@ -1041,9 +1041,8 @@ size_t moe_layer_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t H,
 
 static int layer_forward_impl(const uint16_t* router_in, const uint16_t* router_scale, float scalar_root,
                               const uint16_t* proj_w, const uint16_t* per_expert_scale, float eps,
-                              const uint16_t* hidden, const int32_t* gu_packed, const int32_t* gu_tiled,
-                              const int32_t* gu_ptiled, const uint16_t* gu_scale, const int32_t* dn_packed,
-                              const int32_t* dn_tiled, const int32_t* dn_ptiled, const uint16_t* dn_scale,
+                              const uint16_t* hidden, const int32_t* gu_packed, const uint16_t* gu_scale,
+                              const int32_t* dn_packed, const uint16_t* dn_scale, const Tiles& t,
                               uint16_t* out, int64_t* topk_idx, float* topk_w, int64_t M, int64_t top_k,
                               int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
                               size_t workspace_bytes, void* stream) {
@@ -1084,11 +1083,11 @@ static int layer_forward_impl(const uint16_t* router_in, const uint16_t* router_
     st = moe_plan(hidden, topk_idx, M, top_k, E, H, I, group_size, workspace, moe_bytes, stream);
     if (st != W4A16_OK) return st;
   }
-  st = gate_up_impl(hidden, gu_packed, gu_scale, gu_tiled, gu_ptiled, M, top_k, E, H, I, group_size, workspace,
+  st = gate_up_impl(hidden, gu_packed, gu_scale, t, M, top_k, E, H, I, group_size, workspace,
                     moe_bytes, stream);
   if (st == W4A16_OK)
     st = down_and_combine(dn_packed, dn_scale, topk_idx, topk_w, out, M, top_k, E, H, I,
-                          group_size, workspace, moe_bytes, stream, dn_tiled, dn_ptiled);
+                          group_size, workspace, moe_bytes, stream, t);
   return st;
 }
 
@@ -1099,24 +1098,24 @@ int moe_layer_forward(const uint16_t* router_in, const uint16_t* router_scale, f
                       int64_t* topk_idx, float* topk_w, int64_t M, int64_t top_k, int64_t E,
                       int64_t H, int64_t I, int64_t group_size, void* workspace,
                       size_t workspace_bytes, void* stream) {
-  return layer_forward_impl(router_in, router_scale, scalar_root, proj_w, per_expert_scale, eps, hidden,
-                            gu_packed, nullptr, nullptr, gu_scale, dn_packed, nullptr, nullptr, dn_scale, out, topk_idx,
-                            topk_w, M,
-                            top_k, E, H, I, group_size, workspace, workspace_bytes, stream);
+  return layer_forward_impl(router_in, router_scale, scalar_root, proj_w, per_expert_scale, eps, hidden, gu_packed,
+                            gu_scale, dn_packed, dn_scale, Tiles{}, out, topk_idx, topk_w, M, top_k, E, H, I,
+                            group_size, workspace, workspace_bytes, stream);
 }
 
 int moe_layer_forward_tiled(const uint16_t* router_in, const uint16_t* router_scale, float scalar_root,
                             const uint16_t* proj_w, const uint16_t* per_expert_scale, float eps,
-                            const uint16_t* hidden, const int32_t* gu_packed, const int32_t* gu_tiled,
-                            const int32_t* gu_ptiled, const uint16_t* gu_scale, const int32_t* dn_packed,
-                            const int32_t* dn_tiled, const int32_t* dn_ptiled, const uint16_t* dn_scale,
-                            uint16_t* out, int64_t* topk_idx, float* topk_w, int64_t M, int64_t top_k,
-                            int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
-                            size_t workspace_bytes, void* stream) {
-  return layer_forward_impl(router_in, router_scale, scalar_root, proj_w, per_expert_scale, eps, hidden,
-                            gu_packed, gu_tiled, gu_ptiled, gu_scale, dn_packed, dn_tiled, dn_ptiled, dn_scale, out,
-                            topk_idx, topk_w, M,
-                            top_k, E, H, I, group_size, workspace, workspace_bytes, stream);
+                            const uint16_t* hidden, const int32_t* gu_packed, const uint16_t* gu_scale,
+                            const int32_t* dn_packed, const uint16_t* dn_scale, const w4a16_tiled_experts* tiled,
+                            uint16_t* out, int64_t* topk_idx, float* topk_w, int64_t M, int64_t top_k, int64_t E,
+                            int64_t H, int64_t I, int64_t group_size, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  Tiles t;
+  const int st = resolve_tiles(tiled, E, H, I, group_size, &t);
+  if (st != W4A16_OK) return st;
+  return layer_forward_impl(router_in, router_scale, scalar_root, proj_w, per_expert_scale, eps, hidden, gu_packed,
+                            gu_scale, dn_packed, dn_scale, t, out, topk_idx, topk_w, M, top_k, E, H, I, group_size,
+                            workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

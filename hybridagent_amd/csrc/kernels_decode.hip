@@ -14,7 +14,7 @@
 //                   gated GELU is fused into the epilogue.
 //   MODE = down   : dn[t*k+j] = inter W_d^T          (quantization.py:122-127)
 //
-// k_bias_order, k_combine and k_dequant are the small helpers around it.
+// k_combine and k_dequant are the small helpers around it.
 #include <algorithm>
 #include <type_traits>
 
@@ -33,12 +33,13 @@ __global__ __launch_bounds__(256) void k_dequant(const uint32_t* __restrict__ pa
                                                  int K, int G, int ng) {
   const int words = K >> 3;
   const int64_t total = rows * (int64_t)words;
+  const ExactRegs kr = exact_regs();
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t r = i / words;
     const int wj = (int)(i - r * words);
     const float s = bf16_bits_to_f32(scale[r * ng + (wj * 8) / G]);
-    st16(out + r * K + wj * 8, unpack_exact<false>(packed[i], s));
+    st16(out + r * K + wj * 8, unpack_exact<false>(packed[i], exact_scale(s), kr));
   }
 }
 
@@ -51,27 +52,6 @@ hipError_t launch_dequant(const int32_t* packed, const uint16_t* scale, uint16_t
   if (blocks > 65536) blocks = 65536;
   hipLaunchKernelGGL(k_dequant, dim3((unsigned)blocks), dim3(256), 0, s,
                      reinterpret_cast<const uint32_t*>(packed), scale, out, rows, K, G, ng);
-  return hipGetLastError();
-}
-
-// ---------------------------------------------------------------------------
-// activation rows -> bias order (8-blocks permuted to [0,4,1,5,2,6,3,7])
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_bias_order(const uint16_t* __restrict__ x,
-                                                    uint16_t* __restrict__ xp, int64_t n8) {
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n8;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    st16(xp + i * 8, to_bias_order(ld16(x + i * 8)));
-  }
-}
-
-hipError_t launch_bias_order(const uint16_t* x, uint16_t* xp, int64_t rows, int K,
-                             hipStream_t s) {
-  const int64_t n8 = rows * (K >> 3);
-  if (n8 == 0) return hipSuccess;
-  int64_t blocks = (n8 + 255) / 256;
-  if (blocks > 65536) blocks = 65536;
-  hipLaunchKernelGGL(k_bias_order, dim3((unsigned)blocks), dim3(256), 0, s, x, xp, n8);
   return hipGetLastError();
 }
 
@@ -128,7 +108,17 @@ __device__ __forceinline__ int frag_slot(int b, int rb, int j) {
 // TILED (MoE, bias form): the weights come in the tiled layout written by
 // k_tile_decode, where each wavefront's tile of an item is one contiguous
 // KiB (lane l's 16 bytes at 16 l) instead of 16 rows x 64 bytes.
-template <int MODE, bool BIAS, int TPW, int KSPLIT, bool LONGK, bool WIDE, bool TILED = false>
+// GSTEP (tiled, group size 32 or 64): each MFMA step covers one 32-wide
+// chunk of the k tile (lane chunk kb supplies its elements 8 kb .. 8 kb + 7),
+// so one scale group holds per step and the bias form folds per step:
+// acc += s_group * (g_step - 136 * sum(x_chunk)).  The tiled copy holds, in
+// lane l's 16 bytes of tile t, the words 16 t + 4 s + kb (s = 0..3) of its
+// row, and after an item's TPW tiles the rows' step scales.
+// LSCALE (tiled, exact form, group size 32 or 64): the copy keeps the usual
+// word order and, after an item's TPW tiles, each lane's TPW scales (one per
+// tile: its 32-wide chunk's group), fetched with one load like WIDE's.
+template <int MODE, bool BIAS, int TPW, int KSPLIT, bool LONGK, bool WIDE, bool TILED = false, bool GSTEP = false,
+          bool LSCALE = false>
 __global__ __launch_bounds__(stream_threads(KSPLIT)) __attribute__((amdgpu_waves_per_eu(TPW >= 4 ? 2 : 4, 8)))
 void k_decode(DecodeArgs a) {
   constexpr int kStreamThreads = stream_threads(KSPLIT);
@@ -136,12 +126,18 @@ void k_decode(DecodeArgs a) {
   constexpr int CG = NWAVES / KSPLIT;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   u32x4_t* __restrict__ lds_a = reinterpret_cast<u32x4_t*>(smem_raw);
-  // per (k tile, staged row) bias correction, after the activation fragments
+  // per (k tile -- GSTEP: 32-wide chunk --, staged row) bias correction,
+  // after the activation fragments
   const int ntiles = ((a.K >> 5) + 3) >> 2;
   float* __restrict__ csum = reinterpret_cast<float*>(smem_raw + (size_t)ntiles * 16 * a.rb * 16);
   static_assert(KSPLIT == 1 || KSPLIT == 4, "the split-K epilogue gives wavefront ks output row ks");
-  static_assert(!WIDE || (BIAS && !LONGK), "wide scale loads serve the bias form");
-  static_assert(!TILED || (BIAS && !LONGK && MODE != kModeDense), "tiled expert layout");
+  static_assert(!WIDE || !LONGK, "wide scale loads: one group per k tile");
+  static_assert(!TILED || (!LONGK && MODE != kModeDense), "tiled expert layout");
+  static_assert(!GSTEP || (TILED && BIAS && !WIDE), "per-step groups come with the tiled copy and its scales");
+  static_assert(!LSCALE || (TILED && WIDE && !BIAS), "lane scales come with the exact form's tiled copy");
+  // LDS slot of 16-byte piece b of staged row j: GSTEP keeps pieces in order
+  // (a step reads pieces 16 t + 4 s + kb); otherwise fragment order
+  auto aslot = [&](int b, int j) { return GSTEP ? b * a.rb + j : frag_slot(b, a.rb, j); };
   // split-K partials, double-buffered so one barrier per item suffices
   __shared__ f32x4_t red[2][KSPLIT > 1 ? NWAVES : 1][64];
   __shared__ int tok[16];
@@ -204,9 +200,10 @@ void k_decode(DecodeArgs a) {
   // touched by staging.  Rows past the staged ones hold stale values, which
   // only reach output rows that are not stored.
   for (int b = K8 + tid / rb; b < 16 * ntiles; b += kStreamThreads / rb)
-    lds_a[frag_slot(b, rb, tid & (rb - 1))] = u32x4_t{0u, 0u, 0u, 0u};
+    lds_a[aslot(b, tid & (rb - 1))] = u32x4_t{0u, 0u, 0u, 0u};
 
   const uint32_t kMask = opaque(0x000F000Fu), kBias = opaque(kBiasPair);
+  const ExactRegs kr = exact_regs();
 
   // weight row of this lane's MFMA column for column tile ct (gate_up: lanes
   // j < 8 take gate row n0 + j, lanes j >= 8 up row I + n0 + j - 8)
@@ -227,8 +224,10 @@ void k_decode(DecodeArgs a) {
   // lane carries one byte offset per item.  Rows past the matrix read as
   // zero; chunks past the row end read the next row, harmless because their
   // activation operand is zero.
-  // tiled: an expert is n_ct items of NWAVES x TPW KiB tiles
-  const int64_t wstride = TILED ? (int64_t)a.n_ct * NWAVES * TPW * 256 : (int64_t)a.N * K8;
+  // tiled: an expert is n_ct items of NWAVES blocks of TPW KiB tiles (GSTEP:
+  // each block followed by the TPW x 16 rows x 4 step scales, bf16)
+  constexpr int kBlockBytes = TPW * ((GSTEP || LSCALE) ? 1152 : 1024);
+  const int64_t wstride = TILED ? (int64_t)a.n_ct * NWAVES * (kBlockBytes / 4) : (int64_t)a.N * K8;
   const __amdgpu_buffer_rsrc_t wsrc =
       make_rsrc(reinterpret_cast<const uint32_t*>(a.wp) + (int64_t)e * wstride, (uint32_t)wstride * 4u);
   const __amdgpu_buffer_rsrc_t ssrc = make_rsrc(a.ws + (int64_t)e * a.N * a.ng, (uint32_t)a.N * a.ng * 2u);
@@ -238,6 +237,16 @@ void k_decode(DecodeArgs a) {
   auto off_of = [&](int ct) -> Off {
     bool ok;
     const int wrow = weight_row(ct, &ok);
+    // GSTEP: srow is the byte offset of this lane's scales (row j's TPW x 4)
+    if (GSTEP) {
+      const int blk = (ct * NWAVES + wave) * kBlockBytes;
+      return Off{blk + 16 * lane, blk + TPW * 1024 + j * (TPW * 8)};
+    }
+    // LSCALE: srow is the byte offset of this lane's TPW scales
+    if (LSCALE) {
+      const int blk = (ct * NWAVES + wave) * kBlockBytes;
+      return Off{blk + 16 * lane, blk + TPW * 1024 + lane * (TPW * 2)};
+    }
     if (TILED) return Off{(ct * NWAVES + wave) * (TPW * 1024) + 16 * lane, wrow * a.ng};
     return Off{wrow * K8 * 4 + 16 * kb, wrow * a.ng};
   };
@@ -255,18 +264,23 @@ void k_decode(DecodeArgs a) {
   // WIDE: the item's TPW scales as packed bf16 pairs
   constexpr int SCW = (TPW + 1) / 2;
   uint32_t scw[RING][SCW];
+  // GSTEP: the item's step scales of this lane's row, tiles 2m and 2m + 1 in
+  // sb[m] (TPW is even)
+  static_assert(!GSTEP || TPW % 2 == 0, "step scales come two tiles per 16-byte load");
+  u32x4_t sb[RING][GSTEP ? TPW / 2 : 1];
   auto load_scales_wide = [&](int r, const Off& o) {
-    const int off = (o.srow + tile0) * 2;
+    const __amdgpu_buffer_rsrc_t ssrc_w = LSCALE ? wsrc : ssrc;
+    const int off = LSCALE ? o.srow : (o.srow + tile0) * 2;
     if (SCW == 3) {
       typedef __attribute__((ext_vector_type(3))) uint32_t u32x3_t;
-      const u32x3_t v = __builtin_bit_cast(u32x3_t, __builtin_amdgcn_raw_buffer_load_b96(ssrc, off, 0, 0));
+      const u32x3_t v = __builtin_bit_cast(u32x3_t, __builtin_amdgcn_raw_buffer_load_b96(ssrc_w, off, 0, 0));
       scw[r][0] = v.x; scw[r][SCW > 1 ? 1 : 0] = v.y; scw[r][SCW > 2 ? 2 : 0] = v.z;
     } else if (SCW == 2) {
       typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
-      const u32x2_t v = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(ssrc, off, 0, 0));
+      const u32x2_t v = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(ssrc_w, off, 0, 0));
       scw[r][0] = v.x; scw[r][SCW > 1 ? 1 : 0] = v.y;
     } else {
-      scw[r][0] = __builtin_amdgcn_raw_buffer_load_b32(ssrc, off, 0, 0);
+      scw[r][0] = __builtin_amdgcn_raw_buffer_load_b32(ssrc_w, off, 0, 0);
     }
   };
 
@@ -283,7 +297,11 @@ void k_decode(DecodeArgs a) {
     for (int i = 0; i < TPW; ++i) {
       bw[r][i] = TILED ? buf_ld16(wsrc, tb + i < ntiles ? o.woff : 16 * lane, tb + i < ntiles ? 1024 * i : 0)
                        : buf_ld16(wsrc, o.woff + 64 * tb, 64 * i);
-      if (!WIDE) sc[r][i] = buf_ld_u16(ssrc, scale_off(o, tb + i));
+      if (GSTEP) {
+        if (i & 1) sb[r][i >> 1] = buf_ld16(wsrc, o.srow, 16 * (i >> 1));
+      } else if (!WIDE) {
+        sc[r][i] = buf_ld_u16(ssrc, scale_off(o, tb + i));
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -337,7 +355,7 @@ void k_decode(DecodeArgs a) {
                bf16_bits_to_f32(x.z & 0xFFFFu) + bf16_bits_to_f32(x.z >> 16) +
                bf16_bits_to_f32(x.w & 0xFFFFu) + bf16_bits_to_f32(x.w >> 16);
       }
-      lds_a[frag_slot(16 * t + b, rb, jr)] = x;
+      lds_a[aslot(16 * t + b, jr)] = x;
     };
     auto row_of = [&](int jr) -> int64_t {
       if (MODE == kModeGateUp) return tok[jr];
@@ -357,11 +375,21 @@ void k_decode(DecodeArgs a) {
       }
       first();
       if (has) {
-        float sum = 0.f;
+        if (GSTEP) {
+          // one correction per 32-wide chunk (MFMA step)
+          float sum4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int b = 0; b < 16; ++b)
-          if (b < nb) to_lds(v[b], t, b, jr, sum);
-        if (BIAS) csum[t * 16 + jr] = 136.0f * sum;
+          for (int b = 0; b < 16; ++b)
+            if (b < nb) to_lds(v[b], t, b, jr, sum4[b >> 2]);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) csum[(4 * t + c) * 16 + jr] = 136.0f * sum4[c];
+        } else {
+          float sum = 0.f;
+#pragma unroll
+          for (int b = 0; b < 16; ++b)
+            if (b < nb) to_lds(v[b], t, b, jr, sum);
+          if (BIAS) csum[t * 16 + jr] = 136.0f * sum;
+        }
       }
     } else {
       const int task = tid;
@@ -378,13 +406,24 @@ void k_decode(DecodeArgs a) {
         for (int b = 0; b < 8; ++b) v[b] = ld16(src + 8 * min(8 * hf + b, nb - 1));
       }
       first();
+      if (GSTEP) {
+        // this half's two 32-wide chunks, one correction each
+        float sum2[2] = {0.f, 0.f};
+        if (has) {
+#pragma unroll
+          for (int b = 0; b < 8; ++b)
+            if (8 * hf + b < nb) to_lds(v[b], t, 8 * hf + b, jr, sum2[b >> 2]);
+#pragma unroll
+          for (int c = 0; c < 2; ++c) csum[(4 * t + 2 * hf + c) * 16 + jr] = 136.0f * sum2[c];
+        }
+      }
       float sum = 0.f;
-      if (has) {
+      if (!GSTEP && has) {
 #pragma unroll
         for (int b = 0; b < 8; ++b)
           if (8 * hf + b < nb) to_lds(v[b], t, 8 * hf + b, jr, sum);
       }
-      if (BIAS) {
+      if (BIAS && !GSTEP) {
         // lanes 2i, 2i + 1 hold the halves; both add in the same order
         const float other =
             __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0xB1, 0xF, 0xF, false));
@@ -422,10 +461,10 @@ void k_decode(DecodeArgs a) {
       const int tc = t_ok ? t : ntiles - 1;
       u32x4_t A[4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) A[s] = lds_a[frag_slot(16 * tc + 4 * kb + s, rb, jr_read)];
-      // the bias form scales a whole tile, the exact form one lane chunk
+      for (int s = 0; s < 4; ++s) A[s] = lds_a[aslot(GSTEP ? 16 * tc + 4 * s + kb : 16 * tc + 4 * kb + s, jr_read)];
+      // the bias form scales a whole tile (GSTEP: a step), the exact form one lane chunk
       const bool s_ok = t_ok && (BIAS || 4 * t + kb < nchunks);
-      const float sci = s_ok ? (WIDE ? sfw[i] : bf16_bits_to_f32(sc[r][i])) : 0.f;
+      const float sci = (GSTEP || !s_ok) ? 0.f : (WIDE ? sfw[i] : bf16_bits_to_f32(sc[r][i]));
       u32x4_t bv[4];
       if (BIAS) {
         bv[0] = unpack_bias(bw[r][i].x, kMask, kBias);
@@ -433,19 +472,41 @@ void k_decode(DecodeArgs a) {
         bv[2] = unpack_bias(bw[r][i].z, kMask, kBias);
         bv[3] = unpack_bias(bw[r][i].w, kMask, kBias);
       } else {
-        bv[0] = unpack_exact<false>(bw[r][i].x, sci);
-        bv[1] = unpack_exact<false>(bw[r][i].y, sci);
-        bv[2] = unpack_exact<false>(bw[r][i].z, sci);
-        bv[3] = unpack_exact<false>(bw[r][i].w, sci);
+        // MoE down rows come in bias order (the gate_up epilogue's): the
+        // weights are unpacked in that order too
+        const ExactScale es = exact_scale(sci);
+        bv[0] = unpack_exact<MODE == kModeDown>(bw[r][i].x, es, kr);
+        bv[1] = unpack_exact<MODE == kModeDown>(bw[r][i].y, es, kr);
+        bv[2] = unpack_exact<MODE == kModeDown>(bw[r][i].z, es, kr);
+        bv[3] = unpack_exact<MODE == kModeDown>(bw[r][i].w, es, kr);
       }
       if (REFILL) {
         // tiled: tiles past K read the expert's first KiB (cached; their
         // scale is zero)
         bw[r][i] = TILED ? buf_ld16(wsrc, t_ok ? nx.woff : 16 * lane, t_ok ? 1024 * i : 0)
                          : buf_ld16(wsrc, nx.woff + 64 * tb, 64 * i);
-        if (!WIDE) sc[r][i] = buf_ld_u16(ssrc, scale_off(nx, tc));
+        if (!WIDE && !GSTEP) sc[r][i] = buf_ld_u16(ssrc, scale_off(nx, tc));
       }
-      if (BIAS) {
+      if (GSTEP) {
+        // one group per step: four partial sums, each folded with its scale
+        f32x4_t g[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) g[s] = mfma16(A[s], bv[s], f32x4_t{0.f, 0.f, 0.f, 0.f});
+        const uint32_t d0 = (i & 1) ? sb[r][i >> 1].z : sb[r][i >> 1].x;
+        const uint32_t d1 = (i & 1) ? sb[r][i >> 1].w : sb[r][i >> 1].y;
+        const float ss[4] = {__uint_as_float(d0 << 16), __uint_as_float(d0 & 0xFFFF0000u),
+                             __uint_as_float(d1 << 16), __uint_as_float(d1 & 0xFFFF0000u)};
+        // the scale block's refill once both of its tiles are folded
+        if (REFILL && (i & 1)) sb[r][i >> 1] = buf_ld16(wsrc, nx.srow, 16 * (i >> 1));
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const float scs = t_ok ? ss[s] : 0.f;
+          // output rows 4*kb .. 4*kb+3 of this lane: their 136 * sum(x) of step s's chunk
+          const f32x4_t cr = *reinterpret_cast<const f32x4_t*>(csum + (4 * tc + s) * 16 + 4 * kb);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) acc[q] = __builtin_fmaf(scs, g[s][q] - cr[q], acc[q]);
+        }
+      } else if (BIAS) {
         f32x4_t g = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < 4; ++s) g = mfma16(A[s], bv[s], g);
@@ -542,7 +603,9 @@ void k_decode(DecodeArgs a) {
       } else if (MODE == kModeGateUp) {
         // lane j (< 8) holds gate column n0+j, lane j+8 the matching up column
         const int n0 = colblk * 8;
-        const int pos = BIAS ? ((j & 3) * 2 + ((j >> 2) & 1)) : j;  // bias-order slot
+        // intermediate rows are written in bias order by every decode form
+        // (the down streamers read them so)
+        const int pos = (j & 3) * 2 + ((j >> 2) & 1);
 #pragma unroll
         for (int qq = 0; qq < QPW; ++qq) {
           const float up = lane_xor8(outv[qq]);
@@ -630,27 +693,30 @@ static int device_cus() {
 // LDS bytes of one workgroup: activation fragments + per (tile, row)
 // corrections (16 rows: rows past the staged ones are read for discarded
 // outputs).
-static size_t stream_lds(const DecodeArgs& a) {
+// (GSTEP: one correction per 32-wide chunk, four per tile.)
+static size_t stream_lds(const DecodeArgs& a, bool gstep) {
   const int ntiles = ((a.K >> 5) + 3) >> 2;
-  return (size_t)ntiles * 16 * a.rb * 16 + (size_t)ntiles * 16 * 4;
+  return (size_t)ntiles * 16 * a.rb * 16 + (size_t)ntiles * 16 * 4 * (gstep ? 4 : 1);
 }
 
-template <int MODE, bool BIAS, int TPW, int KSPLIT, bool LONGK, bool WIDE = false, bool TILED = false>
+template <int MODE, bool BIAS, int TPW, int KSPLIT, bool LONGK, bool WIDE = false, bool TILED = false,
+          bool GSTEP = false, bool LSCALE = false>
 static hipError_t launch_stream(DecodeArgs a, int max_slots, hipStream_t s) {
-  auto kern = k_decode<MODE, BIAS, TPW, KSPLIT, LONGK, WIDE, TILED>;
+  auto kern = k_decode<MODE, BIAS, TPW, KSPLIT, LONGK, WIDE, TILED, GSTEP, LSCALE>;
+  const size_t lds = stream_lds(a, GSTEP);
   // the workgroups that fit on the chip at once, at least one per possible
   // expert slot and at most one per item; the kernel spreads them over the
   // experts that turn out active (dense: the row groups)
   int per_cu = 0;
   constexpr int threads = stream_threads(KSPLIT);
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, stream_lds(a)) !=
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, lds) !=
           hipSuccess || per_cu <= 0)
     per_cu = 1;
   const int64_t resident = (int64_t)device_cus() * per_cu;
   int64_t grid = std::min<int64_t>(resident, (int64_t)max_slots * a.n_ct);
   if (grid < max_slots) grid = max_slots;
   if (grid <= 0) return hipSuccess;
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(threads), stream_lds(a), s, a);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(threads), lds, s, a);
   return hipGetLastError();
 }
 
@@ -671,9 +737,9 @@ static hipError_t launch_decode_mode(DecodeArgs a, int max_slots, hipStream_t s)
   const int ntiles = ((a.K >> 5) + 3) >> 2;
   // one load for an item's scales: group size 128 (one group per k tile)
   // and 4-byte aligned scale rows
-  const bool wide = BIAS && a.G == 128 && (a.ng % 2) == 0;
+  const bool wide = a.G == 128 && (a.ng % 2) == 0;
 #define W4A16_DEC(T_, K_)                                                          \
-  return wide ? launch_stream<MODE, BIAS, T_, K_, false, BIAS>(a, max_slots, s) \
+  return wide ? launch_stream<MODE, BIAS, T_, K_, false, true>(a, max_slots, s) \
               : launch_stream<MODE, BIAS, T_, K_, false, false>(a, max_slots, s)
   if (ntiles > 24) return launch_stream<MODE, BIAS, 6, 4, true>(a, max_slots, s);
   if (sh.ksplit == 1) {
@@ -707,95 +773,182 @@ hipError_t launch_decode(int mode, bool bias_form, DecodeArgs a, int max_slots, 
 // Tiled expert weights (a load-time copy for the decode streamer).  The
 // streamer reads, per item and wavefront, TPW tiles of 16 weight rows x 64
 // bytes.  The tiled copy puts each such tile in one contiguous KiB, in the
-// order the streamer reads them:
-//   byte ((((e * n_ct + ct) * NW + w) * TPW + i) * 64 + l) * 16 .. + 15
-//     = packed row r of expert e, bytes 64 (ks TPW + i) + 16 (l / 16) .. + 15
-//   with NW wavefronts per workgroup, w = KS cg + ks (KS wavefronts per K
-//   range), j = l % 16, colblk = 4 ct + cg and
+// order the streamer reads them: expert e, item ct, wavefront w form one
+// block of TPW KiB tiles,
+//   tile i, lane l's 16 bytes = packed row r of expert e, words
+//     group size 128:     16 t + 4 (l / 16) + s,   s = 0..3
+//     group size 32, 64:  16 t + 4 s + (l / 16),   s = 0..3  (GSTEP)
+//   with t = KS ks + i the k tile (KS = TPW), w = KSPLIT cg + ks, j = l % 16,
+//   colblk = CG ct + cg and
 //     gate_up: r = 8 colblk + j % 8 (+ I for j >= 8: the matching up row),
 //     down:    r = 16 colblk + j;
-// pieces past the row's K / 2 bytes or of rows past the matrix are zero.
+// words past the row's K / 8 or of rows past the matrix are zero.  With
+// group size 32 or 64 each block is followed by TPW * 128 bytes of scales
+// (zero past K or for rows past the matrix):
+//   exact form (the default): lane l's TPW scales at byte TPW KiB + 2 TPW l,
+//     tile i's the scale of its chunk, columns 32 (4 t + l / 16) .. + 31;
+//   bias form (GSTEP): row j's TPW x 4 step scales at byte TPW KiB + 8 TPW j,
+//     step s of tile i the scale of columns 32 (4 t + s) .. + 31.
 // Supported where the streamer's shape for that K has no long-K loop (and,
-// for gate_up, I is a multiple of 8).
+// for gate_up, I is a multiple of 8); group size 128 with an even group
+// count per row, or 32, or 64.
 // ---------------------------------------------------------------------------
 struct TiledShape {
   int tpw, ksplit, nwaves, n_ct;
+  int gstep;        // group size 32 / 64, bias form: per-step words and scales
+  int lscale;       // group size 32 / 64, exact form: per-lane scales
+  int block_bytes;  // one (item, wavefront) block
 };
 
-static bool tiled_shape(int mode, int64_t H, int64_t I, TiledShape* t) {
+static bool tiled_shape(int mode, int64_t H, int64_t I, int64_t G, TiledShape* t) {
   if (H <= 0 || I <= 0 || H % 32 != 0 || I % 32 != 0) return false;
   const int64_t K = mode == kModeGateUp ? H : I;
   const DecodeShape sh = decode_shape((int)K);
   const int ntiles = (int)(((K >> 5) + 3) >> 2);
   if (ntiles > 24) return false;
+  t->gstep = t->lscale = 0;
+  if (G == 128) {
+    if (((K + 127) / 128) % 2 != 0) return false;  // one wide scale load per item
+  } else if (G == 32 || G == 64) {
+    (kDecodeBiasForm ? t->gstep : t->lscale) = 1;
+  } else {
+    return false;
+  }
   t->tpw = sh.tpw;
   t->ksplit = sh.ksplit;
   t->nwaves = stream_threads(sh.ksplit) / 64;
   const int cg = t->nwaves / sh.ksplit;
   const int64_t ncolblk = mode == kModeGateUp ? I / 8 : (H + 15) / 16;
   t->n_ct = (int)((ncolblk + cg - 1) / cg);
+  t->block_bytes = t->tpw * ((t->gstep || t->lscale) ? 1152 : 1024);
   return true;
 }
 
-size_t tiled_decode_bytes_per_expert(int mode, int64_t H, int64_t I) {
+size_t tiled_decode_bytes_per_expert(int mode, int64_t H, int64_t I, int64_t G) {
   TiledShape t;
-  if (!tiled_shape(mode, H, I, &t)) return 0;
-  return (size_t)t.n_ct * t.nwaves * t.tpw * 1024;
+  if (!tiled_shape(mode, H, I, G, &t)) return 0;
+  return (size_t)t.n_ct * t.nwaves * t.block_bytes;
 }
 
-// one thread per 16-byte piece of the tiled copy
+bool tiled_decode_needs_scale(int G) { return G == 32 || G == 64; }  // both forms keep them in the copy
+
+bool tiled_decode_down_geometry(int64_t H, int64_t I, int64_t G, int* tpw, int* block_bytes, int64_t* expert_bytes) {
+  TiledShape t;
+  if (!tiled_shape(kModeDown, H, I, G, &t) || t.ksplit != 1) return false;
+  *tpw = t.tpw;
+  *block_bytes = t.block_bytes;
+  *expert_bytes = (int64_t)t.n_ct * t.nwaves * t.block_bytes;
+  return true;
+}
+
+// one thread per 16-byte piece of the tiled copy: TPW * 64 weight pieces,
+// then (GSTEP) TPW * 8 scale pieces per block
 template <int MODE>
 __global__ __launch_bounds__(256) void k_tile_decode(const uint32_t* __restrict__ packed,
-                                                     uint32_t* __restrict__ tiled, int N, int K, int I,
+                                                     const uint16_t* __restrict__ scale,
+                                                     uint32_t* __restrict__ tiled, int N, int K, int I, int G,
                                                      TiledShape t, int64_t pieces) {
   const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (p >= pieces) return;
-  const int l = (int)(p & 63);
-  int64_t q = p >> 6;
-  const int i = (int)(q % t.tpw);
-  q /= t.tpw;
+  const int per_block = t.block_bytes / 16;
+  const int pi = (int)(p % per_block);
+  int64_t q = p / per_block;
   const int w = (int)(q % t.nwaves);
   q /= t.nwaves;
   const int ct = (int)(q % t.n_ct);
   const int64_t e = q / t.n_ct;
   const int cg = w / t.ksplit, ks = w - cg * t.ksplit;
-  const int j = l & 15, kb = l >> 4;
   const int colblk = (t.nwaves / t.ksplit) * ct + cg;
-  int row;
-  bool ok;
-  if (MODE == kModeGateUp) {
-    row = 8 * colblk + (j & 7) + (j >= 8 ? I : 0);
-    ok = 8 * colblk + 8 <= I;
-  } else {
-    row = 16 * colblk + j;
-    ok = row < N;
-  }
-  const int rowbytes = K / 2;
-  const int byte = 64 * (ks * t.tpw + i) + 16 * kb;
+  const int K8 = K / 8;
+  const int ng = (K + G - 1) / G;
+  auto row_of = [&](int j, bool* ok) {
+    if (MODE == kModeGateUp) {
+      *ok = 8 * colblk + 8 <= I;
+      return 8 * colblk + (j & 7) + (j >= 8 ? I : 0);
+    }
+    *ok = 16 * colblk + j < N;
+    return 16 * colblk + j;
+  };
   u32x4_t v = {0u, 0u, 0u, 0u};
-  if (ok && byte + 16 <= rowbytes)
-    v = *reinterpret_cast<const u32x4_t*>(packed + ((e * N + row) * (int64_t)rowbytes + byte) / 4);
+  if (pi < t.tpw * 64) {
+    const int i = pi >> 6, l = pi & 63;
+    const int j = l & 15, kb = l >> 4;
+    bool ok;
+    const int row = row_of(j, &ok);
+    const int tk = ks * t.tpw + i;  // k tile of this slot
+    const uint32_t* src = packed + (e * N + row) * (int64_t)K8;
+    uint32_t wd[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int word = t.gstep ? 16 * tk + 4 * s + kb : 16 * tk + 4 * kb + s;
+      wd[s] = (ok && word < K8) ? src[word] : 0u;
+    }
+    v = u32x4_t{wd[0], wd[1], wd[2], wd[3]};
+  } else {
+    // scale piece: bf16 entries 8 k .. 8 k + 7 of the block's scales, the
+    // exact form's [64 lanes][TPW] or the bias form's [16 rows][TPW][4 steps]
+    const int k = pi - t.tpw * 64;
+    uint32_t h[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int ent = 8 * k + c;
+      int j, i, s;
+      if (t.lscale) {
+        const int l = ent / t.tpw;
+        j = l & 15;
+        i = ent % t.tpw;
+        s = l >> 4;
+      } else {
+        j = ent / (4 * t.tpw);
+        i = (ent / 4) % t.tpw;
+        s = ent % 4;
+      }
+      bool ok;
+      const int row = row_of(j, &ok);
+      const int chunk = 4 * (ks * t.tpw + i) + s;
+      const int g = (chunk * 32) / G;
+      h[c] = (ok && chunk < K / 32) ? scale[(e * N + row) * (int64_t)ng + g] : 0u;
+    }
+    v = u32x4_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+  }
   *reinterpret_cast<u32x4_t*>(tiled + p * 4) = v;
 }
 
-hipError_t launch_tile_decode(int mode, const int32_t* packed, int E, int H, int I, int32_t* tiled,
-                              hipStream_t s) {
+hipError_t launch_tile_decode(int mode, const int32_t* packed, const uint16_t* scale, int E, int H, int I, int G,
+                              int32_t* tiled, hipStream_t s) {
   TiledShape t;
-  if (!tiled_shape(mode, H, I, &t)) return hipErrorInvalidValue;
-  const int64_t pieces = (int64_t)E * t.n_ct * t.nwaves * t.tpw * 64;
+  if (!tiled_shape(mode, H, I, G, &t)) return hipErrorInvalidValue;
+  if ((t.gstep || t.lscale) && scale == nullptr) return hipErrorInvalidValue;
+  const int64_t pieces = (int64_t)E * t.n_ct * t.nwaves * (t.block_bytes / 16);
   if (pieces == 0) return hipSuccess;
   const dim3 grid((unsigned)((pieces + 255) / 256));
   const uint32_t* src = reinterpret_cast<const uint32_t*>(packed);
   uint32_t* dst = reinterpret_cast<uint32_t*>(tiled);
   if (mode == kModeGateUp)
-    hipLaunchKernelGGL(k_tile_decode<kModeGateUp>, grid, dim3(256), 0, s, src, dst, 2 * I, H, I, t, pieces);
+    hipLaunchKernelGGL(k_tile_decode<kModeGateUp>, grid, dim3(256), 0, s, src, scale, dst, 2 * I, H, I, G, t,
+                       pieces);
   else
-    hipLaunchKernelGGL(k_tile_decode<kModeDown>, grid, dim3(256), 0, s, src, dst, H, I, I, t, pieces);
+    hipLaunchKernelGGL(k_tile_decode<kModeDown>, grid, dim3(256), 0, s, src, scale, dst, H, I, I, G, t, pieces);
   return hipGetLastError();
 }
 
-// The MoE streamers on tiled weights (a.wp = the tiled copy): bias form
-// with one scale load per item (group size 128, an even group count).
+// One tiled instantiation: the form (exact, or the bias form in a bias-form
+// build) and the scale source (group size 128: the scale tensor; 32 / 64:
+// the copy).
+template <int MODE, int TPW, int KSPLIT>
+static hipError_t launch_stream_tiled(const TiledShape& t, DecodeArgs a, int max_slots, hipStream_t s) {
+  if (kDecodeBiasForm) {
+    if (t.gstep) return launch_stream<MODE, true, TPW, KSPLIT, false, false, true, true>(a, max_slots, s);
+    return launch_stream<MODE, true, TPW, KSPLIT, false, true, true>(a, max_slots, s);
+  }
+  if (t.lscale) return launch_stream<MODE, false, TPW, KSPLIT, false, true, true, false, true>(a, max_slots, s);
+  return launch_stream<MODE, false, TPW, KSPLIT, false, true, true>(a, max_slots, s);
+}
+
+// The MoE streamers on tiled weights (a.wp = the tiled copy): one scale load
+// per item (group size 128 from the scale tensor, an even group count; 32 /
+// 64 from the copy), exact form -- or, built with the bias form, the
+// per-step groups at 32 / 64.
 hipError_t launch_decode_tiled(int mode, DecodeArgs a, int max_slots, hipStream_t s) {
   if (max_slots <= 0) return hipSuccess;
   if (mode != kModeGateUp && mode != kModeDown) return hipErrorInvalidValue;
@@ -803,32 +956,30 @@ hipError_t launch_decode_tiled(int mode, DecodeArgs a, int max_slots, hipStream_
     return hipErrorInvalidValue;
   TiledShape t;
   const int64_t H = mode == kModeGateUp ? a.K : a.N;
-  if (!tiled_shape(mode, H, a.I, &t) || a.G != 128 || (a.ng % 2) != 0) return hipErrorInvalidValue;
+  if (!tiled_shape(mode, H, a.I, a.G, &t)) return hipErrorInvalidValue;
   a.n_ct = t.n_ct;
   a.rb = stage_rows(a.K, t.ksplit);
   int rows_cap = 1;
   while (rows_cap < a.rows_hint && rows_cap < 16) rows_cap <<= 1;
   if (a.rb > rows_cap) a.rb = rows_cap;
-#define W4A16_DEC_T(M_, T_, K_) return launch_stream<M_, true, T_, K_, false, true, true>(a, max_slots, s)
   if (mode == kModeGateUp) {
     if (t.ksplit == 4) {
-      if (t.tpw == 2) W4A16_DEC_T(kModeGateUp, 2, 4);
-      if (t.tpw == 4) W4A16_DEC_T(kModeGateUp, 4, 4);
-      W4A16_DEC_T(kModeGateUp, 6, 4);
+      if (t.tpw == 2) return launch_stream_tiled<kModeGateUp, 2, 4>(t, a, max_slots, s);
+      if (t.tpw == 4) return launch_stream_tiled<kModeGateUp, 4, 4>(t, a, max_slots, s);
+      return launch_stream_tiled<kModeGateUp, 6, 4>(t, a, max_slots, s);
     }
-    if (t.tpw == 2) W4A16_DEC_T(kModeGateUp, 2, 1);
-    if (t.tpw == 4) W4A16_DEC_T(kModeGateUp, 4, 1);
-    W4A16_DEC_T(kModeGateUp, 6, 1);
+    if (t.tpw == 2) return launch_stream_tiled<kModeGateUp, 2, 1>(t, a, max_slots, s);
+    if (t.tpw == 4) return launch_stream_tiled<kModeGateUp, 4, 1>(t, a, max_slots, s);
+    return launch_stream_tiled<kModeGateUp, 6, 1>(t, a, max_slots, s);
   }
   if (t.ksplit == 4) {
-    if (t.tpw == 2) W4A16_DEC_T(kModeDown, 2, 4);
-    if (t.tpw == 4) W4A16_DEC_T(kModeDown, 4, 4);
-    W4A16_DEC_T(kModeDown, 6, 4);
+    if (t.tpw == 2) return launch_stream_tiled<kModeDown, 2, 4>(t, a, max_slots, s);
+    if (t.tpw == 4) return launch_stream_tiled<kModeDown, 4, 4>(t, a, max_slots, s);
+    return launch_stream_tiled<kModeDown, 6, 4>(t, a, max_slots, s);
   }
-  if (t.tpw == 2) W4A16_DEC_T(kModeDown, 2, 1);
-  if (t.tpw == 4) W4A16_DEC_T(kModeDown, 4, 1);
-  W4A16_DEC_T(kModeDown, 6, 1);
-#undef W4A16_DEC_T
+  if (t.tpw == 2) return launch_stream_tiled<kModeDown, 2, 1>(t, a, max_slots, s);
+  if (t.tpw == 4) return launch_stream_tiled<kModeDown, 4, 1>(t, a, max_slots, s);
+  return launch_stream_tiled<kModeDown, 6, 1>(t, a, max_slots, s);
 }
 
 // ---------------------------------------------------------------------------

@@ -40,30 +40,6 @@ __device__ __forceinline__ int col_block(int wn, int fn) {
   return 4 * wn + fn;
 }
 
-// Exact unpack of one packed word: 8 values bf16_RNE((u - 8) * s) in natural
-// k order.  lo/hi hold nibbles 0,2,4,6 / 1,3,5,7 in their bytes, so each value
-// is one v_cvt_f32_ubyteN and one fma (both products exact in fp32: |u| <= 15,
-// s has 8 significant bits) before the pairwise RNE conversion.  `m0f` is the
-// 0x0F0F0F0F mask held in a register.
-__device__ __forceinline__ u32x4_t unpack_exact_bytes(uint32_t w, float s, float m8, uint32_t m0f) {
-  const uint32_t lo = w & m0f;
-  const uint32_t hi = (w >> 4) & m0f;
-  const float v0 = __builtin_fmaf((float)(lo & 0xFFu), s, m8);
-  const float v1 = __builtin_fmaf((float)(hi & 0xFFu), s, m8);
-  const float v2 = __builtin_fmaf((float)((lo >> 8) & 0xFFu), s, m8);
-  const float v3 = __builtin_fmaf((float)((hi >> 8) & 0xFFu), s, m8);
-  const float v4 = __builtin_fmaf((float)((lo >> 16) & 0xFFu), s, m8);
-  const float v5 = __builtin_fmaf((float)((hi >> 16) & 0xFFu), s, m8);
-  const float v6 = __builtin_fmaf((float)(lo >> 24), s, m8);
-  const float v7 = __builtin_fmaf((float)(hi >> 24), s, m8);
-  u32x4_t r;
-  r.x = pack_bf16x2(v0, v1);
-  r.y = pack_bf16x2(v2, v3);
-  r.z = pack_bf16x2(v4, v5);
-  r.w = pack_bf16x2(v6, v7);
-  return r;
-}
-
 }  // namespace
 
 template <int MODE, int BM>
@@ -105,7 +81,7 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill(PrefillArgs a) {
   const int ar0 = tid >> 3, ac = tid & 7;
   const int bn = (tid & 15) + 16 * (tid >> 5);
   const int bh = (tid >> 4) & 1;
-  const uint32_t m0f = opaque(0x0F0F0F0Fu);
+  const ExactRegs kr = exact_regs();
 
   for (int item = xcd * chunk + (blockIdx.x >> 3); item < it_end; item += per_xcd) {
     const int mt = item / a.n_nt;
@@ -154,13 +130,12 @@ __global__ __launch_bounds__(kPfThreads) void k_prefill(PrefillArgs a) {
       u32x4_t* base = lds + buf * STAGE;
 #pragma unroll
       for (int i = 0; i < AR; ++i) base[(ar0 + 32 * i) * A_PITCH + ac] = ra[slot][i];
-      const float sc = bf16_bits_to_f32(rs[slot]);
-      const float m8 = -8.0f * sc;
+      const ExactScale es = exact_scale(bf16_bits_to_f32(rs[slot]));
       u32x4_t* bb = base + A_SLOTS + (((bn >> 4) << 1) + bh) * 64 + (bn & 15);
-      bb[0] = unpack_exact_bytes(rw[slot].x, sc, m8, m0f);
-      bb[16] = unpack_exact_bytes(rw[slot].y, sc, m8, m0f);
-      bb[32] = unpack_exact_bytes(rw[slot].z, sc, m8, m0f);
-      bb[48] = unpack_exact_bytes(rw[slot].w, sc, m8, m0f);
+      bb[0] = unpack_exact<false>(rw[slot].x, es, kr);
+      bb[16] = unpack_exact<false>(rw[slot].y, es, kr);
+      bb[32] = unpack_exact<false>(rw[slot].z, es, kr);
+      bb[48] = unpack_exact<false>(rw[slot].w, es, kr);
     };
 
     f32x4_t acc[FM][FN];

@@ -119,33 +119,6 @@ __device__ __forceinline__ void px_dma16(__amdgpu_buffer_rsrc_t rsrc, int voff, 
                                           voff, soff, 0, 0);
 }
 
-// byte b of v as a float (v_cvt_f32_ubyte<b>; written out because the
-// compiler otherwise extracts bytes 1..3 with a separate v_bfe_u32 first)
-template <int B>
-__device__ __forceinline__ float cvt_ubyte(uint32_t v) {
-  float r;
-  if (B == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
-  if (B == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
-  if (B == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
-  if (B == 3) asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
-  return r;
-}
-
-// Exact dequantisation of one packed word (k = 8 j .. 8 j + 7 of one weight
-// row) into 8 bf16 in natural k order: bf16_RNE(q * s), q = u - 8, computed
-// as fma(u, s, -8 s) -- both products are exact in fp32 (|u| <= 15, s has 8
-// significant bits) -- then rounded by v_cvt_pk_bf16_f32.  m8 = -8 s.
-__device__ __forceinline__ u32x4_t dequant_word(uint32_t w, float s, float m8) {
-  const uint32_t lo = w & 0x0F0F0F0Fu;         // nibbles 0, 2, 4, 6
-  const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;  // nibbles 1, 3, 5, 7
-  u32x4_t r;
-  r.x = pack_bf16x2(__builtin_fmaf(cvt_ubyte<0>(lo), s, m8), __builtin_fmaf(cvt_ubyte<0>(hi), s, m8));
-  r.y = pack_bf16x2(__builtin_fmaf(cvt_ubyte<1>(lo), s, m8), __builtin_fmaf(cvt_ubyte<1>(hi), s, m8));
-  r.z = pack_bf16x2(__builtin_fmaf(cvt_ubyte<2>(lo), s, m8), __builtin_fmaf(cvt_ubyte<2>(hi), s, m8));
-  r.w = pack_bf16x2(__builtin_fmaf(cvt_ubyte<3>(lo), s, m8), __builtin_fmaf(cvt_ubyte<3>(hi), s, m8));
-  return r;
-}
-
 __device__ __forceinline__ f32x16_t mfma32x(u32x4_t a, u32x4_t b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
 }
@@ -370,6 +343,7 @@ __device__ __forceinline__ int px_run(const PrefillArgs& a, unsigned char* smem,
   u32x4_t af[MB];
   u32x4_t bw = {0u, 0u, 0u, 0u};
   float sc = 0.f;
+  const ExactRegs kr = exact_regs();
   if (work) {
     read_a(stage_ptr(p0), 0, af);
     bw = *reinterpret_cast<const u32x4_t*>(stage_ptr(p0) + boff);
@@ -383,13 +357,13 @@ __device__ __forceinline__ int px_run(const PrefillArgs& a, unsigned char* smem,
     const int nslot = slot == kPxStages - 1 ? 0 : slot + 1;
     if (work) {
       const unsigned char* st = stage_ptr(slot);
-      const float m8 = -8.0f * sc;
+      const ExactScale es = exact_scale(sc);
       const uint32_t wv[4] = {bw.x, bw.y, bw.z, bw.w};
-      u32x4_t bf = dequant_word(wv[0], sc, m8);
+      u32x4_t bf = unpack_exact<false>(wv[0], es, kr);
 #pragma unroll
       for (int s2 = 0; s2 < 3; ++s2) {
         issue(slot2, s2);
-        const u32x4_t bfn = dequant_word(wv[s2 + 1], sc, m8);
+        const u32x4_t bfn = unpack_exact<false>(wv[s2 + 1], es, kr);
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
           acc[mb] = mfma32x(bf, af[mb], acc[mb]);
@@ -650,6 +624,22 @@ hipError_t launch_tile_prefill(int mode, const int32_t* packed, int E, int H, in
   else
     hipLaunchKernelGGL(k_tile_prefill<kModeDown>, grid, dim3(256), 0, s, src, dst, a, pieces);
   return hipGetLastError();
+}
+
+// persistent grid: the workgroups that fit on the device at once (a multiple
+// of the 8 XCDs), at most one per item
+int prefill_grid_size(const void* kern, int threads, size_t lds, int max_items) {
+  int dev = 0, cus = 256, per_cu = 1;
+  hipDeviceProp_t p;
+  if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess &&
+      p.multiProcessorCount > 0)
+    cus = p.multiProcessorCount;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, lds) != hipSuccess ||
+      per_cu <= 0)
+    per_cu = 1;
+  int g = cus * per_cu;
+  if (max_items < g) g = max_items;
+  return ((g + 7) / 8) * 8;
 }
 
 size_t prefill_x_lds_bytes() { return (size_t)kPxLds; }

@@ -15,7 +15,7 @@
 //   large batches    k_router_inv + k_router_tok (the norm folded into the
 //                    logits kernel's A operand)
 //   decode sizes     k_router_norm_logits (norm + logits in one launch),
-//                    k_router_topk_sort[_small] (top-k + sort in one launch)
+//                    k_router_topk_sort_small (top-k + sort in one launch)
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -938,51 +938,10 @@ __global__ __launch_bounds__(kSortThreads) void k_moe_sort(
                 desc, counters, tiles, BM);
 }
 
-// Small batches: top-k of every token and the sort in one workgroup (no
-// hand-off between workgroups).  Wavefront w routes tokens w, w + 16, ...;
-// the routing also lands in LDS, which the sort reads.
-constexpr int kTopkSortMaxEntries = 512;
-constexpr int kTopkSortRounds = 4;  // tokens per wavefront: M <= 64
-
-template <int KS, int PER, int ROUNDS>
-__global__ __launch_bounds__(kSortThreads) void k_router_topk_sort(
-    const float* __restrict__ partial, const uint16_t* __restrict__ pes,
-    int64_t* __restrict__ idx_out, float* __restrict__ w_out, int M, int E, int topk,
-    int32_t* __restrict__ sorted_pos, int32_t* __restrict__ offsets, int32_t* __restrict__ desc,
-    int32_t* __restrict__ counters, int32_t* __restrict__ tiles, int BM) {
-  __shared__ int s_idx[kTopkSortMaxEntries];
-  __shared__ uint16_t s_pes[kMaxExperts];
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  for (int e = threadIdx.x; e < E; e += kSortThreads) s_pes[e] = pes[e];
-  // every token of this wavefront (at most ROUNDS) loaded up front
-  float lg[ROUNDS][PER];
-#pragma unroll
-  for (int rr = 0; rr < ROUNDS; ++rr)
-    load_logits<KS, PER>(partial, nullptr, nullptr, min(wave + kSortWaves * rr, M - 1), M, E, lane,
-                         lg[rr]);
-  __syncthreads();  // s_pes
-#pragma unroll
-  for (int rr = 0; rr < ROUNDS; ++rr) {
-    const int m = wave + kSortWaves * rr;
-    if (m >= M) break;  // uniform per wavefront
-    int se;
-    float sw;
-    select_topk<PER>(lg[rr], s_pes, E, topk, lane, &se, &sw);
-    if (lane < topk) {
-      idx_out[(int64_t)m * topk + lane] = se;
-      w_out[(int64_t)m * topk + lane] = sw;
-      s_idx[m * topk + lane] = se;
-    }
-  }
-  __syncthreads();
-  moe_sort_body([&](int row) -> int64_t { return s_idx[row]; }, M, topk, E, sorted_pos, offsets,
-                desc, counters, tiles, BM);
-}
-
-// The same for at most 64 routed rows (decode sizes): eight wavefronts do the
-// top-k (ROUNDS tokens each), then one wavefront sorts the rows -- one row
-// per lane: expert counts by LDS atomics, plan_wave, the stable rank among
+// Small batches (at most 64 routed rows, decode sizes): top-k of every token
+// and the expert sort in one workgroup, no hand-off between workgroups.
+// Eight wavefronts do the top-k (ROUNDS tokens each; the routing also lands
+// in LDS), then one wavefront sorts the rows -- one row per lane: expert counts by LDS atomics, plan_wave, the stable rank among
 // lower lanes of the same expert by ballots -- with no workgroup barrier
 // after the top-k (a wavefront's LDS operations complete in order).
 constexpr int kSmallSortWaves = 8;
@@ -1047,30 +1006,24 @@ __global__ __launch_bounds__(64 * kSmallSortWaves) void k_router_topk_sort_small
   if (ok) sorted_pos[run[e] + rank] = row;
 }
 
-template <int KS>
-static void launch_topk_sort_ks(const float* partial, const uint16_t* pes, int64_t* idx, float* w,
-                                int M, int E, int topk, int32_t* sorted_pos, int32_t* offsets,
-                                int32_t* desc, int32_t* counters, int32_t* tiles, int BM,
-                                hipStream_t s) {
-  // at most 64 rows: eight wavefronts, one of them sorting; else one token
-  // per wavefront up to M = 16, else up to kTopkSortRounds
-#define W4A16_TS(P_)                                                                            \
-  if (M * topk <= 64 && M <= kSmallSortWaves)                                                   \
+hipError_t launch_topk_sort(const float* partial, int ksplit, const uint16_t* per_expert_scale,
+                            int64_t* idx, float* w, int M, int E, int topk, int32_t* sorted_pos,
+                            int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
+                            int BM, hipStream_t s) {
+  if (M == 0) return hipSuccess;
+  // the decode router's partials (kRouterMaxSplit K splits), at most 64
+  // routed rows: one token per wavefront up to M = 8, else eight rounds
+  if (M * topk > 64 || ksplit != kRouterMaxSplit) return hipErrorInvalidValue;
+  constexpr int KS = kRouterMaxSplit;
+#define W4A16_TS(P_)                                                                             \
+  if (M <= kSmallSortWaves)                                                                      \
     hipLaunchKernelGGL((k_router_topk_sort_small<KS, P_, 1>), dim3(1), dim3(64 * kSmallSortWaves), \
-                       0, s, partial, pes, idx, w, M, E, topk, sorted_pos, offsets, desc,         \
-                       counters, tiles, BM);                                                     \
-  else if (M * topk <= 64)                                                                      \
-    hipLaunchKernelGGL((k_router_topk_sort_small<KS, P_, 64 / kSmallSortWaves>), dim3(1),        \
-                       dim3(64 * kSmallSortWaves), 0, s, partial, pes, idx, w, M, E, topk,        \
-                       sorted_pos, offsets, desc, counters, tiles, BM);                          \
-  else if (M <= kSortWaves)                                                                     \
-    hipLaunchKernelGGL((k_router_topk_sort<KS, P_, 1>), dim3(1), dim3(kSortThreads), 0, s,       \
-                       partial, pes, idx, w, M, E, topk, sorted_pos, offsets, desc, counters,    \
-                       tiles, BM);                                                               \
-  else                                                                                          \
-    hipLaunchKernelGGL((k_router_topk_sort<KS, P_, kTopkSortRounds>), dim3(1), dim3(kSortThreads), \
-                       0, s, partial, pes, idx, w, M, E, topk, sorted_pos, offsets, desc,         \
-                       counters, tiles, BM)
+                       0, s, partial, per_expert_scale, idx, w, M, E, topk, sorted_pos, offsets,   \
+                       desc, counters, tiles, BM);                                                \
+  else                                                                                           \
+    hipLaunchKernelGGL((k_router_topk_sort_small<KS, P_, 64 / kSmallSortWaves>), dim3(1),         \
+                       dim3(64 * kSmallSortWaves), 0, s, partial, per_expert_scale, idx, w, M, E,  \
+                       topk, sorted_pos, offsets, desc, counters, tiles, BM)
   if (E <= 64) {
     W4A16_TS(1);
   } else if (E <= 128) {
@@ -1081,22 +1034,6 @@ static void launch_topk_sort_ks(const float* partial, const uint16_t* pes, int64
     W4A16_TS(kTopkPerLane);
   }
 #undef W4A16_TS
-}
-
-hipError_t launch_topk_sort(const float* partial, int ksplit, const uint16_t* per_expert_scale,
-                            int64_t* idx, float* w, int M, int E, int topk, int32_t* sorted_pos,
-                            int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
-                            int BM, hipStream_t s) {
-  if (M == 0) return hipSuccess;
-  if (M * topk > kTopkSortMaxEntries || M > kTopkSortRounds * kSortWaves) return hipErrorInvalidValue;
-  if (ksplit == kRouterMaxSplit)
-    launch_topk_sort_ks<kRouterMaxSplit>(partial, per_expert_scale, idx, w, M, E, topk,
-                                         sorted_pos, offsets, desc, counters, tiles, BM, s);
-  else if (ksplit == 1)
-    launch_topk_sort_ks<1>(partial, per_expert_scale, idx, w, M, E, topk, sorted_pos, offsets,
-                           desc, counters, tiles, BM, s);
-  else
-    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

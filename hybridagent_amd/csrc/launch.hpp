@@ -52,17 +52,8 @@ struct PrefillArgs {
   const int32_t* counters;    // [1] = number of m-tiles
   int N, K, G, ng, topk, I;
   int n_nt;                   // n-tiles per m-tile
-  // bias form only: 136 * activation sums per (128-wide k tile, segment
-  // row), [ncr][ldc] -- gate_up: of the routed token rows; down: of the
-  // intermediate rows, written by the gate_up epilogue into cr_out
-  const float* cr;
-  float* cr_out;
-  int ncr, ncr_out;
-  // bias form only: row strides (elements) of act and of the gate_up output;
-  // rows hold each 128-wide k tile with its 16-byte chunks transposed
-  // (chunk 4 kb + s of the tile stored at 4 s + kb); ldc = the tile stride
-  // of the correction tables, which are [tile][segment row]
-  int lda, ldo, ldc;
+  // exact-form kernel: row strides (elements) of act and of the gate_up output
+  int lda, ldo;
   // the work queues of this launch, 9 ints (one counter per XCD, then the
   // count of workgroups that have left), zero at launch
   int32_t* queues;
@@ -78,6 +69,16 @@ struct PrefillArgs {
 
 enum DecodeMode { kModeDense = 0, kModeGateUp = 1, kModeDown = 2 };
 
+// The decode-size kernels' arithmetic.  Exact (the default): the weights
+// dequantised to bf16_RNE(q * s) as the reference does, then bf16 MFMA with
+// fp32 accumulation.  Bias form (built with W4A16_DECODE_BIAS_FORM=1): the
+// weights as bf16(128 + u) and the group scale applied to the fp32 group sum
+// -- fewer instructions, but without the reference's rounding of q * s.
+#ifndef W4A16_DECODE_BIAS_FORM
+#define W4A16_DECODE_BIAS_FORM 0
+#endif
+constexpr bool kDecodeBiasForm = W4A16_DECODE_BIAS_FORM != 0;
+
 // Arguments of the fused down projection + weighted combine for decode
 // sizes (kernels_down_combine.hip).
 constexpr int kDownCombineMaxRows = 64;
@@ -92,6 +93,11 @@ struct DownCombineArgs {
   const float* topk_w;        // [M, k]
   uint16_t* out;              // [M, N]
   int M, topk, E, N, K, G, ng;
+  // nullable: the down streamer's tiled copy of the weights (k_tile_decode),
+  // read in place of wp; its TPW, block and per-expert bytes
+  const int32_t* wt;
+  int tpw, block_bytes;
+  int64_t expert_bytes;
 };
 
 // Arguments of the BF16 experts' grouped GEMMs (kernels_bf16_experts.hip).
@@ -108,15 +114,16 @@ struct Bf16ExpertArgs {
 
 hipError_t launch_dequant(const int32_t* packed, const uint16_t* scale, uint16_t* out,
                           int64_t rows, int K, int G, hipStream_t s);
-hipError_t launch_bias_order(const uint16_t* x, uint16_t* xp, int64_t rows, int K, hipStream_t s);
 // max_slots: upper bound of active experts (1 for dense)
 hipError_t launch_decode(int mode, bool bias_form, DecodeArgs a, int max_slots, hipStream_t s);
 // Tiled expert weights for the decode streamers (kernels_decode.hip): bytes
 // per expert of the tiled copy of the gate_up (mode kModeGateUp) or down
-// weights (0: no tiled form for H, I), the copy, and the streamer reading it
-// (group size 128).
-size_t tiled_decode_bytes_per_expert(int mode, int64_t H, int64_t I);
-hipError_t launch_tile_decode(int mode, const int32_t* packed, int E, int H, int I, int32_t* tiled, hipStream_t s);
+// weights for group size G (0: no tiled form for H, I, G), whether that copy
+// carries the group scales too, the copy, and the streamer reading it.
+size_t tiled_decode_bytes_per_expert(int mode, int64_t H, int64_t I, int64_t G);
+bool tiled_decode_needs_scale(int G);
+hipError_t launch_tile_decode(int mode, const int32_t* packed, const uint16_t* scale, int E, int H, int I, int G,
+                              int32_t* tiled, hipStream_t s);
 hipError_t launch_decode_tiled(int mode, DecodeArgs a, int max_slots, hipStream_t s);
 // x = bf16(h + delta) -> h_out (delta may be null), y = bf16(rms_norm(x) * w)
 hipError_t launch_add_rms_norm(const uint16_t* h, const uint16_t* delta, const uint16_t* w,
@@ -124,10 +131,16 @@ hipError_t launch_add_rms_norm(const uint16_t* h, const uint16_t* delta, const u
                                hipStream_t s);
 hipError_t launch_combine(const uint16_t* dn, const int64_t* idx, const float* w, uint16_t* out,
                           int M, int topk, int E, int H, hipStream_t s);
-// down + combine in one launch: M <= 16, M * topk <= kDownCombineMaxRows,
-// K <= 768 and a multiple of 32; bias_form as for the decode streamer
+// down + combine in one launch: M * topk <= kDownCombineMaxRows,
+// K <= 768 and a multiple of 32; the intermediate rows in bias order (as the
+// decode gate_up writes them); the weights in the packed layout (a.wt NULL:
+// bias form for group sizes that are multiples of 128, else the exact form)
+// or the down streamer's tiled copy (a.wt; group size 128, 32 or 64)
 bool down_combine_supported(int64_t M, int64_t topk, int64_t K);
-hipError_t launch_down_combine(bool bias_form, DownCombineArgs a, hipStream_t s);
+hipError_t launch_down_combine(DownCombineArgs a, hipStream_t s);
+// the down streamer's tiled-copy shape for (H, I, G): TPW, block bytes and
+// bytes per expert (false where there is none)
+bool tiled_decode_down_geometry(int64_t H, int64_t I, int64_t G, int* tpw, int* block_bytes, int64_t* expert_bytes);
 // The expert sort; with `queues` (nullable) it also zeroes the
 // kPrefillQueueInts prefill work-queue counters there.
 hipError_t launch_sort(const int64_t* idx, int M, int topk, int E, int32_t* sorted_pos,
@@ -154,7 +167,8 @@ int router_tok_splits(int64_t M, int64_t E);
 hipError_t launch_router_tok(const uint16_t* h, const uint16_t* scale, float scalar_root,
                              float eps, const uint16_t* proj, float* inv, float* partial, int M,
                              int H, int E, hipStream_t s);
-// top-k and expert sort in one workgroup, M * topk <= 512
+// top-k and expert sort in one workgroup, M * topk <= 64, the decode router's
+// kRouterMaxSplit partials
 hipError_t launch_topk_sort(const float* partial, int ksplit, const uint16_t* per_expert_scale,
                             int64_t* idx, float* w, int M, int E, int topk, int32_t* sorted_pos,
                             int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
@@ -194,19 +208,6 @@ hipError_t launch_ffn_post(const uint16_t* mlp, const uint16_t* moe, const uint1
 hipError_t launch_bf16_experts(int mode, Bf16ExpertArgs a, int max_slots, hipStream_t s);
 // prefill grouped GEMM: one launch per stage, items = (m-tile, n-tile)
 hipError_t launch_prefill(int mode, PrefillArgs a, int max_mtiles, hipStream_t s);
-// the bias-form prefill GEMM (group size a multiple of 128) and the pass that
-// writes its gate_up inputs: xb = x in bias order with each 128-wide k tile's
-// chunks transposed, row stride ldx; crx = 136 * the sums of each row's k
-// tiles ([K / 128][M]) and crs = those sums in expert-segment order
-// ([K / 128][ldc]); K a multiple of 128
-// It also zeroes `queues` (kPrefillQueueInts ints: the gate_up and down
-// kernels' work queues).
-hipError_t launch_prefill_prep(const uint16_t* x, uint16_t* xb, float* crx, int M, int K, int ldx,
-                               const int32_t* sorted_pos, const int32_t* rows_total, int topk,
-                               float* crs, int ldc, int32_t* queues, hipStream_t s);
-// the bias-form prefill kernels stage each item's scales in LDS: they take
-// an even number of scale groups per row, at most 24
-bool prefill_bias_supported(int ng);
 // the exact-form prefill GEMM (kernels_prefill_x.hip): H and I multiples of
 // 64, G a power of two >= 32; items of up to kPrefillXBM rows
 bool prefill_x_supported(int64_t H, int64_t I, int64_t G);
@@ -217,7 +218,8 @@ hipError_t launch_prefill_x(int mode, PrefillArgs a, int max_mtiles, hipStream_t
 size_t prefill_tiled_bytes_per_expert(int mode, int64_t H, int64_t I);
 hipError_t launch_tile_prefill(int mode, const int32_t* packed, int E, int H, int I, int32_t* tiled,
                                hipStream_t s);
-hipError_t launch_prefill_bias(int mode, PrefillArgs a, int max_mtiles, hipStream_t s);
+// persistent prefill grid: the workgroups that fit at once (a multiple of the
+// 8 XCDs), at most max_items
 int prefill_grid_size(const void* kern, int threads, size_t lds, int max_items);
 
 }  // namespace w4a16

@@ -29,8 +29,7 @@ class _Layer:
     router: synth.RouterWeights
     experts: synth.MoEWeights
     pre_norm: torch.Tensor  # RMSNorm weight of the MoE input (bf16 [H])
-    gu_tiled: torch.Tensor | None = None  # the decode streamers' tiled weight copies
-    dn_tiled: torch.Tensor | None = None
+    tiles: _lib.TiledWeights | None = None  # the decode streamers' tiled weight copies
 
 
 class LatentStack:
@@ -45,8 +44,9 @@ class LatentStack:
             ew = synth.moe_weights(E, H, I, group_size, seed=seed + 31 * i + 7, device=dev)
             pre = (1.0 + 0.05 * torch.randn(H, generator=g, device=dev)).to(torch.bfloat16)
             ly = _Layer(rw, ew, pre)
-            if tiled and group_size == 128 and dev.type == "cuda":
-                ly.gu_tiled, ly.dn_tiled = _lib.tile_gate_up(ew.gate_up_packed), _lib.tile_down(ew.down_packed)
+            if tiled and dev.type == "cuda":
+                ly.tiles = _lib.tile_experts(ew.gate_up_packed, ew.gate_up_scale, ew.down_packed, ew.down_scale,
+                                             group_size, decode=True, prefill=False)
             self.layers.append(ly)
         std = 1.0 / math.sqrt(H)
         mk = lambda *s, sc=1.0: (sc * torch.randn(*s, generator=g, device=dev)).to(torch.bfloat16)
@@ -73,8 +73,7 @@ class LatentStack:
         rw, ew = ly.router, ly.experts
         out, w, idx = _lib.moe_layer_forward(h, rw.scale, rw.scalar_root, rw.proj, rw.per_expert_scale,
                                              rw.eps, self.top_k, xin, ew.gate_up_packed, ew.gate_up_scale,
-                                             ew.down_packed, ew.down_scale, group_size=self.G,
-                                             gu_tiled=ly.gu_tiled, dn_tiled=ly.dn_tiled)
+                                             ew.down_packed, ew.down_scale, group_size=self.G, tiles=ly.tiles)
         return out, idx, w
 
     def layer(self, h: torch.Tensor, i: int):

@@ -147,34 +147,38 @@ class Gemma4TextExperts4Bit(nn.Module):
         top_k_index: torch.Tensor,
         top_k_weights: torch.Tensor,
     ) -> torch.Tensor:
-        """[T, H] bf16 -> [T, H] bf16 (quantization.py:225-240); GPU only, zero-sync."""
-        tiles = getattr(self, "_tiles", None)
-        if tiles:
-            return _lib.moe_forward(hidden_states, top_k_index, top_k_weights, self.gate_up_packed,
-                                    self.gate_up_scale, self.down_packed, self.down_scale, self.group_size,
-                                    **tiles)
+        """[T, H] bf16 -> [T, H] bf16 (quantization.py:225-240); GPU only, zero-sync.
+        Reads the tiled weight copies when ``tile_weights`` made them."""
         return fused_triton_4bit_moe_forward(
             hidden_states, top_k_index, top_k_weights,
             self.gate_up_packed, self.gate_up_scale, self.down_packed, self.down_scale)
 
-    def tile_weights(self) -> None:
-        """Build the kernels' tiled copies of the loaded expert weights (opt-in; no
-        counterpart in the reference): the decode streamers read them as contiguous KiBs
-        and the prefill GEMMs as 8 KiB blocks, with bit-identical results.  They take
-        about twice the experts' memory; the buffers and the state dict are
-        unchanged.  Call after the weights are loaded, on their device; reloading or
-        moving the weights needs another call (``untile_weights`` drops them)."""
-        gu, dn = self.gate_up_packed, self.down_packed
-        self._tiles = {
-            "gu_tiled": _lib.tile_gate_up(gu) if self.group_size == 128 else None,
-            "dn_tiled": _lib.tile_down(dn) if self.group_size == 128 else None,
-            "gu_ptiled": _lib.tile_prefill(gu, "gate_up"),
-            "dn_ptiled": _lib.tile_prefill(dn, "down"),
-        }
+    def tile_weights(self, decode: bool = True, prefill: bool = True) -> None:
+        """Build the kernels' tiled copies of the loaded expert weights (no counterpart
+        in the reference): the decode streamers read them as contiguous KiBs (group
+        size 128, 32 or 64) and the prefill GEMMs as 8 KiB blocks.  Every forward on
+        these buffers then uses them -- this module's, ``fused_triton_4bit_moe_forward``,
+        the ``hybrid_agent::fused_4bit_moe`` op and ``ffn_moe_4bit_step`` -- with
+        bit-identical results.  They take about
+        one more copy of the experts' memory per kind; the buffers and the state dict
+        are unchanged.  Call after the weights are loaded, on their device; when the
+        buffers are changed in place (a reload) or replaced (moved), the copies are
+        dropped at the next forward and the packed weights serve until this is called
+        again."""
+        tw = _lib.tile_experts(self.gate_up_packed, self.gate_up_scale, self.down_packed, self.down_scale,
+                               self.group_size, decode=decode, prefill=prefill)
+        _lib.register_tiles(self.gate_up_packed, self.gate_up_scale, self.down_packed, self.down_scale, tw)
+        self._tiles = tw
 
     def untile_weights(self) -> None:
         """Drop the tiled copies made by ``tile_weights``."""
+        _lib.unregister_tiles(self.gate_up_packed)
         self._tiles = None
+
+    @property
+    def tiles(self) -> "_lib.TiledWeights | None":
+        """The tiled copies in use for the current buffers, or None."""
+        return _lib.lookup_tiles(self.gate_up_packed, self.gate_up_scale, self.down_packed, self.down_scale)
 
 
 def is_pack_quantized_dir(model_dir: Path) -> bool:
@@ -201,6 +205,7 @@ def load_pack_quantized_backbone(
     dtype: torch.dtype = torch.bfloat16,
     trust_remote_code: bool = False,
     device: str | torch.device | None = None,
+    tile: bool = False,
 ) -> nn.Module:
     """Instantiate Gemma4ForConditionalGeneration with 4-bit experts and stream the
     compressed-tensors shards into it (quantization.py:325-430).
@@ -210,7 +215,9 @@ def load_pack_quantized_backbone(
     each shard is read into pinned host memory, copied to the device whole and
     written from there into the module tensors (experts straight into their
     slices of the stacked buffers); without it everything stays on the CPU,
-    as in the reference.
+    as in the reference.  ``tile`` (with a GPU ``device``) also builds every
+    experts module's tiled weight copies (``Gemma4TextExperts4Bit.tile_weights``),
+    so the decode and prefill kernels read them from the first forward on.
     """
     from transformers import AutoConfig, AutoModelForCausalLM
     from transformers.models.gemma4 import modeling_gemma4
@@ -245,4 +252,9 @@ def load_pack_quantized_backbone(
     loader.stream_shards(loader.shard_files(model_dir), placer, targets, dev)
     if getattr(config, "tie_word_embeddings", True):
         backbone.tie_weights()
+    if tile:
+        if dev.type != "cuda":
+            raise ValueError("tile=True needs a GPU device: the tiled copies live next to the weights")
+        for ly in layers:
+            ly.experts.tile_weights()
     return backbone

@@ -211,78 +211,71 @@ W4A16_API int moe_layer_forward(const uint16_t* router_in, const uint16_t* route
                       size_t workspace_bytes, void* stream);
 
 /* Tiled weight copies: load-time copies of an expert stack's packed weights
- * (the layout the checkpoint loader writes, quantization.py:325-430) in
- * the order a kernel reads them, so each of its load instructions reads one
+ * (the layout the checkpoint loader writes, quantization.py:325-430) in the
+ * order a kernel reads them, so each of its load instructions reads one
  * contiguous KiB instead of 16 or 32 bytes of many rows.  The reference keeps
  * one layout; these copies are extra (their own buffers; the packed tensors
- * are left as they are and still serve every path).
- *   w4a16_tiled_gate_up_bytes  bytes of the decode gate_up streamer's copy
- *                              of gate_up_packed, 0 where the streamer has
- *                              no tiled form for (H, I) (its long-K loop);
- *   w4a16_tile_gate_up         writes it;
- *   w4a16_tiled_down_bytes,    the same for the decode down streamer and
- *   w4a16_tile_down            down_packed;
- *   w4a16_tiled_prefill_bytes  bytes of the prefill GEMM's copy of
- *                              gate_up_packed (which = 0) or down_packed
- *                              (which = 1), 0 where that kernel does not
- *                              serve (H, I);
- *   w4a16_tile_prefill         writes it;
- *   moe_gate_up_tiled          moe_gate_up reading gu_tiled (decode sizes,
- *                              group size 128) and gu_ptiled (the exact-form
- *                              prefill GEMM) where they apply and are not
- *                              NULL, gu_packed elsewhere;
- *   moe_down_tiled             moe_down reading dn_tiled (decode sizes,
- *                              group size 128) and dn_ptiled likewise;
- *   moe_forward_tiled          moe_forward (fused_triton_4bit_moe_forward,
- *                              quantization.py:88-129) through the two above;
- *   moe_layer_forward_tiled    moe_layer_forward (backends.py:111-122)
- *                              through the two above;
- *   moe_ffn_block_forward_tiled moe_ffn_block_forward (backends.py:77-126)
- *                              with its experts through them.
- * The copy functions return W4A16_ERR_SHAPE when the bytes are 0 and
- * W4A16_ERR_WORKSPACE when tiled_bytes is short; the forwards give output
- * bit-identical to the untiled calls.                                      */
-W4A16_API size_t w4a16_tiled_gate_up_bytes(int64_t E, int64_t H, int64_t I);
-W4A16_API int w4a16_tile_gate_up(const int32_t* gu_packed, int64_t E, int64_t H, int64_t I, int32_t* tiled,
-                                 size_t tiled_bytes, void* stream);
-W4A16_API size_t w4a16_tiled_down_bytes(int64_t E, int64_t H, int64_t I);
-W4A16_API int w4a16_tile_down(const int32_t* dn_packed, int64_t E, int64_t H, int64_t I, int32_t* tiled,
-                              size_t tiled_bytes, void* stream);
-W4A16_API size_t w4a16_tiled_prefill_bytes(int which, int64_t E, int64_t H, int64_t I);
-W4A16_API int w4a16_tile_prefill(int which, const int32_t* packed, int64_t E, int64_t H, int64_t I,
-                                 int32_t* tiled, size_t tiled_bytes, void* stream);
-W4A16_API int moe_gate_up_tiled(const uint16_t* hidden, const int32_t* gu_packed, const int32_t* gu_tiled,
-                                const int32_t* gu_ptiled, const uint16_t* gu_scale, int64_t M, int64_t top_k,
-                                int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
-                                size_t workspace_bytes, void* stream);
-W4A16_API int moe_down_tiled(const int32_t* dn_packed, const int32_t* dn_tiled, const int32_t* dn_ptiled,
-                             const uint16_t* dn_scale, int64_t M, int64_t top_k, int64_t E, int64_t H,
-                             int64_t I, int64_t group_size, void* workspace, size_t workspace_bytes,
-                             void* stream);
+ * are left as they are and still serve every path).  Kinds:
+ *   W4A16_TILED_GATE_UP_DECODE / _DOWN_DECODE
+ *       the decode streamers' copies of gate_up_packed / down_packed, for
+ *       group size 128 (an even group count per row) or 32 / 64; at 32 and
+ *       64 the copy also holds the rows' group scales (taken from `scale`),
+ *       laid out so each lane loads the scales of its own weight chunks in
+ *       one 16-byte read beside them;
+ *   W4A16_TILED_GATE_UP_PREFILL / _DOWN_PREFILL
+ *       the exact-form prefill GEMM's copies (any group size; `scale` unused).
+ *   w4a16_tiled_bytes  bytes of a copy of `kind` for (E, H, I, group_size),
+ *                      0 where the kernel that reads it has no tiled form;
+ *   w4a16_tile         writes it (W4A16_ERR_SHAPE where the bytes are 0,
+ *                      W4A16_ERR_WORKSPACE when tiled_bytes is short).
+ * A w4a16_tiled_experts names the copies of one expert stack and the shape
+ * they were made for; the *_tiled entry points below take one (NULL: none)
+ * and check it before any launch: E, H, I and group_size must equal the
+ * call's (else W4A16_ERR_SHAPE), every non-NULL copy must exist for that
+ * shape (W4A16_ERR_SHAPE) and hold at least w4a16_tiled_bytes() bytes
+ * (W4A16_ERR_WORKSPACE), 16-byte aligned (W4A16_ERR_ALIGN).  A NULL copy
+ * leaves its kernel on the packed tensors; each copy serves the kernels that
+ * read it where they run (decode or prefill sizes).  Results are
+ * bit-identical to the untiled calls.
+ *   moe_gate_up_tiled, moe_down_tiled    the stage calls (moe_gate_up, moe_down);
+ *   moe_forward_tiled                    moe_forward (fused_triton_4bit_moe_forward,
+ *                                        quantization.py:88-129);
+ *   moe_layer_forward_tiled              moe_layer_forward (backends.py:111-122);
+ *   moe_ffn_block_forward_tiled          moe_ffn_block_forward (backends.py:77-126).  */
+enum w4a16_tiled_kind {
+  W4A16_TILED_GATE_UP_DECODE = 0,
+  W4A16_TILED_DOWN_DECODE = 1,
+  W4A16_TILED_GATE_UP_PREFILL = 2,
+  W4A16_TILED_DOWN_PREFILL = 3
+};
+typedef struct w4a16_tiled_experts {
+  int64_t E, H, I, group_size;      /* the expert stack the copies were made from */
+  const int32_t* gu_decode;  size_t gu_decode_bytes;   /* W4A16_TILED_GATE_UP_DECODE or NULL */
+  const int32_t* dn_decode;  size_t dn_decode_bytes;   /* W4A16_TILED_DOWN_DECODE or NULL */
+  const int32_t* gu_prefill; size_t gu_prefill_bytes;  /* W4A16_TILED_GATE_UP_PREFILL or NULL */
+  const int32_t* dn_prefill; size_t dn_prefill_bytes;  /* W4A16_TILED_DOWN_PREFILL or NULL */
+} w4a16_tiled_experts;
+W4A16_API size_t w4a16_tiled_bytes(int kind, int64_t E, int64_t H, int64_t I, int64_t group_size);
+W4A16_API int w4a16_tile(int kind, const int32_t* packed, const uint16_t* scale, int64_t E, int64_t H, int64_t I,
+                         int64_t group_size, int32_t* tiled, size_t tiled_bytes, void* stream);
+W4A16_API int moe_gate_up_tiled(const uint16_t* hidden, const int32_t* gu_packed, const uint16_t* gu_scale,
+                                const w4a16_tiled_experts* tiled, int64_t M, int64_t top_k, int64_t E, int64_t H,
+                                int64_t I, int64_t group_size, void* workspace, size_t workspace_bytes,
+                                void* stream);
+W4A16_API int moe_down_tiled(const int32_t* dn_packed, const uint16_t* dn_scale, const w4a16_tiled_experts* tiled,
+                             int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t group_size,
+                             void* workspace, size_t workspace_bytes, void* stream);
 W4A16_API int moe_forward_tiled(const uint16_t* hidden, const int64_t* topk_idx, const float* topk_w,
-                                const int32_t* gu_packed, const int32_t* gu_tiled, const int32_t* gu_ptiled,
-                                const uint16_t* gu_scale, const int32_t* dn_packed, const int32_t* dn_tiled,
-                                const int32_t* dn_ptiled, const uint16_t* dn_scale, uint16_t* out, int64_t M,
-                                int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t group_size,
+                                const int32_t* gu_packed, const uint16_t* gu_scale, const int32_t* dn_packed,
+                                const uint16_t* dn_scale, const w4a16_tiled_experts* tiled, uint16_t* out,
+                                int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t group_size,
                                 void* workspace, size_t workspace_bytes, void* stream);
-W4A16_API int moe_ffn_block_forward_tiled(
-    const uint16_t* residual, const uint16_t* attn_out, const uint16_t* post_attn_ln_w, const uint16_t* pre_ff_ln_w,
-    const uint16_t* mlp_gate_w, const uint16_t* mlp_up_w, const uint16_t* mlp_down_w, const uint16_t* post_ff_ln1_w,
-    const uint16_t* router_scale, float router_scalar_root, const uint16_t* router_proj_w,
-    const uint16_t* router_per_expert_scale, const uint16_t* pre_ff_ln2_w, const int32_t* gu_packed,
-    const int32_t* gu_tiled, const int32_t* gu_ptiled, const uint16_t* gu_scale, const int32_t* dn_packed,
-    const int32_t* dn_tiled, const int32_t* dn_ptiled, const uint16_t* dn_scale, const uint16_t* post_ff_ln2_w,
-    const uint16_t* post_ff_ln_w, const uint16_t* layer_scalar, float eps, uint16_t* out, int64_t M, int64_t top_k,
-    int64_t E, int64_t H, int64_t I, int64_t Im, int64_t group_size, void* workspace, size_t workspace_bytes,
-    void* stream);
 W4A16_API int moe_layer_forward_tiled(const uint16_t* router_in, const uint16_t* router_scale,
                                       float scalar_root, const uint16_t* proj_w,
                                       const uint16_t* per_expert_scale, float eps, const uint16_t* hidden,
-                                      const int32_t* gu_packed, const int32_t* gu_tiled,
-                                      const int32_t* gu_ptiled, const uint16_t* gu_scale,
-                                      const int32_t* dn_packed, const int32_t* dn_tiled,
-                                      const int32_t* dn_ptiled, const uint16_t* dn_scale, uint16_t* out,
-                                      int64_t* topk_idx,
+                                      const int32_t* gu_packed, const uint16_t* gu_scale,
+                                      const int32_t* dn_packed, const uint16_t* dn_scale,
+                                      const w4a16_tiled_experts* tiled, uint16_t* out, int64_t* topk_idx,
                                       float* topk_w, int64_t M, int64_t top_k, int64_t E, int64_t H,
                                       int64_t I, int64_t group_size, void* workspace,
                                       size_t workspace_bytes, void* stream);
@@ -336,6 +329,25 @@ W4A16_API int moe_ffn_block_forward(const uint16_t* residual, const uint16_t* at
                           uint16_t* out, int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I,
                           int64_t Im, int64_t group_size, void* workspace, size_t workspace_bytes,
                           void* stream);
+/* moe_ffn_block_forward with the experts' tiled weight copies (see
+ * w4a16_tiled_experts above; NULL: none).                                  */
+W4A16_API int moe_ffn_block_forward_tiled(
+    const uint16_t* residual, const uint16_t* attn_out, const uint16_t* post_attn_ln_w, const uint16_t* pre_ff_ln_w,
+    const uint16_t* mlp_gate_w, const uint16_t* mlp_up_w, const uint16_t* mlp_down_w, const uint16_t* post_ff_ln1_w,
+    const uint16_t* router_scale, float router_scalar_root, const uint16_t* router_proj_w,
+    const uint16_t* router_per_expert_scale, const uint16_t* pre_ff_ln2_w, const int32_t* gu_packed,
+    const uint16_t* gu_scale, const int32_t* dn_packed, const uint16_t* dn_scale, const w4a16_tiled_experts* tiled,
+    const uint16_t* post_ff_ln2_w, const uint16_t* post_ff_ln_w, const uint16_t* layer_scalar, float eps,
+    uint16_t* out, int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t Im, int64_t group_size,
+    void* workspace, size_t workspace_bytes, void* stream);
+/* Where moe_ffn_block_forward[_tiled] leaves, in its workspace, the routing
+ * its router step took (backends.py:111-117): top_k_index int64 [M, top_k]
+ * at byte *idx_offset and top_k_weights float32 [M, top_k] at *w_offset,
+ * valid after the call until the workspace is reused.  The reference's
+ * compiled block keeps them internal; this lets a caller (or a test) read
+ * the routing each output row used.                                        */
+W4A16_API int moe_ffn_block_routing_offsets(int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I,
+                                            int64_t Im, size_t* idx_offset, size_t* w_offset);
 
 #ifdef __cplusplus
 }

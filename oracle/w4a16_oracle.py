@@ -47,6 +47,11 @@ Pinning (what checks this restatement, see ``tests/test_oracle.py``):
   weights it equals ``moe_forward`` bit for bit (the dequantise-then-matmul
   identity); the torch CPU restatement of ``_bf16_experts_fast_forward``
   (``oracle/torch_cpu.py``) on identical inputs.
+* ``moe_forward_fp32`` (every intermediate unrounded): a float64 brute-force
+  loop over (token, slot, output) on tiny shapes; it stays within the
+  tolerance of ``moe_forward`` (the two differ only by bf16 roundings);
+  ``moe_forward_fp32_dequantized`` equals it bit for bit on the
+  ``dequantize_fp32`` weights.
 * ``ffn_block``: the same lines of ``_ffn_moe_4bit_step`` written with torch CPU
   ``F.rms_norm`` / ``F.linear`` / ``F.gelu`` / ``softmax`` + ``topk`` and the
   torch-CPU experts (``oracle/torch_cpu.py``) on identical inputs; a
@@ -69,6 +74,7 @@ __all__ = [
     "rms_norm", "router_logits", "topk_from_logits", "router",
     "sort_permute", "moe_forward", "max_abs_rel", "hybridlink",
     "layer_norm", "gelu_erf", "ffn_block", "moe_forward_bf16",
+    "dequantize_fp32", "gelu_tanh_fp32", "moe_forward_fp32", "moe_forward_fp32_dequantized",
 ]
 
 
@@ -228,7 +234,7 @@ def layer_norm(x, weight, bias, eps: float = 1e-5) -> np.ndarray:
 def ffn_block(residual, attn_out, post_attn_ln_w, pre_ff_ln_w, mlp_gate_w, mlp_up_w, mlp_down_w,
               post_ff_ln1_w, router_scale, router_scalar_root, router_proj_w, router_per_expert_scale,
               pre_ff_ln2_w, gu_packed, gu_scale, dn_packed, dn_scale, post_ff_ln2_w, post_ff_ln_w,
-              layer_scalar, eps, top_k, G, return_routing: bool = False):
+              layer_scalar, eps, top_k, G, return_routing: bool = False, routing=None):
     """The post-attention FFN block ``_ffn_moe_4bit_step`` (backends.py:101-126), bf16
     rounding after every op as the eager torch ops round:
 
@@ -241,6 +247,9 @@ def ffn_block(residual, attn_out, post_attn_ln_w, pre_ff_ln_w, mlp_gate_w, mlp_u
 
     Dense weights are bf16 values [out, in] (nn.Linear layout); ``layer_scalar``
     is one bf16 value.  Inputs/outputs are bf16 values held as float32.
+    ``routing`` = (top_k_index, top_k_weights) replaces the router's decision
+    (a row whose 8th and 9th logits are one rounding apart can go either way;
+    with the routing a kernel took, every row is checkable).
     """
     h = rms_norm(attn_out, post_attn_ln_w, eps)
     res = bf16_round(np.asarray(residual, np.float32) + h)
@@ -249,8 +258,11 @@ def ffn_block(residual, attn_out, post_attn_ln_w, pre_ff_ln_w, mlp_gate_w, mlp_u
     up = _matmul_bf16(h_ff, mlp_up_w)
     h_mlp = _matmul_bf16(bf16_round(gate * up), mlp_down_w)
     h_1 = rms_norm(h_mlp, post_ff_ln1_w, eps)
-    _, idx, w = router(res, router_scale, router_scalar_root, router_proj_w, router_per_expert_scale, eps,
-                       top_k)
+    if routing is None:
+        _, idx, w = router(res, router_scale, router_scalar_root, router_proj_w, router_per_expert_scale, eps,
+                           top_k)
+    else:
+        idx, w = (np.asarray(routing[0], np.int64), np.asarray(routing[1], np.float32))
     h_2_in = rms_norm(res, pre_ff_ln2_w, eps)
     h_2 = moe_forward(h_2_in, idx, w, gu_packed, gu_scale, dn_packed, dn_scale, G)
     h_2 = rms_norm(h_2, post_ff_ln2_w, eps)
@@ -402,6 +414,64 @@ def moe_forward(hidden, idx, weights, gu_packed, gu_scale, dn_packed, dn_scale, 
     return _moe_core(hidden, idx, weights, E, two_i // 2, dn_packed.shape[1],
                      lambda e, xr: linear(xr, gu_packed[e], gu_scale[e], G),
                      lambda e, ar: linear(ar, dn_packed[e], dn_scale[e], G), path, return_intermediates)
+
+
+def dequantize_fp32(packed, scale_bits, G: int) -> np.ndarray:
+    """q * s in fp32 without the bf16 rounding of the product (exact: |q| <= 8
+    and s has 8 significant bits, so the product needs at most 12)."""
+    q = unpack_int4(packed)
+    K = q.shape[-1]
+    s = from_bf16_bits(scale_bits)
+    s_full = np.repeat(s, G, axis=-1)[..., :K]
+    return q.astype(np.float32) * s_full
+
+
+def gelu_tanh_fp32(x) -> np.ndarray:
+    """F.gelu(x, approximate="tanh") in fp32, not rounded (TF:activations.py:45-48)."""
+    x = np.asarray(x, np.float32)
+    c = np.float32(math.sqrt(2.0 / math.pi))
+    return np.float32(0.5) * x * (np.float32(1.0) + np.tanh(c * (x + np.float32(0.044715) * x * x * x)))
+
+
+def _moe_fp32_core(hidden, idx, weights, E, I, H, gu_of, dn_of) -> np.ndarray:
+    x = np.asarray(hidden, np.float32)
+    idx = np.asarray(idx, np.int64)
+    w = np.asarray(weights, np.float32)
+    M, k = idx.shape
+    y = np.zeros((M, H), np.float32)
+    flat = idx.reshape(-1)
+    for e in np.unique(flat):
+        if e < 0 or e >= E:
+            continue
+        rows = np.nonzero(flat == e)[0]
+        tok = rows // k
+        g = x[tok] @ gu_of(e).T
+        a = gelu_tanh_fp32(g[:, :I]) * g[:, I:]
+        d = a @ dn_of(e).T
+        np.add.at(y, tok, d * w[tok, rows % k][:, None])
+    return y
+
+
+def moe_forward_fp32(hidden, idx, weights, gu_packed, gu_scale, dn_packed, dn_scale, G: int) -> np.ndarray:
+    """The MoE forward of quantization.py:88-129 with every intermediate kept in
+    fp32: weights q * s unrounded, fp32 accumulation, no bf16 rounding of
+    gate_up, GELU, ``gelu * up``, down, the routing weight or the products;
+    output fp32.  The reference's bf16 rounding points (``moe_forward``) are
+    the parity contract; this path measures how far they, and a kernel, sit
+    from the unrounded arithmetic.  Slots whose expert is outside [0, E)
+    contribute nothing."""
+    E, two_i, _ = gu_packed.shape
+    return _moe_fp32_core(hidden, idx, weights, E, two_i // 2, dn_packed.shape[1],
+                          lambda e: dequantize_fp32(gu_packed[e], gu_scale[e], G),
+                          lambda e: dequantize_fp32(dn_packed[e], dn_scale[e], G))
+
+
+def moe_forward_fp32_dequantized(hidden, idx, weights, gu_w, dn_w) -> np.ndarray:
+    """``moe_forward_fp32`` on weights already dequantised by ``dequantize_fp32``
+    (gu_w [E, 2I, H], dn_w [E, H, I] float32), for callers that reuse them."""
+    E, two_i, _ = gu_w.shape
+    return _moe_fp32_core(hidden, idx, weights, E, two_i // 2, dn_w.shape[1], lambda e: gu_w[e],
+                          lambda e: dn_w[e])
 
 
 def moe_forward_bf16(hidden, idx, weights, gate_up_proj, down_proj, path: str = "fused"):

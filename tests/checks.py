@@ -3,6 +3,19 @@ import numpy as np
 
 import oracle
 
+# worst error seen per (config, measure) in this pytest run: the terminal
+# summary (conftest.py) prints them, so a test log shows every margin
+MARGINS = {}
+
+
+def margin(config, err, bound=1e-2, measure="max_abs_rel vs oracle"):
+    """Record ``err`` for ``config`` (the worst one is kept), print it, return it."""
+    key = (config, measure)
+    if key not in MARGINS or err > MARGINS[key][0]:
+        MARGINS[key] = (float(err), bound)
+    print(f"{config}: {measure} = {err:.3e} (bound {bound:g})", flush=True)
+    return err
+
 
 def check_routing_order(got_lg, got_idx, ref_lg, ref_idx, k, what, max_flip_frac=0.05):
     """End-to-end routing against the oracle, in order.

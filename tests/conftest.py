@@ -28,3 +28,19 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+def pytest_terminal_summary(terminalreporter):
+    """The parity margins the tests recorded (checks.margin): the worst error
+    per configuration against its bound."""
+    try:
+        from checks import MARGINS
+    except ImportError:
+        return
+    if not MARGINS:
+        return
+    tr = terminalreporter
+    tr.section("parity margins (worst per config)")
+    for (config, measure), (err, bound) in sorted(MARGINS.items()):
+        frac = err / bound if bound else float("nan")
+        tr.write_line(f"{config:<58} {measure:<34} {err:.3e}  bound {bound:g}  ({100 * frac:5.1f}% of bound)")

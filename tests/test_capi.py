@@ -213,39 +213,92 @@ def test_ffn_block_and_bf16_experts_host_validation(lib):
     assert g(*p9, 0.1, *p10, 1e-6, ctypes.c_void_p(4098), *ok, fake, wsb, NULL) == 4
 
 
-def test_tiled_gate_up_host_side(lib):
-    """Size of the tiled gate_up copy and the validation that returns before any
-    launch (no GPU needed)."""
-    # Gemma shape: 22 column-tile items of 16 wavefronts x 6 KiB tiles per expert
-    assert lib.w4a16_tiled_gate_up_bytes(128, 2816, 704) == 128 * 22 * 16 * 6 * 1024
-    assert lib.w4a16_tiled_gate_up_bytes(1, 2816, 704) == 22 * 16 * 6 * 1024
-    # shapes the streamer runs with its long-K loop have no tiled form; E out
-    # of range neither
-    assert lib.w4a16_tiled_gate_up_bytes(8, 8192, 704) == 0              # long-K loop
-    assert lib.w4a16_tiled_gate_up_bytes(8, 2816, 700) == 0              # I not a multiple of 32
-    # down: 44 items of 4 wavefronts x 6 KiB tiles per expert
-    assert lib.w4a16_tiled_down_bytes(128, 2816, 704) == 128 * 44 * 4 * 6 * 1024
-    assert lib.w4a16_tile_down(None, 2, 2816, 704, ctypes.c_void_p(4096), 1 << 30, None) == 1
-    assert lib.w4a16_tiled_gate_up_bytes(0, 2816, 704) == 0
+GU_DEC, DN_DEC, GU_PRE, DN_PRE = 0, 1, 2, 3
+
+
+def test_tiled_decode_sizes(lib):
+    """Sizes of the decode streamers' tiled copies (no GPU needed)."""
+    tb = lib.w4a16_tiled_bytes
+    # Gemma shape, G = 128: gate_up 22 column-tile items of 16 wavefronts x 6
+    # KiB tiles per expert; down 44 items of 4 wavefronts x 6 KiB
+    assert tb(GU_DEC, 128, 2816, 704, 128) == 128 * 22 * 16 * 6 * 1024
+    assert tb(GU_DEC, 1, 2816, 704, 128) == 22 * 16 * 6 * 1024
+    assert tb(DN_DEC, 128, 2816, 704, 128) == 128 * 44 * 4 * 6 * 1024
+    # G = 32 / 64: each block of 6 tiles carries 16 rows x 6 tiles x 4 step scales
+    for g in (32, 64):
+        assert tb(GU_DEC, 128, 2816, 704, g) == 128 * 22 * 16 * 6 * 1152
+        assert tb(DN_DEC, 128, 2816, 704, g) == 128 * 44 * 4 * 6 * 1152
+    # no tiled decode form: long-K loop, I not a multiple of 32, an odd group
+    # count per row at G = 128, other group sizes, E out of range
+    assert tb(GU_DEC, 8, 8192, 704, 128) == 0
+    assert tb(GU_DEC, 8, 2816, 700, 128) == 0
+    assert tb(GU_DEC, 8, 2816 + 128, 704, 128) == 0     # 23 groups
+    assert tb(GU_DEC, 8, 2816, 704, 256) == 0
+    assert tb(GU_DEC, 0, 2816, 704, 128) == 0
+    assert tb(GU_DEC, 8, 2816, 704, 48) == 0            # not a group size
+    assert tb(7, 8, 2816, 704, 128) == 0                # no such kind
+
+
+def test_tile_host_validation(lib):
     fake = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
-    need = lib.w4a16_tiled_gate_up_bytes(2, 2816, 704)
-    assert lib.w4a16_tile_gate_up(fake, 8, 8192, 704, fake, 1 << 30, NULL) == 2
-    assert lib.w4a16_tile_gate_up(NULL, 2, 2816, 704, fake, need, NULL) == 1
-    assert lib.w4a16_tile_gate_up(fake, 2, 2816, 704, ctypes.c_void_p(4100), need, NULL) == 4
-    assert lib.w4a16_tile_gate_up(fake, 2, 2816, 704, fake, need - 16, NULL) == 5
+    t = lib.w4a16_tile
+    need = lib.w4a16_tiled_bytes(GU_DEC, 2, 2816, 704, 128)
+    assert t(GU_DEC, fake, fake, 8, 8192, 704, 128, fake, 1 << 30, NULL) == 2    # no tiled form
+    assert t(GU_DEC, NULL, fake, 2, 2816, 704, 128, fake, need, NULL) == 1
+    assert t(GU_DEC, fake, fake, 2, 2816, 704, 128, ctypes.c_void_p(4100), need, NULL) == 4
+    assert t(GU_DEC, fake, fake, 2, 2816, 704, 128, fake, need - 16, NULL) == 5
+    assert t(GU_DEC, fake, fake, 2, 2816, 704, 96, fake, need, NULL) == 3        # bad group
+    # G = 32 copies hold the scales: a NULL scale is refused
+    need32 = lib.w4a16_tiled_bytes(DN_DEC, 2, 2816, 704, 32)
+    assert t(DN_DEC, fake, NULL, 2, 2816, 704, 32, fake, need32, NULL) == 1
 
 
 def test_tiled_prefill_host_side(lib):
     """Size of the prefill GEMMs' tiled copies and the validation that returns
     before any launch."""
+    tb = lib.w4a16_tiled_bytes
     # gate_up: 6 n-tiles x 44 k stages x 8 KiB per expert; down: 11 x 11 x 8 KiB
-    assert lib.w4a16_tiled_prefill_bytes(0, 128, 2816, 704) == 128 * 6 * 44 * 8192
-    assert lib.w4a16_tiled_prefill_bytes(1, 128, 2816, 704) == 128 * 11 * 11 * 8192
-    assert lib.w4a16_tiled_prefill_bytes(2, 128, 2816, 704) == 0       # no such matrix
-    assert lib.w4a16_tiled_prefill_bytes(0, 128, 2816, 700) == 0       # I not a multiple of 64
+    assert tb(GU_PRE, 128, 2816, 704, 128) == 128 * 6 * 44 * 8192
+    assert tb(DN_PRE, 128, 2816, 704, 128) == 128 * 11 * 11 * 8192
+    assert tb(DN_PRE, 128, 2816, 704, 32) == 128 * 11 * 11 * 8192     # any group size
+    assert tb(GU_PRE, 128, 2816, 736, 128) == 0       # I not a multiple of 64
     fake = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
-    need = lib.w4a16_tiled_prefill_bytes(1, 2, 2816, 704)
-    assert lib.w4a16_tile_prefill(0, fake, 2, 2816, 700, fake, 1 << 30, NULL) == 2
-    assert lib.w4a16_tile_prefill(1, NULL, 2, 2816, 704, fake, need, NULL) == 1
-    assert lib.w4a16_tile_prefill(1, fake, 2, 2816, 704, ctypes.c_void_p(4100), need, NULL) == 4
-    assert lib.w4a16_tile_prefill(1, fake, 2, 2816, 704, fake, need - 16, NULL) == 5
+    need = tb(DN_PRE, 2, 2816, 704, 128)
+    assert lib.w4a16_tile(GU_PRE, fake, NULL, 2, 2816, 736, 128, fake, 1 << 30, NULL) == 2
+    assert lib.w4a16_tile(DN_PRE, NULL, NULL, 2, 2816, 704, 128, fake, need, NULL) == 1
+    assert lib.w4a16_tile(DN_PRE, fake, NULL, 2, 2816, 704, 128, ctypes.c_void_p(4100), need, NULL) == 4
+    assert lib.w4a16_tile(DN_PRE, fake, NULL, 2, 2816, 704, 128, fake, need - 16, NULL) == 5
+
+
+def test_tiled_experts_descriptor_checks(lib):
+    """The *_tiled entry points check the w4a16_tiled_experts against the call
+    before any launch: the shape tag, each copy's size and alignment."""
+    fake = ctypes.c_void_p(4096)  # never dereferenced: validation fails first
+    E, H, I, G, M, k = 8, 2816, 704, 128, 4, 8
+    ws = lib.moe_workspace_bytes(M, k, E, H, I)
+    need = lib.w4a16_tiled_bytes(GU_DEC, E, H, I, G)
+
+    def call(t):
+        return lib.moe_forward_tiled(fake, fake, fake, fake, fake, fake, fake, ctypes.byref(t), fake,
+                                     M, k, E, H, I, G, fake, ws, NULL)
+
+    def desc(**kw):
+        t = _lib.TiledExpertsC(E, H, I, G)
+        for name, v in kw.items():
+            setattr(t, name, v)
+        return t
+
+    assert call(desc(E=E + 1, gu_decode=4096, gu_decode_bytes=need)) == 2       # made for another stack
+    assert call(desc(group_size=32, gu_decode=4096, gu_decode_bytes=need)) == 2  # another group size
+    assert call(desc(gu_decode=4096, gu_decode_bytes=need - 1)) == 5            # short copy
+    assert call(desc(gu_decode=4100, gu_decode_bytes=need)) == 4                # misaligned
+    # a copy the shape has no tiled form for
+    t = _lib.TiledExpertsC(E, 8192, I, G, 4096, 1 << 30)
+    assert lib.moe_forward_tiled(fake, fake, fake, fake, fake, fake, fake, ctypes.byref(t), fake,
+                                 M, k, E, 8192, I, G, fake, lib.moe_workspace_bytes(M, k, E, 8192, I), NULL) == 2
+    # the FFN block's routing lives at fixed workspace offsets
+    io, wo = ctypes.c_size_t(), ctypes.c_size_t()
+    assert lib.moe_ffn_block_routing_offsets(8, 8, 128, 2816, 704, 2112, ctypes.byref(io), ctypes.byref(wo)) == 0
+    assert wo.value >= io.value + 8 * 8 * 8 and io.value % 256 == 0 and wo.value % 256 == 0
+    assert wo.value + 4 * 64 <= lib.moe_ffn_block_workspace_bytes(8, 8, 128, 2816, 704, 2112)
+    assert lib.moe_ffn_block_routing_offsets(0, 8, 128, 2816, 704, 2112, ctypes.byref(io), ctypes.byref(wo)) == 2

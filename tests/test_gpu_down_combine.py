@@ -75,6 +75,43 @@ def test_fused_invalid_slots(dev, weights):
     assert np.array_equal(_bits(y), _bits(ref))
 
 
+def _repeated_routing(M, k, mode, seed, dev):
+    """Routing where tokens send several k slots to one expert (the reference
+    handles each (token, slot) row on its own, quantization.py:112-129):
+    ``one`` puts every slot of every token on expert 5 (M * k rows on one
+    expert), ``pairs`` gives slots 2i and 2i + 1 of a token the same expert."""
+    g = torch.Generator().manual_seed(seed)
+    if mode == "one":
+        idx = torch.full((M, k), 5, dtype=torch.int64)
+    else:
+        idx = torch.stack([torch.randperm(E, generator=g)[:(k + 1) // 2].repeat_interleave(2)[:k]
+                           for _ in range(M)])
+    w = torch.rand(M, k, generator=g) + 0.05
+    return idx.to(dev), (w / w.sum(1, keepdim=True)).float().to(dev)
+
+
+# an expert with more than 16 routed rows (several slots of one token on it):
+# the fused kernel takes them in 16-row MFMA tiles
+@pytest.mark.parametrize("M,k,mode", [(1, 8, "one"), (3, 8, "one"), (4, 8, "one"), (4, 8, "pairs"),
+                                      (16, 2, "one"), (3, 5, "pairs")])
+def test_fused_repeated_experts(dev, weights, M, k, mode):
+    G, wts, gpu = weights
+    print(f"down+combine repeated experts G={G} M={M} k={k} {mode}", flush=True)
+    x = synth.activations(M, H, seed=4700 + M).to(dev)
+    idx, w = _repeated_routing(M, k, mode, 4701 + M + k, dev)
+    y = _lib.moe_forward(x, idx, w, *gpu, group_size=G)
+    ref = _stages(x, idx, w, G, gpu)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(y), _bits(ref)), f"G={G} M={M} k={k} {mode}: fused down+combine differs"
+    bits = lambda t: t.view(torch.int16).numpy().view(np.uint16)
+    ref_o = oracle.moe_forward(x.float().cpu().numpy(), idx.cpu().numpy(), w.cpu().numpy(),
+                               wts.gate_up_packed.numpy(), bits(wts.gate_up_scale), wts.down_packed.numpy(),
+                               bits(wts.down_scale), G)
+    err = oracle.max_abs_rel(y.float().cpu().numpy(), ref_o)
+    print(f"  max_abs_rel={err:.2e}")
+    assert err <= 1e-2
+
+
 @pytest.mark.parametrize("M", [1, 4])
 def test_fused_against_oracle(dev, weights, M):
     G, wts, gpu = weights

@@ -8,8 +8,9 @@ fed back as the next step's input.
   fed-back second step (hybridlink.py:17-28, backends.py:111-122,
   engine.py:381-390);
 * on three layers of the fed-back step the routing is checked against the
-  oracle router on that layer's own input (ordered, flips counted) and
-  sampled MoE rows against the oracle at max_abs_rel <= 1e-2;
+  oracle router on that layer's own input (ordered, flips counted) and all
+  32 MoE rows against the oracle on the kernel's routing at
+  max_abs_rel <= 1e-2;
 * every output is finite.
 """
 import math
@@ -19,7 +20,7 @@ import pytest
 import torch
 
 import oracle
-from checks import check_routing_order
+from checks import check_routing_order, margin
 from hybridagent_amd import _lib, synth
 from hybridagent_amd.latent import LatentStack
 
@@ -66,7 +67,7 @@ def test_latent_stack_config4_full_shape(dev):
     # HybridLink ends in a LayerNorm: rows have mean ~ bias mean and unit-ish scale before sqrt(H)
     assert 0.5 * math.sqrt(H) < float(out2.float().pow(2).mean().sqrt()) < 2.0 * math.sqrt(H)
 
-    rows = np.array([0, 7, 19, 31])
+    rows = np.arange(B)
     for li in (0, 14, LAYERS - 1):
         ly = st.layers[li]
         rw, ew = ly.router, ly.experts
@@ -80,7 +81,7 @@ def test_latent_stack_config4_full_shape(dev):
         ref_lg, ref_idx, _ = oracle.router(_np(h), _np(rw.scale), rw.scalar_root, _np(rw.proj),
                                            _np(rw.per_expert_scale), rw.eps, K_TOP)
         check_routing_order(_np(lg), idx.cpu().numpy(), ref_lg, ref_idx, K_TOP, f"config4 layer {li} router")
-        # sampled rows against the oracle on the kernel's routing; only the
+        # every row against the oracle on the kernel's routing; only the
         # experts those rows use are copied to the host
         sel = idx.cpu().numpy()[rows]
         used = np.unique(sel)
@@ -90,5 +91,4 @@ def test_latent_stack_config4_full_shape(dev):
                                  ew.gate_up_packed[ut].cpu().numpy(), _bits(ew.gate_up_scale[ut]),
                                  ew.down_packed[ut].cpu().numpy(), _bits(ew.down_scale[ut]), G)
         err = oracle.max_abs_rel(_np(out)[rows], ref)
-        print(f"config4 layer {li}: MoE rows {rows.tolist()} max_abs_rel={err:.2e} ({len(used)} experts)")
-        assert err <= TOL
+        assert margin(f"configs[4] layer {li} MoE (all {B} rows, {len(used)} experts)", err) <= TOL

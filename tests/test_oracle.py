@@ -338,6 +338,78 @@ def test_moe_combine_linear_in_weights():
     assert np.array_equal(y2, 2 * y)
 
 
+def _moe_fp64_bruteforce(x, idx, w, gu, gus, dn, dns, G):
+    """The MoE forward with every product and sum in float64, one scalar at a
+    time: for each (token, slot, output) the dot products written out."""
+    qg = oracle.unpack_int4(gu).astype(np.float64)
+    qd = oracle.unpack_int4(dn).astype(np.float64)
+    sg = from_bf16_bits(gus).astype(np.float64)
+    sd = from_bf16_bits(dns).astype(np.float64)
+    E, two_i, H = qg.shape
+    I = two_i // 2
+    M, k = idx.shape
+    y = np.zeros((M, H))
+    c = math.sqrt(2.0 / math.pi)
+    for t in range(M):
+        for j in range(k):
+            e = idx[t, j]
+            gu_row = np.zeros(two_i)
+            for n in range(two_i):
+                acc = 0.0
+                for kk in range(H):
+                    acc += float(x[t, kk]) * qg[e, n, kk] * sg[e, n, kk // G]
+                gu_row[n] = acc
+            a = np.zeros(I)
+            for i in range(I):
+                g = gu_row[i]
+                a[i] = 0.5 * g * (1.0 + math.tanh(c * (g + 0.044715 * g ** 3))) * gu_row[I + i]
+            for h in range(H):
+                acc = 0.0
+                for i in range(I):
+                    acc += a[i] * qd[e, h, i] * sd[e, h, i // G]
+                y[t, h] += float(w[t, j]) * acc
+    return y
+
+
+def test_moe_fp32_vs_fp64_bruteforce():
+    # G = 32 with H = 64 (two groups per gate_up row) and I = 48 (a partial
+    # last down group); slot 1 of token 2 repeats slot 0's expert
+    x, idx, w, gu, gus, dn, dns = _moe_case(3, E=5, H=64, I=48, k=2, G=32, seed=21)
+    idx[2, 1] = idx[2, 0]
+    got = oracle.moe_forward_fp32(x, idx, w, gu, gus, dn, dns, 32)
+    ref = _moe_fp64_bruteforce(x, idx, w, gu, gus, dn, dns, 32)
+    assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max()
+    # a dropped routing weight, swapped gate/up halves or a transposed group
+    # index each move the result far outside that bound
+    assert np.abs(oracle.moe_forward_fp32(x, idx, np.ones_like(w), gu, gus, dn, dns, 32) - ref).max() > \
+        1e-2 * np.abs(ref).max()
+    I = gu.shape[1] // 2
+    gu_sw = np.concatenate([gu[:, I:], gu[:, :I]], axis=1)
+    gus_sw = np.concatenate([gus[:, I:], gus[:, :I]], axis=1)
+    assert np.abs(oracle.moe_forward_fp32(x, idx, w, gu_sw, gus_sw, dn, dns, 32) - ref).max() > \
+        1e-2 * np.abs(ref).max()
+    gus_rev = gus[:, :, ::-1].copy()
+    assert np.abs(oracle.moe_forward_fp32(x, idx, w, gu, gus_rev, dn, dns, 32) - ref).max() > \
+        1e-3 * np.abs(ref).max()
+
+
+def test_moe_fp32_dequantized_equals_packed_path():
+    x, idx, w, gu, gus, dn, dns = _moe_case(9)
+    a = oracle.moe_forward_fp32(x, idx, w, gu, gus, dn, dns, 64)
+    b = oracle.moe_forward_fp32_dequantized(x, idx, w, oracle.dequantize_fp32(gu, gus, 64),
+                                            oracle.dequantize_fp32(dn, dns, 64))
+    assert np.array_equal(a, b)
+
+
+def test_moe_fp32_within_tolerance_of_bf16_path():
+    # the two paths differ only by the reference's bf16 roundings
+    x, idx, w, gu, gus, dn, dns = _moe_case(24)
+    y_bf16 = oracle.moe_forward(x, idx, w, gu, gus, dn, dns, 64)
+    y_fp32 = oracle.moe_forward_fp32(x, idx, w, gu, gus, dn, dns, 64)
+    err = oracle.max_abs_rel(y_bf16, y_fp32)
+    assert 0 < err < 1e-2
+
+
 # --------------------------------------------------------------------- HybridLink (config-4 harness)
 
 def test_hybridlink_vs_torch_modules():
@@ -470,6 +542,21 @@ def test_ffn_block_vs_torch_ops(M):
     got = _ffn_np(args, G)
     err = oracle.max_abs_rel(got, ref.float().numpy())
     assert err <= 1e-2, err
+
+
+def test_ffn_block_routing_override():
+    # handing the block the routing its own router picks changes nothing;
+    # another routing changes the rows it touches and only those
+    args, G = _ffn_inputs(4)
+    out, idx, w = _ffn_np(args, G, return_routing=True)
+    assert np.array_equal(_ffn_np(args, G, routing=(idx, w)), out)
+    idx2 = idx.copy()
+    idx2[2] = np.roll(idx2[2], 1)
+    w2 = w.copy()
+    w2[2] = w2[2][::-1]
+    alt = _ffn_np(args, G, routing=(idx2, w2))
+    assert np.array_equal(np.delete(alt, 2, 0), np.delete(out, 2, 0))
+    assert not np.array_equal(alt[2], out[2])
 
 
 def test_ffn_block_layer_scalar_scales_exactly():
