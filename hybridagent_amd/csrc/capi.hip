@@ -262,7 +262,6 @@ int w4a16_linear(const uint16_t* x, const int32_t* w_packed, const uint16_t* w_s
   (void)workspace_bytes;
   if (K > kMaxStreamK) return W4A16_ERR_SHAPE;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool bias_form = kDecodeBiasForm && group_size % 128 == 0;
   DecodeArgs a{};
   a.act = x;
   a.wp = w_packed;
@@ -277,7 +276,7 @@ int w4a16_linear(const uint16_t* x, const int32_t* w_packed, const uint16_t* w_s
   a.topk = 1;
   a.I = 0;
   a.rows_hint = (int)(M < 16 ? M : 16);
-  return launch_status(launch_decode(kModeDense, bias_form, a, 1, s));
+  return launch_status(launch_decode(kModeDense, a, 1, s));
 }
 
 size_t moe_router_workspace_bytes(int64_t M, int64_t H, int64_t E) {
@@ -522,7 +521,7 @@ int gate_up_impl(const uint16_t* hidden, const int32_t* gu_packed, const uint16_
     a.wp = t.gu_decode;
     return launch_status(launch_decode_tiled(kModeGateUp, a, max_slots, s));
   }
-  return launch_status(launch_decode(kModeGateUp, kDecodeBiasForm && group_size % 128 == 0, a, max_slots, s));
+  return launch_status(launch_decode(kModeGateUp, a, max_slots, s));
 }
 }  // namespace
 
@@ -622,7 +621,7 @@ static int down_impl(const int32_t* dn_packed, const uint16_t* dn_scale, const T
     a.wp = t.dn_decode;
     return launch_status(launch_decode_tiled(kModeDown, a, max_slots, s));
   }
-  return launch_status(launch_decode(kModeDown, kDecodeBiasForm && group_size % 128 == 0, a, max_slots, s));
+  return launch_status(launch_decode(kModeDown, a, max_slots, s));
 }
 
 int moe_down(const int32_t* dn_packed, const uint16_t* dn_scale, int64_t M, int64_t top_k,

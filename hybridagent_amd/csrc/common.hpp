@@ -4,20 +4,9 @@
 // hybrid_agent/quantization.py:132-137): int32 word p[n, j] holds
 // w[n, 8j+i] for i = 0..7 in bits 4i..4i+3 as offset binary u = q + 8.
 //
-// Two ways of turning a word into a bf16x8 MFMA operand are used:
-//
-//  * "bias" form (decode path, group size a multiple of 128): the bf16 bit
-//    pattern 0x4300 | u is exactly 128 + u, so one v_and_or_b32 per pair
-//    gives two operands.  Pairs come out as (nibble i, nibble i+4), i = 0..3,
-//    so the activation operand must hold its 8-blocks in the order
-//    [0,4,1,5,2,6,3,7] ("bias order").  The MFMA then computes
-//    sum x*(128+u) = sum x*q + 136*sum x; the 136*sum x term is produced by a
-//    second MFMA against a constant-136 operand and removed per group, where
-//    the group scale is applied to the fp32 accumulator.
-//
-//  * "exact" form (prefill path and group sizes below 128): each weight is
-//    dequantised to bf16_RNE(q * s), bit-identical to the reference's
-//    dequantize_int4_packed, in natural K order.
+// Every kernel dequantises exactly: each weight becomes bf16_RNE((u - 8) * s),
+// bit-identical to the reference's dequantize_int4_packed, and enters a bf16
+// MFMA with fp32 accumulation -- the reference's dequantise-then-matmul.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -29,10 +18,6 @@ typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 typedef __attribute__((ext_vector_type(16))) float f32x16_t;
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
-
-// The bias form's per-element offset: 128 + 8 (q = u - 8).
-constexpr uint32_t kBiasPair = 0x43004300u;     // bf16x2 (128, 128)
-constexpr uint32_t kBias136Pair = 0x43084308u;  // bf16x2 (136, 136)
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
   return __uint_as_float(b << 16);
@@ -53,20 +38,6 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 
 __device__ __forceinline__ float round_bf16(float f) {
   return bf16_bits_to_f32(f32_to_bf16_bits(f));
-}
-
-// Bias-form unpack of one packed word: 4 dwords of bf16 pairs
-// (128+u_i, 128+u_{i+4}) for i = 0..3.  `mask` = 0x000F000F and `bias` =
-// 0x43004300 are passed in (already in registers): gfx9 VOP3 instructions take
-// no literal operands, so with register constants each pair is one
-// v_and_or_b32 (7 instructions per word instead of 11).
-__device__ __forceinline__ u32x4_t unpack_bias(uint32_t w, uint32_t mask, uint32_t bias) {
-  u32x4_t r;
-  r.x = (w & mask) | bias;
-  r.y = ((w >> 4) & mask) | bias;
-  r.z = ((w >> 8) & mask) | bias;
-  r.w = ((w >> 12) & mask) | bias;
-  return r;
 }
 
 // p[i] for a wavefront-uniform i, through the scalar data cache (a read of
@@ -105,8 +76,8 @@ __device__ __forceinline__ ExactRegs exact_regs() {
 }
 
 // Exact unpack of one packed word with scale s: 8 values bf16_RNE((u-8)*s).
-// BIAS_ORDER selects the element order: natural (k = 0..7) or bias order
-// (0,4,1,5,2,6,3,7) to pair with bias-ordered activations.
+// PAIRED selects the element order: natural (k = 0..7) or (0,4,1,5,2,6,3,7),
+// the order in which the decode gate_up epilogue writes intermediate rows.
 //
 // Each nibble becomes an fp16 with exponent 2^10 by OR-ing it into the
 // mantissa: nibbles 0/4 and 2/6 (the latter after >> 8) sit at mantissa bits
@@ -120,7 +91,7 @@ __device__ __forceinline__ ExactRegs exact_regs() {
 // each), so the single rounding returns (u-8)*s exactly, which
 // v_cvt_pk_bf16_f32 rounds to bf16 (RNE).  Valid for |s| < 2^118, where
 // 1032 s stays finite (bf16 group scales of quantized weights are far below).
-template <bool BIAS_ORDER>
+template <bool PAIRED>
 __device__ __forceinline__ u32x4_t unpack_exact(uint32_t w, const ExactScale& es, const ExactRegs& k) {
   typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
   const uint32_t w8 = w >> 8;
@@ -137,7 +108,7 @@ __device__ __forceinline__ u32x4_t unpack_exact(uint32_t w, const ExactScale& es
   const float v3 = __builtin_fmaf((float)p3.x, es.s16, es.c1);
   const float v7 = __builtin_fmaf((float)p3.y, es.s16, es.c1);
   u32x4_t r;
-  if (BIAS_ORDER) {
+  if (PAIRED) {
     r.x = pack_bf16x2(v0, v4);
     r.y = pack_bf16x2(v1, v5);
     r.z = pack_bf16x2(v2, v6);
@@ -148,17 +119,6 @@ __device__ __forceinline__ u32x4_t unpack_exact(uint32_t w, const ExactScale& es
     r.z = pack_bf16x2(v4, v5);
     r.w = pack_bf16x2(v6, v7);
   }
-  return r;
-}
-
-// Natural-order 8-block of bf16 (4 dwords) -> bias order [0,4,1,5,2,6,3,7].
-__device__ __forceinline__ u32x4_t to_bias_order(u32x4_t d) {
-  // d.x=(x0,x1) d.y=(x2,x3) d.z=(x4,x5) d.w=(x6,x7)
-  u32x4_t r;
-  r.x = __builtin_amdgcn_perm(d.z, d.x, 0x05040100u);  // (x0, x4)
-  r.y = __builtin_amdgcn_perm(d.z, d.x, 0x07060302u);  // (x1, x5)
-  r.z = __builtin_amdgcn_perm(d.w, d.y, 0x05040100u);  // (x2, x6)
-  r.w = __builtin_amdgcn_perm(d.w, d.y, 0x07060302u);  // (x3, x7)
   return r;
 }
 

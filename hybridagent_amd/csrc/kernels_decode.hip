@@ -2,7 +2,7 @@
 // matrix, so the packed weights stream from HBM once and the arithmetic runs
 // on 16x16x32 bf16 MFMA tiles.
 //
-//   k_decode<MODE, BIAS, TPW, KSPLIT>  persistent workgroups stream the
+//   k_decode<MODE, TPW, KSPLIT, ...>   persistent workgroups stream the
 //                          packed weight rows of the active experts with
 //                          16-byte loads (lanes kb = 0..3 of a column read 64
 //                          contiguous bytes of the row per 128-wide k tile);
@@ -61,8 +61,9 @@ hipError_t launch_dequant(const int32_t* packed, const uint16_t* scale, uint16_t
 // Operand layout of v_mfma_f32_16x16x32_bf16 as used here: lane l supplies
 // A[row l%16][8*(l/16) .. +7] and B[8*(l/16) .. +7][col l%16]; the result lane
 // l holds D[4*(l/16) + r][l%16], r = 0..3.  A and B only need to agree on the
-// k index carried by (l/16, element), so each lane feeds 8 consecutive
-// (bias- or natural-ordered) k values of its own 32-element chunk per step.
+// k index carried by (l/16, element), so each lane feeds 8 consecutive k
+// values of its own 32-element chunk per step (MoE down: in the order
+// (0,4,1,5,2,6,3,7) in which the gate_up epilogue writes its rows).
 //
 // Work split: every workgroup serves exactly one active expert.  The grid
 // holds the workgroups that fit on the chip at once (at least one per
@@ -103,22 +104,18 @@ __device__ __forceinline__ int frag_slot(int b, int rb, int j) {
   return (16 * (b >> 4) + 4 * (b & 3) + ((b >> 2) & 3)) * rb + j;
 }
 
+// Every weight is dequantised exactly, bf16_RNE((u - 8) * s) (unpack_exact),
+// and multiplied as a bf16 operand, as the reference's dequantise-then-matmul
+// does; each lane's 32-wide chunk of a k tile has one scale.
 // WIDE (group size 128, an even number of groups per row): the scales of one
 // item's TPW tiles are consecutive bf16 values, fetched with one load.
-// TILED (MoE, bias form): the weights come in the tiled layout written by
+// TILED (MoE): the weights come in the tiled layout written by
 // k_tile_decode, where each wavefront's tile of an item is one contiguous
 // KiB (lane l's 16 bytes at 16 l) instead of 16 rows x 64 bytes.
-// GSTEP (tiled, group size 32 or 64): each MFMA step covers one 32-wide
-// chunk of the k tile (lane chunk kb supplies its elements 8 kb .. 8 kb + 7),
-// so one scale group holds per step and the bias form folds per step:
-// acc += s_group * (g_step - 136 * sum(x_chunk)).  The tiled copy holds, in
-// lane l's 16 bytes of tile t, the words 16 t + 4 s + kb (s = 0..3) of its
-// row, and after an item's TPW tiles the rows' step scales.
-// LSCALE (tiled, exact form, group size 32 or 64): the copy keeps the usual
-// word order and, after an item's TPW tiles, each lane's TPW scales (one per
-// tile: its 32-wide chunk's group), fetched with one load like WIDE's.
-template <int MODE, bool BIAS, int TPW, int KSPLIT, bool LONGK, bool WIDE, bool TILED = false, bool GSTEP = false,
-          bool LSCALE = false>
+// LSCALE (tiled, group size 32 or 64): after an item's TPW tiles the copy
+// holds each lane's TPW scales (one per tile: its 32-wide chunk's group),
+// fetched with one load like WIDE's.
+template <int MODE, int TPW, int KSPLIT, bool LONGK, bool WIDE, bool TILED = false, bool LSCALE = false>
 __global__ __launch_bounds__(stream_threads(KSPLIT)) __attribute__((amdgpu_waves_per_eu(TPW >= 4 ? 2 : 4, 8)))
 void k_decode(DecodeArgs a) {
   constexpr int kStreamThreads = stream_threads(KSPLIT);
@@ -126,18 +123,11 @@ void k_decode(DecodeArgs a) {
   constexpr int CG = NWAVES / KSPLIT;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   u32x4_t* __restrict__ lds_a = reinterpret_cast<u32x4_t*>(smem_raw);
-  // per (k tile -- GSTEP: 32-wide chunk --, staged row) bias correction,
-  // after the activation fragments
   const int ntiles = ((a.K >> 5) + 3) >> 2;
-  float* __restrict__ csum = reinterpret_cast<float*>(smem_raw + (size_t)ntiles * 16 * a.rb * 16);
   static_assert(KSPLIT == 1 || KSPLIT == 4, "the split-K epilogue gives wavefront ks output row ks");
   static_assert(!WIDE || !LONGK, "wide scale loads: one group per k tile");
   static_assert(!TILED || (!LONGK && MODE != kModeDense), "tiled expert layout");
-  static_assert(!GSTEP || (TILED && BIAS && !WIDE), "per-step groups come with the tiled copy and its scales");
-  static_assert(!LSCALE || (TILED && WIDE && !BIAS), "lane scales come with the exact form's tiled copy");
-  // LDS slot of 16-byte piece b of staged row j: GSTEP keeps pieces in order
-  // (a step reads pieces 16 t + 4 s + kb); otherwise fragment order
-  auto aslot = [&](int b, int j) { return GSTEP ? b * a.rb + j : frag_slot(b, a.rb, j); };
+  static_assert(!LSCALE || (TILED && WIDE), "lane scales come with the tiled copy");
   // split-K partials, double-buffered so one barrier per item suffices
   __shared__ f32x4_t red[2][KSPLIT > 1 ? NWAVES : 1][64];
   __shared__ int tok[16];
@@ -200,9 +190,8 @@ void k_decode(DecodeArgs a) {
   // touched by staging.  Rows past the staged ones hold stale values, which
   // only reach output rows that are not stored.
   for (int b = K8 + tid / rb; b < 16 * ntiles; b += kStreamThreads / rb)
-    lds_a[aslot(b, tid & (rb - 1))] = u32x4_t{0u, 0u, 0u, 0u};
+    lds_a[frag_slot(b, rb, tid & (rb - 1))] = u32x4_t{0u, 0u, 0u, 0u};
 
-  const uint32_t kMask = opaque(0x000F000Fu), kBias = opaque(kBiasPair);
   const ExactRegs kr = exact_regs();
 
   // weight row of this lane's MFMA column for column tile ct (gate_up: lanes
@@ -224,9 +213,9 @@ void k_decode(DecodeArgs a) {
   // lane carries one byte offset per item.  Rows past the matrix read as
   // zero; chunks past the row end read the next row, harmless because their
   // activation operand is zero.
-  // tiled: an expert is n_ct items of NWAVES blocks of TPW KiB tiles (GSTEP:
-  // each block followed by the TPW x 16 rows x 4 step scales, bf16)
-  constexpr int kBlockBytes = TPW * ((GSTEP || LSCALE) ? 1152 : 1024);
+  // tiled: an expert is n_ct items of NWAVES blocks of TPW KiB tiles (LSCALE:
+  // each block followed by the 64 lanes x TPW scales, bf16)
+  constexpr int kBlockBytes = TPW * (LSCALE ? 1152 : 1024);
   const int64_t wstride = TILED ? (int64_t)a.n_ct * NWAVES * (kBlockBytes / 4) : (int64_t)a.N * K8;
   const __amdgpu_buffer_rsrc_t wsrc =
       make_rsrc(reinterpret_cast<const uint32_t*>(a.wp) + (int64_t)e * wstride, (uint32_t)wstride * 4u);
@@ -237,11 +226,6 @@ void k_decode(DecodeArgs a) {
   auto off_of = [&](int ct) -> Off {
     bool ok;
     const int wrow = weight_row(ct, &ok);
-    // GSTEP: srow is the byte offset of this lane's scales (row j's TPW x 4)
-    if (GSTEP) {
-      const int blk = (ct * NWAVES + wave) * kBlockBytes;
-      return Off{blk + 16 * lane, blk + TPW * 1024 + j * (TPW * 8)};
-    }
     // LSCALE: srow is the byte offset of this lane's TPW scales
     if (LSCALE) {
       const int blk = (ct * NWAVES + wave) * kBlockBytes;
@@ -250,10 +234,7 @@ void k_decode(DecodeArgs a) {
     if (TILED) return Off{(ct * NWAVES + wave) * (TPW * 1024) + 16 * lane, wrow * a.ng};
     return Off{wrow * K8 * 4 + 16 * kb, wrow * a.ng};
   };
-  auto scale_off = [&](const Off& o, int t) -> int {
-    const int g = BIAS ? (t * 128) / a.G : ((4 * t + kb) * 32) / a.G;
-    return (o.srow + g) * 2;
-  };
+  auto scale_off = [&](const Off& o, int t) -> int { return (o.srow + ((4 * t + kb) * 32) / a.G) * 2; };
 
   // RING register sets of one item's weight tiles each: the loads of the
   // next RING - 1 items are in flight while one item is multiplied.
@@ -264,10 +245,6 @@ void k_decode(DecodeArgs a) {
   // WIDE: the item's TPW scales as packed bf16 pairs
   constexpr int SCW = (TPW + 1) / 2;
   uint32_t scw[RING][SCW];
-  // GSTEP: the item's step scales of this lane's row, tiles 2m and 2m + 1 in
-  // sb[m] (TPW is even)
-  static_assert(!GSTEP || TPW % 2 == 0, "step scales come two tiles per 16-byte load");
-  u32x4_t sb[RING][GSTEP ? TPW / 2 : 1];
   auto load_scales_wide = [&](int r, const Off& o) {
     const __amdgpu_buffer_rsrc_t ssrc_w = LSCALE ? wsrc : ssrc;
     const int off = LSCALE ? o.srow : (o.srow + tile0) * 2;
@@ -297,20 +274,13 @@ void k_decode(DecodeArgs a) {
     for (int i = 0; i < TPW; ++i) {
       bw[r][i] = TILED ? buf_ld16(wsrc, tb + i < ntiles ? o.woff : 16 * lane, tb + i < ntiles ? 1024 * i : 0)
                        : buf_ld16(wsrc, o.woff + 64 * tb, 64 * i);
-      if (GSTEP) {
-        if (i & 1) sb[r][i >> 1] = buf_ld16(wsrc, o.srow, 16 * (i >> 1));
-      } else if (!WIDE) {
-        sc[r][i] = buf_ld_u16(ssrc, scale_off(o, tb + i));
-      }
+      if (!WIDE) sc[r][i] = buf_ld_u16(ssrc, scale_off(o, tb + i));
     }
     __builtin_amdgcn_sched_barrier(0);
   };
 
   // Stage activation rows [mc, mc + nr) into LDS.  One task = one (row, k
-  // tile): 16 pieces of 16 bytes, reordered for the bias form, stored in
-  // fragment order, and -- for the bias form -- summed into
-  // csum[t][row] = 136 * (sum of the row's tile elements), the correction the
-  // bias form subtracts per group.  Each task is split over two threads.  `first` runs
+  // tile): 16 pieces of 16 bytes, stored in fragment order.  `first` runs
   // right after the activation loads are issued: the first pass issues the
   // weight prologue there.  Loads complete in order, so waiting for the
   // activations then does not wait for the first items' weights (at kernel
@@ -318,7 +288,7 @@ void k_decode(DecodeArgs a) {
   // stream in, and the first item's MFMAs -- and the refills for the next
   // item -- start as soon as its weights land.
   auto stage = [&](int mc, int nr, auto&& first) {
-    __syncthreads();  // previous readers of lds_a / csum / tok are done
+    __syncthreads();  // previous readers of lds_a / tok are done
     // gate_up: token of each staged row; down: the output row t*k+j of each
     // staged row (read here once, so the epilogue issues no load: a load
     // there would wait for every weight refill issued before it).  The
@@ -337,99 +307,37 @@ void k_decode(DecodeArgs a) {
     }
     __syncthreads();
     // One thread per (row, k tile) task, or -- without a K split -- two,
-    // each taking half of its 16 pieces (adjacent lanes, which add their
-    // sums with one DPP swap).  The LDS budget keeps the task count within
-    // the thread count.  Without a K split the staging registers (16 bytes a
-    // piece, all loads issued before any is used) next to the weight
+    // each taking half of its 16 pieces.  The LDS budget keeps the task count
+    // within the thread count.  Without a K split the staging registers (16
+    // bytes a piece, all loads issued before any is used) next to the weight
     // prologue overflow the register budget unless the task is split; the
     // K-split shapes keep whole tasks (split, or in a task loop, the compiler
     // recomputes addresses inside their item loop instead).
-    auto to_lds = [&](const u32x4_t& x0, int t, int b, int jr, float& sum) {
-      u32x4_t x = x0;
-      // gate_up / dense read caller activations in natural order; down
-      // reads intermediate rows the gate_up epilogue wrote in bias order
-      if (BIAS && MODE != kModeDown) x = to_bias_order(x);
-      if (BIAS) {
-        sum += bf16_bits_to_f32(x.x & 0xFFFFu) + bf16_bits_to_f32(x.x >> 16) +
-               bf16_bits_to_f32(x.y & 0xFFFFu) + bf16_bits_to_f32(x.y >> 16) +
-               bf16_bits_to_f32(x.z & 0xFFFFu) + bf16_bits_to_f32(x.z >> 16) +
-               bf16_bits_to_f32(x.w & 0xFFFFu) + bf16_bits_to_f32(x.w >> 16);
-      }
-      lds_a[aslot(16 * t + b, jr)] = x;
-    };
     auto row_of = [&](int jr) -> int64_t {
       if (MODE == kModeGateUp) return tok[jr];
       return seg0 + mc + jr;
     };
-    if constexpr (KSPLIT != 1) {
-      const bool has = tid < nr * ntiles;
-      const int jr = tid / ntiles;
-      const int t = tid - jr * ntiles;
-      const int nb = min(16, K8 - 16 * t);
-      u32x4_t v[16];
-      if (has) {
-        const uint16_t* src = a.act + row_of(jr) * a.K + 128 * t;
-        // pieces past the row end load the last piece again and are dropped
+    constexpr int HALVES = KSPLIT != 1 ? 1 : 2;
+    constexpr int PIECES = 16 / HALVES;
+    const int task = tid;
+    const bool has = task < HALVES * nr * ntiles;  // equal for both halves
+    const int hf = HALVES == 1 ? 0 : (task & 1);
+    const int rt = HALVES == 1 ? task : (task >> 1);
+    const int jr = rt / ntiles;
+    const int t = rt - jr * ntiles;
+    const int nb = min(16, K8 - 16 * t);
+    u32x4_t v[PIECES];
+    if (has) {
+      const uint16_t* src = a.act + row_of(jr) * a.K + 128 * t;
+      // pieces past the row end load the last piece again and are dropped
 #pragma unroll
-        for (int b = 0; b < 16; ++b) v[b] = ld16(src + 8 * min(b, nb - 1));
-      }
-      first();
-      if (has) {
-        if (GSTEP) {
-          // one correction per 32-wide chunk (MFMA step)
-          float sum4[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int b = 0; b < PIECES; ++b) v[b] = ld16(src + 8 * min(PIECES * hf + b, nb - 1));
+    }
+    first();
+    if (has) {
 #pragma unroll
-          for (int b = 0; b < 16; ++b)
-            if (b < nb) to_lds(v[b], t, b, jr, sum4[b >> 2]);
-#pragma unroll
-          for (int c = 0; c < 4; ++c) csum[(4 * t + c) * 16 + jr] = 136.0f * sum4[c];
-        } else {
-          float sum = 0.f;
-#pragma unroll
-          for (int b = 0; b < 16; ++b)
-            if (b < nb) to_lds(v[b], t, b, jr, sum);
-          if (BIAS) csum[t * 16 + jr] = 136.0f * sum;
-        }
-      }
-    } else {
-      const int task = tid;
-      const bool has = task < 2 * nr * ntiles;  // equal for both halves
-      const int hf = task & 1;
-      const int rt = task >> 1;
-      const int jr = rt / ntiles;
-      const int t = rt - jr * ntiles;
-      const int nb = min(16, K8 - 16 * t);
-      u32x4_t v[8];
-      if (has) {
-        const uint16_t* src = a.act + row_of(jr) * a.K + 128 * t;
-#pragma unroll
-        for (int b = 0; b < 8; ++b) v[b] = ld16(src + 8 * min(8 * hf + b, nb - 1));
-      }
-      first();
-      if (GSTEP) {
-        // this half's two 32-wide chunks, one correction each
-        float sum2[2] = {0.f, 0.f};
-        if (has) {
-#pragma unroll
-          for (int b = 0; b < 8; ++b)
-            if (8 * hf + b < nb) to_lds(v[b], t, 8 * hf + b, jr, sum2[b >> 2]);
-#pragma unroll
-          for (int c = 0; c < 2; ++c) csum[(4 * t + 2 * hf + c) * 16 + jr] = 136.0f * sum2[c];
-        }
-      }
-      float sum = 0.f;
-      if (!GSTEP && has) {
-#pragma unroll
-        for (int b = 0; b < 8; ++b)
-          if (8 * hf + b < nb) to_lds(v[b], t, 8 * hf + b, jr, sum);
-      }
-      if (BIAS && !GSTEP) {
-        // lanes 2i, 2i + 1 hold the halves; both add in the same order
-        const float other =
-            __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sum), 0xB1, 0xF, 0xF, false));
-        const float tot = hf == 0 ? sum + other : other + sum;
-        if (has && hf == 0) csum[t * 16 + jr] = 136.0f * tot;
-      }
+      for (int b = 0; b < PIECES; ++b)
+        if (PIECES * hf + b < nb) lds_a[frag_slot(16 * t + PIECES * hf + b, rb, jr)] = v[b];
     }
     __syncthreads();
   };
@@ -461,63 +369,27 @@ void k_decode(DecodeArgs a) {
       const int tc = t_ok ? t : ntiles - 1;
       u32x4_t A[4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) A[s] = lds_a[aslot(GSTEP ? 16 * tc + 4 * s + kb : 16 * tc + 4 * kb + s, jr_read)];
-      // the bias form scales a whole tile (GSTEP: a step), the exact form one lane chunk
-      const bool s_ok = t_ok && (BIAS || 4 * t + kb < nchunks);
-      const float sci = (GSTEP || !s_ok) ? 0.f : (WIDE ? sfw[i] : bf16_bits_to_f32(sc[r][i]));
+      for (int s = 0; s < 4; ++s) A[s] = lds_a[frag_slot(16 * tc + 4 * kb + s, rb, jr_read)];
+      // one scale per lane chunk; chunks past K get 0
+      const bool s_ok = t_ok && 4 * t + kb < nchunks;
+      const float sci = !s_ok ? 0.f : (WIDE ? sfw[i] : bf16_bits_to_f32(sc[r][i]));
+      // MoE down rows come in the gate_up epilogue's order (0,4,1,5,2,6,3,7):
+      // the weights are unpacked in that order too
+      const ExactScale es = exact_scale(sci);
       u32x4_t bv[4];
-      if (BIAS) {
-        bv[0] = unpack_bias(bw[r][i].x, kMask, kBias);
-        bv[1] = unpack_bias(bw[r][i].y, kMask, kBias);
-        bv[2] = unpack_bias(bw[r][i].z, kMask, kBias);
-        bv[3] = unpack_bias(bw[r][i].w, kMask, kBias);
-      } else {
-        // MoE down rows come in bias order (the gate_up epilogue's): the
-        // weights are unpacked in that order too
-        const ExactScale es = exact_scale(sci);
-        bv[0] = unpack_exact<MODE == kModeDown>(bw[r][i].x, es, kr);
-        bv[1] = unpack_exact<MODE == kModeDown>(bw[r][i].y, es, kr);
-        bv[2] = unpack_exact<MODE == kModeDown>(bw[r][i].z, es, kr);
-        bv[3] = unpack_exact<MODE == kModeDown>(bw[r][i].w, es, kr);
-      }
+      bv[0] = unpack_exact<MODE == kModeDown>(bw[r][i].x, es, kr);
+      bv[1] = unpack_exact<MODE == kModeDown>(bw[r][i].y, es, kr);
+      bv[2] = unpack_exact<MODE == kModeDown>(bw[r][i].z, es, kr);
+      bv[3] = unpack_exact<MODE == kModeDown>(bw[r][i].w, es, kr);
       if (REFILL) {
         // tiled: tiles past K read the expert's first KiB (cached; their
         // scale is zero)
         bw[r][i] = TILED ? buf_ld16(wsrc, t_ok ? nx.woff : 16 * lane, t_ok ? 1024 * i : 0)
                          : buf_ld16(wsrc, nx.woff + 64 * tb, 64 * i);
-        if (!WIDE && !GSTEP) sc[r][i] = buf_ld_u16(ssrc, scale_off(nx, tc));
+        if (!WIDE) sc[r][i] = buf_ld_u16(ssrc, scale_off(nx, tc));
       }
-      if (GSTEP) {
-        // one group per step: four partial sums, each folded with its scale
-        f32x4_t g[4];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) g[s] = mfma16(A[s], bv[s], f32x4_t{0.f, 0.f, 0.f, 0.f});
-        const uint32_t d0 = (i & 1) ? sb[r][i >> 1].z : sb[r][i >> 1].x;
-        const uint32_t d1 = (i & 1) ? sb[r][i >> 1].w : sb[r][i >> 1].y;
-        const float ss[4] = {__uint_as_float(d0 << 16), __uint_as_float(d0 & 0xFFFF0000u),
-                             __uint_as_float(d1 << 16), __uint_as_float(d1 & 0xFFFF0000u)};
-        // the scale block's refill once both of its tiles are folded
-        if (REFILL && (i & 1)) sb[r][i >> 1] = buf_ld16(wsrc, nx.srow, 16 * (i >> 1));
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const float scs = t_ok ? ss[s] : 0.f;
-          // output rows 4*kb .. 4*kb+3 of this lane: their 136 * sum(x) of step s's chunk
-          const f32x4_t cr = *reinterpret_cast<const f32x4_t*>(csum + (4 * tc + s) * 16 + 4 * kb);
-#pragma unroll
-          for (int q = 0; q < 4; ++q) acc[q] = __builtin_fmaf(scs, g[s][q] - cr[q], acc[q]);
-        }
-      } else if (BIAS) {
-        f32x4_t g = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < 4; ++s) g = mfma16(A[s], bv[s], g);
-        // output rows 4*kb .. 4*kb+3 of this lane: their 136 * sum(x)
-        const f32x4_t cr = *reinterpret_cast<const f32x4_t*>(csum + tc * 16 + 4 * kb);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) acc[q] = __builtin_fmaf(sci, g[q] - cr[q], acc[q]);
-      } else {
-#pragma unroll
-        for (int s = 0; s < 4; ++s) acc = mfma16(A[s], bv[s], acc);
-      }
+      for (int s = 0; s < 4; ++s) acc = mfma16(A[s], bv[s], acc);
     }
   };
 
@@ -603,8 +475,8 @@ void k_decode(DecodeArgs a) {
       } else if (MODE == kModeGateUp) {
         // lane j (< 8) holds gate column n0+j, lane j+8 the matching up column
         const int n0 = colblk * 8;
-        // intermediate rows are written in bias order by every decode form
-        // (the down streamers read them so)
+        // intermediate rows are written in the order (0,4,1,5,2,6,3,7) per
+        // 8 columns, which the down streamers' unpack pairs up for free
         const int pos = (j & 3) * 2 + ((j >> 2) & 1);
 #pragma unroll
         for (int qq = 0; qq < QPW; ++qq) {
@@ -690,20 +562,16 @@ static int device_cus() {
   return cached[dev];
 }
 
-// LDS bytes of one workgroup: activation fragments + per (tile, row)
-// corrections (16 rows: rows past the staged ones are read for discarded
-// outputs).
-// (GSTEP: one correction per 32-wide chunk, four per tile.)
-static size_t stream_lds(const DecodeArgs& a, bool gstep) {
+// LDS bytes of one workgroup: the staged activation fragments
+static size_t stream_lds(const DecodeArgs& a) {
   const int ntiles = ((a.K >> 5) + 3) >> 2;
-  return (size_t)ntiles * 16 * a.rb * 16 + (size_t)ntiles * 16 * 4 * (gstep ? 4 : 1);
+  return (size_t)ntiles * 16 * a.rb * 16;
 }
 
-template <int MODE, bool BIAS, int TPW, int KSPLIT, bool LONGK, bool WIDE = false, bool TILED = false,
-          bool GSTEP = false, bool LSCALE = false>
+template <int MODE, int TPW, int KSPLIT, bool LONGK, bool WIDE = false, bool TILED = false, bool LSCALE = false>
 static hipError_t launch_stream(DecodeArgs a, int max_slots, hipStream_t s) {
-  auto kern = k_decode<MODE, BIAS, TPW, KSPLIT, LONGK, WIDE, TILED, GSTEP, LSCALE>;
-  const size_t lds = stream_lds(a, GSTEP);
+  auto kern = k_decode<MODE, TPW, KSPLIT, LONGK, WIDE, TILED, LSCALE>;
+  const size_t lds = stream_lds(a);
   // the workgroups that fit on the chip at once, at least one per possible
   // expert slot and at most one per item; the kernel spreads them over the
   // experts that turn out active (dense: the row groups)
@@ -720,7 +588,7 @@ static hipError_t launch_stream(DecodeArgs a, int max_slots, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int MODE, bool BIAS>
+template <int MODE>
 static hipError_t launch_decode_mode(DecodeArgs a, int max_slots, hipStream_t s) {
   const DecodeShape sh = decode_shape(a.K);
   const int cg = stream_threads(sh.ksplit) / 64 / sh.ksplit;  // column groups per item
@@ -739,9 +607,9 @@ static hipError_t launch_decode_mode(DecodeArgs a, int max_slots, hipStream_t s)
   // and 4-byte aligned scale rows
   const bool wide = a.G == 128 && (a.ng % 2) == 0;
 #define W4A16_DEC(T_, K_)                                                          \
-  return wide ? launch_stream<MODE, BIAS, T_, K_, false, true>(a, max_slots, s) \
-              : launch_stream<MODE, BIAS, T_, K_, false, false>(a, max_slots, s)
-  if (ntiles > 24) return launch_stream<MODE, BIAS, 6, 4, true>(a, max_slots, s);
+  return wide ? launch_stream<MODE, T_, K_, false, true>(a, max_slots, s) \
+              : launch_stream<MODE, T_, K_, false, false>(a, max_slots, s)
+  if (ntiles > 24) return launch_stream<MODE, 6, 4, true>(a, max_slots, s);
   if (sh.ksplit == 1) {
     if (sh.tpw == 2) W4A16_DEC(2, 1);
     if (sh.tpw == 4) W4A16_DEC(4, 1);
@@ -753,20 +621,15 @@ static hipError_t launch_decode_mode(DecodeArgs a, int max_slots, hipStream_t s)
 #undef W4A16_DEC
 }
 
-hipError_t launch_decode(int mode, bool bias_form, DecodeArgs a, int max_slots, hipStream_t s) {
+hipError_t launch_decode(int mode, DecodeArgs a, int max_slots, hipStream_t s) {
   if (max_slots <= 0) return hipSuccess;
   // MoE outputs are addressed by 32-bit byte offsets of one buffer descriptor
   if (mode != kModeDense &&
       (int64_t)a.M * a.topk * (mode == kModeGateUp ? a.I : a.N) * 2 >= (int64_t)0x7FFFFFF0)
     return hipErrorInvalidValue;
-  if (mode == kModeDense)
-    return bias_form ? launch_decode_mode<kModeDense, true>(a, max_slots, s)
-                     : launch_decode_mode<kModeDense, false>(a, max_slots, s);
-  if (mode == kModeGateUp)
-    return bias_form ? launch_decode_mode<kModeGateUp, true>(a, max_slots, s)
-                     : launch_decode_mode<kModeGateUp, false>(a, max_slots, s);
-  return bias_form ? launch_decode_mode<kModeDown, true>(a, max_slots, s)
-                   : launch_decode_mode<kModeDown, false>(a, max_slots, s);
+  if (mode == kModeDense) return launch_decode_mode<kModeDense>(a, max_slots, s);
+  if (mode == kModeGateUp) return launch_decode_mode<kModeGateUp>(a, max_slots, s);
+  return launch_decode_mode<kModeDown>(a, max_slots, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -776,27 +639,23 @@ hipError_t launch_decode(int mode, bool bias_form, DecodeArgs a, int max_slots, 
 // order the streamer reads them: expert e, item ct, wavefront w form one
 // block of TPW KiB tiles,
 //   tile i, lane l's 16 bytes = packed row r of expert e, words
-//     group size 128:     16 t + 4 (l / 16) + s,   s = 0..3
-//     group size 32, 64:  16 t + 4 s + (l / 16),   s = 0..3  (GSTEP)
+//     16 t + 4 (l / 16) + s,   s = 0..3
 //   with t = KS ks + i the k tile (KS = TPW), w = KSPLIT cg + ks, j = l % 16,
 //   colblk = CG ct + cg and
 //     gate_up: r = 8 colblk + j % 8 (+ I for j >= 8: the matching up row),
 //     down:    r = 16 colblk + j;
 // words past the row's K / 8 or of rows past the matrix are zero.  With
 // group size 32 or 64 each block is followed by TPW * 128 bytes of scales
-// (zero past K or for rows past the matrix):
-//   exact form (the default): lane l's TPW scales at byte TPW KiB + 2 TPW l,
-//     tile i's the scale of its chunk, columns 32 (4 t + l / 16) .. + 31;
-//   bias form (GSTEP): row j's TPW x 4 step scales at byte TPW KiB + 8 TPW j,
-//     step s of tile i the scale of columns 32 (4 t + s) .. + 31.
+// (zero past K or for rows past the matrix): lane l's TPW scales at byte
+// TPW KiB + 2 TPW l, tile i's the scale of its chunk, columns
+// 32 (4 t + l / 16) .. + 31.
 // Supported where the streamer's shape for that K has no long-K loop (and,
 // for gate_up, I is a multiple of 8); group size 128 with an even group
 // count per row, or 32, or 64.
 // ---------------------------------------------------------------------------
 struct TiledShape {
   int tpw, ksplit, nwaves, n_ct;
-  int gstep;        // group size 32 / 64, bias form: per-step words and scales
-  int lscale;       // group size 32 / 64, exact form: per-lane scales
+  int lscale;       // group size 32 / 64: per-lane scales in the copy
   int block_bytes;  // one (item, wavefront) block
 };
 
@@ -806,11 +665,11 @@ static bool tiled_shape(int mode, int64_t H, int64_t I, int64_t G, TiledShape* t
   const DecodeShape sh = decode_shape((int)K);
   const int ntiles = (int)(((K >> 5) + 3) >> 2);
   if (ntiles > 24) return false;
-  t->gstep = t->lscale = 0;
+  t->lscale = 0;
   if (G == 128) {
     if (((K + 127) / 128) % 2 != 0) return false;  // one wide scale load per item
   } else if (G == 32 || G == 64) {
-    (kDecodeBiasForm ? t->gstep : t->lscale) = 1;
+    t->lscale = 1;
   } else {
     return false;
   }
@@ -820,7 +679,7 @@ static bool tiled_shape(int mode, int64_t H, int64_t I, int64_t G, TiledShape* t
   const int cg = t->nwaves / sh.ksplit;
   const int64_t ncolblk = mode == kModeGateUp ? I / 8 : (H + 15) / 16;
   t->n_ct = (int)((ncolblk + cg - 1) / cg);
-  t->block_bytes = t->tpw * ((t->gstep || t->lscale) ? 1152 : 1024);
+  t->block_bytes = t->tpw * (t->lscale ? 1152 : 1024);
   return true;
 }
 
@@ -830,7 +689,7 @@ size_t tiled_decode_bytes_per_expert(int mode, int64_t H, int64_t I, int64_t G) 
   return (size_t)t.n_ct * t.nwaves * t.block_bytes;
 }
 
-bool tiled_decode_needs_scale(int G) { return G == 32 || G == 64; }  // both forms keep them in the copy
+bool tiled_decode_needs_scale(int G) { return G == 32 || G == 64; }
 
 bool tiled_decode_down_geometry(int64_t H, int64_t I, int64_t G, int* tpw, int* block_bytes, int64_t* expert_bytes) {
   TiledShape t;
@@ -842,7 +701,7 @@ bool tiled_decode_down_geometry(int64_t H, int64_t I, int64_t G, int* tpw, int* 
 }
 
 // one thread per 16-byte piece of the tiled copy: TPW * 64 weight pieces,
-// then (GSTEP) TPW * 8 scale pieces per block
+// then (LSCALE) TPW * 8 scale pieces per block
 template <int MODE>
 __global__ __launch_bounds__(256) void k_tile_decode(const uint32_t* __restrict__ packed,
                                                      const uint16_t* __restrict__ scale,
@@ -880,29 +739,20 @@ __global__ __launch_bounds__(256) void k_tile_decode(const uint32_t* __restrict_
     uint32_t wd[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const int word = t.gstep ? 16 * tk + 4 * s + kb : 16 * tk + 4 * kb + s;
+      const int word = 16 * tk + 4 * kb + s;
       wd[s] = (ok && word < K8) ? src[word] : 0u;
     }
     v = u32x4_t{wd[0], wd[1], wd[2], wd[3]};
   } else {
-    // scale piece: bf16 entries 8 k .. 8 k + 7 of the block's scales, the
-    // exact form's [64 lanes][TPW] or the bias form's [16 rows][TPW][4 steps]
+    // scale piece: bf16 entries 8 k .. 8 k + 7 of the block's [64 lanes][TPW]
+    // scales; lane l's chunk s = l / 16 of tile i
     const int k = pi - t.tpw * 64;
     uint32_t h[8];
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       const int ent = 8 * k + c;
-      int j, i, s;
-      if (t.lscale) {
-        const int l = ent / t.tpw;
-        j = l & 15;
-        i = ent % t.tpw;
-        s = l >> 4;
-      } else {
-        j = ent / (4 * t.tpw);
-        i = (ent / 4) % t.tpw;
-        s = ent % 4;
-      }
+      const int l = ent / t.tpw;
+      const int j = l & 15, i = ent % t.tpw, s = l >> 4;
       bool ok;
       const int row = row_of(j, &ok);
       const int chunk = 4 * (ks * t.tpw + i) + s;
@@ -918,7 +768,7 @@ hipError_t launch_tile_decode(int mode, const int32_t* packed, const uint16_t* s
                               int32_t* tiled, hipStream_t s) {
   TiledShape t;
   if (!tiled_shape(mode, H, I, G, &t)) return hipErrorInvalidValue;
-  if ((t.gstep || t.lscale) && scale == nullptr) return hipErrorInvalidValue;
+  if (t.lscale && scale == nullptr) return hipErrorInvalidValue;
   const int64_t pieces = (int64_t)E * t.n_ct * t.nwaves * (t.block_bytes / 16);
   if (pieces == 0) return hipSuccess;
   const dim3 grid((unsigned)((pieces + 255) / 256));
@@ -932,23 +782,17 @@ hipError_t launch_tile_decode(int mode, const int32_t* packed, const uint16_t* s
   return hipGetLastError();
 }
 
-// One tiled instantiation: the form (exact, or the bias form in a bias-form
-// build) and the scale source (group size 128: the scale tensor; 32 / 64:
-// the copy).
+// One tiled instantiation by scale source (group size 128: the scale tensor;
+// 32 / 64: the copy).
 template <int MODE, int TPW, int KSPLIT>
 static hipError_t launch_stream_tiled(const TiledShape& t, DecodeArgs a, int max_slots, hipStream_t s) {
-  if (kDecodeBiasForm) {
-    if (t.gstep) return launch_stream<MODE, true, TPW, KSPLIT, false, false, true, true>(a, max_slots, s);
-    return launch_stream<MODE, true, TPW, KSPLIT, false, true, true>(a, max_slots, s);
-  }
-  if (t.lscale) return launch_stream<MODE, false, TPW, KSPLIT, false, true, true, false, true>(a, max_slots, s);
-  return launch_stream<MODE, false, TPW, KSPLIT, false, true, true>(a, max_slots, s);
+  if (t.lscale) return launch_stream<MODE, TPW, KSPLIT, false, true, true, true>(a, max_slots, s);
+  return launch_stream<MODE, TPW, KSPLIT, false, true, true>(a, max_slots, s);
 }
 
 // The MoE streamers on tiled weights (a.wp = the tiled copy): one scale load
 // per item (group size 128 from the scale tensor, an even group count; 32 /
-// 64 from the copy), exact form -- or, built with the bias form, the
-// per-step groups at 32 / 64.
+// 64 from the copy).
 hipError_t launch_decode_tiled(int mode, DecodeArgs a, int max_slots, hipStream_t s) {
   if (max_slots <= 0) return hipSuccess;
   if (mode != kModeGateUp && mode != kModeDown) return hipErrorInvalidValue;

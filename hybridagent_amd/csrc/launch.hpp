@@ -69,16 +69,6 @@ struct PrefillArgs {
 
 enum DecodeMode { kModeDense = 0, kModeGateUp = 1, kModeDown = 2 };
 
-// The decode-size kernels' arithmetic.  Exact (the default): the weights
-// dequantised to bf16_RNE(q * s) as the reference does, then bf16 MFMA with
-// fp32 accumulation.  Bias form (built with W4A16_DECODE_BIAS_FORM=1): the
-// weights as bf16(128 + u) and the group scale applied to the fp32 group sum
-// -- fewer instructions, but without the reference's rounding of q * s.
-#ifndef W4A16_DECODE_BIAS_FORM
-#define W4A16_DECODE_BIAS_FORM 0
-#endif
-constexpr bool kDecodeBiasForm = W4A16_DECODE_BIAS_FORM != 0;
-
 // Arguments of the fused down projection + weighted combine for decode
 // sizes (kernels_down_combine.hip).
 constexpr int kDownCombineMaxRows = 64;
@@ -115,7 +105,7 @@ struct Bf16ExpertArgs {
 hipError_t launch_dequant(const int32_t* packed, const uint16_t* scale, uint16_t* out,
                           int64_t rows, int K, int G, hipStream_t s);
 // max_slots: upper bound of active experts (1 for dense)
-hipError_t launch_decode(int mode, bool bias_form, DecodeArgs a, int max_slots, hipStream_t s);
+hipError_t launch_decode(int mode, DecodeArgs a, int max_slots, hipStream_t s);
 // Tiled expert weights for the decode streamers (kernels_decode.hip): bytes
 // per expert of the tiled copy of the gate_up (mode kModeGateUp) or down
 // weights for group size G (0: no tiled form for H, I, G), whether that copy
@@ -132,9 +122,8 @@ hipError_t launch_add_rms_norm(const uint16_t* h, const uint16_t* delta, const u
 hipError_t launch_combine(const uint16_t* dn, const int64_t* idx, const float* w, uint16_t* out,
                           int M, int topk, int E, int H, hipStream_t s);
 // down + combine in one launch: M * topk <= kDownCombineMaxRows,
-// K <= 768 and a multiple of 32; the intermediate rows in bias order (as the
-// decode gate_up writes them); the weights in the packed layout (a.wt NULL:
-// bias form for group sizes that are multiples of 128, else the exact form)
+// K <= 768 and a multiple of 32; the intermediate rows in the order the
+// decode gate_up writes them; the weights in the packed layout (a.wt NULL)
 // or the down streamer's tiled copy (a.wt; group size 128, 32 or 64)
 bool down_combine_supported(int64_t M, int64_t topk, int64_t K);
 hipError_t launch_down_combine(DownCombineArgs a, hipStream_t s);

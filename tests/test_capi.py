@@ -224,7 +224,7 @@ def test_tiled_decode_sizes(lib):
     assert tb(GU_DEC, 128, 2816, 704, 128) == 128 * 22 * 16 * 6 * 1024
     assert tb(GU_DEC, 1, 2816, 704, 128) == 22 * 16 * 6 * 1024
     assert tb(DN_DEC, 128, 2816, 704, 128) == 128 * 44 * 4 * 6 * 1024
-    # G = 32 / 64: each block of 6 tiles carries 16 rows x 6 tiles x 4 step scales
+    # G = 32 / 64: each block of 6 tiles also carries 64 lanes x 6 tile scales
     for g in (32, 64):
         assert tb(GU_DEC, 128, 2816, 704, g) == 128 * 22 * 16 * 6 * 1152
         assert tb(DN_DEC, 128, 2816, 704, g) == 128 * 44 * 4 * 6 * 1152
