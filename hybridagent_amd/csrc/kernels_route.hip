@@ -552,7 +552,7 @@ constexpr int kRouterMaxSplit = 16;
 // Lane i < topk returns selection i in *sel_e / *sel_w.
 // Logits of token m, lane holding experts lane + 64 q, q < PER (PER =
 // ceil(E / 64) rounded up to a power of two).  KS = number of K-split partial
-// sums to add (1, 4, 8 or kRouterMaxSplit), or 0 to read finished bf16 logits.  All
+// sums to add (4, 8 or kRouterMaxSplit), or 0 to read finished bf16 logits.  All
 // loads are issued before any is used (addresses clamped into range,
 // out-of-range values masked after); NaN becomes -inf so it never wins.
 template <int KS, int PER>
@@ -711,8 +711,6 @@ hipError_t launch_router_topk(const float* partial, int ksplit, const uint16_t* 
     launch_topk_ks<8>(partial, logits_in, per_expert_scale, logits_out, idx, w, M, E, topk, s);
   else if (ksplit == 4)
     launch_topk_ks<4>(partial, logits_in, per_expert_scale, logits_out, idx, w, M, E, topk, s);
-  else if (ksplit == 1)
-    launch_topk_ks<1>(partial, logits_in, per_expert_scale, logits_out, idx, w, M, E, topk, s);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
