@@ -57,56 +57,57 @@ __device__ __forceinline__ uint32_t opaque(uint32_t v) {
 
 // Exact dequantization constants of one group scale s (see unpack_exact).
 struct ExactScale {
-  float s, s16, c0, c1;
+  float s, c0, c1;
 };
 
 __device__ __forceinline__ ExactScale exact_scale(float s) {
-  return ExactScale{s, s * 0.0625f, -1032.0f * s, -72.0f * s};
+  return ExactScale{s, -1032.0f * s, -72.0f * s};
 }
 
 // Registers the exact unpack works with: gfx9 VOP3 instructions take no
-// literal operands, so the masks and the fp16 exponent live in registers and
-// each fp16 pair is one v_and_or_b32.
+// literal operands, so the masks and the two fp16 exponents live in
+// registers and each fp16 pair is one v_and_or_b32.
 struct ExactRegs {
-  uint32_t m0, m1, magic;
+  uint32_t m0, m1, magic0, magic1;
 };
 
 __device__ __forceinline__ ExactRegs exact_regs() {
-  return ExactRegs{opaque(0x000F000Fu), opaque(0x00F000F0u), opaque(0x64006400u)};
+  return ExactRegs{opaque(0x000F000Fu), opaque(0x00F000F0u), opaque(0x64006400u), opaque(0x54005400u)};
 }
 
 // Exact unpack of one packed word with scale s: 8 values bf16_RNE((u-8)*s).
 // PAIRED selects the element order: natural (k = 0..7) or (0,4,1,5,2,6,3,7),
 // the order in which the decode gate_up epilogue writes intermediate rows.
 //
-// Each nibble becomes an fp16 with exponent 2^10 by OR-ing it into the
-// mantissa: nibbles 0/4 and 2/6 (the latter after >> 8) sit at mantissa bits
-// 0..3 and read 1024 + u; nibbles 1/5 and 3/7 sit at bits 4..7 and read
-// 1024 + 16u.  One v_fma_mix_f32 per value then takes the fp16 half straight
-// into an fp32 fma:
-//   (1024 + u)  * s      - 1032 s = (u - 8) s
-//   (1024 + 16u) * (s/16) - 72 s  = (u - 8) s
-// The products are exact inside the fma; s/16 is exact and 1032 s, 72 s are
-// exact in fp32 (s has 8 significant bits, 1032 and 72 have two set bits
-// each), so the single rounding returns (u-8)*s exactly, which
-// v_cvt_pk_bf16_f32 rounds to bf16 (RNE).  Valid for |s| < 2^118, where
-// 1032 s stays finite (bf16 group scales of quantized weights are far below).
+// Each nibble becomes an fp16 by OR-ing it into the mantissa of an fp16
+// whose ulp is 1 at the nibble's place: nibbles 0/4 and 2/6 (the latter after
+// >> 8) sit at mantissa bits 0..3 under exponent 2^10 (0x6400) and read
+// 1024 + u; nibbles 1/5 and 3/7 sit at bits 4..7 under exponent 2^6 (0x5400)
+// and read 64 + u.  One v_fma_mix_f32 per value then takes the fp16 half
+// straight into an fp32 fma:
+//   (1024 + u) * s - 1032 s = (u - 8) s
+//   (64 + u)   * s - 72 s   = (u - 8) s
+// The products are exact inside the fma and 1032 s, 72 s are exact in fp32
+// (s has 8 significant bits, 1032 and 72 have two set bits each), so the
+// single rounding returns (u-8)*s exactly, which v_cvt_pk_bf16_f32 rounds to
+// bf16 (RNE).  Valid for |s| < 2^118, where 1032 s stays finite (bf16 group
+// scales of quantized weights are far below).
 template <bool PAIRED>
 __device__ __forceinline__ u32x4_t unpack_exact(uint32_t w, const ExactScale& es, const ExactRegs& k) {
   typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
   const uint32_t w8 = w >> 8;
-  const f16x2_t p0 = __builtin_bit_cast(f16x2_t, (w & k.m0) | k.magic);   // u0, u4
-  const f16x2_t p1 = __builtin_bit_cast(f16x2_t, (w & k.m1) | k.magic);   // 16 u1, 16 u5
-  const f16x2_t p2 = __builtin_bit_cast(f16x2_t, (w8 & k.m0) | k.magic);  // u2, u6
-  const f16x2_t p3 = __builtin_bit_cast(f16x2_t, (w8 & k.m1) | k.magic);  // 16 u3, 16 u7
+  const f16x2_t p0 = __builtin_bit_cast(f16x2_t, (w & k.m0) | k.magic0);   // 1024 + u0, u4
+  const f16x2_t p1 = __builtin_bit_cast(f16x2_t, (w & k.m1) | k.magic1);   // 64 + u1, u5
+  const f16x2_t p2 = __builtin_bit_cast(f16x2_t, (w8 & k.m0) | k.magic0);  // 1024 + u2, u6
+  const f16x2_t p3 = __builtin_bit_cast(f16x2_t, (w8 & k.m1) | k.magic1);  // 64 + u3, u7
   const float v0 = __builtin_fmaf((float)p0.x, es.s, es.c0);
   const float v4 = __builtin_fmaf((float)p0.y, es.s, es.c0);
-  const float v1 = __builtin_fmaf((float)p1.x, es.s16, es.c1);
-  const float v5 = __builtin_fmaf((float)p1.y, es.s16, es.c1);
+  const float v1 = __builtin_fmaf((float)p1.x, es.s, es.c1);
+  const float v5 = __builtin_fmaf((float)p1.y, es.s, es.c1);
   const float v2 = __builtin_fmaf((float)p2.x, es.s, es.c0);
   const float v6 = __builtin_fmaf((float)p2.y, es.s, es.c0);
-  const float v3 = __builtin_fmaf((float)p3.x, es.s16, es.c1);
-  const float v7 = __builtin_fmaf((float)p3.y, es.s16, es.c1);
+  const float v3 = __builtin_fmaf((float)p3.x, es.s, es.c1);
+  const float v7 = __builtin_fmaf((float)p3.y, es.s, es.c1);
   u32x4_t r;
   if (PAIRED) {
     r.x = pack_bf16x2(v0, v4);

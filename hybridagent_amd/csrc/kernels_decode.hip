@@ -451,7 +451,12 @@ void k_decode(DecodeArgs a) {
         for (int qq = 0; qq < QPW; ++qq) {
           float sum = 0.f;
 #pragma unroll
-          for (int w = 0; w < KSPLIT; ++w) sum += red[rbuf][cg * KSPLIT + w][lane][qlo + qq];
+          for (int w = 0; w < KSPLIT; ++w) {
+            // one float at its own LDS address (indexing the f32x4 by the
+            // wavefront's row would select among the four with VALU)
+            const float* rp = reinterpret_cast<const float*>(&red[rbuf][cg * KSPLIT + w][lane]);
+            sum += rp[qlo + qq];
+          }
           outv[qq] = sum;
         }
         rbuf ^= 1;
