@@ -69,8 +69,8 @@ hipError_t launch_dequant(const int32_t* packed, const uint16_t* scale, uint16_t
 // holds the workgroups that fit on the chip at once (at least one per
 // possible expert slot); with U experts active, workgroup w takes slot
 // w / wps, wps = grid / U (exiting if that slot is not active), and every
-// wps-th of that expert's column tiles ("items": NWAVES/KSPLIT groups of 16
-// weight rows).
+// wps-th of that expert's column tiles ("items": CG groups of 16 weight
+// rows).
 // It stages the expert's activation rows into LDS once per pass of rb rows
 // (an expert with more than rb rows makes several passes over its weights),
 // then streams its items.  Inside an item, each 16-row column group's K range
@@ -90,7 +90,10 @@ hipError_t launch_dequant(const int32_t* packed, const uint16_t* scale, uint16_t
 // Threads per workgroup: K-split shapes run four column groups of four
 // wavefronts each (sixteen wavefronts, one workgroup per CU, share one
 // activation stage of up to 16 rows), the others four column groups of one
-// wavefront.
+// wavefront.  With fewer items than CUs the launcher runs narrow workgroups
+// instead: one column group (CG = 1), four times as many workgroups, so the
+// weights spread over every CU.  Both forms read the same weight blocks:
+// column block colblk's wavefront ks reads block colblk * KSPLIT + ks.
 constexpr int stream_threads(int ksplit) { return ksplit == 4 ? 1024 : 256; }
 // LDS bytes for staged activation rows: the K-split workgroup owns its CU's
 // LDS; the others leave room for several workgroups per CU
@@ -118,9 +121,9 @@ __device__ __forceinline__ int frag_slot(int b, int rb, int j) {
 template <int MODE, int TPW, int KSPLIT, bool LONGK, bool WIDE, bool TILED = false, bool LSCALE = false>
 __global__ __launch_bounds__(stream_threads(KSPLIT)) __attribute__((amdgpu_waves_per_eu(TPW >= 4 ? 2 : 4, 8)))
 void k_decode(DecodeArgs a) {
-  constexpr int kStreamThreads = stream_threads(KSPLIT);
+  constexpr int kStreamThreads = stream_threads(KSPLIT);  // the wide form
   constexpr int NWAVES = kStreamThreads / 64;
-  constexpr int CG = NWAVES / KSPLIT;
+  const int CG = a.cg;  // column groups per item: 4 (wide) or 1 (narrow)
   extern __shared__ __align__(16) unsigned char smem_raw[];
   u32x4_t* __restrict__ lds_a = reinterpret_cast<u32x4_t*>(smem_raw);
   const int ntiles = ((a.K >> 5) + 3) >> 2;
@@ -189,7 +192,7 @@ void k_decode(DecodeArgs a) {
   // is the next row's bytes); that padding is written once here and never
   // touched by staging.  Rows past the staged ones hold stale values, which
   // only reach output rows that are not stored.
-  for (int b = K8 + tid / rb; b < 16 * ntiles; b += kStreamThreads / rb)
+  for (int b = K8 + tid / rb; b < 16 * ntiles; b += (int)blockDim.x / rb)
     lds_a[frag_slot(b, rb, tid & (rb - 1))] = u32x4_t{0u, 0u, 0u, 0u};
 
   const ExactRegs kr = exact_regs();
@@ -213,10 +216,11 @@ void k_decode(DecodeArgs a) {
   // lane carries one byte offset per item.  Rows past the matrix read as
   // zero; chunks past the row end read the next row, harmless because their
   // activation operand is zero.
-  // tiled: an expert is n_ct items of NWAVES blocks of TPW KiB tiles (LSCALE:
-  // each block followed by the 64 lanes x TPW scales, bf16)
+  // tiled: an expert is ct_blocks blocks of TPW KiB tiles (LSCALE: each
+  // block followed by the 64 lanes x TPW scales, bf16), block
+  // colblk * KSPLIT + ks holding wavefront ks's tiles of column block colblk
   constexpr int kBlockBytes = TPW * (LSCALE ? 1152 : 1024);
-  const int64_t wstride = TILED ? (int64_t)a.n_ct * NWAVES * (kBlockBytes / 4) : (int64_t)a.N * K8;
+  const int64_t wstride = TILED ? (int64_t)a.ct_blocks * (kBlockBytes / 4) : (int64_t)a.N * K8;
   const __amdgpu_buffer_rsrc_t wsrc =
       make_rsrc(reinterpret_cast<const uint32_t*>(a.wp) + (int64_t)e * wstride, (uint32_t)wstride * 4u);
   const __amdgpu_buffer_rsrc_t ssrc = make_rsrc(a.ws + (int64_t)e * a.N * a.ng, (uint32_t)a.N * a.ng * 2u);
@@ -228,10 +232,10 @@ void k_decode(DecodeArgs a) {
     const int wrow = weight_row(ct, &ok);
     // LSCALE: srow is the byte offset of this lane's TPW scales
     if (LSCALE) {
-      const int blk = (ct * NWAVES + wave) * kBlockBytes;
+      const int blk = ((ct * CG + cg) * KSPLIT + ks) * kBlockBytes;
       return Off{blk + 16 * lane, blk + TPW * 1024 + lane * (TPW * 2)};
     }
-    if (TILED) return Off{(ct * NWAVES + wave) * (TPW * 1024) + 16 * lane, wrow * a.ng};
+    if (TILED) return Off{((ct * CG + cg) * KSPLIT + ks) * (TPW * 1024) + 16 * lane, wrow * a.ng};
     return Off{wrow * K8 * 4 + 16 * kb, wrow * a.ng};
   };
   auto scale_off = [&](const Off& o, int t) -> int { return (o.srow + ((4 * t + kb) * 32) / a.G) * 2; };
@@ -573,19 +577,56 @@ static size_t stream_lds(const DecodeArgs& a) {
   return (size_t)ntiles * 16 * a.rb * 16;
 }
 
+// Narrow workgroups (one column group each) when the wide form would have
+// fewer than W4A16_NARROW_ITEMS_PER_CU items per CU and the narrow
+// workgroups stage at most W4A16_NARROW_ROWS_PER_CU activation rows per CU
+// in all (each narrow workgroup stages its own rows: a dense batch of many
+// rows stays wide).  Measured: dense 2816 x 2816 at M = 1 / 16 9.4 -> 6.1 /
+// 12.0 -> 9.3 us, MoE decode M = 1 / 2 31.0 -> 29.4 / 38.4 -> 35.3 us; dense
+// M = 64 narrow (8 staged rows per workgroup) 12.1 -> 13.9 us.
+#ifndef W4A16_NARROW_ITEMS_PER_CU
+#define W4A16_NARROW_ITEMS_PER_CU 4
+#endif
+#ifndef W4A16_NARROW_ROWS_PER_CU
+#define W4A16_NARROW_ROWS_PER_CU 16
+#endif
+
+// ncolblk: column blocks of 16 weight rows per expert (gate_up: 8 gate and 8
+// up rows).  a.rb holds the rows an expert can stage per pass; dense
+// max_slots follows from the rows staged.
 template <int MODE, int TPW, int KSPLIT, bool LONGK, bool WIDE = false, bool TILED = false, bool LSCALE = false>
-static hipError_t launch_stream(DecodeArgs a, int max_slots, hipStream_t s) {
+static hipError_t launch_stream(DecodeArgs a, int ncolblk, int max_slots, hipStream_t s) {
   auto kern = k_decode<MODE, TPW, KSPLIT, LONGK, WIDE, TILED, LSCALE>;
+  constexpr int kWideCg = stream_threads(KSPLIT) / 64 / KSPLIT;
+  const int cus = device_cus();
+  // every staging task (row, k tile; two threads each without a K split)
+  // has its own thread(s)
+  const int ntiles = ((a.K >> 5) + 3) >> 2;
+  auto rows_for = [&](int threads) {
+    int rb = a.rb;
+    while (rb > 1 && (KSPLIT == 1 ? 2 : 1) * rb * ntiles > threads) rb >>= 1;
+    return rb;
+  };
+  auto slots_for = [&](int rb) { return MODE == kModeDense ? (a.M + rb - 1) / rb : max_slots; };
+  const int rb_wide = rows_for(64 * KSPLIT * kWideCg), rb_narrow = rows_for(64 * KSPLIT);
+  const int64_t wide_items = (int64_t)slots_for(rb_wide) * ((ncolblk + kWideCg - 1) / kWideCg);
+  const int64_t narrow_items = (int64_t)slots_for(rb_narrow) * ncolblk;
+  const bool narrow = wide_items < (int64_t)W4A16_NARROW_ITEMS_PER_CU * cus &&
+                      narrow_items * rb_narrow <= (int64_t)W4A16_NARROW_ROWS_PER_CU * cus;
+  a.cg = narrow ? 1 : kWideCg;
+  a.rb = narrow ? rb_narrow : rb_wide;
+  a.n_ct = (ncolblk + a.cg - 1) / a.cg;
+  max_slots = slots_for(a.rb);
+  const int threads = 64 * KSPLIT * a.cg;
   const size_t lds = stream_lds(a);
   // the workgroups that fit on the chip at once, at least one per possible
   // expert slot and at most one per item; the kernel spreads them over the
   // experts that turn out active (dense: the row groups)
   int per_cu = 0;
-  constexpr int threads = stream_threads(KSPLIT);
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, threads, lds) !=
           hipSuccess || per_cu <= 0)
     per_cu = 1;
-  const int64_t resident = (int64_t)device_cus() * per_cu;
+  const int64_t resident = (int64_t)cus * per_cu;
   int64_t grid = std::min<int64_t>(resident, (int64_t)max_slots * a.n_ct);
   if (grid < max_slots) grid = max_slots;
   if (grid <= 0) return hipSuccess;
@@ -596,25 +637,21 @@ static hipError_t launch_stream(DecodeArgs a, int max_slots, hipStream_t s) {
 template <int MODE>
 static hipError_t launch_decode_mode(DecodeArgs a, int max_slots, hipStream_t s) {
   const DecodeShape sh = decode_shape(a.K);
-  const int cg = stream_threads(sh.ksplit) / 64 / sh.ksplit;  // column groups per item
   const int ncolblk = MODE == kModeGateUp ? a.I / 8 : (a.N + 15) / 16;
-  a.n_ct = (ncolblk + cg - 1) / cg;
   // rows staged per pass: enough for the rows an expert can have (at most
   // the row count of the batch), capped by the LDS budget
   a.rb = stage_rows(a.K, sh.ksplit);
   int rows_cap = 1;
   while (rows_cap < a.rows_hint && rows_cap < 16) rows_cap <<= 1;
   if (a.rb > rows_cap) a.rb = rows_cap;
-  // dense: one slot per group of rb rows
-  if (MODE == kModeDense) max_slots = (a.M + a.rb - 1) / a.rb;
   const int ntiles = ((a.K >> 5) + 3) >> 2;
   // one load for an item's scales: group size 128 (one group per k tile)
   // and 4-byte aligned scale rows
   const bool wide = a.G == 128 && (a.ng % 2) == 0;
 #define W4A16_DEC(T_, K_)                                                          \
-  return wide ? launch_stream<MODE, T_, K_, false, true>(a, max_slots, s) \
-              : launch_stream<MODE, T_, K_, false, false>(a, max_slots, s)
-  if (ntiles > 24) return launch_stream<MODE, 6, 4, true>(a, max_slots, s);
+  return wide ? launch_stream<MODE, T_, K_, false, true>(a, ncolblk, max_slots, s) \
+              : launch_stream<MODE, T_, K_, false, false>(a, ncolblk, max_slots, s)
+  if (ntiles > 24) return launch_stream<MODE, 6, 4, true>(a, ncolblk, max_slots, s);
   if (sh.ksplit == 1) {
     if (sh.tpw == 2) W4A16_DEC(2, 1);
     if (sh.tpw == 4) W4A16_DEC(4, 1);
@@ -790,9 +827,10 @@ hipError_t launch_tile_decode(int mode, const int32_t* packed, const uint16_t* s
 // One tiled instantiation by scale source (group size 128: the scale tensor;
 // 32 / 64: the copy).
 template <int MODE, int TPW, int KSPLIT>
-static hipError_t launch_stream_tiled(const TiledShape& t, DecodeArgs a, int max_slots, hipStream_t s) {
-  if (t.lscale) return launch_stream<MODE, TPW, KSPLIT, false, true, true, true>(a, max_slots, s);
-  return launch_stream<MODE, TPW, KSPLIT, false, true, true>(a, max_slots, s);
+static hipError_t launch_stream_tiled(const TiledShape& t, DecodeArgs a, int ncolblk, int max_slots,
+                                      hipStream_t s) {
+  if (t.lscale) return launch_stream<MODE, TPW, KSPLIT, false, true, true, true>(a, ncolblk, max_slots, s);
+  return launch_stream<MODE, TPW, KSPLIT, false, true, true>(a, ncolblk, max_slots, s);
 }
 
 // The MoE streamers on tiled weights (a.wp = the tiled copy): one scale load
@@ -806,29 +844,30 @@ hipError_t launch_decode_tiled(int mode, DecodeArgs a, int max_slots, hipStream_
   TiledShape t;
   const int64_t H = mode == kModeGateUp ? a.K : a.N;
   if (!tiled_shape(mode, H, a.I, a.G, &t)) return hipErrorInvalidValue;
-  a.n_ct = t.n_ct;
+  a.ct_blocks = t.n_ct * t.nwaves;
+  const int ncolblk = mode == kModeGateUp ? a.I / 8 : (a.N + 15) / 16;
   a.rb = stage_rows(a.K, t.ksplit);
   int rows_cap = 1;
   while (rows_cap < a.rows_hint && rows_cap < 16) rows_cap <<= 1;
   if (a.rb > rows_cap) a.rb = rows_cap;
   if (mode == kModeGateUp) {
     if (t.ksplit == 4) {
-      if (t.tpw == 2) return launch_stream_tiled<kModeGateUp, 2, 4>(t, a, max_slots, s);
-      if (t.tpw == 4) return launch_stream_tiled<kModeGateUp, 4, 4>(t, a, max_slots, s);
-      return launch_stream_tiled<kModeGateUp, 6, 4>(t, a, max_slots, s);
+      if (t.tpw == 2) return launch_stream_tiled<kModeGateUp, 2, 4>(t, a, ncolblk, max_slots, s);
+      if (t.tpw == 4) return launch_stream_tiled<kModeGateUp, 4, 4>(t, a, ncolblk, max_slots, s);
+      return launch_stream_tiled<kModeGateUp, 6, 4>(t, a, ncolblk, max_slots, s);
     }
-    if (t.tpw == 2) return launch_stream_tiled<kModeGateUp, 2, 1>(t, a, max_slots, s);
-    if (t.tpw == 4) return launch_stream_tiled<kModeGateUp, 4, 1>(t, a, max_slots, s);
-    return launch_stream_tiled<kModeGateUp, 6, 1>(t, a, max_slots, s);
+    if (t.tpw == 2) return launch_stream_tiled<kModeGateUp, 2, 1>(t, a, ncolblk, max_slots, s);
+    if (t.tpw == 4) return launch_stream_tiled<kModeGateUp, 4, 1>(t, a, ncolblk, max_slots, s);
+    return launch_stream_tiled<kModeGateUp, 6, 1>(t, a, ncolblk, max_slots, s);
   }
   if (t.ksplit == 4) {
-    if (t.tpw == 2) return launch_stream_tiled<kModeDown, 2, 4>(t, a, max_slots, s);
-    if (t.tpw == 4) return launch_stream_tiled<kModeDown, 4, 4>(t, a, max_slots, s);
-    return launch_stream_tiled<kModeDown, 6, 4>(t, a, max_slots, s);
+    if (t.tpw == 2) return launch_stream_tiled<kModeDown, 2, 4>(t, a, ncolblk, max_slots, s);
+    if (t.tpw == 4) return launch_stream_tiled<kModeDown, 4, 4>(t, a, ncolblk, max_slots, s);
+    return launch_stream_tiled<kModeDown, 6, 4>(t, a, ncolblk, max_slots, s);
   }
-  if (t.tpw == 2) return launch_stream_tiled<kModeDown, 2, 1>(t, a, max_slots, s);
-  if (t.tpw == 4) return launch_stream_tiled<kModeDown, 4, 1>(t, a, max_slots, s);
-  return launch_stream_tiled<kModeDown, 6, 1>(t, a, max_slots, s);
+  if (t.tpw == 2) return launch_stream_tiled<kModeDown, 2, 1>(t, a, ncolblk, max_slots, s);
+  if (t.tpw == 4) return launch_stream_tiled<kModeDown, 4, 1>(t, a, ncolblk, max_slots, s);
+  return launch_stream_tiled<kModeDown, 6, 1>(t, a, ncolblk, max_slots, s);
 }
 
 // ---------------------------------------------------------------------------

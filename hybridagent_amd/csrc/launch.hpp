@@ -38,6 +38,8 @@ struct DecodeArgs {
   int rb;    // activation rows staged in LDS per pass (<= 16)
   int n_ct;  // work items (column tiles) per expert
   int rows_hint;    // most activation rows one expert can have (set by the caller)
+  int cg;           // column groups of 16 weight rows per item (set by the launcher)
+  int ct_blocks;    // tiled: (item, wavefront) blocks per expert in the copy
 };
 
 // Arguments of the prefill-shaped grouped GEMM (kernels_prefill.hip).
