@@ -58,6 +58,21 @@ constexpr int64_t kMaxStreamK = 49152 / 2;
 // Router partial logits.  `r` is workspace of M * H bf16: the normalised
 // rows on the generic path, the rows' inverse norms (M floats) on the
 // large-batch path.
+// decode sizes with rows the fused norm + logits launch takes (the router
+// partials' path below)
+inline bool router_fused_norm_logits(int64_t M, int64_t H) { return M <= 64 && H <= 384 * 8; }
+
+// The FFN block's shared MLP (backends.py:105-108): its gate/up and down
+// linears, which layer_forward_impl runs inside the router's launches where
+// the shapes allow.
+struct SharedMlp {
+  LinearCall gate_up, down;
+};
+
+inline hipError_t launch_linear_call(const LinearCall& l, hipStream_t s) {
+  return launch_linear_bf16(l.epi, l.x, l.W, l.W2, l.bias, l.res, l.out, l.M, l.N, l.K, s);
+}
+
 hipError_t launch_router_partials(const uint16_t* hidden, const uint16_t* scale, float root,
                                   float eps, const uint16_t* proj, uint16_t* r, float* partial,
                                   int64_t M, int64_t H, int64_t E, hipStream_t s) {
@@ -68,7 +83,7 @@ hipError_t launch_router_partials(const uint16_t* hidden, const uint16_t* scale,
                              (int)M, (int)H, (int)E, s);
   // decode sizes: the norm inside the logits launch (each workgroup covers
   // all experts of 16 tokens, so it normalises its rows once)
-  if (H <= 384 * 8)
+  if (router_fused_norm_logits(M, H))
     return launch_router_norm_logits(hidden, scale, root, eps, proj, partial, (int)M, (int)H,
                                      (int)E, ks, s);
   // long rows at decode sizes: a normalisation pass into r, then the K-split
@@ -207,9 +222,11 @@ int w4a16_add_rms_norm(const uint16_t* h, const uint16_t* delta, const uint16_t*
                                            static_cast<hipStream_t>(stream)));
 }
 
+// two fragment-order matrices (rows padded to 16) and one row-major
 size_t w4a16_hybridlink_workspace_bytes(int64_t B, int64_t H) {
   if (B <= 0 || H <= 0) return 0;
-  return 2 * round256(size_t(B) * H * 2);
+  const size_t bp = size_t((B + 15) / 16 * 16);
+  return 2 * round256(bp * H * 2) + round256(size_t(B) * H * 2);
 }
 
 int w4a16_hybridlink(const uint16_t* h, const uint16_t* ln1_w, const uint16_t* ln1_b,
@@ -230,12 +247,14 @@ int w4a16_hybridlink(const uint16_t* h, const uint16_t* ln1_w, const uint16_t* l
   if (!aligned16(workspace)) return W4A16_ERR_ALIGN;
   hipStream_t s = static_cast<hipStream_t>(stream);
   Carve c(workspace);
-  uint16_t* t0 = c.take<uint16_t>(B * H);  // pre_ln(h), later h + proj2(...)
-  uint16_t* t1 = c.take<uint16_t>(B * H);  // GELU(proj1(...))
-  hipError_t e = launch_layer_norm(h, ln1_w, ln1_b, t0, B, (int)H, eps, s);
-  if (e == hipSuccess) e = launch_linear_bf16(kLinGelu, t0, p1_w, nullptr, p1_b, nullptr, t1, B, (int)H, (int)H, s);
-  if (e == hipSuccess) e = launch_linear_bf16(kLinResidual, t1, p2_w, nullptr, p2_b, h, t0, B, (int)H, (int)H, s);
-  if (e == hipSuccess) e = launch_layer_norm(t0, ln2_w, ln2_b, out, B, (int)H, eps, s);
+  const int64_t Bp = (B + 15) / 16 * 16;
+  uint16_t* a = c.take<uint16_t>(Bp * H);  // pre_ln(h), fragment order
+  uint16_t* g = c.take<uint16_t>(Bp * H);  // GELU(proj1(...)), fragment order
+  uint16_t* r = c.take<uint16_t>(B * H);   // h + proj2(...)
+  hipError_t e = launch_layer_norm(h, ln1_w, ln1_b, a, B, (int)H, eps, true, s);
+  if (e == hipSuccess) e = launch_linear_bf16(kLinGelu, a, p1_w, nullptr, p1_b, nullptr, g, B, (int)H, (int)H, s);
+  if (e == hipSuccess) e = launch_linear_bf16(kLinResidual, g, p2_w, nullptr, p2_b, h, r, B, (int)H, (int)H, s);
+  if (e == hipSuccess) e = launch_layer_norm(r, ln2_w, ln2_b, out, B, (int)H, eps, false, s);
   return launch_status(e);
 }
 
@@ -810,7 +829,7 @@ static int layer_forward_impl(const uint16_t* router_in, const uint16_t* router_
                               const int32_t* dn_packed, const uint16_t* dn_scale, const Tiles& t,
                               uint16_t* out, int64_t* topk_idx, float* topk_w, int64_t M, int64_t top_k,
                               int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
-                              size_t workspace_bytes, void* stream);
+                              size_t workspace_bytes, void* stream, const SharedMlp* mlp = nullptr);
 
 static int ffn_block_impl(const uint16_t* residual, const uint16_t* attn_out,
                           const uint16_t* post_attn_ln_w, const uint16_t* pre_ff_ln_w,
@@ -851,17 +870,14 @@ static int ffn_block_impl(const uint16_t* residual, const uint16_t* attn_out,
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = launch_ffn_pre(attn_out, residual, post_attn_ln_w, pre_ff_ln_w, pre_ff_ln2_w, L.res,
                                 L.h_ff, L.h2_in, M, (int)H, eps, s);
-  if (e == hipSuccess)
-    e = launch_linear_bf16(kLinGateUp, L.h_ff, mlp_gate_w, mlp_up_w, nullptr, nullptr, L.inter, M, (int)Im,
-                           (int)H, s);
-  if (e == hipSuccess)
-    e = launch_linear_bf16(kLinPlain, L.inter, mlp_down_w, nullptr, nullptr, nullptr, L.h_mlp, M, (int)H,
-                           (int)Im, s);
   if (e != hipSuccess) return W4A16_ERR_LAUNCH;
-  st = layer_forward_impl(L.res, router_scale, router_scalar_root, router_proj_w, router_per_expert_scale,
-                          eps, L.h2_in, gu_packed, gu_scale, dn_packed, dn_scale, t, L.moe, L.idx, L.w, M, top_k,
-                          E, H, I, group_size, L.moe_ws,
-                               L.moe_bytes, stream);
+  const SharedMlp mlp{LinearCall{kLinGateUp, L.h_ff, mlp_gate_w, mlp_up_w, nullptr, nullptr, L.inter, M, (int)Im,
+                                 (int)H},
+                      LinearCall{kLinPlain, L.inter, mlp_down_w, nullptr, nullptr, nullptr, L.h_mlp, M, (int)H,
+                                 (int)Im}};
+  st = layer_forward_impl(L.res, router_scale, router_scalar_root, router_proj_w, router_per_expert_scale, eps,
+                          L.h2_in, gu_packed, gu_scale, dn_packed, dn_scale, t, L.moe, L.idx, L.w, M, top_k, E, H,
+                          I, group_size, L.moe_ws, L.moe_bytes, stream, &mlp);
   if (st != W4A16_OK) return st;
   return launch_status(launch_ffn_post(L.h_mlp, L.moe, L.res, post_ff_ln1_w, post_ff_ln2_w, post_ff_ln_w,
                                        layer_scalar, out, M, (int)H, eps, s));
@@ -1044,7 +1060,7 @@ static int layer_forward_impl(const uint16_t* router_in, const uint16_t* router_
                               const int32_t* dn_packed, const uint16_t* dn_scale, const Tiles& t,
                               uint16_t* out, int64_t* topk_idx, float* topk_w, int64_t M, int64_t top_k,
                               int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
-                              size_t workspace_bytes, void* stream) {
+                              size_t workspace_bytes, void* stream, const SharedMlp* mlp) {
   if (M < 0 || M > (1 << 24) || top_k > E) return W4A16_ERR_SHAPE;
   if (M == 0) {
     MoeLayout dummy{};
@@ -1066,15 +1082,39 @@ static int layer_forward_impl(const uint16_t* router_in, const uint16_t* router_
   Carve c(static_cast<char*>(workspace) + moe_bytes);
   uint16_t* r = c.take<uint16_t>(M * H);
   float* partial = c.take<float>(size_t(router_ksplit(M, E)) * M * E);
-  hipError_t e = launch_router_partials(router_in, router_scale, scalar_root, eps, proj_w, r,
-                                        partial, M, H, E, s);
-  if (e != hipSuccess) return W4A16_ERR_LAUNCH;
+  // the shared MLP's linears (FFN block) ride in the router's launches where
+  // the shapes allow, else they run as launches of their own
+  bool mlp_gu = mlp == nullptr, mlp_dn = mlp == nullptr;
+  hipError_t e = hipErrorNotSupported;
+  if (!mlp_gu && router_fused_norm_logits(M, H))
+    e = launch_router_norm_logits_with_linear(router_in, router_scale, scalar_root, eps, proj_w, partial, (int)M,
+                                              (int)H, (int)E, router_ksplit(M, E), mlp->gate_up, s);
+  if (e == hipSuccess) {
+    mlp_gu = true;
+  } else {
+    if (e != hipErrorNotSupported) return W4A16_ERR_LAUNCH;
+    e = mlp_gu ? hipSuccess : launch_linear_call(mlp->gate_up, s);
+    mlp_gu = true;
+    if (e == hipSuccess)
+      e = launch_router_partials(router_in, router_scale, scalar_root, eps, proj_w, r, partial, M, H, E, s);
+    if (e != hipSuccess) return W4A16_ERR_LAUNCH;
+  }
   if (M * top_k <= kTopkSortMaxEntries) {
     // small batches: top-k and the expert sort in one workgroup
-    e = launch_topk_sort(partial, router_ksplit(M, E), per_expert_scale, topk_idx, topk_w, (int)M,
-                         (int)E, (int)top_k, L.sorted_pos, L.offsets, L.desc, L.counters, L.tiles,
-                         kPrefillBM, s);
-    if (e != hipSuccess) return W4A16_ERR_LAUNCH;
+    e = hipErrorNotSupported;
+    if (!mlp_dn)
+      e = launch_topk_sort_with_linear(partial, router_ksplit(M, E), per_expert_scale, topk_idx, topk_w, (int)M,
+                                       (int)E, (int)top_k, L.sorted_pos, L.offsets, L.desc, L.counters, L.tiles,
+                                       kPrefillBM, mlp->down, s);
+    if (e == hipSuccess) {
+      mlp_dn = true;
+    } else {
+      if (e != hipErrorNotSupported) return W4A16_ERR_LAUNCH;
+      e = launch_topk_sort(partial, router_ksplit(M, E), per_expert_scale, topk_idx, topk_w, (int)M,
+                           (int)E, (int)top_k, L.sorted_pos, L.offsets, L.desc, L.counters, L.tiles,
+                           kPrefillBM, s);
+      if (e != hipSuccess) return W4A16_ERR_LAUNCH;
+    }
   } else {
     e = launch_router_topk(partial, router_ksplit(M, E), nullptr, per_expert_scale, nullptr, topk_idx,
                            topk_w, (int)M, (int)E, (int)top_k, s);
@@ -1082,6 +1122,7 @@ static int layer_forward_impl(const uint16_t* router_in, const uint16_t* router_
     st = moe_plan(hidden, topk_idx, M, top_k, E, H, I, group_size, workspace, moe_bytes, stream);
     if (st != W4A16_OK) return st;
   }
+  if (!mlp_dn && launch_linear_call(mlp->down, s) != hipSuccess) return W4A16_ERR_LAUNCH;
   st = gate_up_impl(hidden, gu_packed, gu_scale, t, M, top_k, E, H, I, group_size, workspace,
                     moe_bytes, stream);
   if (st == W4A16_OK)

@@ -60,6 +60,23 @@ __device__ __forceinline__ Row8 load8(const uint16_t* row, int c8, bool ok) {
   return r;
 }
 
+// the 16-byte chunk itself, converted only where used (a conversion right
+// after the load would wait for it)
+__device__ __forceinline__ u32x4_t raw8(const uint16_t* row, int c8, bool ok) {
+  return ok ? ld16(row + 8 * c8) : u32x4_t{0u, 0u, 0u, 0u};
+}
+
+__device__ __forceinline__ Row8 conv8(const u32x4_t& u) {
+  Row8 r;
+  const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    r.v[2 * t] = bf16_bits_to_f32(w4[t] & 0xFFFFu);
+    r.v[2 * t + 1] = bf16_bits_to_f32(w4[t] >> 16);
+  }
+  return r;
+}
+
 __device__ __forceinline__ void store8(uint16_t* row, int c8, const float* v) {
   st16(row + 8 * c8, u32x4_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
                              pack_bf16x2(v[6], v[7])});
@@ -88,21 +105,32 @@ __global__ __launch_bounds__(kFfnThreads) void k_ffn_pre(
   const int64_t off = (int64_t)blockIdx.x * H;
   const int n8 = H >> 3;
   Row8 a[kFfnChunks], r[kFfnChunks];
-  float ssa = 0.f;
+  // every load issued before the first reduction: the rows, then the three
+  // norms' weights (one memory round trip instead of three)
+  u32x4_t wa[kFfnChunks], wf[kFfnChunks], wf2[kFfnChunks];
 #pragma unroll
   for (int q = 0; q < kFfnChunks; ++q) {
     const int c8 = threadIdx.x + kFfnThreads * q;
     a[q] = load8(attn + off, c8, c8 < n8);
     r[q] = load8(res + off, c8, c8 < n8);
-    ssa += sumsq8(a[q]);
   }
+#pragma unroll
+  for (int q = 0; q < kFfnChunks; ++q) {
+    const int c8 = threadIdx.x + kFfnThreads * q;
+    wa[q] = raw8(w_pa, c8, c8 < n8);
+    wf[q] = raw8(w_pf, c8, c8 < n8);
+    wf2[q] = raw8(w_pf2, c8, c8 < n8);
+  }
+  float ssa = 0.f;
+#pragma unroll
+  for (int q = 0; q < kFfnChunks; ++q) ssa += sumsq8(a[q]);
   const float rsa = 1.0f / sqrtf(block_sum2(ssa, 0.f, part).x / (float)H + eps);
   float ssr = 0.f;
 #pragma unroll
   for (int q = 0; q < kFfnChunks; ++q) {
     const int c8 = threadIdx.x + kFfnThreads * q;
     const bool ok = c8 < n8;
-    const Row8 w = load8(w_pa, c8, ok);
+    const Row8 w = conv8(wa[q]);
     float h[8];
     norm8(a[q], rsa, w, h);
 #pragma unroll
@@ -116,9 +144,9 @@ __global__ __launch_bounds__(kFfnThreads) void k_ffn_pre(
     const int c8 = threadIdx.x + kFfnThreads * q;
     if (c8 >= n8) continue;
     float o[8];
-    norm8(r[q], rsr, load8(w_pf, c8, true), o);
+    norm8(r[q], rsr, conv8(wf[q]), o);
     store8(h_ff + off, c8, o);
-    norm8(r[q], rsr, load8(w_pf2, c8, true), o);
+    norm8(r[q], rsr, conv8(wf2[q]), o);
     store8(h2_in + off, c8, o);
   }
 }
@@ -131,12 +159,27 @@ __global__ __launch_bounds__(kFfnThreads) void k_ffn_post(
   const int64_t off = (int64_t)blockIdx.x * H;
   const int n8 = H >> 3;
   Row8 m[kFfnChunks], e2[kFfnChunks];
-  float ssm = 0.f, sse = 0.f;
+  // every load issued before the first reduction: the two rows, then the
+  // three norms' weights and the residual row (one memory round trip)
+  u32x4_t w1r[kFfnChunks], w2r[kFfnChunks], w3r[kFfnChunks], rr[kFfnChunks];
 #pragma unroll
   for (int q = 0; q < kFfnChunks; ++q) {
     const int c8 = threadIdx.x + kFfnThreads * q;
     m[q] = load8(mlp + off, c8, c8 < n8);
     e2[q] = load8(moe + off, c8, c8 < n8);
+  }
+#pragma unroll
+  for (int q = 0; q < kFfnChunks; ++q) {
+    const int c8 = threadIdx.x + kFfnThreads * q;
+    w1r[q] = raw8(w1, c8, c8 < n8);
+    w2r[q] = raw8(w2, c8, c8 < n8);
+    w3r[q] = raw8(w3, c8, c8 < n8);
+    rr[q] = raw8(res + off, c8, c8 < n8);
+  }
+  const float ls = bf16_bits_to_f32(layer_scalar[0]);
+  float ssm = 0.f, sse = 0.f;
+#pragma unroll
+  for (int q = 0; q < kFfnChunks; ++q) {
     ssm += sumsq8(m[q]);
     sse += sumsq8(e2[q]);
   }
@@ -150,21 +193,20 @@ __global__ __launch_bounds__(kFfnThreads) void k_ffn_post(
     const int c8 = threadIdx.x + kFfnThreads * q;
     const bool ok = c8 < n8;
     float h1[8], h2[8];
-    norm8(m[q], rm, load8(w1, c8, ok), h1);
-    norm8(e2[q], re, load8(w2, c8, ok), h2);
+    norm8(m[q], rm, conv8(w1r[q]), h1);
+    norm8(e2[q], re, conv8(w2r[q]), h2);
 #pragma unroll
     for (int e = 0; e < 8; ++e) m[q].v[e] = ok ? round_bf16(h1[e] + h2[e]) : 0.f;
     ssc += sumsq8(m[q]);
   }
   const float rc = 1.0f / sqrtf(block_sum2(ssc, 0.f, part).x / (float)H + eps);
-  const float ls = bf16_bits_to_f32(layer_scalar[0]);
 #pragma unroll
   for (int q = 0; q < kFfnChunks; ++q) {
     const int c8 = threadIdx.x + kFfnThreads * q;
     if (c8 >= n8) continue;
     float hc[8];
-    norm8(m[q], rc, load8(w3, c8, true), hc);
-    const Row8 r = load8(res + off, c8, true);
+    norm8(m[q], rc, conv8(w3r[q]), hc);
+    const Row8 r = conv8(rr[q]);
     float o[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = round_bf16(r.v[e] + hc[e]) * ls;

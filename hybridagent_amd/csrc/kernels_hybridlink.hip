@@ -5,11 +5,14 @@
 //   k_linear_bf16<GELU> g = bf16(GELU(bf16(a W1^T + b1)))  (kernels_linear_bf16.hip)
 //   k_linear_bf16<RES>  r = bf16(h + bf16(g W2^T + b2))
 //   k_layer_norm        out = LN(r)
+// a and g are held in the linears' fragment order (linear_bf16.hpp): the
+// first LayerNorm writes a that way, the GELU linear writes g that way.
 // The rounding points are those of the torch bf16 module: every Linear,
 // GELU, the residual add and each LayerNorm round to bf16 once.  At batch 32
 // and H = 2816 each linear launch moves 15.9 MB of weights.
 #include "common.hpp"
 #include "launch.hpp"
+#include "linear_bf16.hpp"
 
 namespace w4a16 {
 
@@ -34,7 +37,9 @@ __device__ __forceinline__ float block_sum(float v, float* part) {
 }  // namespace
 
 // nn.LayerNorm over rows of H (fp32 statistics, two passes: mean, then the
-// mean of squared deviations), affine with bf16 weight / bias, bf16 out.
+// mean of squared deviations), affine with bf16 weight / bias, bf16 out
+// (FRAG: in the bf16 linears' fragment order, rows padded to 16).
+template <bool FRAG>
 __global__ __launch_bounds__(kLnThreads) void k_layer_norm(const uint16_t* __restrict__ x,
                                                           const uint16_t* __restrict__ w,
                                                           const uint16_t* __restrict__ b,
@@ -46,9 +51,15 @@ __global__ __launch_bounds__(kLnThreads) void k_layer_norm(const uint16_t* __res
   const int n8 = H >> 3;
   float v[kLnChunks][8];
   float s = 0.f;
-  // the affine parameters are loaded with the row, so the row's statistics
-  // and the parameters arrive in one memory round trip
-  u32x4_t wv[kLnChunks], bv[kLnChunks];
+  // the row, then the affine parameters, all loads issued before the first
+  // is used: one memory round trip, and the statistics wait only for the
+  // row (loads complete in order)
+  u32x4_t xv[kLnChunks], wv[kLnChunks], bv[kLnChunks];
+#pragma unroll
+  for (int q = 0; q < kLnChunks; ++q) {
+    const int c8 = threadIdx.x + kLnThreads * q;
+    xv[q] = c8 < n8 ? ld16(xr + 8 * c8) : u32x4_t{0u, 0u, 0u, 0u};
+  }
 #pragma unroll
   for (int q = 0; q < kLnChunks; ++q) {
     const int c8 = min(threadIdx.x + kLnThreads * q, n8 - 1);
@@ -57,8 +68,7 @@ __global__ __launch_bounds__(kLnThreads) void k_layer_norm(const uint16_t* __res
   }
 #pragma unroll
   for (int q = 0; q < kLnChunks; ++q) {
-    const int c8 = threadIdx.x + kLnThreads * q;
-    const u32x4_t u = c8 < n8 ? ld16(xr + 8 * c8) : u32x4_t{0u, 0u, 0u, 0u};
+    const u32x4_t u = xv[q];
     const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -97,16 +107,19 @@ __global__ __launch_bounds__(kLnThreads) void k_layer_norm(const uint16_t* __res
                          bf16_bits_to_f32(bw[t] >> 16);
         o[t] = pack_bf16x2(y0, y1);
       }
-      st16(y + row * H + 8 * c8, u32x4_t{o[0], o[1], o[2], o[3]});
+      st16(y + (FRAG ? frag_index(row, 8 * c8, H) : row * H + 8 * c8), u32x4_t{o[0], o[1], o[2], o[3]});
     }
   }
 }
 
 hipError_t launch_layer_norm(const uint16_t* x, const uint16_t* w, const uint16_t* b, uint16_t* y,
-                             int64_t M, int H, float eps, hipStream_t s) {
+                             int64_t M, int H, float eps, bool frag, hipStream_t s) {
   if (M == 0) return hipSuccess;
-  if (H % 8 != 0 || H > kLnThreads * 8 * kLnChunks) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_layer_norm, dim3((unsigned)M), dim3(kLnThreads), 0, s, x, w, b, y, H, eps);
+  if (H % 8 != 0 || H > kLnThreads * 8 * kLnChunks || (frag && H % 32 != 0)) return hipErrorInvalidValue;
+  if (frag)
+    hipLaunchKernelGGL(k_layer_norm<true>, dim3((unsigned)M), dim3(kLnThreads), 0, s, x, w, b, y, H, eps);
+  else
+    hipLaunchKernelGGL(k_layer_norm<false>, dim3((unsigned)M), dim3(kLnThreads), 0, s, x, w, b, y, H, eps);
   return hipGetLastError();
 }
 

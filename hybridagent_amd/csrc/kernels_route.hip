@@ -18,6 +18,7 @@
 //                    k_router_topk_sort_small (top-k + sort in one launch)
 #include "common.hpp"
 #include "launch.hpp"
+#include "linear_bf16.hpp"
 
 namespace w4a16 {
 
@@ -178,10 +179,23 @@ hipError_t launch_router_logits(const uint16_t* r, const uint16_t* proj, float* 
 constexpr int kFusedLogitsThreads = 512;
 constexpr int kFusedLogitsMaxSteps = 12;  // 32-wide k steps per split
 
-__global__ __launch_bounds__(kFusedLogitsThreads) void k_router_norm_logits(
-    const uint16_t* __restrict__ h, const uint16_t* __restrict__ scale, float scalar_root,
-    float eps, const uint16_t* __restrict__ proj, float* __restrict__ partial, int M, int H, int E,
-    int steps_per_split) {
+struct RouterNormLogitsArgs {
+  const uint16_t* h;
+  const uint16_t* scale;
+  float scalar_root, eps;
+  const uint16_t* proj;
+  float* partial;
+  int M, H, E, steps_per_split;
+};
+
+// workgroup (bx: 16 tokens, by: K split) of the launch
+__device__ __forceinline__ void router_norm_logits_block(const RouterNormLogitsArgs& args, int bx, int by) {
+  const uint16_t* __restrict__ h = args.h;
+  const uint16_t* __restrict__ scale = args.scale;
+  const float scalar_root = args.scalar_root, eps = args.eps;
+  const uint16_t* __restrict__ proj = args.proj;
+  float* __restrict__ partial = args.partial;
+  const int M = args.M, H = args.H, E = args.E, steps_per_split = args.steps_per_split;
   constexpr int NW = kFusedLogitsThreads / 64;
   __shared__ u32x4_t afrag[kFusedLogitsMaxSteps][64];
   __shared__ float s_part[16][33];
@@ -189,8 +203,8 @@ __global__ __launch_bounds__(kFusedLogitsThreads) void k_router_norm_logits(
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int j = lane & 15, kb = lane >> 4;
-  const int m0 = blockIdx.x * 16;
-  const int ks = blockIdx.y;
+  const int m0 = bx * 16;
+  const int ks = by;
   const int nchunks = H >> 5;
   const int c0 = ks * steps_per_split;
   const int nsteps = max(0, min(nchunks, c0 + steps_per_split) - c0);
@@ -315,6 +329,10 @@ __global__ __launch_bounds__(kFusedLogitsThreads) void k_router_norm_logits(
   }
 }
 
+__global__ __launch_bounds__(kFusedLogitsThreads) void k_router_norm_logits(RouterNormLogitsArgs a) {
+  router_norm_logits_block(a, blockIdx.x, blockIdx.y);
+}
+
 hipError_t launch_router_norm_logits(const uint16_t* h, const uint16_t* scale, float scalar_root,
                                      float eps, const uint16_t* proj, float* partial, int M,
                                      int H, int E, int ksplit, hipStream_t s) {
@@ -323,8 +341,8 @@ hipError_t launch_router_norm_logits(const uint16_t* h, const uint16_t* scale, f
   const int per = (nchunks + ksplit - 1) / ksplit;
   if (per > kFusedLogitsMaxSteps) return hipErrorInvalidValue;
   dim3 grid((M + 15) / 16, ksplit);
-  hipLaunchKernelGGL(k_router_norm_logits, grid, dim3(kFusedLogitsThreads), 0, s, h, scale,
-                     scalar_root, eps, proj, partial, M, H, E, per);
+  hipLaunchKernelGGL(k_router_norm_logits, grid, dim3(kFusedLogitsThreads), 0, s,
+                     RouterNormLogitsArgs{h, scale, scalar_root, eps, proj, partial, M, H, E, per});
   return hipGetLastError();
 }
 
@@ -943,12 +961,28 @@ __global__ __launch_bounds__(kSortThreads) void k_moe_sort(
 // lower lanes of the same expert by ballots -- with no workgroup barrier
 // after the top-k (a wavefront's LDS operations complete in order).
 constexpr int kSmallSortWaves = 8;
+struct TopkSortArgs {
+  const float* partial;
+  const uint16_t* pes;
+  int64_t* idx_out;
+  float* w_out;
+  int M, E, topk;
+  int32_t *sorted_pos, *offsets, *desc, *counters, *tiles;
+  int BM;
+};
+
 template <int KS, int PER, int ROUNDS>
-__global__ __launch_bounds__(64 * kSmallSortWaves) void k_router_topk_sort_small(
-    const float* __restrict__ partial, const uint16_t* __restrict__ pes,
-    int64_t* __restrict__ idx_out, float* __restrict__ w_out, int M, int E, int topk,
-    int32_t* __restrict__ sorted_pos, int32_t* __restrict__ offsets, int32_t* __restrict__ desc,
-    int32_t* __restrict__ counters, int32_t* __restrict__ tiles, int BM) {
+__device__ __forceinline__ void topk_sort_small_block(const TopkSortArgs& args) {
+  const float* __restrict__ partial = args.partial;
+  const uint16_t* __restrict__ pes = args.pes;
+  int64_t* __restrict__ idx_out = args.idx_out;
+  float* __restrict__ w_out = args.w_out;
+  const int M = args.M, E = args.E, topk = args.topk, BM = args.BM;
+  int32_t* __restrict__ sorted_pos = args.sorted_pos;
+  int32_t* __restrict__ offsets = args.offsets;
+  int32_t* __restrict__ desc = args.desc;
+  int32_t* __restrict__ counters = args.counters;
+  int32_t* __restrict__ tiles = args.tiles;
   __shared__ int s_idx[64];
   __shared__ uint16_t s_pes[kMaxExperts];
   __shared__ int cnt[kMaxExperts];
@@ -1004,6 +1038,11 @@ __global__ __launch_bounds__(64 * kSmallSortWaves) void k_router_topk_sort_small
   if (ok) sorted_pos[run[e] + rank] = row;
 }
 
+template <int KS, int PER, int ROUNDS>
+__global__ __launch_bounds__(64 * kSmallSortWaves) void k_router_topk_sort_small(TopkSortArgs a) {
+  topk_sort_small_block<KS, PER, ROUNDS>(a);
+}
+
 hipError_t launch_topk_sort(const float* partial, int ksplit, const uint16_t* per_expert_scale,
                             int64_t* idx, float* w, int M, int E, int topk, int32_t* sorted_pos,
                             int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
@@ -1013,15 +1052,13 @@ hipError_t launch_topk_sort(const float* partial, int ksplit, const uint16_t* pe
   // routed rows: one token per wavefront up to M = 8, else eight rounds
   if (M * topk > 64 || ksplit != kRouterMaxSplit) return hipErrorInvalidValue;
   constexpr int KS = kRouterMaxSplit;
-#define W4A16_TS(P_)                                                                             \
-  if (M <= kSmallSortWaves)                                                                      \
-    hipLaunchKernelGGL((k_router_topk_sort_small<KS, P_, 1>), dim3(1), dim3(64 * kSmallSortWaves), \
-                       0, s, partial, per_expert_scale, idx, w, M, E, topk, sorted_pos, offsets,   \
-                       desc, counters, tiles, BM);                                                \
-  else                                                                                           \
-    hipLaunchKernelGGL((k_router_topk_sort_small<KS, P_, 64 / kSmallSortWaves>), dim3(1),         \
-                       dim3(64 * kSmallSortWaves), 0, s, partial, per_expert_scale, idx, w, M, E,  \
-                       topk, sorted_pos, offsets, desc, counters, tiles, BM)
+  const TopkSortArgs a{partial, per_expert_scale, idx, w, M, E, topk, sorted_pos, offsets, desc, counters, tiles, BM};
+#define W4A16_TS(P_)                                                                                      \
+  if (M <= kSmallSortWaves)                                                                               \
+    hipLaunchKernelGGL((k_router_topk_sort_small<KS, P_, 1>), dim3(1), dim3(64 * kSmallSortWaves), 0, s, a); \
+  else                                                                                                    \
+    hipLaunchKernelGGL((k_router_topk_sort_small<KS, P_, 64 / kSmallSortWaves>), dim3(1),                  \
+                       dim3(64 * kSmallSortWaves), 0, s, a)
   if (E <= 64) {
     W4A16_TS(1);
   } else if (E <= 128) {
@@ -1032,6 +1069,87 @@ hipError_t launch_topk_sort(const float* partial, int ksplit, const uint16_t* pe
     W4A16_TS(kTopkPerLane);
   }
 #undef W4A16_TS
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// The FFN block's shared MLP (backends.py:105-108) inside the router's
+// launches at decode sizes.  Its gate/up linear runs in the workgroups after
+// the router logits' (both read only the block's normalised inputs), its down
+// linear in the workgroups after the one-workgroup top-k + sort (the gate/up
+// output is complete: it came from the previous launch).  The router chain's
+// workgroups come first in the grid, so they are dispatched first; the
+// linear's workgroups fill the CUs the router leaves idle.  Each workgroup
+// runs one body, chosen by its index, with the same results as the separate
+// kernels (k_router_norm_logits, k_router_topk_sort_small, k_linear_bf16).
+// ---------------------------------------------------------------------------
+static_assert(kFusedLogitsThreads == kLinThreads && 64 * kSmallSortWaves == kLinThreads,
+              "one workgroup size for the fused bodies");
+
+template <int MT>
+__global__ __launch_bounds__(kLinThreads) void k_router_logits_with_linear(RouterNormLogitsArgs ra, int rgx,
+                                                                         int rblocks, LinArgs la, int lgx) {
+  const int b = blockIdx.x;
+  if (b < rblocks) {
+    router_norm_logits_block(ra, b % rgx, b / rgx);
+    return;
+  }
+  const int l = b - rblocks;
+  linear_bf16_block<MT, kLinGateUp>(la, l % lgx, l / lgx);
+}
+
+template <int PER>
+__global__ __launch_bounds__(kLinThreads) void k_topk_sort_with_linear(TopkSortArgs ta, LinArgs la, int lgx) {
+  if (blockIdx.x == 0) {
+    topk_sort_small_block<kRouterMaxSplit, PER, 1>(ta);
+    return;
+  }
+  const int l = blockIdx.x - 1;
+  linear_bf16_block<1, kLinPlain>(la, l % lgx, l / lgx);
+}
+
+hipError_t launch_router_norm_logits_with_linear(const uint16_t* h, const uint16_t* scale, float scalar_root,
+                                                 float eps, const uint16_t* proj, float* partial, int M, int H,
+                                                 int E, int ksplit, const LinearCall& lin, hipStream_t s) {
+  if (M == 0 || lin.M != M || lin.epi != kLinGateUp || lin.K % 32 != 0 || lin.K <= 0 || lin.N <= 0)
+    return hipErrorNotSupported;
+  const int nchunks = H >> 5;
+  const int per = (nchunks + ksplit - 1) / ksplit;
+  if (per > kFusedLogitsMaxSteps) return hipErrorNotSupported;
+  const int mt = lin_row_tiles(lin.M);
+  if (mt > 2) return hipErrorNotSupported;
+  const RouterNormLogitsArgs ra{h, scale, scalar_root, eps, proj, partial, M, H, E, per};
+  const int rgx = (M + 15) / 16, rblocks = rgx * ksplit;
+  const LinArgs la = lin_args(lin.epi, lin.x, lin.W, lin.W2, lin.bias, lin.res, lin.out, lin.M, lin.N, lin.K);
+  const int lgx = lin_grid_x(lin.epi, lin.N);
+  const int64_t blocks = rblocks + (int64_t)lgx * lin_grid_y(lin.M);
+  if (mt == 1)
+    hipLaunchKernelGGL(k_router_logits_with_linear<1>, dim3((unsigned)blocks), dim3(kLinThreads), 0, s, ra, rgx,
+                       rblocks, la, lgx);
+  else
+    hipLaunchKernelGGL(k_router_logits_with_linear<2>, dim3((unsigned)blocks), dim3(kLinThreads), 0, s, ra, rgx,
+                       rblocks, la, lgx);
+  return hipGetLastError();
+}
+
+hipError_t launch_topk_sort_with_linear(const float* partial, int ksplit, const uint16_t* per_expert_scale,
+                                        int64_t* idx, float* w, int M, int E, int topk, int32_t* sorted_pos,
+                                        int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
+                                        int BM, const LinearCall& lin, hipStream_t s) {
+  // one top-k round (a token per wavefront), at most 128 experts, and a
+  // linear of at most 16 rows
+  if (M == 0 || M * topk > 64 || M > kSmallSortWaves || ksplit != kRouterMaxSplit || E > 128 ||
+      lin.epi != kLinPlain || lin.M <= 0 || lin.M > 16 || lin.K % 32 != 0 || lin.K <= 0 || lin.N <= 0)
+    return hipErrorNotSupported;
+  const TopkSortArgs ta{partial, per_expert_scale, idx, w, M, E, topk, sorted_pos, offsets, desc, counters, tiles,
+                        BM};
+  const LinArgs la = lin_args(lin.epi, lin.x, lin.W, lin.W2, lin.bias, lin.res, lin.out, lin.M, lin.N, lin.K);
+  const int lgx = lin_grid_x(lin.epi, lin.N);
+  const unsigned blocks = 1u + (unsigned)lgx;
+  if (E <= 64)
+    hipLaunchKernelGGL(k_topk_sort_with_linear<1>, dim3(blocks), dim3(kLinThreads), 0, s, ta, la, lgx);
+  else
+    hipLaunchKernelGGL(k_topk_sort_with_linear<2>, dim3(blocks), dim3(kLinThreads), 0, s, ta, la, lgx);
   return hipGetLastError();
 }
 

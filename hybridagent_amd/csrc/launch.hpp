@@ -168,9 +168,10 @@ hipError_t launch_router_topk(const float* partial, int ksplit, const uint16_t* 
                               const uint16_t* per_expert_scale, uint16_t* logits_out,
                               int64_t* idx, float* w, int M, int E, int topk, hipStream_t s);
 // HybridLink pieces (kernels_hybridlink.hip): nn.LayerNorm with bf16 affine
-// parameters (H % 8 == 0, H <= 8192)
+// parameters (H % 8 == 0, H <= 8192); frag: y in the bf16 linears' fragment
+// order (linear_bf16.hpp; H % 32 == 0, rows padded to a multiple of 16)
 hipError_t launch_layer_norm(const uint16_t* x, const uint16_t* w, const uint16_t* b, uint16_t* y,
-                             int64_t M, int H, float eps, hipStream_t s);
+                             int64_t M, int H, float eps, bool frag, hipStream_t s);
 // bf16-weight linear for small batches (kernels_linear_bf16.hip), K % 32 ==
 // 0, with a fused epilogue:
 //   kLinGelu      out = bf16(GELU_erf(bf16(x W^T + b)))
@@ -182,6 +183,26 @@ enum LinearEpilogue { kLinGelu = 0, kLinResidual = 1, kLinGateUp = 2, kLinPlain 
 hipError_t launch_linear_bf16(int epi, const uint16_t* x, const uint16_t* W, const uint16_t* W2,
                               const uint16_t* bias, const uint16_t* res, uint16_t* out, int64_t M, int N,
                               int K, hipStream_t s);
+// One bf16 linear (launch_linear_bf16's arguments), for the launches that run
+// it beside other work.
+struct LinearCall {
+  int epi;
+  const uint16_t *x, *W, *W2, *bias, *res;
+  uint16_t* out;
+  int64_t M;
+  int N, K;
+};
+// launch_router_norm_logits with a kLinGateUp linear of at most 32 rows in the
+// same launch; launch_topk_sort (one top-k round, E <= 128) with a kLinPlain
+// linear of at most 16 rows.  hipErrorNotSupported (nothing launched) where
+// the shapes need separate launches.
+hipError_t launch_router_norm_logits_with_linear(const uint16_t* h, const uint16_t* scale, float scalar_root,
+                                                 float eps, const uint16_t* proj, float* partial, int M, int H,
+                                                 int E, int ksplit, const LinearCall& lin, hipStream_t s);
+hipError_t launch_topk_sort_with_linear(const float* partial, int ksplit, const uint16_t* per_expert_scale,
+                                        int64_t* idx, float* w, int M, int E, int topk, int32_t* sorted_pos,
+                                        int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
+                                        int BM, const LinearCall& lin, hipStream_t s);
 // FFN block row kernels (kernels_ffn.hip), one workgroup per row, H % 8 == 0,
 // H <= 8192:
 //   pre : h = rms(attn) * w_pa; res_out = bf16(res + h);

@@ -192,3 +192,32 @@ def test_patch_ffn_4bit_matches_hf_decoder_layer(dev):
     print(f"patched layer vs transformers' Gemma4TextDecoderLayer: max_abs_rel={err:.2e} "
           f"on {clear.sum()}/{M} rows with a clear routing margin")
     assert err <= TOL
+
+
+# The shared MLP runs on a second stream beside the routed experts (forked
+# after the pre-norms, joined before the post-norm).  Captured into a graph,
+# the fork and join become parallel branches: every replay, with eager calls
+# and synchronisations between replays, gives the eager result bit for bit.
+@pytest.mark.parametrize("M", [1, 32])
+def test_ffn_block_graph_replay(dev, M):
+    H, I, Im, E, K, G = 2816, 704, 2112, 128, 8, 128
+    a = _block_inputs(M, H, I, Im, E, G, seed=2300 + M, dev=dev)
+    other = dict(a, residual=synth.activations(M, H, seed=2310 + M, device=dev))
+    eager = backends.ffn_moe_4bit_step(**a, top_k=K).clone()
+    eager_other = backends.ffn_moe_4bit_step(**other, top_k=K).clone()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        backends.ffn_moe_4bit_step(**a, top_k=K)  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = backends.ffn_moe_4bit_step(**a, top_k=K)
+    for rep in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {rep} differs from the eager result"
+        assert torch.equal(backends.ffn_moe_4bit_step(**other, top_k=K), eager_other)
+        torch.cuda.synchronize()
