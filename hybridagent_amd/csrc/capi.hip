@@ -111,7 +111,7 @@ MoeLayout moe_layout(void* ws, int64_t M, int64_t k, int64_t E, int64_t H, int64
   Carve c(ws);
   MoeLayout L;
   L.offsets = c.take<int32_t>(E + 1);
-  L.desc = c.take<int32_t>(4 * E);
+  L.desc = c.take<int32_t>(4 * plan_desc_capacity(M, k, E));
   L.counters = c.take<int32_t>(2);
   L.queues = c.take<int32_t>(kPrefillQueueInts);
   L.sorted_pos = c.take<int32_t>(M * k);
@@ -369,9 +369,9 @@ int moe_sort_permute(const int64_t* topk_idx, int64_t M, int64_t top_k, int64_t 
   if (M * top_k > kSortMultiMinRows)
     return launch_status(launch_sort_multi(topk_idx, (int)M, (int)top_k, (int)E, sorted_pos,
                                            expert_offsets, desc, counters, tiles, blockcnt,
-                                           kPrefillBM, s));
+                                           kPrefillBM, 0, s));
   return launch_status(launch_sort(topk_idx, (int)M, (int)top_k, (int)E, sorted_pos,
-                                   expert_offsets, desc, counters, tiles, kPrefillBM, s));
+                                   expert_offsets, desc, counters, tiles, kPrefillBM, 0, s));
 }
 
 size_t moe_workspace_bytes(int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I) {
@@ -472,12 +472,14 @@ int moe_plan(const uint16_t* hidden, const int64_t* topk_idx, int64_t M, int64_t
   if (!aligned16(hidden)) return W4A16_ERR_ALIGN;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int bm = plan_bm(M, H, I, group_size);
+  // the decode streamers take an expert's rows as slots of kDecodeSlotRows
+  const int sr = use_prefill(M, H, I) ? 0 : kDecodeSlotRows;
   hipError_t e =
       M * top_k > kSortMultiMinRows
           ? launch_sort_multi(topk_idx, (int)M, (int)top_k, (int)E, L.sorted_pos, L.offsets,
-                              L.desc, L.counters, L.tiles, L.blockcnt, bm, s, L.queues)
+                              L.desc, L.counters, L.tiles, L.blockcnt, bm, sr, s, L.queues)
           : launch_sort(topk_idx, (int)M, (int)top_k, (int)E, L.sorted_pos, L.offsets, L.desc,
-                        L.counters, L.tiles, bm, s, L.queues);
+                        L.counters, L.tiles, bm, sr, s, L.queues);
   return launch_status(e);
 }
 
@@ -527,7 +529,8 @@ int gate_up_impl(const uint16_t* hidden, const int32_t* gu_packed, const uint16_
     p.n_nt = (int)(I / 64);
     return launch_status(launch_prefill(kModeGateUp, p, max_mtiles(M, top_k, E), s));
   }
-  const int max_slots = (int)(M * top_k < E ? M * top_k : E);
+  // the plan's slots: kDecodeSlotRows rows of an expert each
+  const int max_slots = (int)std::min<int64_t>(M * top_k, plan_desc_capacity(M, top_k, E));
   DecodeArgs a = expert_args(L, M, top_k, I, group_size);
   a.act = hidden;
   a.wp = gu_packed;
@@ -627,7 +630,8 @@ static int down_impl(const int32_t* dn_packed, const uint16_t* dn_scale, const T
     p.n_nt = (int)(H / kPfBN);
     return launch_status(launch_prefill(kModeDown, p, max_mtiles(M, top_k, E), s));
   }
-  const int max_slots = (int)(M * top_k < E ? M * top_k : E);
+  // the plan's slots: kDecodeSlotRows rows of an expert each
+  const int max_slots = (int)std::min<int64_t>(M * top_k, plan_desc_capacity(M, top_k, E));
   DecodeArgs a = expert_args(L, M, top_k, I, group_size);
   a.act = L.inter;
   a.wp = dn_packed;
@@ -954,9 +958,9 @@ int moe_bf16_experts_forward(const uint16_t* hidden, const int64_t* topk_idx, co
   hipError_t e =
       M * top_k > kSortMultiMinRows
           ? launch_sort_multi(topk_idx, (int)M, (int)top_k, (int)E, L.sorted_pos, L.offsets, L.desc,
-                              L.counters, L.tiles, L.blockcnt, kPrefillBM, s)
+                              L.counters, L.tiles, L.blockcnt, kPrefillBM, 0, s)
           : launch_sort(topk_idx, (int)M, (int)top_k, (int)E, L.sorted_pos, L.offsets, L.desc,
-                        L.counters, L.tiles, kPrefillBM, s);
+                        L.counters, L.tiles, kPrefillBM, 0, s);
   const int max_slots = (int)(M * top_k < E ? M * top_k : E);
   Bf16ExpertArgs a{};
   a.sorted_pos = L.sorted_pos;
@@ -1105,14 +1109,14 @@ static int layer_forward_impl(const uint16_t* router_in, const uint16_t* router_
     if (!mlp_dn)
       e = launch_topk_sort_with_linear(partial, router_ksplit(M, E), per_expert_scale, topk_idx, topk_w, (int)M,
                                        (int)E, (int)top_k, L.sorted_pos, L.offsets, L.desc, L.counters, L.tiles,
-                                       kPrefillBM, mlp->down, s);
+                                       kPrefillBM, kDecodeSlotRows, mlp->down, s);
     if (e == hipSuccess) {
       mlp_dn = true;
     } else {
       if (e != hipErrorNotSupported) return W4A16_ERR_LAUNCH;
       e = launch_topk_sort(partial, router_ksplit(M, E), per_expert_scale, topk_idx, topk_w, (int)M,
                            (int)E, (int)top_k, L.sorted_pos, L.offsets, L.desc, L.counters, L.tiles,
-                           kPrefillBM, s);
+                           kPrefillBM, kDecodeSlotRows, s);
       if (e != hipSuccess) return W4A16_ERR_LAUNCH;
     }
   } else {

@@ -766,18 +766,32 @@ __device__ int block_excl_scan(int v, int* wsum, int* total) {
   return res;
 }
 
+// Work descriptors of an expert with c rows: one, or with SR > 0 one per
+// SR rows (the decode streamers' slots: an expert with more rows than one
+// pass stages runs as several slots side by side instead of several passes
+// in one workgroup).
+__device__ __forceinline__ int plan_slots(int c, int SR) {
+  return c <= 0 ? 0 : SR > 0 ? (c + SR - 1) / SR : 1;
+}
+
+// descriptor i of expert e (rows [off, off + c) of the segment order)
+__device__ __forceinline__ int4 plan_desc(int e, int off, int c, int SR, int i) {
+  return SR > 0 ? make_int4(e, off + i * SR, min(SR, c - i * SR), 0) : make_int4(e, off, c, 0);
+}
+
 // From the per-expert counts (thread e holds expert e's count c, e < E <= 512):
-// the segment offsets, one work descriptor per active expert and the m-tile
+// the segment offsets, the work descriptors (plan_slots) and the m-tile
 // list; written when `write` (one workgroup writes them).  Returns thread e's
 // segment start.  All threads of the kSortThreads-thread workgroup call it.
 __device__ int write_plan(int c, int E, int32_t* __restrict__ offsets, int32_t* __restrict__ desc,
-                          int32_t* __restrict__ counters, int32_t* __restrict__ tiles, int BM,
+                          int32_t* __restrict__ counters, int32_t* __restrict__ tiles, int BM, int SR,
                           int* wsum, bool write) {
   const int tid = threadIdx.x;
   int tot;
   const int off = block_excl_scan(c, wsum, &tot);
   int nact;
-  const int apos = block_excl_scan(c > 0 ? 1 : 0, wsum, &nact);
+  const int ns = plan_slots(c, SR);
+  const int apos = block_excl_scan(ns, wsum, &nact);
   const int rem = c % BM;
   const int nsmall = (rem > 0 && rem <= BM / 2) ? 1 : 0;
   const int nbig = (c + BM - 1) / BM - nsmall;
@@ -791,10 +805,8 @@ __device__ int write_plan(int c, int E, int32_t* __restrict__ offsets, int32_t* 
       counters[0] = nact;
       counters[1] = nbig_tot + nsmall_tot;
     }
-    if (tid < E && c > 0) {
-      const int4 d = make_int4(tid, off, c, 0);
-      *reinterpret_cast<int4*>(desc + 4 * apos) = d;
-    }
+    if (tid < E)
+      for (int i = 0; i < ns; ++i) *reinterpret_cast<int4*>(desc + 4 * (apos + i)) = plan_desc(tid, off, c, SR, i);
     if (tid < E) {
       for (int i = 0; i < nbig; ++i) tiles[bpos + i] = (tid << 16) | i;
       if (nsmall) tiles[nbig_tot + spos] = (tid << 16) | nbig;
@@ -810,7 +822,7 @@ __device__ int write_plan(int c, int E, int32_t* __restrict__ offsets, int32_t* 
 // without workgroup barriers.
 __device__ void plan_wave(const int* cnt, int* run, int E, int32_t* __restrict__ offsets,
                           int32_t* __restrict__ desc, int32_t* __restrict__ counters,
-                          int32_t* __restrict__ tiles, int BM) {
+                          int32_t* __restrict__ tiles, int BM, int SR) {
   constexpr int PE = kMaxExperts / 64;
   const int lane = threadIdx.x & 63;
   const int pe = (E + 63) >> 6;
@@ -822,7 +834,7 @@ __device__ void plan_wave(const int* cnt, int* run, int E, int32_t* __restrict__
     const int e = lane * pe + q;
     c[q] = (q < pe && e < E) ? cnt[e] : 0;
     cs += c[q];
-    as += c[q] > 0 ? 1 : 0;
+    as += plan_slots(c[q], SR);
     ss += n_small(c[q]);
     bs += (c[q] + BM - 1) / BM - n_small(c[q]);
   }
@@ -836,10 +848,9 @@ __device__ void plan_wave(const int* cnt, int* run, int E, int32_t* __restrict__
     if (q < pe && e < E) {
       offsets[e] = off;
       run[e] = off;
-      if (c[q] > 0) {
-        *reinterpret_cast<int4*>(desc + 4 * apos) = make_int4(e, off, c[q], 0);
-        ++apos;
-      }
+      const int ns = plan_slots(c[q], SR);
+      for (int i = 0; i < ns; ++i) *reinterpret_cast<int4*>(desc + 4 * (apos + i)) = plan_desc(e, off, c[q], SR, i);
+      apos += ns;
       const int sm = n_small(c[q]);
       const int nb = (c[q] + BM - 1) / BM - sm;
       for (int i = 0; i < nb; ++i) tiles[bpos + i] = (e << 16) | i;
@@ -861,7 +872,7 @@ template <typename ExpertOf>
 __device__ void moe_sort_body(ExpertOf expert_of, int M, int topk, int E,
                               int32_t* __restrict__ sorted_pos, int32_t* __restrict__ offsets,
                               int32_t* __restrict__ desc, int32_t* __restrict__ counters,
-                              int32_t* __restrict__ tiles, int BM) {
+                              int32_t* __restrict__ tiles, int BM, int SR) {
   __shared__ int cnt[kMaxExperts];
   __shared__ int run[kMaxExperts];
   __shared__ int wcnt[kSortWaves][kMaxExperts];
@@ -902,7 +913,7 @@ __device__ void moe_sort_body(ExpertOf expert_of, int M, int topk, int E,
   __syncthreads();
 
   // offsets, work descriptors, tile list and scatter bases, by wavefront 0
-  if (wave == 0) plan_wave(cnt, run, E, offsets, desc, counters, tiles, BM);
+  if (wave == 0) plan_wave(cnt, run, E, offsets, desc, counters, tiles, BM, SR);
   __syncthreads();
 
   // stable scatter in k-major order p = j*M + t
@@ -948,10 +959,10 @@ __device__ void moe_sort_body(ExpertOf expert_of, int M, int topk, int E,
 __global__ __launch_bounds__(kSortThreads) void k_moe_sort(
     const int64_t* __restrict__ idx_in, int M, int topk, int E, int32_t* __restrict__ sorted_pos,
     int32_t* __restrict__ offsets, int32_t* __restrict__ desc, int32_t* __restrict__ counters,
-    int32_t* __restrict__ tiles, int BM, int32_t* __restrict__ queues) {
+    int32_t* __restrict__ tiles, int BM, int SR, int32_t* __restrict__ queues) {
   if (queues != nullptr && threadIdx.x < kPrefillQueueInts) queues[threadIdx.x] = 0;
   moe_sort_body([&](int row) -> int64_t { return idx_in[row]; }, M, topk, E, sorted_pos, offsets,
-                desc, counters, tiles, BM);
+                desc, counters, tiles, BM, SR);
 }
 
 // Small batches (at most 64 routed rows, decode sizes): top-k of every token
@@ -968,7 +979,7 @@ struct TopkSortArgs {
   float* w_out;
   int M, E, topk;
   int32_t *sorted_pos, *offsets, *desc, *counters, *tiles;
-  int BM;
+  int BM, slot_rows;
 };
 
 template <int KS, int PER, int ROUNDS>
@@ -1025,7 +1036,7 @@ __device__ __forceinline__ void topk_sort_small_block(const TopkSortArgs& args) 
   }
   const bool ok = e >= 0;
   if (ok) atomicAdd(&cnt[e], 1);
-  plan_wave(cnt, run, E, offsets, desc, counters, tiles, BM);
+  plan_wave(cnt, run, E, offsets, desc, counters, tiles, BM, args.slot_rows);
   int nbits = 0;
   while ((1 << nbits) < E) ++nbits;
   unsigned long long same = __ballot(ok);
@@ -1046,13 +1057,14 @@ __global__ __launch_bounds__(64 * kSmallSortWaves) void k_router_topk_sort_small
 hipError_t launch_topk_sort(const float* partial, int ksplit, const uint16_t* per_expert_scale,
                             int64_t* idx, float* w, int M, int E, int topk, int32_t* sorted_pos,
                             int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
-                            int BM, hipStream_t s) {
+                            int BM, int slot_rows, hipStream_t s) {
   if (M == 0) return hipSuccess;
   // the decode router's partials (kRouterMaxSplit K splits), at most 64
   // routed rows: one token per wavefront up to M = 8, else eight rounds
   if (M * topk > 64 || ksplit != kRouterMaxSplit) return hipErrorInvalidValue;
   constexpr int KS = kRouterMaxSplit;
-  const TopkSortArgs a{partial, per_expert_scale, idx, w, M, E, topk, sorted_pos, offsets, desc, counters, tiles, BM};
+  const TopkSortArgs a{partial, per_expert_scale, idx, w, M, E, topk, sorted_pos, offsets, desc, counters, tiles, BM,
+                       slot_rows};
 #define W4A16_TS(P_)                                                                                      \
   if (M <= kSmallSortWaves)                                                                               \
     hipLaunchKernelGGL((k_router_topk_sort_small<KS, P_, 1>), dim3(1), dim3(64 * kSmallSortWaves), 0, s, a); \
@@ -1135,14 +1147,14 @@ hipError_t launch_router_norm_logits_with_linear(const uint16_t* h, const uint16
 hipError_t launch_topk_sort_with_linear(const float* partial, int ksplit, const uint16_t* per_expert_scale,
                                         int64_t* idx, float* w, int M, int E, int topk, int32_t* sorted_pos,
                                         int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
-                                        int BM, const LinearCall& lin, hipStream_t s) {
+                                        int BM, int slot_rows, const LinearCall& lin, hipStream_t s) {
   // one top-k round (a token per wavefront), at most 128 experts, and a
   // linear of at most 16 rows
   if (M == 0 || M * topk > 64 || M > kSmallSortWaves || ksplit != kRouterMaxSplit || E > 128 ||
       lin.epi != kLinPlain || lin.M <= 0 || lin.M > 16 || lin.K % 32 != 0 || lin.K <= 0 || lin.N <= 0)
     return hipErrorNotSupported;
   const TopkSortArgs ta{partial, per_expert_scale, idx, w, M, E, topk, sorted_pos, offsets, desc, counters, tiles,
-                        BM};
+                        BM, slot_rows};
   const LinArgs la = lin_args(lin.epi, lin.x, lin.W, lin.W2, lin.bias, lin.res, lin.out, lin.M, lin.N, lin.K);
   const int lgx = lin_grid_x(lin.epi, lin.N);
   const unsigned blocks = 1u + (unsigned)lgx;
@@ -1181,7 +1193,7 @@ __global__ __launch_bounds__(kSortThreads) void k_sort_hist(const int64_t* __res
 __global__ __launch_bounds__(kSortThreads) void k_sort_scatter(
     const int64_t* __restrict__ idx, int M, int topk, int E, const int32_t* __restrict__ blockcnt,
     int32_t* __restrict__ sorted_pos, int32_t* __restrict__ offsets, int32_t* __restrict__ desc,
-    int32_t* __restrict__ counters, int32_t* __restrict__ tiles, int BM, int32_t* __restrict__ queues) {
+    int32_t* __restrict__ counters, int32_t* __restrict__ tiles, int BM, int SR, int32_t* __restrict__ queues) {
   __shared__ int base[kMaxExperts];
   __shared__ int wcnt[kSortWaves][kMaxExperts];
   __shared__ int wsum[kSortWaves];
@@ -1216,7 +1228,7 @@ __global__ __launch_bounds__(kSortThreads) void k_sort_scatter(
   }
   for (int x = tid; x < E; x += kSortThreads)
     for (int w = 0; w < kSortWaves; ++w) wcnt[w][x] = 0;
-  const int off = write_plan(tot, E, offsets, desc, counters, tiles, BM, wsum, b == 0);
+  const int off = write_plan(tot, E, offsets, desc, counters, tiles, BM, SR, wsum, b == 0);
   if (tid < E) base[tid] = off + pre;
   __syncthreads();
   if (ev >= 0 && ev < E) e = (int)ev;
@@ -1245,20 +1257,20 @@ int sort_blocks(int64_t rows) { return (int)((rows + kSortThreads - 1) / kSortTh
 
 hipError_t launch_sort_multi(const int64_t* idx, int M, int topk, int E, int32_t* sorted_pos,
                              int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
-                             int32_t* blockcnt, int BM, hipStream_t s, int32_t* queues) {
+                             int32_t* blockcnt, int BM, int SR, hipStream_t s, int32_t* queues) {
   const int nb = sort_blocks((int64_t)M * topk);
   if (nb <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_sort_hist, dim3(nb), dim3(kSortThreads), 0, s, idx, M, topk, E, blockcnt);
   hipLaunchKernelGGL(k_sort_scatter, dim3(nb), dim3(kSortThreads), 0, s, idx, M, topk, E, blockcnt,
-                     sorted_pos, offsets, desc, counters, tiles, BM, queues);
+                     sorted_pos, offsets, desc, counters, tiles, BM, SR, queues);
   return hipGetLastError();
 }
 
 hipError_t launch_sort(const int64_t* idx, int M, int topk, int E, int32_t* sorted_pos,
                        int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
-                       int BM, hipStream_t s, int32_t* queues) {
+                       int BM, int SR, hipStream_t s, int32_t* queues) {
   hipLaunchKernelGGL(k_moe_sort, dim3(1), dim3(kSortThreads), 0, s, idx, M, topk, E, sorted_pos,
-                     offsets, desc, counters, tiles, BM, queues);
+                     offsets, desc, counters, tiles, BM, SR, queues);
   return hipGetLastError();
 }
 

@@ -132,17 +132,26 @@ hipError_t launch_down_combine(DownCombineArgs a, hipStream_t s);
 // the down streamer's tiled-copy shape for (H, I, G): TPW, block bytes and
 // bytes per expert (false where there is none)
 bool tiled_decode_down_geometry(int64_t H, int64_t I, int64_t G, int* tpw, int* block_bytes, int64_t* expert_bytes);
+// Every plan writer's slot_rows: 0 gives one work descriptor per active
+// expert; kDecodeSlotRows (the decode streamers' plans) one per 16 rows of an
+// expert, so an expert with more rows than a streamer stages per pass runs as
+// several slots side by side.  The descriptor array then holds up to
+// plan_desc_capacity entries.
+constexpr int kDecodeSlotRows = 16;
+inline int64_t plan_desc_capacity(int64_t M, int64_t topk, int64_t E) {
+  return E + (M * topk + kDecodeSlotRows - 1) / kDecodeSlotRows;
+}
 // The expert sort; with `queues` (nullable) it also zeroes the
 // kPrefillQueueInts prefill work-queue counters there.
 hipError_t launch_sort(const int64_t* idx, int M, int topk, int E, int32_t* sorted_pos,
                        int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
-                       int BM, hipStream_t s, int32_t* queues = nullptr);
+                       int BM, int slot_rows, hipStream_t s, int32_t* queues = nullptr);
 // the sort over several workgroups (large batches); blockcnt holds
 // sort_blocks(M * topk) * E ints
 int sort_blocks(int64_t rows);
 hipError_t launch_sort_multi(const int64_t* idx, int M, int topk, int E, int32_t* sorted_pos,
                              int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
-                             int32_t* blockcnt, int BM, hipStream_t s, int32_t* queues = nullptr);
+                             int32_t* blockcnt, int BM, int slot_rows, hipStream_t s, int32_t* queues = nullptr);
 hipError_t launch_router_norm(const uint16_t* h, const uint16_t* scale, float scalar_root,
                               float eps, uint16_t* r, int M, int H, hipStream_t s);
 hipError_t launch_router_logits(const uint16_t* r, const uint16_t* proj, float* partial, int M,
@@ -163,7 +172,7 @@ hipError_t launch_router_tok(const uint16_t* h, const uint16_t* scale, float sca
 hipError_t launch_topk_sort(const float* partial, int ksplit, const uint16_t* per_expert_scale,
                             int64_t* idx, float* w, int M, int E, int topk, int32_t* sorted_pos,
                             int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
-                            int BM, hipStream_t s);
+                            int BM, int slot_rows, hipStream_t s);
 hipError_t launch_router_topk(const float* partial, int ksplit, const uint16_t* logits_in,
                               const uint16_t* per_expert_scale, uint16_t* logits_out,
                               int64_t* idx, float* w, int M, int E, int topk, hipStream_t s);
@@ -202,7 +211,7 @@ hipError_t launch_router_norm_logits_with_linear(const uint16_t* h, const uint16
 hipError_t launch_topk_sort_with_linear(const float* partial, int ksplit, const uint16_t* per_expert_scale,
                                         int64_t* idx, float* w, int M, int E, int topk, int32_t* sorted_pos,
                                         int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
-                                        int BM, const LinearCall& lin, hipStream_t s);
+                                        int BM, int slot_rows, const LinearCall& lin, hipStream_t s);
 // FFN block row kernels (kernels_ffn.hip), one workgroup per row, H % 8 == 0,
 // H <= 8192:
 //   pre : h = rms(attn) * w_pa; res_out = bf16(res + h);

@@ -654,8 +654,9 @@ def _hybridlink_params(H, seed, dev):
 
 # batch 32 at H = 2816 is the latent loop's shape; 1 / 17 / 100 cover one,
 # two and several row tiles (ragged); H = 32 leaves seven of the eight
-# K-split wavefronts without k steps
-@pytest.mark.parametrize("B,Hh", [(32, 2816), (1, 2816), (17, 256), (100, 1024), (5, 32)])
+# K-split wavefronts without k steps; H = 4096 the LayerNorm's long-row form
+# (more than 3072 values per row)
+@pytest.mark.parametrize("B,Hh", [(32, 2816), (1, 2816), (17, 256), (100, 1024), (5, 32), (3, 4096)])
 def test_hybridlink(dev, B, Hh):
     p = _hybridlink_params(Hh, seed=900 + Hh, dev=dev)
     h = synth.activations(B, Hh, seed=901 + B, device=dev)
