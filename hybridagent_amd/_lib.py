@@ -86,6 +86,9 @@ SIGNATURES = {
                                          _I64, _VP, _SZ, _VP]),
     "moe_layer_forward_tiled": (ctypes.c_int, [_VP, _VP, _F32, _VP, _VP, _F32, _VP, _VP, _VP, _VP, _VP, _TP,
                                                _VP, _VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
+    "moe_layer_forward_add_norm": (ctypes.c_int, [_VP, _VP, _F32, _VP, _VP, _F32, _VP, _VP, _VP, _VP, _VP, _TP,
+                                                  _VP, _VP, _VP, _VP, _F32, _VP, _VP, _I64, _I64, _I64, _I64, _I64,
+                                                  _I64, _VP, _SZ, _VP]),
     "moe_ffn_block_forward_tiled": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _F32, _VP, _VP,
                                                    _VP, _VP, _VP, _VP, _VP, _TP, _VP, _VP, _VP, _F32, _VP, _I64,
                                                    _I64, _I64, _I64, _I64, _I64, _I64, _VP, _SZ, _VP]),
@@ -609,6 +612,53 @@ def moe_layer_forward(router_in: torch.Tensor, router_scale: torch.Tensor, scala
         else:
             _check(lib.moe_layer_forward_tiled(*common, ctypes.byref(st), *tail), "moe_layer_forward_tiled")
     return out.reshape(*hidden_states.shape[:-1], H), w, idx
+
+
+def moe_layer_forward_add_norm(router_in: torch.Tensor, router_scale: torch.Tensor, scalar_root: float,
+                               proj_w: torch.Tensor, per_expert_scale: torch.Tensor, eps: float, top_k: int,
+                               hidden_states: torch.Tensor, gu_packed: torch.Tensor, gu_scale: torch.Tensor,
+                               dn_packed: torch.Tensor, dn_scale: torch.Tensor, norm_weight: torch.Tensor,
+                               norm_eps: float, group_size: int | None = None, *, tiles="auto"):
+    """moe_layer_forward on (router_in = h, hidden_states), then h_out = bf16(h + out) and
+    y = RMSNorm(h_out) * norm_weight (add_rms_norm's arithmetic), the combine, the add and
+    the norm in one launch where the layer has a combine launch of its own (the latent
+    harness's step) -> (h_out, y, out, top_k_weights, top_k_index)."""
+    dev = _require_gpu(router_in, router_scale, proj_w, per_expert_scale, hidden_states, gu_packed,
+                       gu_scale, dn_packed, dn_scale, norm_weight)
+    H = hidden_states.shape[-1]
+    r2 = _bf16(router_in, "router_in").reshape(-1, H)
+    x = _bf16(hidden_states, "hidden_states").reshape(-1, H)
+    if r2.shape != x.shape:
+        raise ValueError("router input and expert input must have the same shape")
+    norm_weight = _bf16(norm_weight, "norm weight")
+    if norm_weight.shape != (H,):
+        raise ValueError(f"norm weight must be [{H}]")
+    router_scale = _bf16(router_scale, "router scale")
+    proj_w = _bf16(proj_w, "router proj weight")
+    per_expert_scale = _bf16(per_expert_scale, "per_expert_scale")
+    gu_packed, dn_packed = _i32(gu_packed, "gate_up_packed"), _i32(dn_packed, "down_packed")
+    gu_scale, dn_scale = _bf16(gu_scale, "gate_up_scale"), _bf16(dn_scale, "down_scale")
+    E, H, I, G = _expert_shape(gu_packed, gu_scale, dn_packed, dn_scale, group_size)
+    if proj_w.shape != (E, H):
+        raise ValueError("router weight shape does not match the experts")
+    M = x.shape[0]
+    out = torch.empty((M, H), dtype=torch.bfloat16, device=dev)
+    h_out = torch.empty((M, H), dtype=torch.bfloat16, device=dev)
+    y = torch.empty((M, H), dtype=torch.bfloat16, device=dev)
+    idx = torch.empty((M, top_k), dtype=torch.int64, device=dev)
+    w = torch.empty((M, top_k), dtype=torch.float32, device=dev)
+    lib = load()
+    ws = _workspace(lib.moe_layer_workspace_bytes(max(M, 1), top_k, E, H, I), dev)
+    st = _resolve_tiles(tiles, gu_packed, gu_scale, dn_packed, dn_scale, E, H, I, G)
+    with torch.cuda.device(dev):
+        _check(lib.moe_layer_forward_add_norm(
+            _ptr(r2), _ptr(router_scale), float(scalar_root), _ptr(proj_w), _ptr(per_expert_scale), float(eps),
+            _ptr(x), _ptr(gu_packed), _ptr(gu_scale), _ptr(dn_packed), _ptr(dn_scale),
+            None if st is None else ctypes.byref(st), _ptr(out), _ptr(idx), _ptr(w), _ptr(norm_weight),
+            float(norm_eps), _ptr(h_out), _ptr(y), M, top_k, E, H, I, G, _ptr(ws),
+            0 if ws is None else ws.numel(), _stream(dev)), "moe_layer_forward_add_norm")
+    shape = hidden_states.shape
+    return h_out.reshape(shape), y.reshape(shape), out.reshape(shape), w, idx
 
 
 def bf16_experts_forward(hidden_states: torch.Tensor, top_k_index: torch.Tensor, top_k_weights: torch.Tensor,

@@ -69,6 +69,17 @@ struct SharedMlp {
   LinearCall gate_up, down;
 };
 
+// The latent harness's residual add and next norm after a layer:
+// h_out = bf16(h + out), y = RMSNorm(h_out) * w (w4a16_add_rms_norm's
+// arithmetic), fused into the combine launch where the layer has one.
+struct AddNorm {
+  const uint16_t* h;
+  const uint16_t* w;
+  float eps;
+  uint16_t* h_out;
+  uint16_t* y;
+};
+
 inline hipError_t launch_linear_call(const LinearCall& l, hipStream_t s) {
   return launch_linear_bf16(l.epi, l.x, l.W, l.W2, l.bias, l.res, l.out, l.M, l.N, l.K, s);
 }
@@ -692,13 +703,23 @@ constexpr int64_t kFuseDownCombineRows = 32;
 int down_and_combine(const int32_t* dn_packed, const uint16_t* dn_scale, const int64_t* topk_idx,
                      const float* topk_w, uint16_t* out, int64_t M, int64_t top_k, int64_t E,
                      int64_t H, int64_t I, int64_t group_size, void* workspace,
-                     size_t workspace_bytes, void* stream, const Tiles& t) {
+                     size_t workspace_bytes, void* stream, const Tiles& t, const AddNorm* an = nullptr) {
   if (use_prefill(M, H, I) || M * top_k > kFuseDownCombineRows || !down_combine_supported(M, top_k, I)) {
     int st = down_impl(dn_packed, dn_scale, t, M, top_k, E, H, I, group_size, workspace, workspace_bytes,
                        stream);
-    if (st == W4A16_OK)
-      st = moe_combine(topk_idx, topk_w, out, M, top_k, E, H, I, workspace, workspace_bytes,
-                       stream);
+    if (st != W4A16_OK) return st;
+    if (an != nullptr && top_k <= 8) {
+      MoeLayout L{};
+      st = moe_check(M, top_k, E, H, I, group_size, workspace, workspace_bytes, &L);
+      if (st != W4A16_OK) return st;
+      return launch_status(launch_combine_add_rms_norm(L.dn, topk_idx, topk_w, an->h, an->w, out, an->h_out,
+                                                       an->y, M, (int)top_k, (int)E, (int)H, an->eps,
+                                                       static_cast<hipStream_t>(stream)));
+    }
+    st = moe_combine(topk_idx, topk_w, out, M, top_k, E, H, I, workspace, workspace_bytes, stream);
+    if (st == W4A16_OK && an != nullptr)
+      st = launch_status(launch_add_rms_norm(an->h, out, an->w, an->h_out, an->y, M, (int)H, an->eps,
+                                             static_cast<hipStream_t>(stream)));
     return st;
   }
   MoeLayout L{};
@@ -727,7 +748,11 @@ int down_and_combine(const int32_t* dn_packed, const uint16_t* dn_scale, const i
   if (t.dn_decode != nullptr &&
       tiled_decode_down_geometry(H, I, group_size, &a.tpw, &a.block_bytes, &a.expert_bytes))
     a.wt = t.dn_decode;
-  return launch_status(launch_down_combine(a, static_cast<hipStream_t>(stream)));
+  st = launch_status(launch_down_combine(a, static_cast<hipStream_t>(stream)));
+  if (st == W4A16_OK && an != nullptr)
+    st = launch_status(launch_add_rms_norm(an->h, out, an->w, an->h_out, an->y, M, (int)H, an->eps,
+                                           static_cast<hipStream_t>(stream)));
+  return st;
 }
 
 }  // namespace
@@ -833,7 +858,8 @@ static int layer_forward_impl(const uint16_t* router_in, const uint16_t* router_
                               const int32_t* dn_packed, const uint16_t* dn_scale, const Tiles& t,
                               uint16_t* out, int64_t* topk_idx, float* topk_w, int64_t M, int64_t top_k,
                               int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
-                              size_t workspace_bytes, void* stream, const SharedMlp* mlp = nullptr);
+                              size_t workspace_bytes, void* stream, const SharedMlp* mlp = nullptr,
+                              const AddNorm* an = nullptr);
 
 static int ffn_block_impl(const uint16_t* residual, const uint16_t* attn_out,
                           const uint16_t* post_attn_ln_w, const uint16_t* pre_ff_ln_w,
@@ -1064,7 +1090,7 @@ static int layer_forward_impl(const uint16_t* router_in, const uint16_t* router_
                               const int32_t* dn_packed, const uint16_t* dn_scale, const Tiles& t,
                               uint16_t* out, int64_t* topk_idx, float* topk_w, int64_t M, int64_t top_k,
                               int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
-                              size_t workspace_bytes, void* stream, const SharedMlp* mlp) {
+                              size_t workspace_bytes, void* stream, const SharedMlp* mlp, const AddNorm* an) {
   if (M < 0 || M > (1 << 24) || top_k > E) return W4A16_ERR_SHAPE;
   if (M == 0) {
     MoeLayout dummy{};
@@ -1131,7 +1157,7 @@ static int layer_forward_impl(const uint16_t* router_in, const uint16_t* router_
                     moe_bytes, stream);
   if (st == W4A16_OK)
     st = down_and_combine(dn_packed, dn_scale, topk_idx, topk_w, out, M, top_k, E, H, I,
-                          group_size, workspace, moe_bytes, stream, t);
+                          group_size, workspace, moe_bytes, stream, t, an);
   return st;
 }
 
@@ -1160,6 +1186,29 @@ int moe_layer_forward_tiled(const uint16_t* router_in, const uint16_t* router_sc
   return layer_forward_impl(router_in, router_scale, scalar_root, proj_w, per_expert_scale, eps, hidden, gu_packed,
                             gu_scale, dn_packed, dn_scale, t, out, topk_idx, topk_w, M, top_k, E, H, I, group_size,
                             workspace, workspace_bytes, stream);
+}
+
+int moe_layer_forward_add_norm(const uint16_t* router_in, const uint16_t* router_scale, float scalar_root,
+                               const uint16_t* proj_w, const uint16_t* per_expert_scale, float eps,
+                               const uint16_t* hidden, const int32_t* gu_packed, const uint16_t* gu_scale,
+                               const int32_t* dn_packed, const uint16_t* dn_scale,
+                               const w4a16_tiled_experts* tiled, uint16_t* out, int64_t* topk_idx, float* topk_w,
+                               const uint16_t* norm_w, float norm_eps, uint16_t* h_out, uint16_t* y_out, int64_t M,
+                               int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  // the norm kernels hold a row in one 256-thread workgroup: H <= 8192
+  if (H > 8192) return W4A16_ERR_SHAPE;
+  if (M > 0 && (!norm_w || !h_out || !y_out)) return W4A16_ERR_NULL;
+  if (M > 0 && (!aligned16(norm_w) || !aligned16(h_out) || !aligned16(y_out))) return W4A16_ERR_ALIGN;
+  Tiles t;
+  if (tiled != nullptr) {
+    const int st = resolve_tiles(tiled, E, H, I, group_size, &t);
+    if (st != W4A16_OK) return st;
+  }
+  const AddNorm an{router_in, norm_w, norm_eps, h_out, y_out};
+  return layer_forward_impl(router_in, router_scale, scalar_root, proj_w, per_expert_scale, eps, hidden, gu_packed,
+                            gu_scale, dn_packed, dn_scale, t, out, topk_idx, topk_w, M, top_k, E, H, I, group_size,
+                            workspace, workspace_bytes, stream, nullptr, &an);
 }
 
 }  // extern "C"

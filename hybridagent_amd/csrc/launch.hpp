@@ -123,6 +123,12 @@ hipError_t launch_add_rms_norm(const uint16_t* h, const uint16_t* delta, const u
                                hipStream_t s);
 hipError_t launch_combine(const uint16_t* dn, const int64_t* idx, const float* w, uint16_t* out,
                           int M, int topk, int E, int H, hipStream_t s);
+// the combine (out nullable), h_out = bf16(h + out) and y = RMSNorm(h_out) * w
+// in one launch (kernels_norm.hip), the bits of launch_combine followed by
+// launch_add_rms_norm; topk <= 8
+hipError_t launch_combine_add_rms_norm(const uint16_t* dn, const int64_t* idx, const float* tw, const uint16_t* h,
+                                       const uint16_t* w, uint16_t* out, uint16_t* h_out, uint16_t* y, int64_t M,
+                                       int topk, int E, int H, float eps, hipStream_t s);
 // down + combine in one launch: M * topk <= kDownCombineMaxRows,
 // K <= 768 and a multiple of 32; the intermediate rows in the order the
 // decode gate_up writes them; the weights in the packed layout (a.wt NULL)

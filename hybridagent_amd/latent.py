@@ -9,8 +9,9 @@ last layer the HybridLink map R(h) = LN(h + proj2(GELU(proj1(LN(h)))))
 
 The MoE layers run through the HIP library (router + experts in one C-ABI
 call per layer), and so do the residual add and RMSNorm in front of each
-(one w4a16_add_rms_norm launch: the previous layer's MoE output is added to
-the residual while it is normalised), and so does the HybridLink map
+(inside the previous layer's combine launch, moe_layer_forward_add_norm; in
+front of the first layer one w4a16_add_rms_norm launch), and so does the
+HybridLink map
 (w4a16_hybridlink: two LayerNorm launches and two bf16 weight-streaming
 linear launches with the bias, GELU and residual fused).
 """
@@ -89,9 +90,23 @@ class LatentStack:
     def step(self, h: torch.Tensor) -> torch.Tensor:
         """One latent step: all MoE layers, then HybridLink x sqrt(H).  The same
         arithmetic as calling layer() in turn: layer i's output is added to the
-        residual inside layer i + 1's norm launch."""
-        out = None
-        for i, ly in enumerate(self.layers):
-            h, xin = _lib.add_rms_norm(h, ly.pre_norm, self.eps, delta=out)
-            out, _, _ = self.moe_on(h, xin, i)
+        residual, and layer i + 1's input normalised, inside layer i's combine
+        launch (moe_layer_forward_add_norm)."""
+        n = len(self.layers)
+        if n == 0:
+            return self.hybridlink(h) * math.sqrt(self.H)
+        h, xin = _lib.add_rms_norm(h, self.layers[0].pre_norm, self.eps)
+        for i in range(n - 1):
+            h, xin = self.moe_add_norm(h, xin, i, self.layers[i + 1].pre_norm)
+        out, _, _ = self.moe_on(h, xin, n - 1)
         return self.hybridlink(h + out) * math.sqrt(self.H)
+
+    def moe_add_norm(self, h: torch.Tensor, xin: torch.Tensor, i: int, next_norm: torch.Tensor):
+        """Layer i on (h, xin = RMSNorm(h)), then h + out and its RMSNorm with next_norm."""
+        ly = self.layers[i]
+        rw, ew = ly.router, ly.experts
+        h_out, y, _, _, _ = _lib.moe_layer_forward_add_norm(
+            h, rw.scale, rw.scalar_root, rw.proj, rw.per_expert_scale, rw.eps, self.top_k, xin,
+            ew.gate_up_packed, ew.gate_up_scale, ew.down_packed, ew.down_scale, next_norm, self.eps,
+            group_size=self.G, tiles=ly.tiles)
+        return h_out, y

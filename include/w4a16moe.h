@@ -280,6 +280,28 @@ W4A16_API int moe_layer_forward_tiled(const uint16_t* router_in, const uint16_t*
                                       int64_t I, int64_t group_size, void* workspace,
                                       size_t workspace_bytes, void* stream);
 
+/* The latent harness's layer step (configs[4]: h <- h + MoE(RMSNorm(h)) per
+ * layer, hybridlink.py's latent loop over the MoE stack): moe_layer_forward
+ * on router_in = h and hidden = RMSNorm(h) (tiled: NULL or the copies, as for
+ * moe_layer_forward_tiled), then the residual add and the next layer's norm
+ *   h_out = bf16(h + out),  y_out = bf16((h_out * rsqrt(mean(h_out^2) + norm_eps)) * norm_w)
+ * -- bit for bit moe_layer_forward followed by w4a16_add_rms_norm(h, out,
+ * norm_w) -- with the combine, the add and the norm in one launch where the
+ * layer combines in a launch of its own (more than 32 routed rows, top_k <= 8).
+ * No function of the reference matches it: it fuses the harness's residual
+ * add and norm around moe_layer_forward.  norm_w [H], h_out, y_out [M, H]
+ * bf16, 16-byte aligned; H <= 8192; workspace as for moe_layer_forward.    */
+W4A16_API int moe_layer_forward_add_norm(const uint16_t* router_in, const uint16_t* router_scale,
+                                         float scalar_root, const uint16_t* proj_w,
+                                         const uint16_t* per_expert_scale, float eps, const uint16_t* hidden,
+                                         const int32_t* gu_packed, const uint16_t* gu_scale,
+                                         const int32_t* dn_packed, const uint16_t* dn_scale,
+                                         const w4a16_tiled_experts* tiled, uint16_t* out, int64_t* topk_idx,
+                                         float* topk_w, const uint16_t* norm_w, float norm_eps, uint16_t* h_out,
+                                         uint16_t* y_out, int64_t M, int64_t top_k, int64_t E, int64_t H,
+                                         int64_t I, int64_t group_size, void* workspace,
+                                         size_t workspace_bytes, void* stream);
+
 /* The BF16 experts (unquantised Gemma4TextExperts weights) on the same
  * routing machinery: _bf16_experts_fast_forward  -- backends.py:209-283
  * (installed on every BF16 experts module by patch_bf16_experts_fastpath,

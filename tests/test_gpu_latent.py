@@ -2,8 +2,9 @@
 I = 704, top-8, G = 128; 11.8 GB of weights), batch 32, HybridLink x sqrt(H)
 fed back as the next step's input.
 
-* ``LatentStack.step`` (the residual add of layer i fused into layer i + 1's
-  RMSNorm launch) is bit-identical to the 30 layers called one after the
+* ``LatentStack.step`` (layer i's combine, the residual add and layer
+  i + 1's RMSNorm in one launch: moe_layer_forward_add_norm) is
+  bit-identical to the 30 layers called one after the
   other followed by HybridLink x sqrt(2816), on the first step and on the
   fed-back second step (hybridlink.py:17-28, backends.py:111-122,
   engine.py:381-390);
@@ -92,3 +93,29 @@ def test_latent_stack_config4_full_shape(dev):
                                  ew.down_packed[ut].cpu().numpy(), _bits(ew.down_scale[ut]), G)
         err = oracle.max_abs_rel(_np(out)[rows], ref)
         assert margin(f"configs[4] layer {li} MoE (all {B} rows, {len(used)} experts)", err) <= TOL
+
+
+# moe_layer_forward_add_norm on its own: the same bits as moe_layer_forward
+# followed by add_rms_norm, where the add and norm ride in the combine launch
+# (M = 32: 256 routed rows), after the fused down + combine (M = 2) and after
+# the any-k combine (top_k = 10); packed and tiled weights
+@pytest.mark.parametrize("M,k,tiled", [(32, 8, False), (32, 8, True), (2, 8, True), (8, 10, False)])
+def test_layer_forward_add_norm_matches_separate(dev, M, k, tiled):
+    Hh, Ii, Ee, Gg = 1024, 256, 32, 128
+    rw = synth.router_weights(Ee, Hh, seed=7900 + M, device=dev)
+    ew = synth.moe_weights(Ee, Hh, Ii, Gg, seed=7901 + M, device=dev)
+    tiles = _lib.tile_experts(ew.gate_up_packed, ew.gate_up_scale, ew.down_packed, ew.down_scale, Gg,
+                              prefill=False) if tiled else None
+    g = torch.Generator(device=dev).manual_seed(7902 + M)
+    norm_w = (1.0 + 0.05 * torch.randn(Hh, generator=g, device=dev)).to(torch.bfloat16)
+    h = synth.activations(M, Hh, seed=7903 + M, device=dev)
+    xin = _lib.add_rms_norm(h, norm_w, 1e-6)[1]
+    args = (h, rw.scale, rw.scalar_root, rw.proj, rw.per_expert_scale, rw.eps, k, xin, ew.gate_up_packed,
+            ew.gate_up_scale, ew.down_packed, ew.down_scale)
+    out, w, idx = _lib.moe_layer_forward(*args, group_size=Gg, tiles=tiles)
+    h_ref, y_ref = _lib.add_rms_norm(h, norm_w, 1e-6, delta=out)
+    h2, y2, out2, w2, idx2 = _lib.moe_layer_forward_add_norm(*args, norm_w, 1e-6, group_size=Gg, tiles=tiles)
+    assert torch.equal(idx2, idx) and torch.equal(w2, w)
+    assert torch.equal(out2, out)
+    assert torch.equal(h2, h_ref)
+    assert torch.equal(y2, y_ref)
