@@ -581,14 +581,16 @@ static size_t stream_lds(const DecodeArgs& a) {
 // fewer than W4A16_NARROW_ITEMS_PER_CU items per CU and the narrow
 // workgroups stage at most W4A16_NARROW_ROWS_PER_CU activation rows per CU
 // in all (each narrow workgroup stages its own rows: a dense batch of many
-// rows stays wide).  Measured: dense 2816 x 2816 at M = 1 / 16 9.4 -> 6.1 /
-// 12.0 -> 9.3 us, MoE decode M = 1 / 2 31.0 -> 29.4 / 38.4 -> 35.3 us; dense
-// M = 64 narrow (8 staged rows per workgroup) 12.1 -> 13.9 us.
+// rows stays wide; a MoE slot stages its routed rows, M * top_k / slots on
+// average).  Measured: dense 2816 x 2816 at M = 1 / 16 9.4 -> 6.1 / 12.0 ->
+// 9.3 us, MoE decode M = 1 / 2 / 8 31.0 -> 29.4 / 38.4 -> 35.3 / 66.0 -> 63.0
+// us, M = 16 unchanged; dense M = 64 narrow (8 staged rows per workgroup)
+// 12.1 -> 13.9 us.
 #ifndef W4A16_NARROW_ITEMS_PER_CU
-#define W4A16_NARROW_ITEMS_PER_CU 4
+#define W4A16_NARROW_ITEMS_PER_CU 8
 #endif
 #ifndef W4A16_NARROW_ROWS_PER_CU
-#define W4A16_NARROW_ROWS_PER_CU 16
+#define W4A16_NARROW_ROWS_PER_CU 32
 #endif
 
 // ncolblk: column blocks of 16 weight rows per expert (gate_up: 8 gate and 8
@@ -611,8 +613,11 @@ static hipError_t launch_stream(DecodeArgs a, int ncolblk, int max_slots, hipStr
   const int rb_wide = rows_for(64 * KSPLIT * kWideCg), rb_narrow = rows_for(64 * KSPLIT);
   const int64_t wide_items = (int64_t)slots_for(rb_wide) * ((ncolblk + kWideCg - 1) / kWideCg);
   const int64_t narrow_items = (int64_t)slots_for(rb_narrow) * ncolblk;
+  const int64_t slot_rows =
+      MODE == kModeDense ? rb_narrow
+                         : std::min<int64_t>(rb_narrow, ((int64_t)a.M * a.topk + max_slots - 1) / std::max(max_slots, 1));
   const bool narrow = wide_items < (int64_t)W4A16_NARROW_ITEMS_PER_CU * cus &&
-                      narrow_items * rb_narrow <= (int64_t)W4A16_NARROW_ROWS_PER_CU * cus;
+                      narrow_items * slot_rows <= (int64_t)W4A16_NARROW_ROWS_PER_CU * cus;
   a.cg = narrow ? 1 : kWideCg;
   a.rb = narrow ? rb_narrow : rb_wide;
   a.n_ct = (ncolblk + a.cg - 1) / a.cg;
