@@ -131,6 +131,17 @@ def test_ffn_block_small_shapes(dev, G, ls):
     assert torch.equal(backends.ffn_moe_4bit_step(**sub, top_k=K), out[1:4])
 
 
+# Where the router's launches cannot take the shared MLP's linears they run as
+# launches of their own (k_linear_bf16): more than 64 routed rows (M = 12,
+# top-8: the down linear), rows longer than the fused router takes (H = 4096:
+# the gate/up linear, 16 and 32 rows per workgroup)
+@pytest.mark.parametrize("M,K,H", [(12, 8, 512), (4, 4, 4096), (20, 4, 4096)])
+def test_ffn_block_separate_mlp_launches(dev, M, K, H):
+    I, Im, E, G = 192, 384, 16, 128
+    a = _block_inputs(M, H, I, Im, E, G, seed=2400 + M + H, dev=dev)
+    _check(a, K, G, f"ffn block M={M} top_k={K} H={H} (separate linears)")
+
+
 class _AttnStub(torch.nn.Module):
     """Stands in for self-attention (attention is outside this path): a fixed
     elementwise map of the normalised input."""
