@@ -230,22 +230,24 @@ def dense_sweep(dev, steps, warmup):
     return out
 
 
-def prefill(dev, steps, warmup, n_layers, g: int = G, stages: bool = True):
+def prefill(dev, steps, warmup, n_layers, g: int = G, stages: bool = True, layer: bool = True):
     """the whole layer (router + sort + gate_up + down + combine) at
     M = 4096 with Zipf routing; with ``stages`` also the gate_up stage alone
-    (the grouped gate_up GEMM, the dominant kernel)."""
+    (the grouped gate_up GEMM, the dominant kernel); without ``layer`` only
+    that stage (a kernel trace then holds the stage's dispatches alone)."""
     layers = [Layer(seed=9000 + 17 * i, dev=dev, zipf=True, g=g) for i in range(n_layers)]
     x = synth.zipf_activations(PREFILL_M, H, seed=9999, device=dev)
     _, idx = layers[0].route(x)
     counts = torch.bincount(idx.flatten(), minlength=E).cpu()
-    t = time_graph(lambda: [ly.forward(x) for ly in layers], len(layers), steps, warmup)
     flops = 2.0 * PREFILL_M * TOPK * (H * 2 * I + I * H) + 2.0 * PREFILL_M * H * E
     srt = torch.sort(counts, descending=True).values
-    res = {"group_size": g, "ms": t * 1e3, "tflops": flops / t / 1e12,
-           "frac_mfma": flops / t / 1e12 / PEAK_BF16_TFLOPS, "gflop": flops / 1e9,
-           "empty_experts": int((counts == 0).sum()), "hot_expert_rows": srt[:4].tolist()}
-    log(f"prefill G={g} M={PREFILL_M}: {t*1e3:.3f} ms/layer, {res['tflops']:.1f} TFLOP/s, "
-        f"empty={res['empty_experts']} hot={res['hot_expert_rows']}")
+    res = {"group_size": g, "gflop": flops / 1e9, "empty_experts": int((counts == 0).sum()),
+           "hot_expert_rows": srt[:4].tolist()}
+    if layer:
+        t = time_graph(lambda: [ly.forward(x) for ly in layers], len(layers), steps, warmup)
+        res.update({"ms": t * 1e3, "tflops": flops / t / 1e12, "frac_mfma": flops / t / 1e12 / PEAK_BF16_TFLOPS})
+        log(f"prefill G={g} M={PREFILL_M}: {t*1e3:.3f} ms/layer, {res['tflops']:.1f} TFLOP/s, "
+            f"empty={res['empty_experts']} hot={res['hot_expert_rows']}")
     if stages:
         sts = []
         for ly in layers:
@@ -305,10 +307,28 @@ def roofline_prefill(pre):
         "algorithmic_gflop_per_launch": round(st["gflop"], 3),
         "mfma_busy_frac_counter": counter_summary(PREFILL_COUNTERS_FILE, "mfma_busy_frac_gate_up"),
         "counter_source": os.path.relpath(PREFILL_COUNTERS_FILE, ROOT),
+        # GFLOP / us = PFLOP/s: x 1e3 for TFLOP/s
+        **trace_fields(PREFILL_TRACE_FILE, st["gflop"], PEAK_BF16_TFLOPS, 1e3),
     }
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gateup_decode_M64_traffic.md")
+# the committed kernel traces of the two roofline kernels: their per-dispatch
+# mean durations (``trace_us_per_launch:`` lines), stated beside this run's
+# HIP-event figure so each line's frac can be checked against profiles/
+ROOF_TRACE_FILE = os.path.join(ROOT, "profiles", "gateup_decode_M64_kernel_stats.md")
+PREFILL_TRACE_FILE = os.path.join(ROOT, "profiles", "prefill_M4096_kernel_stats.md")
+
+
+def trace_fields(path, work, peak, unit_scale):
+    """The committed trace's per-dispatch mean and the fraction of peak it gives
+    for ``work`` (bytes or flops per launch; unit_scale turns work/us into the
+    peak's unit)."""
+    us = counter_summary(path, "trace_us_per_launch")
+    if us is None or us <= 0:
+        return {"trace_us_per_launch": None, "frac_from_trace": None, "trace_source": None}
+    return {"trace_us_per_launch": us, "frac_from_trace": round(work / us * unit_scale / peak, 4),
+            "trace_source": os.path.relpath(path, ROOT)}
 
 
 def measured_traffic():
@@ -340,6 +360,8 @@ def roofline(kern):
         "us_per_launch_graph_replay": round(kern["us_graph"], 3),
         "timing": "per-dispatch HIP events (each launch bracketed), as a kernel trace reports it",
         "algorithmic_bytes_per_launch": int(kern["bytes"]),
+        # B / us = MB/s: / 1e3 for GB/s
+        **trace_fields(ROOF_TRACE_FILE, kern["bytes"], PEAK_HBM_GBS, 1e-3),
     }
 
 
@@ -695,6 +717,8 @@ def main(argv=None):
     ap.add_argument("--only-latent", action="store_true")
     ap.add_argument("--only-prefill", action="store_true",
                     help="time only the prefill layer (for rocprofv3 counter runs)")
+    ap.add_argument("--only-prefill-stage", action="store_true",
+                    help="time only the prefill gate_up stage, the prefill roofline kernel (for its kernel trace)")
     ap.add_argument("--no-ffn", action="store_true", help="skip the FFN-block leg")
     ap.add_argument("--no-bf16", action="store_true", help="skip the BF16-experts leg")
     ap.add_argument("--no-loader", action="store_true", help="skip the checkpoint-loading leg")
@@ -734,6 +758,10 @@ def main(argv=None):
         return 0
     if args.only_dense:
         print(json.dumps({"dense": dense_sweep(dev, args.steps, args.warmup)}), flush=True)
+        return 0
+    if args.only_prefill_stage:
+        pre = prefill(dev, max(8, args.steps // 4), max(2, args.warmup // 4), 4, layer=False)
+        print(json.dumps({"roofline_prefill": roofline_prefill(pre)}), flush=True)
         return 0
     if args.only_prefill:
         pre = prefill(dev, max(8, args.steps // 4), max(2, args.warmup // 4), 4)
