@@ -46,7 +46,7 @@ M = 1, 8, 64 over 8 rotated copies of a layer's bf16 experts.
 ``loader`` times checkpoint loading (quantization.py:325-430) of a synthetic
 4-layer pack-quantized checkpoint: the reference's host flow against the
 device-direct loader.
-``latent`` is BASELINE configs[4] (30 MoE layers + HybridLink per step, batch
+``latent`` is benchmark configs[4] (30 MoE layers + HybridLink per step, batch
 32); ``hybridlink`` times the HybridLink map alone at that batch (weights
 rotated through HBM).
 """
@@ -398,7 +398,7 @@ def hybridlink_leg(dev, steps: int = 64):
 
 
 def latent(dev, steps: int = LATENT_STEPS):
-    """30 MoE layers (h += MoE(RMSNorm(h))) + HybridLink x sqrt(H),
+    """benchmark configs[4]: 30 MoE layers (h += MoE(RMSNorm(h))) + HybridLink x sqrt(H),
     batch 32, the output fed back as the next step's input.  One HIP graph
     replay = one latent step."""
     from hybridagent_amd.latent import LatentStack
@@ -817,7 +817,7 @@ def main(argv=None):
         "data": "synthetic (seeded random int4 weights, bf16 scales ~U(0.005,0.02), activations ~N(0,1))",
         "config": {
             "workload": "Gemma-4-26B-A4B-shaped W4A16 MoE layer (router + experts): decode M=1,8,32,64 "
-                        "uniform routing (BASELINE configs[2]); prefill M=4096 Zipf(1.1) routing (configs[3])",
+                        "uniform routing (benchmark configs[2]); prefill M=4096 Zipf(1.1) routing (configs[3])",
             "hidden": H, "experts": E, "top_k": TOPK, "intermediate": I, "group_size": G,
             "layers_rotated": args.layers, "timing": "HIP graph replay, HIP events",
             "weights": "decode legs read load-time tiled copies of the experts (+1x expert HBM, "

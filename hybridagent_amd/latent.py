@@ -1,4 +1,4 @@
-"""Latent-mode MoE stack: the decode step of the
+"""Latent-mode MoE stack (benchmark configs[4]): the decode step of the
 HybridAgent latent loop reduced to its MoE layers.
 
 Each layer: ``h <- h + MoE(RMSNorm(h))``, the router reading the residual

@@ -280,8 +280,10 @@ W4A16_API int moe_layer_forward_tiled(const uint16_t* router_in, const uint16_t*
                                       int64_t I, int64_t group_size, void* workspace,
                                       size_t workspace_bytes, void* stream);
 
-/* The latent harness's layer step (configs[4]: h <- h + MoE(RMSNorm(h)) per
- * layer, hybridlink.py's latent loop over the MoE stack): moe_layer_forward
+/* The latent harness's layer step (configs[4], the latent loop's MoE
+ * stack: h <- h + MoE(RMSNorm(h)) per layer, the RMSNorm of
+ * modeling_gemma4.py:197-215, the router lines of backends.py:111-122):
+ * moe_layer_forward
  * on router_in = h and hidden = RMSNorm(h) (tiled: NULL or the copies, as for
  * moe_layer_forward_tiled), then the residual add and the next layer's norm
  *   h_out = bf16(h + out),  y_out = bf16((h_out * rsqrt(mean(h_out^2) + norm_eps)) * norm_w)

@@ -1,4 +1,4 @@
-"""BASELINE configs[4] at its stated shape: 30 MoE layers (E = 128, H = 2816,
+"""benchmark configs[4] at its stated shape: 30 MoE layers (E = 128, H = 2816,
 I = 704, top-8, G = 128; 11.8 GB of weights), batch 32, HybridLink x sqrt(H)
 fed back as the next step's input.
 

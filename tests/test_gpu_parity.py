@@ -496,7 +496,7 @@ def test_moe_large_batch_untiled_shape(dev):
 
 
 def test_moe_prefill_config3_zipf(dev, moe128):
-    # M=4096 with Zipf routing, every row against the
+    # benchmark configs[3]: M=4096 with Zipf routing, every row against the
     # oracle (and the distances to the unrounded fp32 arithmetic reported),
     # plus two size-independent properties of the tiled GEMM:
     #  * batch invariance: a token's output does not depend on which other
@@ -525,7 +525,7 @@ def test_moe_prefill_config3_zipf(dev, moe128):
     assert torch.equal(y_perm, y[perm])
 
 
-# ------------------------------------------- latent stack
+# ------------------------------------------- latent stack (benchmark configs[4])
 
 def test_latent_stack_layers_and_hybridlink(dev):
     # a small latent stack: every MoE layer against the oracle on the layer's
