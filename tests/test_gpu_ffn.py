@@ -112,8 +112,10 @@ def _check(a, top_k, G, what):
 
 
 # Gemma-4-26B-A4B shape; the shared MLP's intermediate size (2112) is an
-# assumption: the checkpoint's config.json is not available here
-@pytest.mark.parametrize("M", [1, 32, 300])
+# assumption: the checkpoint's config.json is not available here.  M = 1 and
+# 8: the shared MLP's gate/up in the router's launch, its down in the
+# top-k's; M = 32: down on its own; M = 300: both on their own
+@pytest.mark.parametrize("M", [1, 8, 32, 300])
 def test_ffn_block_gemma_shape(dev, M):
     H, I, Im, E, K, G = 2816, 704, 2112, 128, 8, 128
     a = _block_inputs(M, H, I, Im, E, G, seed=2000 + M, dev=dev)
@@ -135,7 +137,9 @@ def test_ffn_block_small_shapes(dev, G, ls):
 # launches of their own (k_linear_bf16): more than 64 routed rows (M = 12,
 # top-8: the down linear), rows longer than the fused router takes (H = 4096:
 # the gate/up linear, 16 and 32 rows per workgroup)
-@pytest.mark.parametrize("M,K,H", [(12, 8, 512), (4, 4, 4096), (20, 4, 4096)])
+# (and M = 8, top-8 over 16 experts: down with the one-round top-k of few
+# experts)
+@pytest.mark.parametrize("M,K,H", [(12, 8, 512), (4, 4, 4096), (20, 4, 4096), (8, 8, 512)])
 def test_ffn_block_separate_mlp_launches(dev, M, K, H):
     I, Im, E, G = 192, 384, 16, 128
     a = _block_inputs(M, H, I, Im, E, G, seed=2400 + M + H, dev=dev)
