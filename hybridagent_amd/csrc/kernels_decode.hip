@@ -298,7 +298,10 @@ void k_decode(DecodeArgs a) {
     // there would wait for every weight refill issued before it).  The
     // positions are read with scalar loads, which do not wait for the
     // vector loads in flight.
-    if (MODE != kModeDense) {
+    if (MODE == kModeGateUp && a.M == 1) {
+      // one token: every routed row is token 0, no position load to wait for
+      if (tid < 16) tok[tid] = 0;
+    } else if (MODE != kModeDense) {
       int sp[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) sp[i] = ld_uniform(a.sorted_pos, seg0 + mc + min(i, nr - 1));
