@@ -616,7 +616,7 @@ __device__ __forceinline__ void load_logits(const float* __restrict__ partial,
 // softmax (fp32) / top-k / renormalise / per_expert_scale of one token whose
 // logits `lg` were loaded by load_logits; lane `it` < topk returns selection it.
 template <int PER>
-__device__ void select_topk(const float (&lg)[PER], const uint16_t* __restrict__ pes, int E,
+__device__ __forceinline__ void select_topk(const float (&lg)[PER], const uint16_t* __restrict__ pes, int E,
                             int topk, int lane, int* sel_e, float* sel_w) {
   const int per = (E + 63) >> 6;
   // softmax denominator over all experts (fp32)
@@ -749,7 +749,7 @@ constexpr int kSortWaves = kSortThreads / 64;
 
 // exclusive block scan of one int per thread; returns the exclusive prefix,
 // *total gets the block total.  All threads must call it.
-__device__ int block_excl_scan(int v, int* wsum, int* total) {
+__device__ __forceinline__ int block_excl_scan(int v, int* wsum, int* total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int incl = wave_incl_scan(v, lane);
   if (lane == 63) wsum[wave] = incl;
@@ -783,7 +783,7 @@ __device__ __forceinline__ int4 plan_desc(int e, int off, int c, int SR, int i) 
 // the segment offsets, the work descriptors (plan_slots) and the m-tile
 // list; written when `write` (one workgroup writes them).  Returns thread e's
 // segment start.  All threads of the kSortThreads-thread workgroup call it.
-__device__ int write_plan(int c, int E, int32_t* __restrict__ offsets, int32_t* __restrict__ desc,
+__device__ __forceinline__ int write_plan(int c, int E, int32_t* __restrict__ offsets, int32_t* __restrict__ desc,
                           int32_t* __restrict__ counters, int32_t* __restrict__ tiles, int BM, int SR,
                           int* wsum, bool write) {
   const int tid = threadIdx.x;
@@ -820,7 +820,7 @@ __device__ int write_plan(int c, int E, int32_t* __restrict__ offsets, int32_t* 
 // starts into offsets[] and run[] (LDS), one descriptor per active expert,
 // the m-tile list and the two counters -- the same output as write_plan,
 // without workgroup barriers.
-__device__ void plan_wave(const int* cnt, int* run, int E, int32_t* __restrict__ offsets,
+__device__ __forceinline__ void plan_wave(const int* cnt, int* run, int E, int32_t* __restrict__ offsets,
                           int32_t* __restrict__ desc, int32_t* __restrict__ counters,
                           int32_t* __restrict__ tiles, int BM, int SR) {
   constexpr int PE = kMaxExperts / 64;
