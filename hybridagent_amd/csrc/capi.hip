@@ -482,9 +482,11 @@ int moe_plan(const uint16_t* hidden, const int64_t* topk_idx, int64_t M, int64_t
   if (!hidden || !topk_idx) return W4A16_ERR_NULL;
   if (!aligned16(hidden)) return W4A16_ERR_ALIGN;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int bm = plan_bm(M, H, I, group_size);
   // the decode streamers take an expert's rows as slots of kDecodeSlotRows
-  const int sr = use_prefill(M, H, I) ? 0 : kDecodeSlotRows;
+  // and read no m-tile list
+  const bool pf = use_prefill(M, H, I);
+  const int bm = pf ? plan_bm(M, H, I, group_size) : 0;
+  const int sr = pf ? 0 : kDecodeSlotRows;
   hipError_t e =
       M * top_k > kSortMultiMinRows
           ? launch_sort_multi(topk_idx, (int)M, (int)top_k, (int)E, L.sorted_pos, L.offsets,
@@ -1135,14 +1137,14 @@ static int layer_forward_impl(const uint16_t* router_in, const uint16_t* router_
     if (!mlp_dn)
       e = launch_topk_sort_with_linear(partial, router_ksplit(M, E), per_expert_scale, topk_idx, topk_w, (int)M,
                                        (int)E, (int)top_k, L.sorted_pos, L.offsets, L.desc, L.counters, L.tiles,
-                                       kPrefillBM, kDecodeSlotRows, mlp->down, s);
+                                       0, kDecodeSlotRows, mlp->down, s);
     if (e == hipSuccess) {
       mlp_dn = true;
     } else {
       if (e != hipErrorNotSupported) return W4A16_ERR_LAUNCH;
       e = launch_topk_sort(partial, router_ksplit(M, E), per_expert_scale, topk_idx, topk_w, (int)M,
                            (int)E, (int)top_k, L.sorted_pos, L.offsets, L.desc, L.counters, L.tiles,
-                           kPrefillBM, kDecodeSlotRows, s);
+                           0, kDecodeSlotRows, s);
       if (e != hipSuccess) return W4A16_ERR_LAUNCH;
     }
   } else {

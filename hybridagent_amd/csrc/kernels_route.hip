@@ -792,9 +792,10 @@ __device__ __forceinline__ int write_plan(int c, int E, int32_t* __restrict__ of
   int nact;
   const int ns = plan_slots(c, SR);
   const int apos = block_excl_scan(ns, wsum, &nact);
-  const int rem = c % BM;
+  // BM = 0: no m-tile list (the decode streamers read none)
+  const int rem = BM > 0 ? c % BM : 0;
   const int nsmall = (rem > 0 && rem <= BM / 2) ? 1 : 0;
-  const int nbig = (c + BM - 1) / BM - nsmall;
+  const int nbig = BM > 0 ? (c + BM - 1) / BM - nsmall : 0;
   int nbig_tot, nsmall_tot;
   const int bpos = block_excl_scan(nbig, wsum, &nbig_tot);
   const int spos = block_excl_scan(nsmall, wsum, &nsmall_tot);
@@ -816,27 +817,35 @@ __device__ __forceinline__ int write_plan(int c, int E, int32_t* __restrict__ of
 }
 
 // The plan from the per-expert counts cnt[0..E), by one wavefront (lane l
-// owns the consecutive experts l*pe .. l*pe+pe-1, pe = ceil(E / 64)): segment
-// starts into offsets[] and run[] (LDS), one descriptor per active expert,
-// the m-tile list and the two counters -- the same output as write_plan,
-// without workgroup barriers.
+// owns the consecutive experts l*pe .. l*pe+pe-1, pe = ceil(E / 64) <= PE):
+// segment starts into offsets[] and run[] (LDS), the descriptors, the m-tile
+// list and the two counters -- the same output as write_plan, without
+// workgroup barriers.  SR and BM are 0 or powers of two (shifts, not
+// divisions: this runs on the decode layer's critical path); BM = 0 writes
+// no tile list (counters[1] = 0), which the decode streamers do not read.
+template <int PE = kMaxExperts / 64>
 __device__ __forceinline__ void plan_wave(const int* cnt, int* run, int E, int32_t* __restrict__ offsets,
-                          int32_t* __restrict__ desc, int32_t* __restrict__ counters,
-                          int32_t* __restrict__ tiles, int BM, int SR) {
-  constexpr int PE = kMaxExperts / 64;
+                                          int32_t* __restrict__ desc, int32_t* __restrict__ counters,
+                                          int32_t* __restrict__ tiles, int BM, int SR) {
   const int lane = threadIdx.x & 63;
   const int pe = (E + 63) >> 6;
+  const int srs = SR > 0 ? __builtin_ctz(SR) : 0, bms = BM > 0 ? __builtin_ctz(BM) : 0;
+  auto n_slots = [&](int cc) { return cc <= 0 ? 0 : SR > 0 ? (cc + SR - 1) >> srs : 1; };
+  auto n_small = [&](int cc) {
+    const int rem = cc & (BM - 1);
+    return (BM > 0 && rem > 0 && rem <= BM / 2) ? 1 : 0;
+  };
+  auto n_big = [&](int cc) { return BM > 0 ? ((cc + BM - 1) >> bms) - n_small(cc) : 0; };
   int c[PE];
   int cs = 0, as = 0, bs = 0, ss = 0;
-  auto n_small = [&](int cc) { const int rem = cc % BM; return (rem > 0 && rem <= BM / 2) ? 1 : 0; };
 #pragma unroll
   for (int q = 0; q < PE; ++q) {
     const int e = lane * pe + q;
     c[q] = (q < pe && e < E) ? cnt[e] : 0;
     cs += c[q];
-    as += plan_slots(c[q], SR);
+    as += n_slots(c[q]);
     ss += n_small(c[q]);
-    bs += (c[q] + BM - 1) / BM - n_small(c[q]);
+    bs += n_big(c[q]);
   }
   const int ci = wave_incl_scan(cs, lane), ai = wave_incl_scan(as, lane);
   const int bi = wave_incl_scan(bs, lane), si = wave_incl_scan(ss, lane);
@@ -848,14 +857,13 @@ __device__ __forceinline__ void plan_wave(const int* cnt, int* run, int E, int32
     if (q < pe && e < E) {
       offsets[e] = off;
       run[e] = off;
-      const int ns = plan_slots(c[q], SR);
+      const int ns = n_slots(c[q]);
       for (int i = 0; i < ns; ++i) *reinterpret_cast<int4*>(desc + 4 * (apos + i)) = plan_desc(e, off, c[q], SR, i);
       apos += ns;
-      const int sm = n_small(c[q]);
-      const int nb = (c[q] + BM - 1) / BM - sm;
+      const int nb = n_big(c[q]);
       for (int i = 0; i < nb; ++i) tiles[bpos + i] = (e << 16) | i;
       bpos += nb;
-      if (sm) tiles[spos++] = (e << 16) | nb;
+      if (n_small(c[q])) tiles[spos++] = (e << 16) | nb;
       off += c[q];
     }
   }
@@ -1036,7 +1044,7 @@ __device__ __forceinline__ void topk_sort_small_block(const TopkSortArgs& args) 
   }
   const bool ok = e >= 0;
   if (ok) atomicAdd(&cnt[e], 1);
-  plan_wave(cnt, run, E, offsets, desc, counters, tiles, BM, args.slot_rows);
+  plan_wave<PER>(cnt, run, E, offsets, desc, counters, tiles, BM, args.slot_rows);
   int nbits = 0;
   while ((1 << nbits) < E) ++nbits;
   unsigned long long same = __ballot(ok);
@@ -1054,6 +1062,9 @@ __global__ __launch_bounds__(64 * kSmallSortWaves) void k_router_topk_sort_small
   topk_sort_small_block<KS, PER, ROUNDS>(a);
 }
 
+// plan_wave's BM and slot rows: 0 or a power of two
+static bool pow2_or_zero(int v) { return v >= 0 && (v & (v - 1)) == 0; }
+
 hipError_t launch_topk_sort(const float* partial, int ksplit, const uint16_t* per_expert_scale,
                             int64_t* idx, float* w, int M, int E, int topk, int32_t* sorted_pos,
                             int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
@@ -1061,7 +1072,8 @@ hipError_t launch_topk_sort(const float* partial, int ksplit, const uint16_t* pe
   if (M == 0) return hipSuccess;
   // the decode router's partials (kRouterMaxSplit K splits), at most 64
   // routed rows: one token per wavefront up to M = 8, else eight rounds
-  if (M * topk > 64 || ksplit != kRouterMaxSplit) return hipErrorInvalidValue;
+  if (M * topk > 64 || ksplit != kRouterMaxSplit || !pow2_or_zero(BM) || !pow2_or_zero(slot_rows))
+    return hipErrorInvalidValue;
   constexpr int KS = kRouterMaxSplit;
   const TopkSortArgs a{partial, per_expert_scale, idx, w, M, E, topk, sorted_pos, offsets, desc, counters, tiles, BM,
                        slot_rows};
@@ -1153,6 +1165,7 @@ hipError_t launch_topk_sort_with_linear(const float* partial, int ksplit, const 
   if (M == 0 || M * topk > 64 || M > kSmallSortWaves || ksplit != kRouterMaxSplit || E > 128 ||
       lin.epi != kLinPlain || lin.M <= 0 || lin.M > 16 || lin.K % 32 != 0 || lin.K <= 0 || lin.N <= 0)
     return hipErrorNotSupported;
+  if (!pow2_or_zero(BM) || !pow2_or_zero(slot_rows)) return hipErrorInvalidValue;
   const TopkSortArgs ta{partial, per_expert_scale, idx, w, M, E, topk, sorted_pos, offsets, desc, counters, tiles,
                         BM, slot_rows};
   const LinArgs la = lin_args(lin.epi, lin.x, lin.W, lin.W2, lin.bias, lin.res, lin.out, lin.M, lin.N, lin.K);
@@ -1269,6 +1282,7 @@ hipError_t launch_sort_multi(const int64_t* idx, int M, int topk, int E, int32_t
 hipError_t launch_sort(const int64_t* idx, int M, int topk, int E, int32_t* sorted_pos,
                        int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
                        int BM, int SR, hipStream_t s, int32_t* queues) {
+  if (!pow2_or_zero(BM) || !pow2_or_zero(SR)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_moe_sort, dim3(1), dim3(kSortThreads), 0, s, idx, M, topk, E, sorted_pos,
                      offsets, desc, counters, tiles, BM, SR, queues);
   return hipGetLastError();

@@ -148,7 +148,10 @@ inline int64_t plan_desc_capacity(int64_t M, int64_t topk, int64_t E) {
   return E + (M * topk + kDecodeSlotRows - 1) / kDecodeSlotRows;
 }
 // The expert sort; with `queues` (nullable) it also zeroes the
-// kPrefillQueueInts prefill work-queue counters there.
+// kPrefillQueueInts prefill work-queue counters there.  Every plan writer's
+// BM is the prefill m-tile height of the tile list (a power of two), or 0 for
+// plans with no tile list (counters[1] = 0): the decode streamers read none.
+// slot_rows is 0 or kDecodeSlotRows.
 hipError_t launch_sort(const int64_t* idx, int M, int topk, int E, int32_t* sorted_pos,
                        int32_t* offsets, int32_t* desc, int32_t* counters, int32_t* tiles,
                        int BM, int slot_rows, hipStream_t s, int32_t* queues = nullptr);
