@@ -146,6 +146,26 @@ void k_decode(DecodeArgs a) {
   const int j = lane & 15;   // MFMA column (weight row in the group) / A row
   const int kb = lane >> 4;  // 32-element chunk of the 128-wide k tile
 
+  // Staging tasks (see stage): one thread per (row, k tile), or -- without a
+  // K split -- two, each taking half of the task's 16 pieces.
+  constexpr int HALVES = KSPLIT != 1 ? 1 : 2;
+  constexpr int PIECES = 16 / HALVES;
+  // gate_up with one token: every staged row is token 0's row whatever the
+  // plan holds, so each stage stages that row alone (all MFMA A rows read
+  // it) and the first stage's activation loads are issued here, before the
+  // plan's two dependent loads (active experts, then the descriptor), whose
+  // round trips they overlap instead of following.
+  const bool one_tok = MODE == kModeGateUp && a.M == 1;
+  u32x4_t vpre[PIECES];
+  if (one_tok) {
+    const int rt = HALVES == 1 ? tid : (tid >> 1), hf = HALVES == 1 ? 0 : (tid & 1);
+    if (rt < ntiles) {
+      const int nb = min(16, (a.K >> 3) - 16 * rt);
+#pragma unroll
+      for (int b = 0; b < PIECES; ++b) vpre[b] = ld16(a.act + 128 * rt + 8 * min(PIECES * hf + b, nb - 1));
+    }
+  }
+
   // this workgroup's expert and item range.  The grid is spread over the
   // experts that are active in this batch (known only here): wps
   // workgroups each, so the chip fills whatever the routing.
@@ -184,8 +204,9 @@ void k_decode(DecodeArgs a) {
   const int K8 = a.K >> 3;
   const int nchunks = a.K >> 5;
   const int rb = a.rb;                 // staged rows per pass, a power of two <= 16
-  const int jr_read = j & (rb - 1);    // A row this lane reads (rows >= rb only
-                                       // feed output rows that are discarded)
+  // A row this lane reads (rows >= rb only feed output rows that are
+  // discarded; one token: the one staged row)
+  const int jr_read = one_tok ? 0 : j & (rb - 1);
   const int tile0 = ks * TPW;          // this wavefront's first k tile
 
   // Chunks past K in the last tile read zeros from LDS (their weight operand
@@ -291,7 +312,7 @@ void k_decode(DecodeArgs a) {
   // start every CU requests those at once); the stage completes while they
   // stream in, and the first item's MFMAs -- and the refills for the next
   // item -- start as soon as its weights land.
-  auto stage = [&](int mc, int nr, auto&& first) {
+  auto stage = [&](int mc, int nr, auto&& first, bool preloaded) {
     __syncthreads();  // previous readers of lds_a / tok are done
     // gate_up: token of each staged row; down: the output row t*k+j of each
     // staged row (read here once, so the epilogue issues no load: a load
@@ -324,8 +345,6 @@ void k_decode(DecodeArgs a) {
       if (MODE == kModeGateUp) return tok[jr];
       return seg0 + mc + jr;
     };
-    constexpr int HALVES = KSPLIT != 1 ? 1 : 2;
-    constexpr int PIECES = 16 / HALVES;
     const int task = tid;
     const bool has = task < HALVES * nr * ntiles;  // equal for both halves
     const int hf = HALVES == 1 ? 0 : (task & 1);
@@ -334,7 +353,10 @@ void k_decode(DecodeArgs a) {
     const int t = rt - jr * ntiles;
     const int nb = min(16, K8 - 16 * t);
     u32x4_t v[PIECES];
-    if (has) {
+    if (preloaded) {
+#pragma unroll
+      for (int b = 0; b < PIECES; ++b) v[b] = vpre[b];
+    } else if (has) {
       const uint16_t* src = a.act + row_of(jr) * a.K + 128 * t;
       // pieces past the row end load the last piece again and are dropped
 #pragma unroll
@@ -521,16 +543,16 @@ void k_decode(DecodeArgs a) {
   // last items load its first items again).  (Folding the first pass into
   // the loop of the later ones was measured twice as slow at decode sizes:
   // the compiler then waits for the prologue's loads before staging.)
-  stage(0, min(rb, rows), [&] {
+  stage(0, one_tok ? 1 : min(rb, rows), [&] {
     if (!LONGK) {
 #pragma unroll
       for (int r = 0; r < RING; ++r) load_batch(r, off_of(phys(begin + r)), tile0);
     }
-  });
+  }, one_tok);
   pass(0, min(rb, rows), rows <= rb);
   for (int mc = rb; mc < rows; mc += rb) {
     const int nr = min(rb, rows - mc);
-    stage(mc, nr, [] {});
+    stage(mc, one_tok ? 1 : nr, [] {}, false);
     pass(mc, nr, mc + nr >= rows);
   }
 }
