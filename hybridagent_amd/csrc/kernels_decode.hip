@@ -171,20 +171,36 @@ void k_decode(DecodeArgs a) {
   // workgroups each, so the chip fills whatever the routing.
   // Dense: the slots are the groups of rb rows (all of them run at once, so
   // each workgroup stages its rows once and streams its items once).
+  // MoE: the active count is known only here.  The descriptor of the slot
+  // this workgroup gets when u_guess slots are active (the launcher's
+  // likeliest count; at one token, the count) is requested together with
+  // the active count, and with the guess the launcher's slot arithmetic
+  // (workgroups per slot, items per workgroup, slot = blockIdx.x * magic >>
+  // 32) replaces the divisions: one scalar round trip, no division chain.
   int U = MODE == kModeDense ? (a.M + a.rb - 1) / a.rb : 1;
+  int e = 0, seg0 = 0, rows = a.M;
+  const int ug = a.u_guess;
+  const int slot_raw = a.wps_guess > 1 ? (int)__umulhi(blockIdx.x, a.slot_magic) : (int)blockIdx.x;
   if (MODE != kModeDense) {
+    const int slot_g = min(slot_raw, ug - 1);
+    e = ld_uniform(a.desc, 4 * slot_g);
+    seg0 = ld_uniform(a.desc, 4 * slot_g + 1);
+    rows = ld_uniform(a.desc, 4 * slot_g + 2);
     U = ld_uniform(a.n_active, 0);
+    asm volatile("" ::"s"(e), "s"(seg0), "s"(rows), "s"(U));  // all four in flight before the first wait
     if (U <= 0) return;
   }
-  const int wps = max(1, min(a.n_ct, (int)gridDim.x / U));
-  const int slot = (int)blockIdx.x / wps;
+  const bool guessed = U == ug;  // dense: always (u_guess is its slot count)
+  const int wps = guessed ? a.wps_guess : max(1, min(a.n_ct, (int)gridDim.x / U));
+  const int slot = guessed ? slot_raw : (int)blockIdx.x / wps;
   const int part = (int)blockIdx.x - slot * wps;
   if (slot >= U) return;  // uniform across the workgroup
-  int e = 0, seg0 = 0, rows = a.M;
   if (MODE != kModeDense) {
-    e = ld_uniform(a.desc, 4 * slot);
-    seg0 = ld_uniform(a.desc, 4 * slot + 1);
-    rows = ld_uniform(a.desc, 4 * slot + 2);
+    if (!guessed) {
+      e = ld_uniform(a.desc, 4 * slot);
+      seg0 = ld_uniform(a.desc, 4 * slot + 1);
+      rows = ld_uniform(a.desc, 4 * slot + 2);
+    }
   } else {
     seg0 = slot * a.rb;
     rows = min(a.rb, a.M - seg0);
@@ -195,7 +211,7 @@ void k_decode(DecodeArgs a) {
   // they read the expert's weights as one front moving through memory.
   // Items past n_ct (padding) compute on row 0 and store nothing.
   constexpr int RING = LONGK ? 1 : kRing;
-  int per = (a.n_ct + wps - 1) / wps;
+  int per = guessed ? a.per_guess : (a.n_ct + wps - 1) / wps;
   per = (per + RING - 1) / RING * RING;
   if (part >= a.n_ct || rows <= 0) return;
   const int begin = 0, end_pad = per;
@@ -660,6 +676,15 @@ static hipError_t launch_stream(DecodeArgs a, int ncolblk, int max_slots, hipStr
   int64_t grid = std::min<int64_t>(resident, (int64_t)max_slots * a.n_ct);
   if (grid < max_slots) grid = max_slots;
   if (grid <= 0) return hipSuccess;
+  // the kernel's slot arithmetic for max_slots active slots (MoE: the
+  // likeliest count; dense: the count), so it divides only when the plan
+  // differs; slot_magic = floor(2^32 / wps) + 1 gives blockIdx.x / wps
+  // exactly for blockIdx.x < 2^16
+  a.u_guess = std::max(max_slots, 1);
+  a.wps_guess = (int)std::max<int64_t>(1, std::min<int64_t>(a.n_ct, grid / a.u_guess));
+  a.slot_magic = a.wps_guess > 1 ? (uint32_t)((1ull << 32) / (uint64_t)a.wps_guess + 1ull) : 0u;
+  a.per_guess = (a.n_ct + a.wps_guess - 1) / a.wps_guess;
+  if (grid >= (1 << 16)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(threads), lds, s, a);
   return hipGetLastError();
 }

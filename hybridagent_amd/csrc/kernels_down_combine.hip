@@ -122,7 +122,10 @@ __global__ __launch_bounds__(kDcThreads) void k_down_combine(DownCombineArgs a) 
   u32x4_t bw0[kDcTiles], bw1[kDcTiles];
   uint32_t sc0[kDcTiles], sc1[kDcTiles];
   __builtin_amdgcn_sched_barrier(0);
-  weights(max(min(wave, U - 1), 0), bw0, sc0);
+  // the first slot's descriptor is read without waiting for the active
+  // count: a wavefront past the active slots loads (clamped, in-bounds)
+  // weights it never uses, as it did before with the last slot's
+  weights(min(wave, a.E - 1), bw0, sc0);
   __builtin_amdgcn_sched_barrier(0);
   slot_pos[tid] = spos;  // entries past R are not read
   wts[tid] = round_bf16(wrt);

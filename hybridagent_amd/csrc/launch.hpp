@@ -40,6 +40,11 @@ struct DecodeArgs {
   int rows_hint;    // most activation rows one expert can have (set by the caller)
   int cg;           // column groups of 16 weight rows per item (set by the launcher)
   int ct_blocks;    // tiled: (item, wavefront) blocks per expert in the copy
+  // set by the launcher: the likeliest number of active slots (MoE) and the
+  // slot arithmetic for it (workgroups per slot, its division magic, items
+  // per workgroup)
+  int u_guess, wps_guess, per_guess;
+  uint32_t slot_magic;
 };
 
 // Arguments of the prefill-shaped grouped GEMM (kernels_prefill.hip).
