@@ -178,11 +178,17 @@ __global__ __launch_bounds__(kDcThreads) void k_down_combine(DownCombineArgs a) 
   // slots u, u + 8 with the two register sets; each set is refilled with
   // the slot two steps ahead right after it has been used (a third set,
   // two slots in flight, measured slower)
-  for (int u = wave; u < U; u += 2 * kDcWaves) {
-    weights(min(u + kDcWaves, U - 1), bw1, sc1);
-    expert(u, bw0, sc0);
-    weights(min(u + 2 * kDcWaves, U - 1), bw0, sc0);
-    if (u + kDcWaves < U) expert(u + kDcWaves, bw1, sc1);
+  if (U <= kDcWaves) {
+    // at most one slot per wavefront (one token): no loads after the first
+    // weights, so nothing is left in flight when the wavefront is done
+    if (wave < U) expert(wave, bw0, sc0);
+  } else {
+    for (int u = wave; u < U; u += 2 * kDcWaves) {
+      weights(min(u + kDcWaves, U - 1), bw1, sc1);
+      expert(u, bw0, sc0);
+      weights(min(u + 2 * kDcWaves, U - 1), bw0, sc0);
+      if (u + kDcWaves < U) expert(u + kDcWaves, bw1, sc1);
+    }
   }
   __syncthreads();
 
