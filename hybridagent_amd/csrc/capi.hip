@@ -503,7 +503,7 @@ namespace {
 // resolve_tiles) serve the kernels that read them, gu_packed everything else
 int gate_up_impl(const uint16_t* hidden, const int32_t* gu_packed, const uint16_t* gu_scale, const Tiles& t,
                  int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
-                 size_t workspace_bytes, void* stream) {
+                 size_t workspace_bytes, void* stream, const TopkSortArgs* route = nullptr) {
   MoeLayout L{};
   int st = moe_check(M, top_k, E, H, I, group_size, workspace, workspace_bytes, &L);
   if (st != W4A16_OK || M == 0) return st;
@@ -554,9 +554,9 @@ int gate_up_impl(const uint16_t* hidden, const int32_t* gu_packed, const uint16_
   a.ng = (int)((H + group_size - 1) / group_size);
   if (t.gu_decode != nullptr) {
     a.wp = t.gu_decode;
-    return launch_status(launch_decode_tiled(kModeGateUp, a, max_slots, s));
+    return launch_status(launch_decode_tiled(kModeGateUp, a, max_slots, s, route));
   }
-  return launch_status(launch_decode(kModeGateUp, a, max_slots, s));
+  return launch_status(launch_decode(kModeGateUp, a, max_slots, s, route));
 }
 }  // namespace
 
@@ -1130,6 +1130,20 @@ static int layer_forward_impl(const uint16_t* router_in, const uint16_t* router_
     if (e == hipSuccess)
       e = launch_router_partials(router_in, router_scale, scalar_root, eps, proj_w, r, partial, M, H, E, s);
     if (e != hipSuccess) return W4A16_ERR_LAUNCH;
+  }
+  // one token (and no shared MLP to place): the gate_up launch routes too --
+  // its last workgroup runs the top-k + sort, which writes the routing and
+  // the plan the down stage reads, and every other workgroup finds its
+  // expert from the router partials itself -- one launch fewer on the chain
+  if (M == 1 && mlp == nullptr && decode_route_supported(t.gu_decode != nullptr, H, I, group_size, E, top_k)) {
+    const TopkSortArgs ta{partial, per_expert_scale, topk_idx, topk_w, 1, (int)E, (int)top_k,
+                          L.sorted_pos, L.offsets, L.desc, L.counters, L.tiles, 0, kDecodeSlotRows};
+    st = gate_up_impl(hidden, gu_packed, gu_scale, t, M, top_k, E, H, I, group_size, workspace, moe_bytes, stream,
+                      &ta);
+    if (st == W4A16_OK)
+      st = down_and_combine(dn_packed, dn_scale, topk_idx, topk_w, out, M, top_k, E, H, I, group_size, workspace,
+                            moe_bytes, stream, t, an);
+    return st;
   }
   if (M * top_k <= kTopkSortMaxEntries) {
     // small batches: top-k and the expert sort in one workgroup

@@ -20,6 +20,7 @@
 
 #include "common.hpp"
 #include "launch.hpp"
+#include "route_device.hpp"
 
 namespace w4a16 {
 
@@ -118,7 +119,18 @@ __device__ __forceinline__ int frag_slot(int b, int rb, int j) {
 // LSCALE (tiled, group size 32 or 64): after an item's TPW tiles the copy
 // holds each lane's TPW scales (one per tile: its 32-wide chunk's group),
 // fetched with one load like WIDE's.
-template <int MODE, int TPW, int KSPLIT, bool LONGK, bool WIDE, bool TILED = false, bool LSCALE = false>
+//
+// ROUTE (gate_up, one token, E <= kRouteMaxExperts): the launch also routes.
+// Its last workgroup runs the top-k + sort (a.route: routing outputs and the
+// plan the down stage reads); every other workgroup finds its own expert
+// from the router's K-split partials -- the same keys the top-k compares,
+// ranked in parallel -- as the s-th smallest selected expert for its slot s
+// (the plan's ascending order, one row per expert), so no workgroup waits
+// for the plan.
+constexpr int kRouteMaxExperts = 128;
+
+template <int MODE, int TPW, int KSPLIT, bool LONGK, bool WIDE, bool TILED = false, bool LSCALE = false,
+          bool ROUTE = false>
 __global__ __launch_bounds__(stream_threads(KSPLIT)) __attribute__((amdgpu_waves_per_eu(TPW >= 4 ? 2 : 4, 8)))
 void k_decode(DecodeArgs a) {
   constexpr int kStreamThreads = stream_threads(KSPLIT);  // the wide form
@@ -181,7 +193,67 @@ void k_decode(DecodeArgs a) {
   int e = 0, seg0 = 0, rows = a.M;
   const int ug = a.u_guess;
   const int slot_raw = a.wps_guess > 1 ? (int)__umulhi(blockIdx.x, a.slot_magic) : (int)blockIdx.x;
-  if (MODE != kModeDense) {
+  if constexpr (ROUTE) {
+    static_assert(MODE == kModeGateUp && KSPLIT == 4, "gate_up routes, 256 threads or more");
+    if (blockIdx.x == gridDim.x - 1) {
+      topk_sort_small_block<kRouterMaxSplit, 2, 1>(a.route);
+      return;
+    }
+    // keys of every expert (token 0: partial[ks][0][e], splits summed in
+    // order and rounded to bf16, NaN as -inf, as load_logits does); past E, 0
+    __shared__ __align__(16) uint32_t rkey[kRouteMaxExperts];
+    __shared__ unsigned long long rsel[kRouteMaxExperts / 32];
+    const int E = a.route.E;
+    if (tid < kRouteMaxExperts) {
+      uint32_t key = 0u;
+      if (tid < E) {
+        float pv[kRouterMaxSplit];
+#pragma unroll
+        for (int q = 0; q < kRouterMaxSplit; ++q) pv[q] = a.route.partial[q * E + tid];
+        float sum = 0.f;
+#pragma unroll
+        for (int q = 0; q < kRouterMaxSplit; ++q) sum += pv[q];
+        const float v = bf16_bits_to_f32(f32_to_bf16_bits(sum));
+        key = topk_key(v == v ? v : -INFINITY, tid);
+      }
+      rkey[tid] = key;
+    }
+    __syncthreads();
+    // rank of expert x = tid / 2 among all: lanes 2x and 2x + 1 count the
+    // larger keys among experts [0, 64) and [64, 128), then add the pair
+    const int x = tid >> 1, h = tid & 1;
+    int above = 0;
+    if (tid < 2 * kRouteMaxExperts) {
+      const uint32_t kx = rkey[x];
+#pragma unroll
+      for (int u = 0; u < 64; u += 4) {
+        const uint4 k4 = *reinterpret_cast<const uint4*>(&rkey[64 * h + u]);
+        above += (k4.x > kx) + (k4.y > kx) + (k4.z > kx) + (k4.w > kx);
+      }
+    }
+    above += __builtin_amdgcn_mov_dpp(above, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]: the pair's other half
+    const bool selected = tid < 2 * kRouteMaxExperts && h == 0 && x < E && above < a.route.topk;
+    const unsigned long long bal = __ballot(selected);  // wavefront w: experts 32 w + bit / 2
+    if (lane == 0 && wave < kRouteMaxExperts / 32) rsel[wave] = bal;
+    __syncthreads();
+    // slot s: the s-th smallest selected expert (clamped for the slots past
+    // the top k, which return below)
+    int s_left = min(slot_raw, a.route.topk - 1), ex = 0;
+#pragma unroll
+    for (int w = 0; w < kRouteMaxExperts / 32; ++w) {
+      unsigned long long m = rsel[w];
+      const int c = __popcll(m);
+      if (s_left >= 0 && s_left < c) {
+        for (int i = 0; i < s_left; ++i) m &= m - 1ull;
+        ex = 32 * w + (__builtin_ctzll(m) >> 1);
+      }
+      s_left -= c;
+    }
+    e = __builtin_amdgcn_readfirstlane(ex);
+    U = a.route.topk;
+    seg0 = slot_raw;
+    rows = 1;
+  } else if (MODE != kModeDense) {
     const int slot_g = min(slot_raw, ug - 1);
     e = ld_uniform(a.desc, 4 * slot_g);
     seg0 = ld_uniform(a.desc, 4 * slot_g + 1);
@@ -195,15 +267,13 @@ void k_decode(DecodeArgs a) {
   const int slot = guessed ? slot_raw : (int)blockIdx.x / wps;
   const int part = (int)blockIdx.x - slot * wps;
   if (slot >= U) return;  // uniform across the workgroup
-  if (MODE != kModeDense) {
-    if (!guessed) {
-      e = ld_uniform(a.desc, 4 * slot);
-      seg0 = ld_uniform(a.desc, 4 * slot + 1);
-      rows = ld_uniform(a.desc, 4 * slot + 2);
-    }
-  } else {
+  if (MODE == kModeDense) {
     seg0 = slot * a.rb;
     rows = min(a.rb, a.M - seg0);
+  } else if (!ROUTE && !guessed) {
+    e = ld_uniform(a.desc, 4 * slot);
+    seg0 = ld_uniform(a.desc, 4 * slot + 1);
+    rows = ld_uniform(a.desc, 4 * slot + 2);
   }
   // Items per workgroup, a multiple of the register ring depth so every
   // workgroup walks whole rounds.  The expert's workgroups interleave: local
@@ -637,9 +707,10 @@ static size_t stream_lds(const DecodeArgs& a) {
 // ncolblk: column blocks of 16 weight rows per expert (gate_up: 8 gate and 8
 // up rows).  a.rb holds the rows an expert can stage per pass; dense
 // max_slots follows from the rows staged.
-template <int MODE, int TPW, int KSPLIT, bool LONGK, bool WIDE = false, bool TILED = false, bool LSCALE = false>
+template <int MODE, int TPW, int KSPLIT, bool LONGK, bool WIDE = false, bool TILED = false, bool LSCALE = false,
+          bool ROUTE = false>
 static hipError_t launch_stream(DecodeArgs a, int ncolblk, int max_slots, hipStream_t s) {
-  auto kern = k_decode<MODE, TPW, KSPLIT, LONGK, WIDE, TILED, LSCALE>;
+  auto kern = k_decode<MODE, TPW, KSPLIT, LONGK, WIDE, TILED, LSCALE, ROUTE>;
   constexpr int kWideCg = stream_threads(KSPLIT) / 64 / KSPLIT;
   const int cus = device_cus();
   // every staging task (row, k tile; two threads each without a K split)
@@ -685,7 +756,8 @@ static hipError_t launch_stream(DecodeArgs a, int ncolblk, int max_slots, hipStr
   a.slot_magic = a.wps_guess > 1 ? (uint32_t)((1ull << 32) / (uint64_t)a.wps_guess + 1ull) : 0u;
   a.per_guess = (a.n_ct + a.wps_guess - 1) / a.wps_guess;
   if (grid >= (1 << 16)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(threads), lds, s, a);
+  // ROUTE: one more workgroup, the last, runs the top-k + sort
+  hipLaunchKernelGGL(kern, dim3((unsigned)(grid + (ROUTE ? 1 : 0))), dim3(threads), lds, s, a);
   return hipGetLastError();
 }
 
@@ -718,8 +790,16 @@ static hipError_t launch_decode_mode(DecodeArgs a, int max_slots, hipStream_t s)
 #undef W4A16_DEC
 }
 
-hipError_t launch_decode(int mode, DecodeArgs a, int max_slots, hipStream_t s) {
+hipError_t launch_decode(int mode, DecodeArgs a, int max_slots, hipStream_t s, const TopkSortArgs* route) {
   if (max_slots <= 0) return hipSuccess;
+  if (route != nullptr) {
+    if (mode != kModeGateUp || a.M != 1 || route->M != 1 ||
+        !decode_route_supported(false, a.K, a.I, a.G, route->E, route->topk))
+      return hipErrorNotSupported;
+    a.route = *route;
+    a.rb = 1;
+    return launch_stream<kModeGateUp, 6, 4, false, true, false, false, true>(a, a.I / 8, max_slots, s);
+  }
   // MoE outputs are addressed by 32-bit byte offsets of one buffer descriptor
   if (mode != kModeDense &&
       (int64_t)a.M * a.topk * (mode == kModeGateUp ? a.I : a.N) * 2 >= (int64_t)0x7FFFFFF0)
@@ -778,6 +858,20 @@ static bool tiled_shape(int mode, int64_t H, int64_t I, int64_t G, TiledShape* t
   t->n_ct = (int)((ncolblk + cg - 1) / cg);
   t->block_bytes = t->tpw * (t->lscale ? 1152 : 1024);
   return true;
+}
+
+// the one-token routing form (k_decode's ROUTE): gate_up streamer shape
+// (6 tiles, K split 4) with one scale load per item, E <= kRouteMaxExperts
+bool decode_route_supported(bool tiled, int64_t H, int64_t I, int64_t G, int64_t E, int64_t topk) {
+  if (E > kRouteMaxExperts || topk <= 0 || topk > E || topk > 64 || H <= 0 || H % 32 != 0) return false;
+  const DecodeShape sh = decode_shape((int)H);
+  const int ntiles = (int)(((H >> 5) + 3) >> 2);
+  if (sh.tpw != 6 || sh.ksplit != 4 || ntiles > 24) return false;
+  if (tiled) {
+    TiledShape t;
+    return tiled_shape(kModeGateUp, H, I, G, &t) && t.tpw == 6 && t.ksplit == 4;
+  }
+  return G == 128 && ((H + 127) / 128) % 2 == 0;
 }
 
 size_t tiled_decode_bytes_per_expert(int mode, int64_t H, int64_t I, int64_t G) {
@@ -891,8 +985,11 @@ static hipError_t launch_stream_tiled(const TiledShape& t, DecodeArgs a, int nco
 // The MoE streamers on tiled weights (a.wp = the tiled copy): one scale load
 // per item (group size 128 from the scale tensor, an even group count; 32 /
 // 64 from the copy).
-hipError_t launch_decode_tiled(int mode, DecodeArgs a, int max_slots, hipStream_t s) {
+hipError_t launch_decode_tiled(int mode, DecodeArgs a, int max_slots, hipStream_t s, const TopkSortArgs* route) {
   if (max_slots <= 0) return hipSuccess;
+  if (route != nullptr && (mode != kModeGateUp || a.M != 1 || route->M != 1 ||
+                           !decode_route_supported(true, a.K, a.I, a.G, route->E, route->topk)))
+    return hipErrorNotSupported;
   if (mode != kModeGateUp && mode != kModeDown) return hipErrorInvalidValue;
   if ((int64_t)a.M * a.topk * (mode == kModeGateUp ? a.I : a.N) * 2 >= (int64_t)0x7FFFFFF0)
     return hipErrorInvalidValue;
@@ -905,6 +1002,11 @@ hipError_t launch_decode_tiled(int mode, DecodeArgs a, int max_slots, hipStream_
   int rows_cap = 1;
   while (rows_cap < a.rows_hint && rows_cap < 16) rows_cap <<= 1;
   if (a.rb > rows_cap) a.rb = rows_cap;
+  if (route != nullptr) {
+    a.route = *route;
+    return t.lscale ? launch_stream<kModeGateUp, 6, 4, false, true, true, true, true>(a, ncolblk, max_slots, s)
+                    : launch_stream<kModeGateUp, 6, 4, false, true, true, false, true>(a, ncolblk, max_slots, s);
+  }
   if (mode == kModeGateUp) {
     if (t.ksplit == 4) {
       if (t.tpw == 2) return launch_stream_tiled<kModeGateUp, 2, 4>(t, a, ncolblk, max_slots, s);

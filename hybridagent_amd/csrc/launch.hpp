@@ -18,6 +18,18 @@ constexpr int kPrefillXBM = 256;
 // prefill work-queue counters in the MoE workspace: gate_up [0, 16), down [16, 32)
 constexpr int kPrefillQueueInts = 32;
 
+// One-workgroup top-k + expert sort of the decode router's K-split partials
+// (M * topk <= 64): the routing outputs and the plan it writes.
+struct TopkSortArgs {
+  const float* partial;
+  const uint16_t* pes;
+  int64_t* idx_out;
+  float* w_out;
+  int M, E, topk;
+  int32_t *sorted_pos, *offsets, *desc, *counters, *tiles;
+  int BM, slot_rows;
+};
+
 // Arguments of the decode-shaped (few rows per weight matrix) MFMA kernel.
 struct DecodeArgs {
   const uint16_t* act;        // activation rows (bf16), row length K
@@ -45,6 +57,9 @@ struct DecodeArgs {
   // per workgroup)
   int u_guess, wps_guess, per_guess;
   uint32_t slot_magic;
+  // gate_up at one token routing in its own launch (launch_decode's route):
+  // the top-k + sort's arguments, run by the launch's last workgroup
+  TopkSortArgs route;
 };
 
 // Arguments of the prefill-shaped grouped GEMM (kernels_prefill.hip).
@@ -111,8 +126,13 @@ struct Bf16ExpertArgs {
 
 hipError_t launch_dequant(const int32_t* packed, const uint16_t* scale, uint16_t* out,
                           int64_t rows, int K, int G, hipStream_t s);
-// max_slots: upper bound of active experts (1 for dense)
-hipError_t launch_decode(int mode, DecodeArgs a, int max_slots, hipStream_t s);
+// max_slots: upper bound of active experts (1 for dense).  route (gate_up at
+// one token, nullable): the launch also runs the top-k + sort of the router's
+// K-split partials (TopkSortArgs, M = 1) and each workgroup finds its expert
+// itself; hipErrorNotSupported (nothing launched) where
+// decode_route_supported says no.
+hipError_t launch_decode(int mode, DecodeArgs a, int max_slots, hipStream_t s, const TopkSortArgs* route = nullptr);
+bool decode_route_supported(bool tiled, int64_t H, int64_t I, int64_t G, int64_t E, int64_t topk);
 // Tiled expert weights for the decode streamers (kernels_decode.hip): bytes
 // per expert of the tiled copy of the gate_up (mode kModeGateUp) or down
 // weights for group size G (0: no tiled form for H, I, G), whether that copy
@@ -121,7 +141,8 @@ size_t tiled_decode_bytes_per_expert(int mode, int64_t H, int64_t I, int64_t G);
 bool tiled_decode_needs_scale(int G);
 hipError_t launch_tile_decode(int mode, const int32_t* packed, const uint16_t* scale, int E, int H, int I, int G,
                               int32_t* tiled, hipStream_t s);
-hipError_t launch_decode_tiled(int mode, DecodeArgs a, int max_slots, hipStream_t s);
+hipError_t launch_decode_tiled(int mode, DecodeArgs a, int max_slots, hipStream_t s,
+                               const TopkSortArgs* route = nullptr);
 // x = bf16(h + delta) -> h_out (delta may be null), y = bf16(rms_norm(x) * w)
 hipError_t launch_add_rms_norm(const uint16_t* h, const uint16_t* delta, const uint16_t* w,
                                uint16_t* h_out, uint16_t* y, int64_t M, int H, float eps,
@@ -152,6 +173,7 @@ constexpr int kDecodeSlotRows = 16;
 inline int64_t plan_desc_capacity(int64_t M, int64_t topk, int64_t E) {
   return E + (M * topk + kDecodeSlotRows - 1) / kDecodeSlotRows;
 }
+
 // The expert sort; with `queues` (nullable) it also zeroes the
 // kPrefillQueueInts prefill work-queue counters there.  Every plan writer's
 // BM is the prefill m-tile height of the tile list (a power of two), or 0 for

@@ -626,7 +626,7 @@ def test_graph_replay_prefill_experts(dev, moe128, M):
     _replays_match(fwd, fwd, lambda: _lib.moe_forward(x2, i2, w2, *args))
 
 
-@pytest.mark.parametrize("M", [8, 64])
+@pytest.mark.parametrize("M", [1, 8, 64])
 def test_graph_replay_decode_layer(dev, moe128, M):
     cpu, gpu = moe128
     h, rw = _router_inputs(M, seed=810 + M)
