@@ -275,13 +275,15 @@ void k_decode(DecodeArgs a) {
     seg0 = ld_uniform(a.desc, 4 * slot + 1);
     rows = ld_uniform(a.desc, 4 * slot + 2);
   }
-  // Items per workgroup, a multiple of the register ring depth so every
-  // workgroup walks whole rounds.  The expert's workgroups interleave: local
-  // item c of workgroup `part` is item part + c * wps, so together
-  // they read the expert's weights as one front moving through memory.
-  // Items past n_ct (padding) compute on row 0 and store nothing.
+  // Items of this workgroup.  The expert's workgroups interleave: local
+  // item c of workgroup `part` is item part + c * wps, so together they read
+  // the expert's weights as one front moving through memory.  Each takes
+  // its own items only (the last parts one fewer when wps does not divide
+  // n_ct), rounded up to the register ring depth so it walks whole rounds;
+  // items past n_ct (ring padding) compute on row 0 and store nothing.
   constexpr int RING = LONGK ? 1 : kRing;
   int per = guessed ? a.per_guess : (a.n_ct + wps - 1) / wps;
+  if (part >= a.n_ct - (per - 1) * wps) per -= 1;
   per = (per + RING - 1) / RING * RING;
   if (part >= a.n_ct || rows <= 0) return;
   const int begin = 0, end_pad = per;
