@@ -503,7 +503,8 @@ namespace {
 // resolve_tiles) serve the kernels that read them, gu_packed everything else
 int gate_up_impl(const uint16_t* hidden, const int32_t* gu_packed, const uint16_t* gu_scale, const Tiles& t,
                  int64_t M, int64_t top_k, int64_t E, int64_t H, int64_t I, int64_t group_size, void* workspace,
-                 size_t workspace_bytes, void* stream, const TopkSortArgs* route = nullptr) {
+                 size_t workspace_bytes, void* stream, const TopkSortArgs* self_args = nullptr,
+                 int self_mode = kSelfNone) {
   MoeLayout L{};
   int st = moe_check(M, top_k, E, H, I, group_size, workspace, workspace_bytes, &L);
   if (st != W4A16_OK || M == 0) return st;
@@ -554,9 +555,9 @@ int gate_up_impl(const uint16_t* hidden, const int32_t* gu_packed, const uint16_
   a.ng = (int)((H + group_size - 1) / group_size);
   if (t.gu_decode != nullptr) {
     a.wp = t.gu_decode;
-    return launch_status(launch_decode_tiled(kModeGateUp, a, max_slots, s, route));
+    return launch_status(launch_decode_tiled(kModeGateUp, a, max_slots, s, self_args, self_mode));
   }
-  return launch_status(launch_decode(kModeGateUp, a, max_slots, s, route));
+  return launch_status(launch_decode(kModeGateUp, a, max_slots, s, self_args, self_mode));
 }
 }  // namespace
 
@@ -1135,11 +1136,11 @@ static int layer_forward_impl(const uint16_t* router_in, const uint16_t* router_
   // its last workgroup runs the top-k + sort, which writes the routing and
   // the plan the down stage reads, and every other workgroup finds its
   // expert from the router partials itself -- one launch fewer on the chain
-  if (M == 1 && mlp == nullptr && decode_route_supported(t.gu_decode != nullptr, H, I, group_size, E, top_k)) {
+  if (mlp == nullptr && decode_self_supported(kSelfRoute, t.gu_decode != nullptr, M, H, I, group_size, E, top_k)) {
     const TopkSortArgs ta{partial, per_expert_scale, topk_idx, topk_w, 1, (int)E, (int)top_k,
                           L.sorted_pos, L.offsets, L.desc, L.counters, L.tiles, 0, kDecodeSlotRows};
     st = gate_up_impl(hidden, gu_packed, gu_scale, t, M, top_k, E, H, I, group_size, workspace, moe_bytes, stream,
-                      &ta);
+                      &ta, kSelfRoute);
     if (st == W4A16_OK)
       st = down_and_combine(dn_packed, dn_scale, topk_idx, topk_w, out, M, top_k, E, H, I, group_size, workspace,
                             moe_bytes, stream, t, an);
@@ -1165,6 +1166,22 @@ static int layer_forward_impl(const uint16_t* router_in, const uint16_t* router_
     e = launch_router_topk(partial, router_ksplit(M, E), nullptr, per_expert_scale, nullptr, topk_idx,
                            topk_w, (int)M, (int)E, (int)top_k, s);
     if (e != hipSuccess) return W4A16_ERR_LAUNCH;
+    if (!mlp_dn && launch_linear_call(mlp->down, s) != hipSuccess) return W4A16_ERR_LAUNCH;
+    mlp_dn = true;
+    // decode sizes: the gate_up launch sorts the finished top-k itself (its
+    // last workgroup writes the plan the down stage reads) -- no sort launch
+    if (!use_prefill(M, H, I) &&
+        decode_self_supported(kSelfPlan, t.gu_decode != nullptr, M, H, I, group_size, E, top_k)) {
+      const TopkSortArgs ta{nullptr, nullptr, topk_idx, nullptr, (int)M, (int)E, (int)top_k,
+                            L.sorted_pos, L.offsets, L.desc, L.counters, L.tiles, 0, kDecodeSlotRows};
+      // (a shape the launcher runs narrow is refused before any launch and
+      // takes the sort launch below)
+      st = gate_up_impl(hidden, gu_packed, gu_scale, t, M, top_k, E, H, I, group_size, workspace, moe_bytes, stream,
+                        &ta, kSelfPlan);
+      if (st == W4A16_OK)
+        return down_and_combine(dn_packed, dn_scale, topk_idx, topk_w, out, M, top_k, E, H, I, group_size,
+                                workspace, moe_bytes, stream, t, an);
+    }
     st = moe_plan(hidden, topk_idx, M, top_k, E, H, I, group_size, workspace, moe_bytes, stream);
     if (st != W4A16_OK) return st;
   }

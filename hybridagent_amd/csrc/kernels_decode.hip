@@ -120,17 +120,27 @@ __device__ __forceinline__ int frag_slot(int b, int rb, int j) {
 // holds each lane's TPW scales (one per tile: its 32-wide chunk's group),
 // fetched with one load like WIDE's.
 //
-// ROUTE (gate_up, one token, E <= kRouteMaxExperts): the launch also routes.
-// Its last workgroup runs the top-k + sort (a.route: routing outputs and the
-// plan the down stage reads); every other workgroup finds its own expert
-// from the router's K-split partials -- the same keys the top-k compares,
-// ranked in parallel -- as the s-th smallest selected expert for its slot s
-// (the plan's ascending order, one row per expert), so no workgroup waits
-// for the plan.
-constexpr int kRouteMaxExperts = 128;
+// SELF (gate_up, E <= kSelfMaxExperts): the launch works out its own plan
+// instead of reading one, and its last workgroup writes that plan (and at
+// one token the routing) for the down stage (a.route):
+//   kSelfRoute  one token: the last workgroup runs the top-k + sort; every
+//               other finds its own expert from the router's K-split
+//               partials -- the same keys the top-k compares, ranked in
+//               parallel -- as the s-th smallest selected expert for its
+//               slot s (the plan's ascending order, one row per expert);
+//   kSelfPlan   M * topk <= blockDim.x (the wide form) routed rows of a
+//               finished top-k: every workgroup ranks the rows by expert
+//               in the sort's k-major order (ballots per wavefront, the
+//               wavefronts' counts in LDS), scans the counts into segment
+//               offsets and 16-row slots, and takes its slot's expert,
+//               segment rows and tokens; the last writes the positions,
+//               offsets, descriptors and counts the sort would.
+// No workgroup waits for a plan written by another launch.
+constexpr int kSelfMaxExperts = 128;
+constexpr int kSortWavesMax = 16;  // wavefronts of the wide form
 
 template <int MODE, int TPW, int KSPLIT, bool LONGK, bool WIDE, bool TILED = false, bool LSCALE = false,
-          bool ROUTE = false>
+          int SELF = kSelfNone>
 __global__ __launch_bounds__(stream_threads(KSPLIT)) __attribute__((amdgpu_waves_per_eu(TPW >= 4 ? 2 : 4, 8)))
 void k_decode(DecodeArgs a) {
   constexpr int kStreamThreads = stream_threads(KSPLIT);  // the wide form
@@ -193,7 +203,7 @@ void k_decode(DecodeArgs a) {
   int e = 0, seg0 = 0, rows = a.M;
   const int ug = a.u_guess;
   const int slot_raw = a.wps_guess > 1 ? (int)__umulhi(blockIdx.x, a.slot_magic) : (int)blockIdx.x;
-  if constexpr (ROUTE) {
+  if constexpr (SELF == kSelfRoute) {
     static_assert(MODE == kModeGateUp && KSPLIT == 4, "gate_up routes, 256 threads or more");
     if (blockIdx.x == gridDim.x - 1) {
       topk_sort_small_block<kRouterMaxSplit, 2, 1>(a.route);
@@ -201,10 +211,10 @@ void k_decode(DecodeArgs a) {
     }
     // keys of every expert (token 0: partial[ks][0][e], splits summed in
     // order and rounded to bf16, NaN as -inf, as load_logits does); past E, 0
-    __shared__ __align__(16) uint32_t rkey[kRouteMaxExperts];
-    __shared__ unsigned long long rsel[kRouteMaxExperts / 32];
+    __shared__ __align__(16) uint32_t rkey[kSelfMaxExperts];
+    __shared__ unsigned long long rsel[kSelfMaxExperts / 32];
     const int E = a.route.E;
-    if (tid < kRouteMaxExperts) {
+    if (tid < kSelfMaxExperts) {
       uint32_t key = 0u;
       if (tid < E) {
         float pv[kRouterMaxSplit];
@@ -223,7 +233,7 @@ void k_decode(DecodeArgs a) {
     // larger keys among experts [0, 64) and [64, 128), then add the pair
     const int x = tid >> 1, h = tid & 1;
     int above = 0;
-    if (tid < 2 * kRouteMaxExperts) {
+    if (tid < 2 * kSelfMaxExperts) {
       const uint32_t kx = rkey[x];
 #pragma unroll
       for (int u = 0; u < 64; u += 4) {
@@ -232,15 +242,15 @@ void k_decode(DecodeArgs a) {
       }
     }
     above += __builtin_amdgcn_mov_dpp(above, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]: the pair's other half
-    const bool selected = tid < 2 * kRouteMaxExperts && h == 0 && x < E && above < a.route.topk;
+    const bool selected = tid < 2 * kSelfMaxExperts && h == 0 && x < E && above < a.route.topk;
     const unsigned long long bal = __ballot(selected);  // wavefront w: experts 32 w + bit / 2
-    if (lane == 0 && wave < kRouteMaxExperts / 32) rsel[wave] = bal;
+    if (lane == 0 && wave < kSelfMaxExperts / 32) rsel[wave] = bal;
     __syncthreads();
     // slot s: the s-th smallest selected expert (clamped for the slots past
     // the top k, which return below)
     int s_left = min(slot_raw, a.route.topk - 1), ex = 0;
 #pragma unroll
-    for (int w = 0; w < kRouteMaxExperts / 32; ++w) {
+    for (int w = 0; w < kSelfMaxExperts / 32; ++w) {
       unsigned long long m = rsel[w];
       const int c = __popcll(m);
       if (s_left >= 0 && s_left < c) {
@@ -253,7 +263,112 @@ void k_decode(DecodeArgs a) {
     U = a.route.topk;
     seg0 = slot_raw;
     rows = 1;
-  } else if (MODE != kModeDense) {
+  }
+  if constexpr (SELF == kSelfPlan) {
+    // entry p = tid of the sort's k-major order (p = j M + t, routed row
+    // t k + j), its expert, its rank among the entries of that expert, and
+    // the experts' segment offsets and first slots
+    static_assert(MODE == kModeGateUp && KSPLIT == 4, "gate_up plans, the wide form");
+    __shared__ int pwc[kSortWavesMax][kSelfMaxExperts];
+    __shared__ int poff[kSelfMaxExperts + 1], pslot[kSelfMaxExperts + 1];
+    __shared__ int psel;
+    int ep = -1, prank = 0, ptok = 0;
+    const TopkSortArgs& r = a.route;
+    const int E = r.E, R = r.M * r.topk;
+    for (int q = tid; q < kSortWavesMax * kSelfMaxExperts; q += (int)blockDim.x) (&pwc[0][0])[q] = 0;
+    int prow = 0;
+    if (tid < R) {
+      const int jj = (int)__umulhi((uint32_t)tid, a.plan_m_magic);
+      ptok = tid - jj * r.M;
+      prow = ptok * r.topk + jj;
+      const int64_t ev = r.idx_out[prow];
+      ep = (ev >= 0 && ev < E) ? (int)ev : -1;
+    }
+    __syncthreads();  // pwc cleared
+    // rank among this wavefront's entries of the same expert (ballots over
+    // the expert's 7 bits); the lowest such lane records the count
+    const bool ok = ep >= 0;
+    unsigned long long same = __ballot(ok);
+#pragma unroll
+    for (int b = 0; b < 7; ++b) {
+      const bool bit = ok && ((ep >> b) & 1);
+      const unsigned long long bb = __ballot(bit);
+      same &= bit ? bb : ~bb;
+    }
+    const unsigned long long lt = (1ull << lane) - 1ull;
+    prank = __popcll(same & lt);
+    if (ok && (same & lt) == 0ull) pwc[wave][ep] = __popcll(same);
+    __syncthreads();
+    // wavefront 0: expert counts (lane l: experts 2 l, 2 l + 1), exclusive
+    // scans of rows and of 16-row slots, in expert order as the sort's plan
+    const int nw = (int)blockDim.x >> 6;
+    if (wave == 0) {
+      int c2[2], cs = 0, ss = 0;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int x = 2 * lane + q;
+        int c = 0;
+        if (x < E)
+          for (int w = 0; w < nw; ++w) c += pwc[w][x];
+        c2[q] = c;
+        cs += c;
+        ss += (c + kDecodeSlotRows - 1) / kDecodeSlotRows;
+      }
+      const int ci = wave_incl_scan(cs, lane), si = wave_incl_scan(ss, lane);
+      int off = ci - cs, sp = si - ss;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int x = 2 * lane + q;
+        if (x < E) {
+          poff[x] = off;
+          pslot[x] = sp;
+        }
+        off += c2[q];
+        sp += (c2[q] + kDecodeSlotRows - 1) / kDecodeSlotRows;
+      }
+      if (lane == 63) {
+        poff[E] = ci;
+        pslot[E] = si;
+      }
+    }
+    // the entry's rank within its expert: the earlier wavefronts' entries first
+    if (ok)
+      for (int w = 0; w < wave; ++w) prank += pwc[w][ep];
+    __syncthreads();  // poff, pslot
+    U = pslot[E];
+    if (blockIdx.x == gridDim.x - 1) {
+      // the plan of the sort (segment positions, offsets, one descriptor per
+      // 16-row slot, the slot count; no m-tile list) for the down stage
+      if (ok) r.sorted_pos[poff[ep] + prank] = prow;
+      if (tid < E) {
+        const int c = poff[tid + 1] - poff[tid];
+        r.offsets[tid] = poff[tid];
+        for (int i = 0; i < (c + kDecodeSlotRows - 1) / kDecodeSlotRows; ++i)
+          *reinterpret_cast<int4*>(r.desc + 4 * (pslot[tid] + i)) = plan_desc(tid, poff[tid], c, kDecodeSlotRows, i);
+      }
+      if (tid == 0) {
+        r.offsets[E] = poff[E];
+        r.counters[0] = U;
+        r.counters[1] = 0;
+      }
+      return;
+    }
+    if (U <= 0) return;
+    // this workgroup's slot (the arithmetic below), its expert (the one whose
+    // slots hold it), its 16-row chunk and the chunk's tokens, in the sort's
+    // order; workgroups past the slots return below
+    const int wps_p = U == ug ? a.wps_guess : max(1, min(a.n_ct, ((int)gridDim.x - 1) / U));
+    const int slot_p = U == ug ? slot_raw : (int)blockIdx.x / wps_p;
+    if (slot_p < U) {
+      if (tid < E && pslot[tid] <= slot_p && slot_p < pslot[tid + 1]) psel = tid;
+      __syncthreads();
+      e = __builtin_amdgcn_readfirstlane(psel);
+      const int i16 = (slot_p - pslot[e]) * kDecodeSlotRows;
+      seg0 = poff[e] + i16;
+      rows = min(kDecodeSlotRows, poff[e + 1] - seg0);
+      if (ep == e && prank >= i16 && prank < i16 + kDecodeSlotRows) tok[prank - i16] = ptok;
+    }
+  } else if (MODE != kModeDense && SELF == kSelfNone) {
     const int slot_g = min(slot_raw, ug - 1);
     e = ld_uniform(a.desc, 4 * slot_g);
     seg0 = ld_uniform(a.desc, 4 * slot_g + 1);
@@ -263,14 +378,15 @@ void k_decode(DecodeArgs a) {
     if (U <= 0) return;
   }
   const bool guessed = U == ug;  // dense: always (u_guess is its slot count)
-  const int wps = guessed ? a.wps_guess : max(1, min(a.n_ct, (int)gridDim.x / U));
+  const int work_grid = (int)gridDim.x - (SELF != kSelfNone ? 1 : 0);
+  const int wps = guessed ? a.wps_guess : max(1, min(a.n_ct, work_grid / U));
   const int slot = guessed ? slot_raw : (int)blockIdx.x / wps;
   const int part = (int)blockIdx.x - slot * wps;
   if (slot >= U) return;  // uniform across the workgroup
   if (MODE == kModeDense) {
     seg0 = slot * a.rb;
     rows = min(a.rb, a.M - seg0);
-  } else if (!ROUTE && !guessed) {
+  } else if (SELF == kSelfNone && !guessed) {
     e = ld_uniform(a.desc, 4 * slot);
     seg0 = ld_uniform(a.desc, 4 * slot + 1);
     rows = ld_uniform(a.desc, 4 * slot + 2);
@@ -407,7 +523,9 @@ void k_decode(DecodeArgs a) {
     // there would wait for every weight refill issued before it).  The
     // positions are read with scalar loads, which do not wait for the
     // vector loads in flight.
-    if (MODE == kModeGateUp && a.M == 1) {
+    if (SELF == kSelfPlan) {
+      // the tokens came with the workgroup's own plan
+    } else if (MODE == kModeGateUp && a.M == 1) {
       // one token: every routed row is token 0, no position load to wait for
       if (tid < 16) tok[tid] = 0;
     } else if (MODE != kModeDense) {
@@ -710,9 +828,9 @@ static size_t stream_lds(const DecodeArgs& a) {
 // up rows).  a.rb holds the rows an expert can stage per pass; dense
 // max_slots follows from the rows staged.
 template <int MODE, int TPW, int KSPLIT, bool LONGK, bool WIDE = false, bool TILED = false, bool LSCALE = false,
-          bool ROUTE = false>
+          int SELF = kSelfNone>
 static hipError_t launch_stream(DecodeArgs a, int ncolblk, int max_slots, hipStream_t s) {
-  auto kern = k_decode<MODE, TPW, KSPLIT, LONGK, WIDE, TILED, LSCALE, ROUTE>;
+  auto kern = k_decode<MODE, TPW, KSPLIT, LONGK, WIDE, TILED, LSCALE, SELF>;
   constexpr int kWideCg = stream_threads(KSPLIT) / 64 / KSPLIT;
   const int cus = device_cus();
   // every staging task (row, k tile; two threads each without a K split)
@@ -734,6 +852,10 @@ static hipError_t launch_stream(DecodeArgs a, int ncolblk, int max_slots, hipStr
                       narrow_items * slot_rows <= (int64_t)W4A16_NARROW_ROWS_PER_CU * cus;
   a.cg = narrow ? 1 : kWideCg;
   a.rb = narrow ? rb_narrow : rb_wide;
+  // kSelfPlan: one routed row per thread of the wide form, one 16-row pass
+  if (SELF == kSelfPlan && (narrow || a.rb != kDecodeSlotRows || a.M < 2 ||
+                            (int64_t)a.M * a.topk > 64 * KSPLIT * kWideCg))
+    return hipErrorNotSupported;
   a.n_ct = (ncolblk + a.cg - 1) / a.cg;
   max_slots = slots_for(a.rb);
   const int threads = 64 * KSPLIT * a.cg;
@@ -758,8 +880,8 @@ static hipError_t launch_stream(DecodeArgs a, int ncolblk, int max_slots, hipStr
   a.slot_magic = a.wps_guess > 1 ? (uint32_t)((1ull << 32) / (uint64_t)a.wps_guess + 1ull) : 0u;
   a.per_guess = (a.n_ct + a.wps_guess - 1) / a.wps_guess;
   if (grid >= (1 << 16)) return hipErrorInvalidValue;
-  // ROUTE: one more workgroup, the last, runs the top-k + sort
-  hipLaunchKernelGGL(kern, dim3((unsigned)(grid + (ROUTE ? 1 : 0))), dim3(threads), lds, s, a);
+  // SELF: one more workgroup, the last, writes the plan
+  hipLaunchKernelGGL(kern, dim3((unsigned)(grid + (SELF != kSelfNone ? 1 : 0))), dim3(threads), lds, s, a);
   return hipGetLastError();
 }
 
@@ -792,15 +914,28 @@ static hipError_t launch_decode_mode(DecodeArgs a, int max_slots, hipStream_t s)
 #undef W4A16_DEC
 }
 
-hipError_t launch_decode(int mode, DecodeArgs a, int max_slots, hipStream_t s, const TopkSortArgs* route) {
-  if (max_slots <= 0) return hipSuccess;
-  if (route != nullptr) {
-    if (mode != kModeGateUp || a.M != 1 || route->M != 1 ||
-        !decode_route_supported(false, a.K, a.I, a.G, route->E, route->topk))
-      return hipErrorNotSupported;
-    a.route = *route;
+// the SELF launch arguments: the plan's arguments, the stage rows, the slot magic
+static void self_args_into(DecodeArgs& a, const TopkSortArgs& sa, int self_mode) {
+  a.route = sa;
+  if (self_mode == kSelfRoute) {
     a.rb = 1;
-    return launch_stream<kModeGateUp, 6, 4, false, true, false, false, true>(a, a.I / 8, max_slots, s);
+  } else {
+    a.rb = kDecodeSlotRows;
+    a.plan_m_magic = (uint32_t)((1ull << 32) / (uint64_t)a.M + 1ull);
+  }
+}
+
+hipError_t launch_decode(int mode, DecodeArgs a, int max_slots, hipStream_t s, const TopkSortArgs* self_args,
+                         int self_mode) {
+  if (max_slots <= 0) return hipSuccess;
+  if (self_args != nullptr) {
+    if (mode != kModeGateUp || self_args->M != a.M ||
+        !decode_self_supported(self_mode, false, a.M, a.K, a.I, a.G, self_args->E, self_args->topk))
+      return hipErrorNotSupported;
+    self_args_into(a, *self_args, self_mode);
+    if (self_mode == kSelfRoute)
+      return launch_stream<kModeGateUp, 6, 4, false, true, false, false, kSelfRoute>(a, a.I / 8, max_slots, s);
+    return launch_stream<kModeGateUp, 6, 4, false, true, false, false, kSelfPlan>(a, a.I / 8, max_slots, s);
   }
   // MoE outputs are addressed by 32-bit byte offsets of one buffer descriptor
   if (mode != kModeDense &&
@@ -862,10 +997,15 @@ static bool tiled_shape(int mode, int64_t H, int64_t I, int64_t G, TiledShape* t
   return true;
 }
 
-// the one-token routing form (k_decode's ROUTE): gate_up streamer shape
-// (6 tiles, K split 4) with one scale load per item, E <= kRouteMaxExperts
-bool decode_route_supported(bool tiled, int64_t H, int64_t I, int64_t G, int64_t E, int64_t topk) {
-  if (E > kRouteMaxExperts || topk <= 0 || topk > E || topk > 64 || H <= 0 || H % 32 != 0) return false;
+// The gate_up launch's own plan (k_decode's SELF): the gate_up streamer's
+// 6-tile, 4-way-split shape with one scale load per item, E <=
+// kSelfMaxExperts; kSelfRoute at one token, kSelfPlan for 2 <= M, M * topk <=
+// 1024 (whether the wide form runs is the launcher's to say).
+bool decode_self_supported(int self_mode, bool tiled, int64_t M, int64_t H, int64_t I, int64_t G, int64_t E,
+                           int64_t topk) {
+  if (E > kSelfMaxExperts || topk <= 0 || topk > E || H <= 0 || H % 32 != 0) return false;
+  if (self_mode == kSelfRoute ? (M != 1 || topk > 64) : (self_mode != kSelfPlan || M < 2 || M * topk > 1024))
+    return false;
   const DecodeShape sh = decode_shape((int)H);
   const int ntiles = (int)(((H >> 5) + 3) >> 2);
   if (sh.tpw != 6 || sh.ksplit != 4 || ntiles > 24) return false;
@@ -987,10 +1127,12 @@ static hipError_t launch_stream_tiled(const TiledShape& t, DecodeArgs a, int nco
 // The MoE streamers on tiled weights (a.wp = the tiled copy): one scale load
 // per item (group size 128 from the scale tensor, an even group count; 32 /
 // 64 from the copy).
-hipError_t launch_decode_tiled(int mode, DecodeArgs a, int max_slots, hipStream_t s, const TopkSortArgs* route) {
+hipError_t launch_decode_tiled(int mode, DecodeArgs a, int max_slots, hipStream_t s, const TopkSortArgs* self_args,
+                               int self_mode) {
   if (max_slots <= 0) return hipSuccess;
-  if (route != nullptr && (mode != kModeGateUp || a.M != 1 || route->M != 1 ||
-                           !decode_route_supported(true, a.K, a.I, a.G, route->E, route->topk)))
+  if (self_args != nullptr && (mode != kModeGateUp || self_args->M != a.M ||
+                               !decode_self_supported(self_mode, true, a.M, a.K, a.I, a.G, self_args->E,
+                                                      self_args->topk)))
     return hipErrorNotSupported;
   if (mode != kModeGateUp && mode != kModeDown) return hipErrorInvalidValue;
   if ((int64_t)a.M * a.topk * (mode == kModeGateUp ? a.I : a.N) * 2 >= (int64_t)0x7FFFFFF0)
@@ -1004,10 +1146,13 @@ hipError_t launch_decode_tiled(int mode, DecodeArgs a, int max_slots, hipStream_
   int rows_cap = 1;
   while (rows_cap < a.rows_hint && rows_cap < 16) rows_cap <<= 1;
   if (a.rb > rows_cap) a.rb = rows_cap;
-  if (route != nullptr) {
-    a.route = *route;
-    return t.lscale ? launch_stream<kModeGateUp, 6, 4, false, true, true, true, true>(a, ncolblk, max_slots, s)
-                    : launch_stream<kModeGateUp, 6, 4, false, true, true, false, true>(a, ncolblk, max_slots, s);
+  if (self_args != nullptr) {
+    self_args_into(a, *self_args, self_mode);
+    if (self_mode == kSelfRoute)
+      return t.lscale ? launch_stream<kModeGateUp, 6, 4, false, true, true, true, kSelfRoute>(a, ncolblk, max_slots, s)
+                      : launch_stream<kModeGateUp, 6, 4, false, true, true, false, kSelfRoute>(a, ncolblk, max_slots, s);
+    return t.lscale ? launch_stream<kModeGateUp, 6, 4, false, true, true, true, kSelfPlan>(a, ncolblk, max_slots, s)
+                    : launch_stream<kModeGateUp, 6, 4, false, true, true, false, kSelfPlan>(a, ncolblk, max_slots, s);
   }
   if (mode == kModeGateUp) {
     if (t.ksplit == 4) {

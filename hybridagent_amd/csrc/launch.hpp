@@ -30,6 +30,11 @@ struct TopkSortArgs {
   int BM, slot_rows;
 };
 
+// The decode gate_up launch's own plan (k_decode's SELF): none (it reads the
+// plan), kSelfRoute (one token: it also routes), kSelfPlan (it sorts a
+// finished top-k itself).
+enum DecodeSelf { kSelfNone = 0, kSelfRoute = 1, kSelfPlan = 2 };
+
 // Arguments of the decode-shaped (few rows per weight matrix) MFMA kernel.
 struct DecodeArgs {
   const uint16_t* act;        // activation rows (bf16), row length K
@@ -57,9 +62,12 @@ struct DecodeArgs {
   // per workgroup)
   int u_guess, wps_guess, per_guess;
   uint32_t slot_magic;
-  // gate_up at one token routing in its own launch (launch_decode's route):
-  // the top-k + sort's arguments, run by the launch's last workgroup
+  // the gate_up launch's own plan (launch_decode's self_args / self_mode):
+  // the top-k + sort's arguments (kSelfPlan: idx_out is the finished top-k
+  // it reads), the plan written by the launch's last workgroup, and
+  // floor(2^32 / M) + 1 (k-major position -> slot j, exact below 2^16)
   TopkSortArgs route;
+  uint32_t plan_m_magic;
 };
 
 // Arguments of the prefill-shaped grouped GEMM (kernels_prefill.hip).
@@ -126,13 +134,16 @@ struct Bf16ExpertArgs {
 
 hipError_t launch_dequant(const int32_t* packed, const uint16_t* scale, uint16_t* out,
                           int64_t rows, int K, int G, hipStream_t s);
-// max_slots: upper bound of active experts (1 for dense).  route (gate_up at
-// one token, nullable): the launch also runs the top-k + sort of the router's
-// K-split partials (TopkSortArgs, M = 1) and each workgroup finds its expert
-// itself; hipErrorNotSupported (nothing launched) where
-// decode_route_supported says no.
-hipError_t launch_decode(int mode, DecodeArgs a, int max_slots, hipStream_t s, const TopkSortArgs* route = nullptr);
-bool decode_route_supported(bool tiled, int64_t H, int64_t I, int64_t G, int64_t E, int64_t topk);
+// max_slots: upper bound of active experts (1 for dense).  self_args
+// (gate_up, nullable) with self_mode (DecodeSelf): the launch works out its
+// own plan and its last workgroup writes it (kSelfRoute: the routing too,
+// from the router's K-split partials, TopkSortArgs with M = 1; kSelfPlan:
+// from the finished top-k in idx_out); hipErrorNotSupported (nothing
+// launched) where decode_self_supported or the launcher says no.
+hipError_t launch_decode(int mode, DecodeArgs a, int max_slots, hipStream_t s, const TopkSortArgs* self_args = nullptr,
+                         int self_mode = kSelfNone);
+bool decode_self_supported(int self_mode, bool tiled, int64_t M, int64_t H, int64_t I, int64_t G, int64_t E,
+                           int64_t topk);
 // Tiled expert weights for the decode streamers (kernels_decode.hip): bytes
 // per expert of the tiled copy of the gate_up (mode kModeGateUp) or down
 // weights for group size G (0: no tiled form for H, I, G), whether that copy
@@ -142,7 +153,7 @@ bool tiled_decode_needs_scale(int G);
 hipError_t launch_tile_decode(int mode, const int32_t* packed, const uint16_t* scale, int E, int H, int I, int G,
                               int32_t* tiled, hipStream_t s);
 hipError_t launch_decode_tiled(int mode, DecodeArgs a, int max_slots, hipStream_t s,
-                               const TopkSortArgs* route = nullptr);
+                               const TopkSortArgs* self_args = nullptr, int self_mode = kSelfNone);
 // x = bf16(h + delta) -> h_out (delta may be null), y = bf16(rms_norm(x) * w)
 hipError_t launch_add_rms_norm(const uint16_t* h, const uint16_t* delta, const uint16_t* w,
                                uint16_t* h_out, uint16_t* y, int64_t M, int H, float eps,
