@@ -340,10 +340,13 @@ def test_moe_small_groups(dev, G):
     assert margin(f"moe small shape G={G} M={M}", oracle.max_abs_rel(_np(y), ref)) <= TOL
 
 
-@pytest.mark.parametrize("M", [1, 8, 64, 100])
+@pytest.mark.parametrize("M", [1, 2, 3, 5, 8, 9, 24, 64, 100])
 def test_layer_forward_router_plus_experts(dev, moe128, M):
     # router + experts in one call: routing equals the standalone router's,
     # output equals moe_forward on that routing and the oracle within tolerance
+    # (M = 1: the gate_up launch routes; 2 <= M <= 8: the top-k + sort launch;
+    # larger: the gate_up launch sorts the top-k itself where its wide form
+    # runs, else the sort launch does)
     cpu, gpu = moe128
     h, rw = _router_inputs(M, seed=500 + M)
     x = synth.activations(M, H, seed=600 + M)
