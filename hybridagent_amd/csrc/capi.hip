@@ -123,7 +123,7 @@ MoeLayout moe_layout(void* ws, int64_t M, int64_t k, int64_t E, int64_t H, int64
   MoeLayout L;
   L.offsets = c.take<int32_t>(E + 1);
   L.desc = c.take<int32_t>(4 * plan_desc_capacity(M, k, E));
-  L.counters = c.take<int32_t>(2);
+  L.counters = c.take<int32_t>(4);
   L.queues = c.take<int32_t>(kPrefillQueueInts);
   L.sorted_pos = c.take<int32_t>(M * k);
   L.tiles = c.take<int32_t>(M * k / kPrefillBM + E + 1);
@@ -357,7 +357,7 @@ int moe_topk_from_logits(const uint16_t* logits, const uint16_t* per_expert_scal
 
 size_t moe_sort_workspace_bytes(int64_t M, int64_t top_k, int64_t E) {
   if (M <= 0 || top_k <= 0 || E <= 0) return 0;
-  return round256(size_t(E) * 16) + round256(8) + round256(size_t(M * top_k / kPrefillBM + E + 1) * 4) +
+  return round256(size_t(E) * 16) + round256(16) + round256(size_t(M * top_k / kPrefillBM + E + 1) * 4) +
          round256(size_t(sort_blocks(M * top_k)) * E * 4);
 }
 
@@ -373,7 +373,7 @@ int moe_sort_permute(const int64_t* topk_idx, int64_t M, int64_t top_k, int64_t 
   if (workspace == nullptr || workspace_bytes < need) return W4A16_ERR_WORKSPACE;
   Carve c(workspace);
   int32_t* desc = c.take<int32_t>(4 * E);
-  int32_t* counters = c.take<int32_t>(2);
+  int32_t* counters = c.take<int32_t>(4);
   int32_t* tiles = c.take<int32_t>(M * top_k / kPrefillBM + E + 1);
   int32_t* blockcnt = c.take<int32_t>(size_t(sort_blocks(M * top_k)) * E);
   hipStream_t s = static_cast<hipStream_t>(stream);

@@ -350,6 +350,8 @@ void k_decode(DecodeArgs a) {
         r.offsets[E] = poff[E];
         r.counters[0] = U;
         r.counters[1] = 0;
+        r.counters[2] = 0;
+        r.counters[3] = 0;
       }
       return;
     }

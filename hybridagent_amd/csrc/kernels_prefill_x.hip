@@ -14,7 +14,11 @@
 // the chip.  Each of the eight wavefronts owns 32
 // weight rows (gate_up: 16 gate + their 16 up rows) for all the item's
 // rows: MB m-blocks of v_mfma_f32_32x32x16_bf16 accumulators (MB = 8 for
-// 256 rows; 4, 2, 1 for segment tails of up to 128, 64, 32 rows).
+// 256 rows; 4, 2, 1 for segment tails of up to 128, 64, 32 rows).  A tail of
+// at most 32 rows (most of them are whole experts of few rows) is a wide
+// item of three n-tiles: its stages carry three n-tiles' weights, so the
+// per-stage cost that such an item pays for little MFMA work is paid once
+// for three n-tiles, and each output is the one-n-tile item's bit for bit.
 //
 // Per 64-wide k stage, all by direct global -> LDS loads of 16 bytes per
 // lane (one instruction fills 1 KiB).  Every load of the main loop is one,
@@ -85,6 +89,17 @@ constexpr int kPxLds = kPxQSlot + 16;
 // fewer rows), then one B-word load and one scale-chunk load (wavefronts
 // 0..3)
 constexpr int kPxNA = 4;
+// Wide items: a segment tail of at most kPrefillTinyRows rows (one m-block,
+// listed last by the sort) takes kPxWide n-tiles at once, so its per-stage
+// latency is paid once for three n-tiles' weights.  Its stage holds 32
+// activation rows (4 KiB of the A region); the other n-tiles' words and
+// scale chunks go in the rest of that region: n-tile b of the item has its
+// words at px_wide_b(b) and its scale chunks at px_wide_s(b).
+constexpr int kPxWide = 3;
+constexpr int px_wide_b(int b) { return b == 0 ? kPxBOff : 4096 + 8192 * (b - 1); }
+constexpr int px_wide_s(int b) { return b == 0 ? kPxSOff : 4096 + 8192 * (kPxWide - 1) + 4096 * (b - 1); }
+static_assert(px_wide_s(kPxWide - 1) + 4096 <= kPxBOff, "a wide stage's blocks fit in the A region");
+static_assert(kPrefillTinyRows == 32, "a wide item is one 32-row m-block");
 
 
 // s_waitcnt immediate for vmcnt <= n with expcnt and lgkmcnt not waited for
@@ -126,16 +141,36 @@ __device__ __forceinline__ f32x16_t mfma32x(u32x4_t a, u32x4_t b, f32x16_t c) {
 }  // namespace
 
 
-// One work item: (m-tile, n-tile) and what that fixes.
+// One work item: (m-tile, first n-tile, n-tiles nb) and what that fixes.
 struct PxItem {
-  int nt, e, seg0, nrows, mb;
+  int nt, e, seg0, nrows, mb, nb;
 };
 
-// Item `item` of a queue whose m-tiles are tile list entries x0, x0 + xs, ...
-__device__ __forceinline__ PxItem px_item_info(const PrefillArgs& a, int x0, int xs, int item) {
+// Item `item` of a queue whose m-tiles are tile list entries x0, x0 + xs, ...:
+// m-tiles [t0, t1) of the queue (the tails of at most kPrefillTinyRows rows)
+// have n_wide items of kPxWide n-tiles each (n-tiles past the matrix compute
+// on its last rows and store nothing), the others n_nt items of one n-tile.
+__device__ __forceinline__ PxItem px_item_info(const PrefillArgs& a, int x0, int xs, int t0, int t1, int n_wide,
+                                               int item) {
   PxItem it;
-  const int lm = item / a.n_nt;
-  it.nt = item - lm * a.n_nt;
+  const int i0 = t0 * a.n_nt, i1 = i0 + (t1 - t0) * n_wide;
+  int lm;
+  it.nb = 1;
+  if (item < i0) {
+    lm = item / a.n_nt;
+    it.nt = item - lm * a.n_nt;
+  } else if (item < i1) {
+    const int j = item - i0;
+    const int q = j / n_wide;
+    lm = t0 + q;
+    it.nt = kPxWide * (j - q * n_wide);
+    it.nb = kPxWide;
+  } else {
+    const int j = item - i1;
+    const int q = j / a.n_nt;
+    lm = t1 + q;
+    it.nt = j - q * a.n_nt;
+  }
   const int tile = ld_uniform(a.tiles, x0 + xs * lm);
   it.e = tile >> 16;
   it.seg0 = ld_uniform(a.offsets, it.e) + (tile & 0xFFFF) * kPxBM;
@@ -252,6 +287,93 @@ __device__ __forceinline__ void px_issue_table(const PrefillArgs& a, unsigned ch
   const int half = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 1;
   px_dma16(make_rsrc(a.sorted_pos, (uint32_t)a.rows_total * 4u), 4 * ((tseg & ~3) + 256 * half + 4 * lane), 0,
            smem + kPxTable + 1024 * half);
+}
+
+// A wide item's load sources: wavefronts 0..3 bring its 32 activation rows
+// (one A load each, as a one-m-block item's); every wavefront the words of
+// its 32 tile rows of each n-tile, wavefronts 0..3 the scale chunks of each.
+struct PxLoadsW {
+  __amdgpu_buffer_rsrc_t wsrc, ssrc;
+  int avoff, bstride;
+  int bvoff[kPxWide], svoff[kPxWide];
+  int na, n;
+};
+
+template <int MODE>
+__device__ __forceinline__ PxLoadsW px_loads_w(const PrefillArgs& a, const PxItem& it, const unsigned char* smem) {
+  PxLoadsW L;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int* table = reinterpret_cast<const int*>(smem + kPxTable);
+  const bool areal = wave < 4;
+  const int r = 8 * wave + (lane >> 3);
+  const int rr = min(r, it.nrows - 1);
+  const int64_t src = MODE == kModeGateUp ? (areal ? table[(it.seg0 & 3) + rr] : 0) / a.topk : it.seg0 + rr;
+  const int chunk = (lane & 7) ^ ((r >> 1) & 7);
+  L.avoff = areal ? (int)(src * a.lda * 2) + 16 * chunk : 0;
+  L.na = areal ? 1 : 0;
+  L.n = L.na + kPxWide + (wave < 4 ? kPxWide : 0);
+  const int K2 = a.K >> 1;
+  if (a.wt != nullptr) {
+    // tiled copy: n-tiles past the expert's read past the descriptor's range
+    // (zeros); their results are not stored
+    const int nkt = a.K / kPxKT;
+    const int64_t per_e = (int64_t)a.n_nt * nkt * 2048;
+    L.wsrc = make_rsrc(reinterpret_cast<const uint32_t*>(a.wt) + (int64_t)it.e * per_e, (uint32_t)(per_e * 4));
+#pragma unroll
+    for (int b = 0; b < kPxWide; ++b) L.bvoff[b] = (it.nt + b) * nkt * 8192 + wave * 1024 + 16 * lane;
+    L.bstride = 8192;
+  } else {
+    L.wsrc = make_rsrc(reinterpret_cast<const uint32_t*>(a.wp) + (int64_t)it.e * a.N * (a.K >> 3),
+                       (uint32_t)a.N * K2);
+#pragma unroll
+    for (int b = 0; b < kPxWide; ++b)
+      L.bvoff[b] = px_weight_row<MODE>(a, it.nt + b, 32 * wave + (lane >> 1)) * K2 + 16 * (lane & 1);
+    L.bstride = kPxKT / 2;
+  }
+  const uintptr_t sbase = reinterpret_cast<uintptr_t>(a.ws + (int64_t)it.e * a.N * a.ng);
+  L.ssrc = make_rsrc(reinterpret_cast<const void*>(sbase & ~uintptr_t(15)), (uint32_t)a.N * a.ng * 2u + 16u);
+#pragma unroll
+  for (int b = 0; b < kPxWide; ++b)
+    L.svoff[b] = wave < 4 ? (int)(sbase & 15) + px_weight_row<MODE>(a, it.nt + b, 64 * wave + lane) * a.ng * 2 : 0;
+  return L;
+}
+
+// Part `part` (0..3, issued before MFMA step `part`) of a wide item's stage
+// kt into ring slot `slot`: part 0 the A load, part p < kPxWide the words of
+// n-tile p, part p >= 1 the scale chunks of n-tile p - 1.
+__device__ __forceinline__ void px_issue_w(const PrefillArgs& a, const PxLoadsW& L, unsigned char* smem, int kt,
+                                           int slot, int part) {
+  static_assert(kPxWide <= 3, "four parts carry the loads of three n-tiles");
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  unsigned char* st = smem + slot * kPxStageBytes;
+  if (part == 0 && L.na > 0)
+    px_dma16(make_rsrc(a.act, (uint32_t)a.act_bytes), L.avoff, kt * (kPxKT * 2), st + wave * 1024);
+  if (part < kPxWide) px_dma16(L.wsrc, L.bvoff[part < kPxWide ? part : 0], kt * L.bstride, st + px_wide_b(part) + wave * 1024);
+  if (part >= 1 && part <= kPxWide && wave < 4) {
+    const int b = part >= 1 ? part - 1 : 0;
+    const int gpair = ((kt * kPxKT) >> a.gshift) & ~1;
+    px_dma16(L.ssrc, (L.svoff[b] + 2 * gpair) & ~15, 0, st + px_wide_s(b) + 1024 * wave);
+  }
+}
+
+// Issues an item's stages 0 and 1 into ring slots q0 and q0 + 1; returns the
+// wavefront's loads per stage.  Gate_up: the LDS table holds the item's rows.
+template <int MODE>
+__device__ __forceinline__ int px_issue_first(const PrefillArgs& a, const PxItem& it, unsigned char* smem, int q0) {
+  const int q1 = q0 == kPxStages - 1 ? 0 : q0 + 1;
+  if (it.nb > 1) {
+    const PxLoadsW L = px_loads_w<MODE>(a, it, smem);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) px_issue_w(a, L, smem, 0, q0, p);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) px_issue_w(a, L, smem, 1, q1, p);
+    return L.n;
+  }
+  const PxLoads L = px_loads<MODE>(a, it, smem);
+  px_issue_all(a, L, smem, 0, q0);
+  px_issue_all(a, L, smem, 1, q1);
+  return L.n;
 }
 
 // Multiply one item.  On entry its stages 0 and 1 are issued into slots p0
@@ -417,14 +539,7 @@ __device__ __forceinline__ int px_run(const PrefillArgs& a, unsigned char* smem,
        });
   // every wavefront is past the last barrier: the next item's first two
   // stages go into the slots of this item's stages nkt - 3 and nkt - 2
-  int n_next = 0;
-  if (has_next) {
-    const PxLoads ln = px_loads<MODE>(a, nx, smem);
-    const int q0 = (p0 + nkt) % kPxStages;
-    px_issue_all(a, ln, smem, 0, q0);
-    px_issue_all(a, ln, smem, 1, q0 == kPxStages - 1 ? 0 : q0 + 1);
-    n_next = ln.n;
-  }
+  const int n_next = has_next ? px_issue_first<MODE>(a, nx, smem, (p0 + nkt) % kPxStages) : 0;
   if (!work) return n_next;
 
   // ---- epilogue.  Lane l holds, for activation row 32 mb + c of block mb,
@@ -478,10 +593,150 @@ __device__ __forceinline__ int px_run(const PrefillArgs& a, unsigned char* smem,
   return n_next;
 }
 
+// Multiply one wide item (kPxWide n-tiles of a tail of at most 32 rows), in
+// px_run's stage protocol.  Each n-tile's outputs are px_run<MODE, 1>'s for
+// that n-tile bit for bit: the same MFMA on the same operands, one k step
+// after the other.
+template <int MODE>
+__device__ __forceinline__ int px_run_w(const PrefillArgs& a, unsigned char* smem, const PxItem& it,
+                                        const PxItem& nx, bool has_next, int p0, int n_inflight,
+                                        int* fetch_q) {
+  constexpr int NB = kPxWide;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nkt = a.K / kPxKT;
+  const int h = lane >> 5;
+  const int c = lane & 31;
+  const int gshift = a.gshift;
+  const int nt0 = it.nt, seg0 = it.seg0, nrows = it.nrows;
+
+  int aoff[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) aoff[s] = c * 128 + 16 * ((4 * h + s) ^ ((c >> 1) & 7));
+  int boff[NB], soffb[NB], srow2[NB];
+  const int sb15 = (int)(reinterpret_cast<uintptr_t>(a.ws + (int64_t)it.e * a.N * a.ng) & 15);
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    boff[b] = px_wide_b(b) + (32 * wave + c) * 32 + 16 * h;
+    soffb[b] = px_wide_s(b) + (32 * wave + c) * 16;
+    srow2[b] = sb15 + px_weight_row<MODE>(a, nt0 + b, 32 * wave + c) * a.ng * 2;
+  }
+  f32x16_t acc[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int q = 0; q < 16; ++q) acc[b][q] = 0.f;
+  auto scale_of = [&](int t, uint32_t sp) -> float {
+    const int g = (t * kPxKT + 32 * h) >> gshift;
+    const int sel = g - (((t * kPxKT) >> gshift) & ~1);  // 0 or 1
+    return bf16_bits_to_f32((sp >> (16 * sel)) & 0xFFFFu);
+  };
+  auto stage_ptr = [&](int sl) -> const unsigned char* { return smem + sl * kPxStageBytes; };
+  auto no_hook = [] {};
+  auto wait_and_sync = [&](int n, auto hook) {
+    __builtin_amdgcn_sched_barrier(0);
+    px_wait_vm(n);
+    __builtin_amdgcn_sched_barrier(0);
+    hook();
+    px_barrier();
+  };
+  const ExactRegs kr = exact_regs();
+
+  wait_and_sync(n_inflight, no_hook);  // stage 0 landed
+  int slot = p0;
+  int slot2 = p0 + 2 >= kPxStages ? p0 + 2 - kPxStages : p0 + 2;
+  // one k stage: read its words and scales, refill the slot stage t - 1 used
+  // (issue(slot2)) while multiplying, wait for stage t + 1 and meet
+  auto iter = [&](int t, int n, auto issue, auto hook) {
+    const unsigned char* st = stage_ptr(slot);
+    u32x4_t bw[NB];
+    ExactScale es[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      bw[b] = *reinterpret_cast<const u32x4_t*>(st + boff[b]);
+      const int so = soffb[b] + ((srow2[b] + 2 * (((t * kPxKT) >> gshift) & ~1)) & 15);
+      es[b] = exact_scale(scale_of(t, *reinterpret_cast<const uint32_t*>(st + so)));
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      issue(slot2, s);
+      const u32x4_t af = *reinterpret_cast<const u32x4_t*>(st + aoff[s]);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const uint32_t w = s == 0 ? bw[b].x : s == 1 ? bw[b].y : s == 2 ? bw[b].z : bw[b].w;
+        acc[b] = mfma32x(unpack_exact<false>(w, es[b], kr), af, acc[b]);
+      }
+    }
+    wait_and_sync(n, hook);  // stage t + 1 landed (stage t + 2 may still be loading)
+    slot = slot == kPxStages - 1 ? 0 : slot + 1;
+    slot2 = slot2 == kPxStages - 1 ? 0 : slot2 + 1;
+  };
+  {
+    const PxLoadsW lc = px_loads_w<MODE>(a, it, smem);
+    for (int t = 0; t + 2 < nkt; ++t)
+      iter(t, lc.n, [&](int sl, int p) { px_issue_w(a, lc, smem, t + 2, sl, p); }, no_hook);
+  }
+  const int tseg = MODE == kModeGateUp ? (has_next ? nx.seg0 : seg0) : seg0;
+  iter(nkt - 2, 1, [&](int, int p) {
+    if (p == 0) px_issue_table(a, smem, tseg);
+  }, no_hook);
+  const bool fetch = fetch_q != nullptr && wave == 0;  // wavefront-uniform
+  int fv = 0;
+  iter(nkt - 1, 0,
+       [&](int, int p) {
+         if (p == 0 && fetch && lane == 0) fv = __hip_atomic_fetch_add(fetch_q, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+       },
+       [&] {
+         if (fetch && lane == 0) *reinterpret_cast<int*>(smem + kPxQSlot) = fv;
+       });
+  const int n_next = has_next ? px_issue_first<MODE>(a, nx, smem, (p0 + nkt) % kPxStages) : 0;
+
+  // epilogue per n-tile, as px_run's for m-block 0 (n-tiles past the
+  // matrix, and gate_up columns past I, store nothing)
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const int nt = nt0 + b;
+    if (MODE == kModeGateUp) {
+      if (128 * nt + 16 * wave < a.I && c < nrows) {
+        uint16_t* orow = a.out + (int64_t)(seg0 + c) * a.ldo + 128 * nt + 16 * wave + 4 * h;
+#pragma unroll
+        for (int J = 0; J < 2; ++J) {
+          float hv[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float g = round_bf16(acc[b][4 * J + i]);
+            const float u = round_bf16(acc[b][4 * J + i + 8]);
+            hv[i] = round_bf16(gelu_tanh_f32(g)) * u;
+          }
+          *reinterpret_cast<uint2*>(orow + 8 * J) = make_uint2(pack_bf16x2(hv[0], hv[1]), pack_bf16x2(hv[2], hv[3]));
+        }
+      }
+    } else if (kPxBN * nt + 32 * wave < a.N) {
+      const int* table = reinterpret_cast<const int*>(smem + kPxTable);
+      unsigned char* ob = smem + kPxEpiOff + wave * kPxEpiBytes;
+#pragma unroll
+      for (int J = 0; J < 4; ++J)
+        *reinterpret_cast<uint2*>(ob + c * kPxEpiPitch + 2 * (8 * J + 4 * h)) =
+            make_uint2(pack_bf16x2(acc[b][4 * J], acc[b][4 * J + 1]), pack_bf16x2(acc[b][4 * J + 2], acc[b][4 * J + 3]));
+#pragma unroll
+      for (int itr = 0; itr < 2; ++itr) {
+        const int idx = lane + 64 * itr;
+        const int row = idx >> 2, q4 = idx & 3;
+        if (row < nrows) {
+          const u32x4_t v = *reinterpret_cast<const u32x4_t*>(ob + row * kPxEpiPitch + 16 * q4);
+          st16(a.out + (int64_t)table[(seg0 & 3) + row] * a.N + kPxBN * nt + 32 * wave + 8 * q4, v);
+        }
+      }
+    }
+  }
+  return n_next;
+}
+
 template <int MODE>
 __device__ __forceinline__ int px_dispatch(const PrefillArgs& a, unsigned char* smem, const PxItem& it,
                                            const PxItem& nx, bool has_next, int p0, int n_inflight,
                                            int* fetch_q) {
+  if (it.nb > 1) return px_run_w<MODE>(a, smem, it, nx, has_next, p0, n_inflight, fetch_q);
   if constexpr (MODE == kModeGateUp) {
     if (a.I - 128 * it.nt == 64 && it.mb >= 2) {
       // half n-tile: eight wavefronts on four wavefronts' columns
@@ -518,11 +773,16 @@ __global__ __launch_bounds__(kPxThreads) __attribute__((amdgpu_waves_per_eu(2, 2
 void k_prefill_x(PrefillArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int ntiles = ld_uniform(a.counters, 1);
+  const int tiny0 = ld_uniform(a.counters, 2), tiny1 = ld_uniform(a.counters, 3);  // the smallest tails
   constexpr bool kChip = MODE == kModeGateUp;  // one queue for the chip
   const int x0 = kChip ? 0 : (int)(blockIdx.x & 7);
   const int xs = kChip ? 1 : 8;
   const int n_local = kChip ? ntiles : (ntiles > x0 ? (ntiles - x0 + 7) >> 3 : 0);  // the queue's m-tiles
-  const int it_end = n_local * a.n_nt;
+  // the queue's m-tiles before list entry b
+  auto local = [&](int b) { return kChip ? b : (b > x0 ? (b - x0 + 7) >> 3 : 0); };
+  const int t0 = local(tiny0), t1 = local(tiny1);
+  const int n_wide = (a.n_nt + kPxWide - 1) / kPxWide;
+  const int it_end = (n_local - (t1 - t0)) * a.n_nt + (t1 - t0) * n_wide;
   const int P = kChip ? (int)gridDim.x : (int)(gridDim.x >> 3);
   int* const queue = a.queues != nullptr ? a.queues + x0 : nullptr;
   // the last workgroup to leave resets the counters for the next launch
@@ -541,7 +801,7 @@ void k_prefill_x(PrefillArgs a) {
     return;
   }
   const int nkt = a.K / kPxKT;
-  PxItem cur = px_item_info(a, x0, xs, item);
+  PxItem cur = px_item_info(a, x0, xs, t0, t1, n_wide, item);
   if (MODE == kModeGateUp) {
     // the first item's gathered rows into the table (nothing else in flight)
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -551,18 +811,12 @@ void k_prefill_x(PrefillArgs a) {
     __builtin_amdgcn_s_waitcnt(px_vm_wait(0));
     px_barrier();
   }
-  int n_inflight;
-  {
-    const PxLoads lc = px_loads<MODE>(a, cur, smem);
-    px_issue_all(a, lc, smem, 0, 0);
-    px_issue_all(a, lc, smem, 1, 1);
-    n_inflight = lc.n;
-  }
+  int n_inflight = px_issue_first<MODE>(a, cur, smem, 0);
   int p0 = 0;
   int nitem = item + P;
   for (;;) {
     const bool has_next = nitem < it_end;
-    const PxItem nxt = has_next ? px_item_info(a, x0, xs, nitem) : cur;
+    const PxItem nxt = has_next ? px_item_info(a, x0, xs, t0, t1, n_wide, nitem) : cur;
     // with a next item, take the index of the one after it during this item
     n_inflight = px_dispatch<MODE>(a, smem, cur, nxt, has_next, p0, n_inflight, has_next ? queue : nullptr);
     if (!has_next) break;

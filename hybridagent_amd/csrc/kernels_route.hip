@@ -618,11 +618,15 @@ hipError_t launch_router_topk(const float* partial, int ksplit, const uint16_t* 
 // expert sort: one workgroup of 1024 threads
 //   desc[4*u .. 4*u+3] = (expert, segment start, segment rows, 0) for the u-th
 //     active expert in ascending expert order
-//   counters[0] = number of active experts, counters[1] = number of prefill tiles
+//   counters[0] = number of active experts, counters[1] = number of prefill
+//     tiles, counters[2] / [3] = where the tails of at most kPrefillTinyRows
+//     rows start / end in the list
 //   tiles[i] = (expert << 16) | m_tile for the i-th (expert, m-tile) pair:
-//     first every tile of more than BM / 2 rows (expert order), then the
-//     segment tails of at most BM / 2 rows (expert order), so work queues
-//     that hand tiles out in list order start with the large ones
+//     first every tile of more than BM / 2 rows, then the segment tails of at
+//     most kPrefillTinyRows rows, then the other tails of at most BM / 2 rows
+//     (expert order each).  Work queues hand tiles out in list order, and the
+//     prefill GEMM takes the smallest tails three n-tiles at a time, which
+//     makes those items longer than the other tails'.
 // ---------------------------------------------------------------------------
 constexpr int kSortThreads = 1024;
 constexpr int kSortWaves = kSortThreads / 64;
@@ -659,25 +663,34 @@ __device__ __forceinline__ int write_plan(int c, int E, int32_t* __restrict__ of
   int nact;
   const int ns = plan_slots(c, SR);
   const int apos = block_excl_scan(ns, wsum, &nact);
-  // BM = 0: no m-tile list (the decode streamers read none)
+  // BM = 0: no m-tile list (the decode streamers read none); BM is uniform,
+  // so every thread takes the same branch to the scans' barriers
   const int rem = BM > 0 ? c % BM : 0;
-  const int nsmall = (rem > 0 && rem <= BM / 2) ? 1 : 0;
-  const int nbig = BM > 0 ? (c + BM - 1) / BM - nsmall : 0;
-  int nbig_tot, nsmall_tot;
-  const int bpos = block_excl_scan(nbig, wsum, &nbig_tot);
-  const int spos = block_excl_scan(nsmall, wsum, &nsmall_tot);
+  const int ntail = (rem > 0 && rem <= BM / 2) ? 1 : 0;
+  const int ntiny = (ntail && rem <= kPrefillTinyRows) ? 1 : 0;
+  const int nmid = ntail - ntiny;
+  const int nbig = BM > 0 ? (c + BM - 1) / BM - ntail : 0;
+  int nbig_tot = 0, nmid_tot = 0, ntiny_tot = 0, bpos = 0, mpos = 0, tpos = 0;
+  if (BM > 0) {
+    bpos = block_excl_scan(nbig, wsum, &nbig_tot);
+    mpos = block_excl_scan(nmid, wsum, &nmid_tot);
+    tpos = block_excl_scan(ntiny, wsum, &ntiny_tot);
+  }
   if (write) {
     if (tid < E) offsets[tid] = off;
     if (tid == 0) {
       offsets[E] = tot;
       counters[0] = nact;
-      counters[1] = nbig_tot + nsmall_tot;
+      counters[1] = nbig_tot + nmid_tot + ntiny_tot;
+      counters[2] = nbig_tot;
+      counters[3] = nbig_tot + ntiny_tot;
     }
     if (tid < E)
       for (int i = 0; i < ns; ++i) *reinterpret_cast<int4*>(desc + 4 * (apos + i)) = plan_desc(tid, off, c, SR, i);
     if (tid < E) {
       for (int i = 0; i < nbig; ++i) tiles[bpos + i] = (tid << 16) | i;
-      if (nsmall) tiles[nbig_tot + spos] = (tid << 16) | nbig;
+      if (ntiny) tiles[nbig_tot + tpos] = (tid << 16) | nbig;
+      if (nmid) tiles[nbig_tot + ntiny_tot + mpos] = (tid << 16) | nbig;
     }
   }
   return off;

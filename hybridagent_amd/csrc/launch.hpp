@@ -15,6 +15,9 @@ constexpr int kPrefillBM = 128;
 constexpr int kPfBN = 128;
 // m-tile of the exact-form prefill GEMM (kernels_prefill_x.hip)
 constexpr int kPrefillXBM = 256;
+// segment tails of at most this many rows (one 32-row MFMA block) are listed
+// apart, and the exact-form prefill GEMM takes them three n-tiles per item
+constexpr int kPrefillTinyRows = 32;
 // prefill work-queue counters in the MoE workspace: gate_up [0, 16), down [16, 32)
 constexpr int kPrefillQueueInts = 32;
 
@@ -79,7 +82,7 @@ struct PrefillArgs {
   const int32_t* sorted_pos;  // [M*k] rows t*k+j in expert-segment order
   const int32_t* offsets;     // [E+1] segment starts
   const int32_t* tiles;       // m-tiles (expert << 16 | tile index in the segment)
-  const int32_t* counters;    // [1] = number of m-tiles
+  const int32_t* counters;    // [1] = number of m-tiles, [2] / [3] = start / end of the tails of <= kPrefillTinyRows rows
   int N, K, G, ng, topk, I;
   int n_nt;                   // n-tiles per m-tile
   // exact-form kernel: row strides (elements) of act and of the gate_up output

@@ -152,7 +152,9 @@ __device__ __forceinline__ int4 plan_desc(int e, int off, int c, int SR, int i) 
 // The plan from the per-expert counts cnt[0..E), by one wavefront (lane l
 // owns the consecutive experts l*pe .. l*pe+pe-1, pe = ceil(E / 64) <= PE):
 // segment starts into offsets[] and run[] (LDS), the descriptors, the m-tile
-// list and the two counters -- the same output as write_plan, without
+// list and the counters -- the tiles in write_plan's order except that the
+// smallest tails are not listed apart (counters[2] = counters[3] =
+// counters[1]) -- without
 // workgroup barriers.  SR and BM are 0 or powers of two (shifts, not
 // divisions: this runs on the decode layer's critical path); BM = 0 writes
 // no tile list (counters[1] = 0), which the decode streamers do not read.
@@ -204,6 +206,8 @@ __device__ __forceinline__ void plan_wave(const int* cnt, int* run, int E, int32
     offsets[E] = ci;
     counters[0] = ai;
     counters[1] = bi + si;
+    counters[2] = bi + si;  // no tails listed apart
+    counters[3] = bi + si;
   }
 }
 
