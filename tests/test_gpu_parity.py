@@ -481,6 +481,36 @@ def test_moe_prefill_half_items(dev, h, i, G):
     assert torch.equal(y_sub.cpu(), y.cpu()[sub])
 
 
+@pytest.mark.parametrize("h,i,G", [(1024, 704, 128), (896, 960, 256)])
+def test_moe_prefill_wide_items_bit_identical(dev, h, i, G):
+    # an expert's tail of at most 32 rows runs as a wide item (three n-tiles
+    # per workgroup item), of more rows as a one-n-tile item: the same token
+    # rows give the same bits either way.  Batch A: expert 0 holds 20 rows
+    # (wide); batch B = A + 20 tokens on experts 0 and 7: expert 0 holds 40
+    # rows (one-n-tile item of two m-blocks)
+    e, k = 8, 2
+    wts = synth.moe_weights(e, h, i, G, seed=790)
+    counts = [20, 180, 100, 60, 33, 30, 97, 80]
+    M = sum(counts) // k
+    slots = np.repeat(np.arange(e), counts)
+    idx = np.stack([slots[:M], slots[M:]], 1)
+    assert (idx[:, 0] != idx[:, 1]).all()
+    idx = idx[np.random.default_rng(791).permutation(M)]
+    extra = np.tile(np.array([[0, 7]]), (20, 1))
+    idx_b = torch.from_numpy(np.concatenate([idx, extra])).long()
+    x_b = synth.activations(M + 20, h, seed=792)
+    w_b = torch.rand(M + 20, k, generator=torch.Generator().manual_seed(793)).float()
+    gpu = [wts.gate_up_packed.to(dev), wts.gate_up_scale.to(dev), wts.down_packed.to(dev), wts.down_scale.to(dev)]
+    print(f"prefill wide items h={h} i={i} G={G} M={M} / {M + 20}", flush=True)
+    y_a = _lib.moe_forward(x_b[:M].to(dev), idx_b[:M].to(dev), w_b[:M].to(dev), *gpu).cpu()
+    y_b = _lib.moe_forward(x_b.to(dev), idx_b.to(dev), w_b.to(dev), *gpu).cpu()
+    assert torch.equal(y_a, y_b[:M])
+    ref = oracle.moe_forward(_np(x_b), idx_b.numpy(), w_b.numpy(), wts.gate_up_packed.numpy(),
+                             _bits(wts.gate_up_scale), wts.down_packed.numpy(), _bits(wts.down_scale), G)
+    assert margin(f"moe prefill wide items h={h} i={i} G={G} M={M + 20} (all rows)",
+                  oracle.max_abs_rel(_np(y_b), ref)) <= TOL
+
+
 def test_moe_large_batch_untiled_shape(dev):
     # H not a multiple of 128 / I not a multiple of 64: large batches stay on
     # the streaming kernels and must still match
